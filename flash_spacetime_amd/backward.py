@@ -1,0 +1,90 @@
+"""Deterministic fused backward of spacetime-bias attention.
+
+Mirrors the reference launcher `flash_spacetime_backward`
+(src/flash_spacetime/backward.py:488-630): same arguments and return
+value `(dq, dk, dv, dW, db)`. The host prologue (u, w~ = dO W, dO.b), both
+kernels and the host epilogue (dq projection, dW, db) run inside the HIP
+library; the softmax row term is formed in-kernel as
+D = sum(p * dp) / sum(p) from the very p and dp that build dS, so
+rowsum(dS) vanishes by construction (backward.py:23-32, 371-377).
+"""
+
+from __future__ import annotations
+
+from typing import Optional, Tuple
+
+import torch
+from torch import Tensor
+
+from . import _lib
+from .forward import _Prepared
+
+
+def _run_backward(dims, q, k, v, pos4, w32, b32, lens, lse, grad_out, scale, vec_shape,
+                  rowsum: Optional[Tensor] = None):
+    lib = _lib.load()
+    _lib.require_gpu(grad_out)
+    do = grad_out.to(q.dtype).contiguous()
+    if do.shape != q.shape:
+        raise ValueError(f"grad_out must have the shape of the output {tuple(q.shape)}")
+    dq = torch.empty_like(q)
+    dk = torch.empty_like(k)
+    dv = torch.empty_like(v)
+    dw = torch.empty(w32.shape, device=q.device, dtype=torch.float32)
+    db = torch.empty(q.shape[-1], device=q.device, dtype=torch.float32) if b32 is not None else None
+    ws_bytes = lib.fst_backward_workspace_bytes(*dims)
+    ws = torch.empty(max(ws_bytes, 1), device=q.device, dtype=torch.uint8)
+    with torch.cuda.device(q.device):
+        rc = lib.fst_backward(
+            *dims,
+            _lib.ptr(q), _lib.ptr(k), _lib.ptr(v), _lib.ptr(pos4), _lib.ptr(w32), _lib.ptr(b32),
+            _lib.ptr(lens), _lib.ptr(lse), _lib.ptr(do), scale,
+            _lib.ptr(dq), _lib.ptr(dk), _lib.ptr(dv), _lib.ptr(dw), _lib.ptr(db), _lib.ptr(rowsum),
+            _lib.ptr(ws), ws_bytes, _lib.stream_handle(q.device),
+        )
+    _lib.check(rc, "flash_spacetime_backward")
+    return dq, dk, dv, dw, db
+
+
+def flash_spacetime_backward(
+    q: Tensor,
+    k: Tensor,
+    v: Tensor,
+    feats: Tensor,
+    weight: Tensor,
+    bias: Optional[Tensor],
+    seqlens: Optional[Tensor],
+    lse: Tensor,
+    grad_out: Tensor,
+    scale: Optional[float] = None,
+    use_attn_bias: bool = True,
+    use_activation_bias: bool = True,
+    block_m: int = 16,
+    block_n: int = 16,
+    num_warps: int = 8,
+    num_stages: int = 1,
+    cu_seqlens: Optional[Tensor] = None,
+    rowsum: Optional[Tensor] = None,
+) -> Tuple[Tensor, Tensor, Tensor, Tensor, Optional[Tensor]]:
+    """Deterministic backward from the saved lse; returns (dq, dk, dv, dW, db).
+
+    Gradients come back in the input dtypes (dW in the weight dtype, db in
+    the bias dtype, or None without a bias). Upstream gradients on padding
+    rows are ignored (backward.py:526-532). `rowsum`, if given (float32,
+    shaped like lse), receives sum_j dS_ij per row and head. The Triton
+    tuning arguments are accepted and ignored.
+    """
+    del block_m, block_n, num_warps, num_stages
+    prep = _Prepared(q, k, v, feats, weight, bias, seqlens, scale, use_attn_bias,
+                     use_activation_bias, cu_seqlens)
+    dq, dk, dv, dw, db = _run_backward(
+        prep.dims(), prep.q, prep.k, prep.v, prep.pos4, prep.weight, prep.bias, prep.lens,
+        lse.to(torch.float32).contiguous(), grad_out, prep.scale, prep.vec_shape(), rowsum,
+    )
+    return (
+        dq,
+        dk,
+        dv,
+        dw.to(weight.dtype),
+        db.to(bias.dtype) if (db is not None and bias is not None) else db,
+    )

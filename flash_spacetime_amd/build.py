@@ -1,0 +1,85 @@
+"""Build the gfx950 HIP library `libflash_spacetime.so` in the package directory.
+
+Every kernel instance family is its own translation unit so hipcc runs them
+in parallel; the objects are linked into one shared library whose C ABI is
+declared in include/flash_spacetime.h. Usage: python -m flash_spacetime_amd.build
+"""
+
+from __future__ import annotations
+
+import os
+import shutil
+import subprocess
+import sys
+from concurrent.futures import ThreadPoolExecutor
+from pathlib import Path
+
+PKG = Path(__file__).resolve().parent
+CSRC = PKG / "csrc"
+BUILD = CSRC / "_build"
+LIB = PKG / "libflash_spacetime.so"
+
+ARCH = os.environ.get("FST_OFFLOAD_ARCH", "gfx950")
+HIPCC = os.environ.get("HIPCC", shutil.which("hipcc") or "/opt/rocm/bin/hipcc")
+FLAGS = [
+    f"--offload-arch={ARCH}",
+    "-O3",
+    "-std=c++17",
+    "-fPIC",
+    "-Wall",
+    "-Wno-unused-function",
+    # Packed fp32 VALU forms are kept out of the device code.
+    "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
+]
+
+DTYPES = {"bf16": "bf16", "f32": "float"}
+HEAD_DIMS = (16, 32, 48, 64)
+
+
+def _units():
+    units = [("capi", CSRC / "fst_capi.hip", [])]
+    for tag, ctype in DTYPES.items():
+        for d in HEAD_DIMS:
+            name = f"{tag}_{d}"
+            defs = [f"-DFST_T={ctype}", f"-DFST_D={d}", f"-DFST_NAME={name}"]
+            units.append((f"fwd_{name}", CSRC / "fst_fwd_inst.hip", defs))
+            units.append((f"bwd_{name}", CSRC / "fst_bwd_inst.hip", defs))
+    return [u for u in units if u[1].exists()]
+
+
+def _compile(unit):
+    name, src, defs = unit
+    obj = BUILD / f"{name}.o"
+    cmd = [HIPCC, *FLAGS, *defs, "-c", str(src), "-o", str(obj)]
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    out = "\n".join(
+        line for line in (res.stdout + res.stderr).splitlines()
+        if "packed-fp32-ops" not in line
+    )
+    return name, obj, res.returncode, out
+
+
+def build(jobs: int | None = None, verbose: bool = False) -> Path:
+    """Compile every unit (always) and link the shared library."""
+    BUILD.mkdir(parents=True, exist_ok=True)
+    units = _units()
+    jobs = jobs or min(len(units), max(1, min(16, os.cpu_count() or 1)))
+    with ThreadPoolExecutor(max_workers=jobs) as pool:
+        results = list(pool.map(_compile, units))
+    failed = [r for r in results if r[2] != 0]
+    for name, _, rc, out in results:
+        if out.strip() and (verbose or rc != 0):
+            print(f"--- {name} ---\n{out}", file=sys.stderr)
+    if failed:
+        raise RuntimeError("hipcc failed for: " + ", ".join(r[0] for r in failed))
+    tmp = LIB.with_suffix(".so.tmp")
+    cmd = [HIPCC, f"--offload-arch={ARCH}", "-shared", "-o", str(tmp), *(str(r[1]) for r in results)]
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        raise RuntimeError("link failed:\n" + res.stdout + res.stderr)
+    os.replace(tmp, LIB)
+    return LIB
+
+
+if __name__ == "__main__":
+    print(build(verbose="-v" in sys.argv))

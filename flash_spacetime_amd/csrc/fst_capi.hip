@@ -1,0 +1,234 @@
+// C ABI of the flash-spacetime library (declared in include/flash_spacetime.h):
+// argument validation, the frequency table, the per-event work list and the
+// kernel launches. Nothing here allocates, frees or synchronises; all work
+// goes onto the caller's stream.
+#include <cmath>
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+
+#include "fst_kernels.h"
+
+namespace fst {
+
+static thread_local char g_last_error[512] = "";
+
+static int fail(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
+static int fail(int code, const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_last_error, sizeof(g_last_error), fmt, ap);
+  va_end(ap);
+  return code;
+}
+
+static size_t align_up(size_t x, size_t a) { return (x + a - 1) / a * a; }
+
+static bool supported_dim(int x) { return x == 16 || x == 32 || x == 48 || x == 64; }
+
+static int head_padding(int H) { return H <= 4 ? 4 : (H <= 8 ? 8 : (H <= 12 ? 12 : 16)); }
+
+// fp32 frequency ladder exp(-i * ln(1e4) / (C/2)) evaluated with the same
+// fp32 steps as the reference (reference.py:45-56): fp32 log of 1e4, fp32
+// division by C/2, fp32 product with i, exponential rounded to fp32.
+static void frequencies(int C, float* out) {
+  const float half = (float)C / 2.0f;
+  const float lg = (float)std::log(10000.0);
+  const float step = -(lg / half);
+  for (int i = 0; i < C / 2; ++i) {
+    const float arg = (float)i * step;
+    out[i] = (float)std::exp((double)arg);
+  }
+}
+
+static void freq_table(int C, FreqTable& ft) {
+  std::memset(&ft, 0, sizeof(ft));
+  float f[32];
+  frequencies(C, f);
+  const double inv2pi = 0.15915494309189533576888376337251;
+  for (int i = 0; i < C / 2; ++i) {
+    const double gd = (double)f[i] * inv2pi;
+    ft.ghi[i] = (float)gd;
+    ft.glo[i] = (float)(gd - (double)ft.ghi[i]);
+    // |x| <= 4096; v_sin_f32 / v_cos_f32 accept +-256 revolutions.
+    if (4096.0 * gd > 255.0) ft.reduce_mask |= 1u << i;
+  }
+}
+
+// Number of row blocks of each event and their prefix sum (one workgroup).
+// Padded events always get one block so that their padding rows are zeroed.
+__global__ __launch_bounds__(1024) void blkcum_kernel(const int32_t* lens, int packed, int B, int L, int T, int rows,
+                                                      int32_t* blkcum) {
+  __shared__ int buf[1024];
+  __shared__ int carry;
+  const int t = threadIdx.x;
+  if (t == 0) {
+    carry = 0;
+    blkcum[0] = 0;
+  }
+  __syncthreads();
+  EventSpec ev;
+  ev.lens = lens;
+  ev.packed = packed;
+  ev.B = B;
+  ev.L = L;
+  ev.T = T;
+  for (int base = 0; base < B; base += 1024) {
+    const int b = base + t;
+    int nb = 0;
+    if (b < B) {
+      int tok0, len;
+      event_range(ev, b, tok0, len);
+      nb = len > 0 ? (len + rows - 1) / rows : (packed ? 0 : 1);
+    }
+    buf[t] = nb;
+    __syncthreads();
+    for (int off = 1; off < 1024; off <<= 1) {
+      const int add = t >= off ? buf[t - off] : 0;
+      __syncthreads();
+      buf[t] += add;
+      __syncthreads();
+    }
+    if (b < B) blkcum[b + 1] = carry + buf[t];
+    __syncthreads();
+    if (t == 1023) carry += buf[1023];
+    __syncthreads();
+  }
+}
+
+typedef int (*fwd_dispatch_fn)(const FwdParams&, int, int, hipStream_t, int, bool, int*);
+
+static fwd_dispatch_fn fwd_table(int dtype, int D) {
+  if (dtype == FST_BF16) {
+    switch (D) {
+      case 16: return fwd_dispatch_bf16_16;
+      case 32: return fwd_dispatch_bf16_32;
+      case 48: return fwd_dispatch_bf16_48;
+      case 64: return fwd_dispatch_bf16_64;
+    }
+  } else if (dtype == FST_F32) {
+    switch (D) {
+      case 16: return fwd_dispatch_f32_16;
+      case 32: return fwd_dispatch_f32_32;
+      case 48: return fwd_dispatch_f32_48;
+      case 64: return fwd_dispatch_f32_64;
+    }
+  }
+  return nullptr;
+}
+
+static int check_common(int dtype, int flags, int B, int H, int L, int T, int D, int C) {
+  if (dtype != FST_BF16 && dtype != FST_F32) return fail(FST_EINVAL, "dtype must be FST_BF16 or FST_F32, got %d", dtype);
+  if (flags & ~(FST_ATTN_BIAS | FST_ACT_BIAS | FST_PACKED)) return fail(FST_EINVAL, "unknown flag bits 0x%x", flags);
+  if (B < 0 || L < 0 || T < 0) return fail(FST_EINVAL, "negative size (B=%d, L=%d, T=%d)", B, L, T);
+  if (H < 1 || H > 16) return fail(FST_EUNSUPPORTED, "heads must be in [1, 16], got %d", H);
+  if (!supported_dim(D)) return fail(FST_EUNSUPPORTED, "head_dim D must be one of 16, 32, 48, 64, got %d", D);
+  if (!supported_dim(C)) return fail(FST_EUNSUPPORTED, "channel count C must be one of 16, 32, 48, 64, got %d", C);
+  return FST_OK;
+}
+
+static size_t blkcum_bytes(int B) { return align_up((size_t)(B + 1) * sizeof(int32_t), 256); }
+
+}  // namespace fst
+
+using namespace fst;
+
+extern "C" {
+
+const char* fst_last_error(void) { return g_last_error; }
+
+const char* fst_version(void) { return "flash-spacetime-gfx950 0.1.0"; }
+
+void fst_frequencies(int C, float* out) {
+  if (C > 0 && C <= 64 && C % 2 == 0 && out) frequencies(C, out);
+}
+
+int fst_supported(int dtype, int H, int D, int C) {
+  if (check_common(dtype, 0, 0, H, 0, 0, D, C) != FST_OK) return 0;
+  int rows = 0;
+  FwdParams dummy;
+  std::memset(&dummy, 0, sizeof(dummy));
+  if (fwd_table(dtype, D)(dummy, head_padding(H), C, nullptr, 0, true, &rows) != FST_OK) return 0;
+  return rows > 0;
+}
+
+size_t fst_forward_workspace_bytes(int dtype, int flags, int B, int H, int L, int T, int D, int C) {
+  (void)dtype;
+  (void)flags;
+  (void)H;
+  (void)L;
+  (void)T;
+  (void)D;
+  (void)C;
+  return blkcum_bytes(B < 0 ? 0 : B);
+}
+
+int fst_forward(int dtype, int flags, int B, int H, int L, int T, int D, int C, const void* q, const void* k,
+                const void* v, const float* pos4, const float* weight, const float* bias, const int32_t* lens,
+                float scale, void* out, float* lse, void* workspace, size_t workspace_bytes, void* stream) {
+  g_last_error[0] = 0;
+  int rc = check_common(dtype, flags, B, H, L, T, D, C);
+  if (rc != FST_OK) return rc;
+  const bool packed = flags & FST_PACKED;
+  const bool use_w = flags & (FST_ATTN_BIAS | FST_ACT_BIAS);
+  const long rows_total = packed ? (long)T : (long)B * L;
+  if (B == 0 || rows_total == 0) return FST_OK;
+  if (!q || !k || !v || !lens || !out || !lse) return fail(FST_EINVAL, "null tensor pointer");
+  if (use_w && (!pos4 || !weight)) return fail(FST_EINVAL, "pos4 and weight are required when a bias flag is set");
+  if (!std::isfinite(scale)) return fail(FST_EINVAL, "scale must be finite");
+  const size_t need = fst_forward_workspace_bytes(dtype, flags, B, H, L, T, D, C);
+  if (!workspace || workspace_bytes < need)
+    return fail(FST_EWORKSPACE, "workspace of %zu bytes is smaller than the %zu required", workspace_bytes, need);
+
+  fwd_dispatch_fn fn = fwd_table(dtype, D);
+  const int HP = head_padding(H);
+  FwdParams prm;
+  std::memset(&prm, 0, sizeof(prm));
+  int rows = 0;
+  rc = fn(prm, HP, C, nullptr, 0, true, &rows);
+  if (rc != FST_OK || rows <= 0)
+    return fail(FST_EUNSUPPORTED, "no compiled kernel for dtype=%d H=%d D=%d C=%d", dtype, H, D, C);
+
+  int32_t* blkcum = reinterpret_cast<int32_t*>(workspace);
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  hipLaunchKernelGGL(blkcum_kernel, dim3(1), dim3(1024), 0, st, lens, packed ? 1 : 0, B, L, T, rows, blkcum);
+  if (hipGetLastError() != hipSuccess) return fail(FST_ELAUNCH, "work-list kernel launch failed");
+
+  prm.ev.lens = lens;
+  prm.ev.blkcum = blkcum;
+  prm.ev.pos4 = reinterpret_cast<const float4*>(pos4);
+  prm.ev.B = B;
+  prm.ev.H = H;
+  prm.ev.L = L;
+  prm.ev.T = T;
+  prm.ev.packed = packed ? 1 : 0;
+  prm.H = H;
+  prm.flags = flags;
+  prm.scale = scale;
+  prm.q = q;
+  prm.k = k;
+  prm.v = v;
+  prm.weight = weight;
+  prm.bias = bias;
+  prm.out = out;
+  prm.lse = lse;
+  freq_table(C, prm.freq);
+  const long grid = packed ? ((long)T + rows - 1) / rows + B : (long)B * ((L + rows - 1) / rows);
+  if (grid > 0x7fffffffL) return fail(FST_EUNSUPPORTED, "problem too large for one launch");
+  rc = fn(prm, HP, C, st, (int)grid, false, &rows);
+  if (rc != FST_OK) return fail(rc, "forward kernel launch failed (%s)", hipGetErrorString(hipGetLastError()));
+  return FST_OK;
+}
+
+size_t fst_backward_workspace_bytes(int dtype, int flags, int B, int H, int L, int T, int D, int C) {
+  return fst_forward_workspace_bytes(dtype, flags, B, H, L, T, D, C);
+}
+
+int fst_backward(int dtype, int flags, int B, int H, int L, int T, int D, int C, const void* q, const void* k,
+                 const void* v, const float* pos4, const float* weight, const float* bias, const int32_t* lens,
+                 const float* lse, const void* grad_out, float scale, void* dq, void* dk, void* dv, float* dweight,
+                 float* dbias, float* rowsum, void* workspace, size_t workspace_bytes, void* stream) {
+  return fail(FST_EUNSUPPORTED, "backward kernels are not built yet");
+}
+
+}  // extern "C"

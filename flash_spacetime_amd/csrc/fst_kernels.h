@@ -1,0 +1,293 @@
+// Shared kernel parameters and helpers of the flash-spacetime HIP library.
+#pragma once
+
+#include "fst_device.h"
+#include "../../include/flash_spacetime.h"
+
+namespace fst {
+
+// Event layout shared by every kernel: padded [B, H, L, X] with seqlens, or
+// packed [T, H, X] with cu_seqlens (forward.py:247-255, _tiles.py:80-117).
+struct EventSpec {
+  const int32_t* lens;    // seqlens [B] (padded) or cu_seqlens [B+1] (packed)
+  const int32_t* blkcum;  // [B+1] prefix sums of row blocks per event
+  const float4* pos4;     // [B*L] or [T] (x, y, z, t) fp32
+  int B, H, L, T, packed;
+};
+
+struct EventBlock {
+  int b, blk, len, tok0;
+};
+
+// Row addressing of one event. Offsets are in elements of a row of width X.
+struct RowAddr {
+  long base_row;  // row index of (token 0, head 0)
+  long hs, ts;    // row strides of head and token
+  long pos_base;
+  __device__ __forceinline__ long vec(int h, int i) const { return base_row + h * hs + i * ts; }
+  __device__ __forceinline__ long off(int h, int i, int width) const { return vec(h, i) * width; }
+  __device__ __forceinline__ float4 pos(const float4* p4, int i) const { return p4[pos_base + i]; }
+};
+
+// Token range of event b, clamped into the tensor so that malformed
+// lengths can never address memory outside it: padded lengths to [0, L],
+// packed offsets to [0, T] and non-decreasing.
+__device__ __forceinline__ void event_range(const EventSpec& ev, int b, int& tok0, int& len) {
+  if (ev.packed) {
+    int a = ev.lens[b], e = ev.lens[b + 1];
+    a = a < 0 ? 0 : (a > ev.T ? ev.T : a);
+    e = e < a ? a : (e > ev.T ? ev.T : e);
+    tok0 = a;
+    len = e - a;
+  } else {
+    const int l = ev.lens[b];
+    tok0 = 0;
+    len = l < 0 ? 0 : (l > ev.L ? ev.L : l);
+  }
+}
+
+// Work item of workgroup w: binary search of blkcum (blkcum[0] == 0).
+__device__ __forceinline__ bool locate_block(const EventSpec& ev, int w, EventBlock& eb) {
+  if (w >= ev.blkcum[ev.B]) return false;
+  int lo = 0, hi = ev.B;
+  while (hi - lo > 1) {
+    const int mid = (lo + hi) >> 1;
+    if (ev.blkcum[mid] <= w)
+      lo = mid;
+    else
+      hi = mid;
+  }
+  eb.b = lo;
+  eb.blk = w - ev.blkcum[lo];
+  event_range(ev, lo, eb.tok0, eb.len);
+  return true;
+}
+
+__device__ __forceinline__ RowAddr row_addr(const EventSpec& ev, const EventBlock& eb) {
+  RowAddr r;
+  if (ev.packed) {
+    r.base_row = (long)eb.tok0 * ev.H;
+    r.hs = 1;
+    r.ts = ev.H;
+    r.pos_base = eb.tok0;
+  } else {
+    r.base_row = (long)eb.b * ev.H * ev.L;
+    r.hs = ev.L;
+    r.ts = 1;
+    r.pos_base = (long)eb.b * ev.L;
+  }
+  return r;
+}
+
+struct FwdParams {
+  EventSpec ev;
+  int H, flags;
+  float scale;
+  const void *q, *k, *v;
+  const float* weight;  // [D, C]
+  const float* bias;    // [D] or null
+  void* out;
+  float* lse;
+  FreqTable freq;
+};
+
+template <typename T>
+struct VecOf;
+template <>
+struct VecOf<bf16> {
+  typedef bf16x8 type;
+  static __device__ __forceinline__ bf16x8 zero() {
+    bf16x8 z;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) z[e] = (bf16)0.f;
+    return z;
+  }
+};
+template <>
+struct VecOf<float> {
+  typedef f32x4 type;
+  static __device__ __forceinline__ f32x4 zero() { return zero4(); }
+};
+
+__device__ __forceinline__ float exp2f_fast(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// Four consecutive output elements from an fp32 quad.
+template <typename T>
+__device__ __forceinline__ void store4(T* p, const f32x4& v);
+template <>
+__device__ __forceinline__ void store4<bf16>(bf16* p, const f32x4& v) {
+  bf16x4 o;
+#pragma unroll
+  for (int r = 0; r < 4; ++r) o[r] = (bf16)v[r];
+  *reinterpret_cast<bf16x4*>(p) = o;
+}
+template <>
+__device__ __forceinline__ void store4<float>(float* p, const f32x4& v) {
+  *reinterpret_cast<f32x4*>(p) = v;
+}
+
+// ---------------------------------------------------------------------------
+// Channel operand of the u.E / w~.E contractions (K = C). Slot r of lane
+// group g in channel tile ct is channel 16ct + 4g + r -- the C layout of a
+// 16x16 fp32 MFMA tile -- so U computed on the MFMA feeds the next one
+// directly. bf16 contracts each tile with one 16x16x16 step; fp32 with four
+// 16x16x4 steps (step r covers channels 16ct + r + {0, 4, 8, 12}).
+// ---------------------------------------------------------------------------
+template <typename T, int C>
+struct CFrag;
+
+template <int C>
+struct CFrag<bf16, C> {
+  bf16x4 v[C / 16];
+  __device__ __forceinline__ void zero() {
+#pragma unroll
+    for (int ct = 0; ct < C / 16; ++ct)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) v[ct][r] = (bf16)0.f;
+  }
+  __device__ __forceinline__ void load(const bf16* p, int g) {
+#pragma unroll
+    for (int ct = 0; ct < C / 16; ++ct) v[ct] = *reinterpret_cast<const bf16x4*>(p + 16 * ct + 4 * g);
+  }
+  __device__ __forceinline__ void from_acc(const f32x4* acc) {
+#pragma unroll
+    for (int ct = 0; ct < C / 16; ++ct)
+#pragma unroll
+      for (int r = 0; r < 4; ++r) v[ct][r] = (bf16)acc[ct][r];
+  }
+};
+
+template <int C>
+struct CFrag<float, C> {
+  f32x4 v[C / 16];
+  __device__ __forceinline__ void zero() {
+#pragma unroll
+    for (int ct = 0; ct < C / 16; ++ct) v[ct] = zero4();
+  }
+  __device__ __forceinline__ void load(const float* p, int g) {
+#pragma unroll
+    for (int ct = 0; ct < C / 16; ++ct) v[ct] = *reinterpret_cast<const f32x4*>(p + 16 * ct + 4 * g);
+  }
+  __device__ __forceinline__ void from_acc(const f32x4* acc) {
+#pragma unroll
+    for (int ct = 0; ct < C / 16; ++ct) v[ct] = acc[ct];
+  }
+};
+
+template <int C>
+__device__ __forceinline__ f32x4 mma_c(const CFrag<bf16, C>& a, const CFrag<bf16, C>& b, f32x4 c) {
+#pragma unroll
+  for (int ct = 0; ct < C / 16; ++ct) c = mfma_x16(a.v[ct], b.v[ct], c);
+  return c;
+}
+template <int C>
+__device__ __forceinline__ f32x4 mma_c(const CFrag<float, C>& a, const CFrag<float, C>& b, f32x4 c) {
+#pragma unroll
+  for (int ct = 0; ct < C / 16; ++ct)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) c = mfma_f32(a.v[ct][r], b.v[ct][r], c);
+  return c;
+}
+
+// Projection of one row's heads onto the channels, in fp32 MFMA:
+//   acc[ct] = (x_row[h] * mult) @ W[:, 16ct..16ct+15]  as U^T[c, h]
+// lane (g, n = h) ends with channels 16ct + 4g + r. Step s contracts
+// d = (D/4) g + s (lane group g holds a contiguous quarter of the row).
+// x_row points at head 0 of the row; hstride = element stride between heads.
+template <typename T, int D, int C>
+__device__ __forceinline__ void project_row(const T* x_row, long hstride, bool valid, float mult,
+                                            const float* __restrict__ W, int g, int n, f32x4* acc) {
+  constexpr int Q = D / 4;
+  float xv[Q];
+  if (valid) {
+    const T* p = x_row + n * hstride + Q * g;
+#pragma unroll
+    for (int s = 0; s < Q; ++s) xv[s] = (float)p[s] * mult;
+  } else {
+#pragma unroll
+    for (int s = 0; s < Q; ++s) xv[s] = 0.f;
+  }
+#pragma unroll
+  for (int ct = 0; ct < C / 16; ++ct) {
+    f32x4 a = zero4();
+#pragma unroll
+    for (int s = 0; s < Q; ++s) a = mfma_f32(W[(Q * g + s) * C + 16 * ct + n], xv[s], a);
+    acc[ct] = a;
+  }
+}
+
+// Pair embedding of one (row, key) into an LDS row: channel f is
+// sin(x f_f), channel C/2 + f is cos(x f_f) (reference.py:82-84 order).
+template <typename T, int C>
+__device__ __forceinline__ void write_embedding(T* erow, float x, const FreqTable& ft) {
+  constexpr int F = C / 2;
+  float sv[F], cv[F];
+#pragma unroll
+  for (int f = 0; f < F; ++f)
+    sincos_rev<!is_bf16<T>::value>(x, ft.ghi[f], ft.glo[f], (ft.reduce_mask >> f) & 1u, sv[f], cv[f]);
+  if constexpr (is_bf16<T>::value) {
+    static_assert(F % 4 == 0, "C must be a multiple of 8");
+#pragma unroll
+    for (int f = 0; f < F; f += 4) {
+      bf16x4 a, b;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        a[e] = (bf16)sv[f + e];
+        b[e] = (bf16)cv[f + e];
+      }
+      *reinterpret_cast<bf16x4*>(erow + f) = a;
+      *reinterpret_cast<bf16x4*>(erow + F + f) = b;
+    }
+  } else {
+#pragma unroll
+    for (int f = 0; f < F; f += 4) {
+      *reinterpret_cast<f32x4*>(erow + f) = f32x4{sv[f], sv[f + 1], sv[f + 2], sv[f + 3]};
+      *reinterpret_cast<f32x4*>(erow + F + f) = f32x4{cv[f], cv[f + 1], cv[f + 2], cv[f + 3]};
+    }
+  }
+}
+
+// Zero the outputs of padding rows [max(row0, len), end) of a padded event,
+// where end is the block's last row, or L for the event's last block
+// (pad-row contract: forward.py:19-22, 288-304).
+template <typename T>
+__device__ __forceinline__ void zero_pad_rows(const EventSpec& ev, const EventBlock& eb, const RowAddr& ra,
+                                              int row0, int rows, int width, int tid, int nthreads, T* out,
+                                              float* vec_out, int vec_count) {
+  if (ev.packed) return;
+  const int nblk = eb.len > 0 ? (eb.len + rows - 1) / rows : 1;
+  const int first = row0 > eb.len ? row0 : eb.len;
+  const int end = (eb.blk == nblk - 1) ? ev.L : (row0 + rows < ev.L ? row0 + rows : ev.L);
+  if (first >= end) return;
+  const int nrows = end - first;
+  const int total = ev.H * nrows * width;
+  for (int idx = tid; idx < total; idx += nthreads) {
+    const int c = idx % width;
+    const int r = (idx / width) % nrows;
+    const int h = idx / (width * nrows);
+    out[ra.off(h, first + r, width) + c] = (T)0.f;
+  }
+  if (vec_out)
+    for (int idx = tid; idx < ev.H * nrows * vec_count; idx += nthreads) {
+      const int r = (idx / vec_count) % nrows;
+      const int h = idx / (vec_count * nrows);
+      vec_out[ra.vec(h, first + r) * vec_count + idx % vec_count] = 0.f;
+    }
+}
+
+// Forward dispatch per (dtype, D), one translation unit each
+// (fst_fwd_inst.hip). With query set, only reports the rows per workgroup
+// of the kernel that (HP, C) selects (0 = unsupported) in *rows.
+#define FST_DECL_FWD(NAME) \
+  int fwd_dispatch_##NAME(const FwdParams& prm, int HP, int C, hipStream_t stream, int grid, bool query, int* rows);
+FST_DECL_FWD(bf16_16)
+FST_DECL_FWD(bf16_32)
+FST_DECL_FWD(bf16_48)
+FST_DECL_FWD(bf16_64)
+FST_DECL_FWD(f32_16)
+FST_DECL_FWD(f32_32)
+FST_DECL_FWD(f32_48)
+FST_DECL_FWD(f32_64)
+#undef FST_DECL_FWD
+
+}  // namespace fst

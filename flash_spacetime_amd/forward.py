@@ -1,0 +1,305 @@
+"""Fused spacetime-bias attention: public operators and the forward launcher.
+
+Mirrors the operator interface of the reference (src/flash_spacetime/
+forward.py): `flash_spacetime_attention`, `flash_spacetime_attention_varlen`,
+the test-visible launcher `flash_spacetime_forward` and the autograd
+Function, with the same argument meaning, return values, padding contract
+(padding rows exactly zero) and errors. The work runs in the gfx950 HIP
+library through its C ABI; the projection of the pair embedding (`u = qt W`
+before the kernel, `o2 = A' W^T + b` after it, forward.py:279-346) is fused
+into the kernel. There is no other backend: a missing library or a CPU
+tensor raises.
+"""
+
+from __future__ import annotations
+
+import os
+from typing import Any, Optional, Tuple
+
+import torch
+from torch import Tensor
+
+from . import _lib
+
+_DTYPES = {torch.bfloat16: _lib.FST_BF16, torch.float32: _lib.FST_F32}
+
+
+def _next_pow2(n: int, floor: int = 16) -> int:
+    """Power-of-two bucket (reference _tiles.py:300-304); kept for API parity."""
+    p = floor
+    while p < n:
+        p *= 2
+    return p
+
+
+def lengths_from_mask(mask: Tensor, length: int) -> Tensor:
+    """`[B]` int32 valid lengths from a front-packed `[B, L]` padding mask.
+
+    Accepts a bool mask (True marks PADDING, torch.nn.MultiheadAttention's
+    `key_padding_mask` convention) or the float mask of the reference's
+    `float_padding_mask` (0 valid, -inf padding). The kernels address valid
+    tokens as a prefix of each event (forward.py:241-242), so a mask whose
+    valid tokens are not a prefix raises ValueError; the check reads one
+    flag back from the device.
+    """
+    if mask.dim() != 2 or mask.shape[1] != length:
+        raise ValueError(f"key_padding_mask must be [B, L={length}], got {tuple(mask.shape)}")
+    valid = ~mask if mask.dtype == torch.bool else (mask == 0)
+    seqlens = valid.sum(1, dtype=torch.int32)
+    prefix = torch.arange(length, device=mask.device)[None, :] < seqlens[:, None]
+    if not bool(torch.equal(prefix, valid)):
+        raise ValueError("key_padding_mask must be front-packed (valid tokens first in every event)")
+    return seqlens
+
+
+def _resolve_lengths(seqlens: Optional[Tensor], key_padding_mask: Optional[Tensor], batch: int,
+                     length: int) -> Tensor:
+    if key_padding_mask is not None and seqlens is not None:
+        raise ValueError("pass either seqlens or key_padding_mask, not both")
+    if key_padding_mask is not None:
+        return lengths_from_mask(key_padding_mask, length)
+    if seqlens is None:
+        raise ValueError("seqlens (or key_padding_mask) is required")
+    if seqlens.dim() == 2:
+        return lengths_from_mask(seqlens, length)
+    if seqlens.dim() != 1 or seqlens.shape[0] != batch:
+        raise ValueError(f"seqlens must be [B={batch}], got {tuple(seqlens.shape)}")
+    if seqlens.dtype.is_floating_point or seqlens.dtype == torch.bool:
+        raise ValueError(f"seqlens must be an integer tensor, got {seqlens.dtype}")
+    return seqlens
+
+
+class _Prepared:
+    """Validated, contiguous kernel operands shared by forward and backward."""
+
+    def __init__(self, q, k, v, feats, weight, bias, seqlens, scale, use_attn_bias,
+                 use_activation_bias, cu_seqlens):
+        for t in (q, k, v, feats, weight):
+            _lib.require_gpu(t)
+        if q.dtype not in _DTYPES:
+            raise ValueError(f"q must be bfloat16 or float32, got {q.dtype}")
+        if k.dtype != q.dtype or v.dtype != q.dtype:
+            raise ValueError("q, k and v must share one dtype")
+        self.packed = cu_seqlens is not None
+        if self.packed:
+            if q.dim() != 3:
+                raise ValueError(f"packed q must be [T, H, D], got {tuple(q.shape)}")
+            total, heads, dim = q.shape
+            self.batch = int(cu_seqlens.numel()) - 1
+            self.length = 0
+            self.tokens = total
+            lens = cu_seqlens
+            if feats.dim() != 2 or feats.shape[0] != total:
+                raise ValueError(f"packed feats must be [T={total}, F>=4], got {tuple(feats.shape)}")
+        else:
+            if q.dim() != 4:
+                raise ValueError(f"q must be [B, H, L, D], got {tuple(q.shape)}")
+            self.batch, heads, self.length, dim = q.shape
+            self.tokens = 0
+            lens = _resolve_lengths(seqlens, None, self.batch, self.length)
+            if feats.dim() != 3 or feats.shape[:2] != (self.batch, self.length):
+                raise ValueError(f"feats must be [B, L, F>=4], got {tuple(feats.shape)}")
+        if k.shape != q.shape or v.shape != q.shape:
+            raise ValueError("q, k and v must have the same shape")
+        if feats.shape[-1] < 4:
+            raise ValueError("feats needs at least 4 columns (x, y, z, t)")
+        if weight.dim() != 2 or weight.shape[0] != dim:
+            raise ValueError(f"weight must be [D={dim}, C] (nn.Linear layout), got {tuple(weight.shape)}")
+        c = weight.shape[1]
+        if c not in (16, 32, 48, 64):
+            raise ValueError(f"kernel supports C in (16, 32, 48, 64), got {c}")
+        if dim not in (16, 32, 48, 64):
+            raise ValueError(f"kernel supports head_dim in (16, 32, 48, 64), got {dim}")
+        if not 1 <= heads <= 16:
+            raise ValueError(f"kernel supports 1 to 16 heads, got {heads}")
+        if bias is not None and bias.shape != (dim,):
+            raise ValueError(f"bias must be [D={dim}], got {tuple(bias.shape)}")
+        self.heads, self.dim, self.channels = heads, dim, c
+        self.dtype = _DTYPES[q.dtype]
+        self.scale = float(dim ** -0.5 if scale is None else scale)
+        self.flags = ((_lib.FST_ATTN_BIAS if use_attn_bias else 0)
+                      | (_lib.FST_ACT_BIAS if use_activation_bias else 0)
+                      | (_lib.FST_PACKED if self.packed else 0))
+        self.q, self.k, self.v = (t.contiguous() for t in (q, k, v))
+        self.pos4 = feats[..., :4].to(torch.float32).contiguous()
+        self.weight = weight.detach().to(torch.float32).contiguous()
+        self.bias = bias.detach().to(torch.float32).contiguous() if bias is not None else None
+        self.lens = lens.to(device=q.device, dtype=torch.int32).contiguous()
+        self.device = q.device
+
+    def dims(self):
+        return (self.dtype, self.flags, self.batch, self.heads, self.length, self.tokens,
+                self.dim, self.channels)
+
+    def vec_shape(self):
+        if self.packed:
+            return (self.tokens, self.heads)
+        return (self.batch, self.heads, self.length)
+
+
+def _run_forward(prep: _Prepared) -> Tuple[Tensor, Tensor]:
+    lib = _lib.load()
+    out = torch.empty_like(prep.q)
+    lse = torch.empty(prep.vec_shape(), device=prep.device, dtype=torch.float32)
+    ws_bytes = lib.fst_forward_workspace_bytes(*prep.dims())
+    ws = torch.empty(max(ws_bytes, 1), device=prep.device, dtype=torch.uint8)
+    with torch.cuda.device(prep.device):
+        rc = lib.fst_forward(
+            *prep.dims(),
+            _lib.ptr(prep.q), _lib.ptr(prep.k), _lib.ptr(prep.v), _lib.ptr(prep.pos4),
+            _lib.ptr(prep.weight), _lib.ptr(prep.bias), _lib.ptr(prep.lens), prep.scale,
+            _lib.ptr(out), _lib.ptr(lse), _lib.ptr(ws), ws_bytes, _lib.stream_handle(prep.device),
+        )
+    _lib.check(rc, "flash_spacetime_forward")
+    return out, lse
+
+
+def flash_spacetime_forward(
+    q: Tensor,
+    k: Tensor,
+    v: Tensor,
+    feats: Tensor,
+    weight: Tensor,
+    bias: Optional[Tensor],
+    seqlens: Optional[Tensor],
+    scale: Optional[float] = None,
+    use_attn_bias: bool = True,
+    use_activation_bias: bool = True,
+    block_m: int = 16,
+    block_n: Optional[int] = None,
+    num_warps: int = 8,
+    num_stages: int = 1,
+    cu_seqlens: Optional[Tensor] = None,
+) -> Tuple[Tensor, Tensor]:
+    """Fused forward: (out `[B, H, L, D]` with padding rows 0, lse `[B, H, L]`).
+
+    Same contract as the reference launcher (forward.py:222-346): `seqlens`
+    is the `[B]` integer tensor of valid lengths (a front-packed `[B, L]`
+    padding mask is also accepted); with `cu_seqlens` (`[B+1]` token
+    offsets) the tensors are packed `[T, H, D]` / `[T, F]` and `seqlens` is
+    ignored. `weight` is `[D, C]` (nn.Linear layout; the reference's
+    `[C, C]` with C == D is the special case). lse excludes the row-constant
+    `qt . b` term, as the reference kernel's does. The Triton tuning
+    arguments (block_m, block_n, num_warps, num_stages) are accepted for
+    signature compatibility and ignored: tiles are fixed per shape for
+    gfx950's 160 KiB LDS.
+    """
+    del block_m, block_n, num_warps, num_stages
+    prep = _Prepared(q, k, v, feats, weight, bias, seqlens, scale, use_attn_bias,
+                     use_activation_bias, cu_seqlens)
+    return _run_forward(prep)
+
+
+class _FlashSpacetimeAttention(torch.autograd.Function):
+    """Fused forward and deterministic HIP backward (forward.py:349-478)."""
+
+    @staticmethod
+    def forward(  # type: ignore[override]
+        ctx: Any,
+        q: Tensor,
+        k: Tensor,
+        v: Tensor,
+        feats: Tensor,
+        weight: Tensor,
+        bias: Optional[Tensor],
+        seqlens: Optional[Tensor],
+        scale: Optional[float],
+        use_attn_bias: bool,
+        use_activation_bias: bool,
+        cu_seqlens: Optional[Tensor] = None,
+    ) -> Tensor:
+        if feats.requires_grad:
+            raise ValueError("feats (detector data) must not require grad")
+        prep = _Prepared(q, k, v, feats, weight, bias, seqlens, scale, use_attn_bias,
+                         use_activation_bias, cu_seqlens)
+        out, lse = _run_forward(prep)
+        # Only inputs and the LSE are kept: the backward forms its own softmax
+        # row sums and never needs the output (forward.py:381-388).
+        ctx.save_for_backward(prep.q, prep.k, prep.v, prep.pos4, prep.lens, lse)
+        ctx.prep_meta = (prep.weight, prep.bias, weight.dtype,
+                         None if bias is None else bias.dtype)
+        ctx.dims = prep.dims()
+        ctx.scale = prep.scale
+        ctx.packed = prep.packed
+        ctx.flags = (use_attn_bias, use_activation_bias)
+        ctx.vec_shape = prep.vec_shape()
+        return out
+
+    @staticmethod
+    def backward(ctx: Any, grad_out: Tensor) -> Tuple[Optional[Tensor], ...]:  # type: ignore[override]
+        if os.environ.get("FLASH_ST_REFERENCE_BWD", "0") == "1":
+            raise RuntimeError(
+                "FLASH_ST_REFERENCE_BWD=1 (autograd through the materialised reference) is not "
+                "offered: this build has only the fused HIP backward"
+            )
+        from .backward import _run_backward
+
+        q, k, v, pos4, lens, lse = ctx.saved_tensors
+        w32, b32, w_dtype, b_dtype = ctx.prep_meta
+        dq, dk, dv, dw, db = _run_backward(
+            ctx.dims, q, k, v, pos4, w32, b32, lens, lse, grad_out, ctx.scale, ctx.vec_shape
+        )
+        use_attn_bias, use_activation_bias = ctx.flags
+        proj_used = use_attn_bias or use_activation_bias
+        w_needed, b_needed = ctx.needs_input_grad[4], ctx.needs_input_grad[5]
+        return (
+            dq if ctx.needs_input_grad[0] else None,
+            dk if ctx.needs_input_grad[1] else None,
+            dv if ctx.needs_input_grad[2] else None,
+            None,
+            dw.to(w_dtype) if (w_needed and proj_used) else None,
+            db.to(b_dtype) if (b_needed and proj_used and db is not None) else None,
+            None, None, None, None, None,
+        )
+
+
+def flash_spacetime_attention(
+    q: Tensor,
+    k: Tensor,
+    v: Tensor,
+    feats: Tensor,
+    weight: Tensor,
+    bias: Optional[Tensor],
+    seqlens: Optional[Tensor] = None,
+    scale: Optional[float] = None,
+    use_attn_bias: bool = True,
+    use_activation_bias: bool = True,
+    *,
+    key_padding_mask: Optional[Tensor] = None,
+) -> Tensor:
+    """Fused spacetime-bias attention (public op, forward.py:481-501).
+
+    Semantics of `spacetime_attention_reference` on valid rows; padding rows
+    of the output are exactly zero. The 7th argument is the `[B]` integer
+    tensor of valid lengths; a front-packed `[B, L]` padding mask may be
+    given instead, positionally or as `key_padding_mask=`.
+    """
+    if key_padding_mask is not None:
+        seqlens = _resolve_lengths(seqlens, key_padding_mask, q.shape[0], q.shape[2])
+    return _FlashSpacetimeAttention.apply(
+        q, k, v, feats, weight, bias, seqlens, scale, use_attn_bias, use_activation_bias, None
+    )
+
+
+def flash_spacetime_attention_varlen(
+    q: Tensor,
+    k: Tensor,
+    v: Tensor,
+    feats: Tensor,
+    weight: Tensor,
+    bias: Optional[Tensor],
+    cu_seqlens: Tensor,
+    scale: Optional[float] = None,
+    use_attn_bias: bool = True,
+    use_activation_bias: bool = True,
+) -> Tensor:
+    """Packed (uncapped) fused spacetime-bias attention (forward.py:504-527).
+
+    q/k/v are `[T, H, D]` and feats `[T, F]` with events delimited by
+    `cu_seqlens` (`[B+1]` token offsets, cu[0] = 0, cu[-1] = T) -- the values
+    layout of a jagged NestedTensor. No padding exists and event lengths are
+    unbounded; nothing is read back to the host.
+    """
+    return _FlashSpacetimeAttention.apply(
+        q, k, v, feats, weight, bias, None, scale, use_attn_bias, use_activation_bias, cu_seqlens
+    )

@@ -1,0 +1,107 @@
+/*
+ * flash_spacetime.h -- C ABI of the MI355X (gfx950) flash-spacetime library.
+ *
+ * Spacetime-interval-biased attention (sevmag/flash-spacetime) as plain C
+ * entry points over caller-owned device buffers. No entry point allocates,
+ * frees or synchronises: every buffer, including the scratch workspace
+ * whose size the *_workspace_bytes queries return, belongs to the caller,
+ * and all work is enqueued on the caller's HIP stream.
+ *
+ * Layouts (all contiguous, row-major):
+ *   padded : q, k, v, out, dq, dk, dv  [B, H, L, D]   lse, rowsum [B, H, L]
+ *            pos4 [B, L, 4] fp32 (x, y, z, t), lens = seqlens [B] int32
+ *            (valid tokens of event b are 0 .. seqlens[b]-1)
+ *   packed : q, k, v, out, dq, dk, dv  [T, H, D]      lse, rowsum [T, H]
+ *            pos4 [T, 4] fp32, lens = cu_seqlens [B+1] int32 (cu[0] = 0,
+ *            cu[B] = T)
+ *   weight [D, C] fp32 (nn.Linear layout), bias [D] fp32 or NULL.
+ *   dtype FST_BF16: q, k, v, out, grad_out, dq, dk, dv are bfloat16;
+ *   dtype FST_F32 : they are float32. lse, pos4, weight, bias, dweight,
+ *   dbias, rowsum are float32 in both.
+ *
+ * Supported shapes: 1 <= H <= 16, D in {16, 32, 48, 64}, C in {16, 32, 48,
+ * 64} (C even, sin/cos halves); see fst_supported().
+ *
+ * Return value: 0 on success, a negative FST_E* code otherwise; the message
+ * of the last failure on the calling thread is in fst_last_error().
+ */
+#ifndef FLASH_SPACETIME_H
+#define FLASH_SPACETIME_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum fst_dtype { FST_BF16 = 0, FST_F32 = 1 };
+
+enum fst_flags {
+  FST_ATTN_BIAS = 1, /* add qt_i . R_ij to the logits (use_attn_bias)        */
+  FST_ACT_BIAS = 2,  /* add sum_j P_ij R_ij to the output (use_activation_bias) */
+  FST_PACKED = 4     /* packed [T, H, D] layout with cu_seqlens              */
+};
+
+enum fst_status {
+  FST_OK = 0,
+  FST_EINVAL = -1,       /* bad argument (shape, pointer, flag)             */
+  FST_EUNSUPPORTED = -2, /* valid request outside the compiled shape set    */
+  FST_EWORKSPACE = -3,   /* workspace smaller than *_workspace_bytes()       */
+  FST_ELAUNCH = -4       /* HIP launch error                                 */
+};
+
+/* 1 if (dtype, H, D, C) has a compiled kernel, else 0.
+ * No reference counterpart: the Triton reference JIT-compiles per shape and
+ * raises ValueError for C outside {16, 32, 48} (forward.py:261-265). */
+int fst_supported(int dtype, int H, int D, int C);
+
+/* Scratch bytes fst_forward needs for these sizes (rows = B*L padded, T packed). */
+size_t fst_forward_workspace_bytes(int dtype, int flags, int B, int H, int L, int T,
+                                   int D, int C);
+
+/* Fused forward. Writes out (pad rows exactly 0) and lse (log-sum-exp of the
+ * logits without the row-constant qt.b term; 0 on pad rows).
+ * Replaces flash_spacetime_forward (reference forward.py:222-346) together
+ * with the Triton kernel launch it makes (forward.py:306-331); the o2
+ * epilogue (forward.py:333-346) is fused into the kernel. */
+int fst_forward(int dtype, int flags, int B, int H, int L, int T, int D, int C,
+                const void* q, const void* k, const void* v, const float* pos4,
+                const float* weight, const float* bias, const int32_t* lens,
+                float scale, void* out, float* lse, void* workspace,
+                size_t workspace_bytes, void* stream);
+
+/* Scratch bytes fst_backward needs. */
+size_t fst_backward_workspace_bytes(int dtype, int flags, int B, int H, int L, int T,
+                                    int D, int C);
+
+/* Deterministic backward from the saved lse. Writes dq, dk, dv (pad rows 0),
+ * dweight [D, C] and, when bias != NULL, dbias [D] (all float32 for the
+ * weight-side). rowsum (nullable, float32 like lse) receives sum_j dS_ij,
+ * which the normalised softmax row term makes zero up to rounding.
+ * Replaces flash_spacetime_backward (reference backward.py:488-630): the
+ * host prologue (:526-556), both Triton kernels (:589-598) and the host
+ * epilogue (:600-630). */
+int fst_backward(int dtype, int flags, int B, int H, int L, int T, int D, int C,
+                 const void* q, const void* k, const void* v, const float* pos4,
+                 const float* weight, const float* bias, const int32_t* lens,
+                 const float* lse, const void* grad_out, float scale, void* dq,
+                 void* dk, void* dv, float* dweight, float* dbias, float* rowsum,
+                 void* workspace, size_t workspace_bytes, void* stream);
+
+/* The fp32 frequency ladder exp(-i ln(1e4) / (C/2)), i < C/2, that the kernels
+ * embed with, written to out[0 .. C/2). Counterpart of sinusoidal_frequencies
+ * (reference.py:45-56); evaluated with the same fp32 steps. */
+void fst_frequencies(int C, float* out);
+
+/* Message of the last failed call on this thread ("" if none). */
+const char* fst_last_error(void);
+
+/* Library version string. */
+const char* fst_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* FLASH_SPACETIME_H */
