@@ -1,0 +1,777 @@
+// Deterministic backward kernels of flash-spacetime attention for gfx950.
+//
+// Gradients of the spec (reference.py:106-167) in the fused form of
+// backward.py:3-32. With qt = q*scale, u = T(qt W), w~ = T(dO W), dob = dO.b:
+//   s_ij  = qt_i.k_j + [A] u_i.E_ij,          P_ij = exp(s_ij - lse_i)
+//   dP_ij = dO_i.v_j + [V] (w~_i.E_ij + dob_i)
+//   D_i   = sum_j P_ij dP_ij / sum_j P_ij   (same P and dP as dS below)
+//   dS_ij = P_ij (dP_ij - D_i)
+//   dq_i  = scale (sum_j dS_ij k_j + [A] (W sum_j dS_ij E_ij + sigma_i b))
+//   dk_j  = sum_i dS_ij qt_i,      dv_j = sum_i P_ij dO_i
+//   dW    = [A] sum qt (x) H + [V] sum dO (x) G,   H_i = sum_j dS_ij E_ij,
+//           G_i = sum_j P_ij E_ij,  sigma_i = sum_j dS_ij,  db = [V] sum dO
+// Forming D from the very P and dP that build dS makes sigma (the row sum of
+// dS) vanish by construction (backward.py:371-407); normalising by sum P
+// makes it invariant to an O(1) mismatch between the saved LSE and the
+// recomputed logits at large logits.
+//
+// Two kernels, each the single writer of its outputs (no atomics, fixed
+// loop order => bitwise deterministic):
+//  * rows: workgroups own query rows, same head-owner / row-owner split as
+//    the forward. Pass 1 over the keys forms D; pass 2 recomputes the tile
+//    exactly as pass 1 did and accumulates dq (head-owner), H and G
+//    (row-owner), sigma. The epilogue projects H through W into dq, and
+//    reduces qt (x) H + dO (x) G and dO over the block's rows into per-block
+//    partials of dW and db. u, w~, dob and D go to scratch for the cols
+//    kernel.
+//  * cols: workgroups own keys and stream query rows -- the forward's
+//    structure mirrored (S = Qt K^T with keys on the lanes) -- and
+//    accumulate dk and dv. The u.E and w~.E terms of the streamed rows are
+//    formed by the pair-owner waves and staged for the head-owners.
+//  * a final reduction sums the dW / db block partials in block order.
+#include "fst_kernels.h"
+
+namespace fst {
+
+// ---------------------------------------------------------------------------
+// Helpers shared by both kernels.
+// ---------------------------------------------------------------------------
+
+// One 16-row MFMA tile (rows = the lane index of the C tile's columns) of
+// P and dP for one head: s = mma(A_s, B_s) + init_s, dP = mma(A_p, B_p) +
+// init_p, both already computed by the caller; this applies masking, the
+// exponential and the dob term. Written once and used by every pass so the
+// arithmetic of P and dP is identical wherever they are recomputed.
+__device__ __forceinline__ void finish_p_dp(f32x4& s, f32x4& dp, float lse2, float dob, unsigned valid_mask) {
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const bool ok = (valid_mask >> r) & 1u;
+    const float p = exp2f_fast(__builtin_fmaf(s[r], kLog2e, -lse2));
+    s[r] = ok ? p : 0.f;
+    dp[r] = dp[r] + dob;
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Rows kernel.
+// ---------------------------------------------------------------------------
+template <typename T, int HP, int D, int C, int NW, int NS>
+struct BwdRowsCfg {
+  static constexpr bool BF = is_bf16<T>::value;
+  static constexpr int HW = HP / NW, RW = 16 / NW, TILES = 4 / NW, ROWS = 16 * TILES;
+  static constexpr int KC = 16 * NS;
+  static constexpr int ESZ = sizeof(T);
+  static constexpr int PAD = 16 / ESZ;
+  static constexpr int KV_ROW = D + PAD;
+  static constexpr int KV_BYTES = BF ? 2 * HP * KC * KV_ROW * ESZ : 0;  // K and V (bf16 only)
+  static constexpr int DW_BYTES = 4 * (D * C + D) * 4;                  // per-wave dW/db partials
+  static constexpr int R0_BYTES = KV_BYTES > DW_BYTES ? KV_BYTES : DW_BYTES;
+  static constexpr int E_ROW = C + PAD;
+  static constexpr int E_TILE = 16 * KC * E_ROW * ESZ;
+  static constexpr int U_ROW = KC + 4;   // fp32 per staged u.E / w~.E
+  static constexpr int P_ROW = KC + PAD; // T per staged P / dS
+  static constexpr int SLOT_A = 2 * U_ROW * 4;
+  static constexpr int SLOT_B = 2 * P_ROW * ESZ;
+  static constexpr int SLOT_O = 20 * 4;
+  static constexpr int SLOT_HG = 2 * 20 * 4;  // one 16-channel tile of H and G
+  static constexpr int SLOT_1 = SLOT_A > SLOT_B ? SLOT_A : SLOT_B;
+  static constexpr int SLOT_2 = SLOT_O > SLOT_HG ? SLOT_O : SLOT_HG;
+  static constexpr int SLOT = SLOT_1 > SLOT_2 ? SLOT_1 : SLOT_2;
+  static constexpr int STAGE_TILE = 16 * HP * SLOT;
+  static constexpr int TILE_BYTES = E_TILE + STAGE_TILE;
+  static constexpr int LDS_BYTES = R0_BYTES + TILES * TILE_BYTES;
+  static constexpr bool FITS = LDS_BYTES <= 160 * 1024 && HP % NW == 0;
+  static_assert(SLOT % 16 == 0, "slot alignment");
+};
+
+template <typename T, int HP, int D, int C, int NW, int NS>
+__global__ __launch_bounds__(256, 1) void bwd_rows_kernel(BwdParams prm) {
+  using Cfg = BwdRowsCfg<T, HP, D, C, NW, NS>;
+  constexpr bool BF = Cfg::BF;
+  constexpr int HW = Cfg::HW, RW = Cfg::RW, KC = Cfg::KC;
+  constexpr int SLOT_F = Cfg::SLOT / 4, SLOT_T = Cfg::SLOT / Cfg::ESZ;
+  extern __shared__ __align__(16) unsigned char smem[];
+
+  const int tid = threadIdx.x;
+  const int wave = tid >> 6, lane = tid & 63, g = lane >> 4, n = lane & 15;
+  const int tile = wave / NW, ws = wave % NW;
+
+  EventBlock eb;
+  if (!locate_block(prm.ev, blockIdx.x, eb)) return;
+  const int len = eb.len;
+  const int H = prm.H;
+  const bool attn = prm.flags & FST_ATTN_BIAS;
+  const bool act = prm.flags & FST_ACT_BIAS;
+  const bool use_e = attn || act;
+  const bool use_b = act && prm.bias;
+  const RowAddr ra = row_addr(prm.ev, eb);
+  const int row0 = eb.blk * Cfg::ROWS;
+  const int i0 = row0 + 16 * tile;
+
+  T* Ks = reinterpret_cast<T*>(smem);
+  T* Vs = Ks + HP * KC * Cfg::KV_ROW;
+  float* Wred = reinterpret_cast<float*>(smem);  // epilogue: [4][D*C + D]
+  unsigned char* tbase = smem + Cfg::R0_BYTES + tile * Cfg::TILE_BYTES;
+  T* Es = reinterpret_cast<T*>(tbase);
+  float* Sf = reinterpret_cast<float*>(tbase + Cfg::E_TILE);
+  T* St = reinterpret_cast<T*>(tbase + Cfg::E_TILE);
+
+  const T* __restrict__ qg = reinterpret_cast<const T*>(prm.q);
+  const T* __restrict__ kg = reinterpret_cast<const T*>(prm.k);
+  const T* __restrict__ vg = reinterpret_cast<const T*>(prm.v);
+  const T* __restrict__ dog = reinterpret_cast<const T*>(prm.dout);
+
+  // ---- head-owner state (rows on lane n) ----
+  const int my_row = i0 + n;
+  const bool row_ok = my_row < len;
+  KFrag<T, D> qf[HW], dof[HW];
+  f32x4 dQ[HW][D / 16];
+  float lse2[HW], dobv[HW], nsum[HW], zsum[HW], dval[HW], sig[HW];
+#pragma unroll
+  for (int hl = 0; hl < HW; ++hl) {
+    const int h = ws * HW + hl;
+    const bool ok = h < H && row_ok;
+    if (ok) {
+      qf[hl].load_scaled(qg + ra.off(h, my_row, D), g, prm.scale);
+      dof[hl].load(dog + ra.off(h, my_row, D), g);
+    } else {
+      qf[hl].zero();
+      dof[hl].zero();
+    }
+    lse2[hl] = ok ? prm.lse[ra.vec(h, my_row)] * kLog2e : 0.f;
+    // dob = dO . b in fp32 (backward.py:548-552): each lane group holds a
+    // quarter of the row; the four partial sums are combined.
+    float part = 0.f;
+    if (use_b && ok) {
+      const T* dp = dog + ra.off(h, my_row, D);
+#pragma unroll
+      for (int d4 = 0; d4 < D / 4; ++d4) {
+        const int d = (D / 4) * g + d4;
+        part = __builtin_fmaf((float)dp[d], prm.bias[d], part);
+      }
+    }
+    dobv[hl] = group_allsum(part);
+    if (g == 0 && ok) prm.dob[ra.vec(h, my_row)] = dobv[hl];
+    nsum[hl] = zsum[hl] = sig[hl] = dval[hl] = 0.f;
+#pragma unroll
+    for (int dt = 0; dt < D / 16; ++dt) dQ[hl][dt] = zero4();
+  }
+
+  // ---- row-owner state (heads on lane n) ----
+  CFrag<T, C> uf[RW], wf[RW];
+  f32x4 Hacc[RW][C / 16], Gacc[RW][C / 16];
+  T* __restrict__ ug = reinterpret_cast<T*>(prm.u);
+  T* __restrict__ wg_ = reinterpret_cast<T*>(prm.wt);
+#pragma unroll
+  for (int ri = 0; ri < RW; ++ri) {
+    const int row = i0 + ws * RW + ri;
+    const bool ok = row < len && n < H;
+    f32x4 acc[C / 16];
+    if (attn) {
+      project_row<T, D, C>(qg + ra.off(0, ok ? row : 0, D), ra.hs * D, ok, prm.scale, prm.weight, g, n, acc);
+      uf[ri].from_acc(acc);
+      if (ok)
+#pragma unroll
+        for (int ct = 0; ct < C / 16; ++ct) {
+          f32x4 rq;
+#pragma unroll
+          for (int r = 0; r < 4; ++r) rq[r] = (float)(T)acc[ct][r];
+          store4<T>(ug + ra.off(n, row, C) + 16 * ct + 4 * g, rq);
+        }
+    } else {
+      uf[ri].zero();
+    }
+    if (act) {
+      project_row<T, D, C>(dog + ra.off(0, ok ? row : 0, D), ra.hs * D, ok, 1.f, prm.weight, g, n, acc);
+      wf[ri].from_acc(acc);
+      if (ok)
+#pragma unroll
+        for (int ct = 0; ct < C / 16; ++ct) {
+          f32x4 rq;
+#pragma unroll
+          for (int r = 0; r < 4; ++r) rq[r] = (float)(T)acc[ct][r];
+          store4<T>(wg_ + ra.off(n, row, C) + 16 * ct + 4 * g, rq);
+        }
+    } else {
+      wf[ri].zero();
+    }
+#pragma unroll
+    for (int ct = 0; ct < C / 16; ++ct) Hacc[ri][ct] = Gacc[ri][ct] = zero4();
+  }
+  constexpr int EPL = RW * KC / 64;
+  constexpr int ESTEP = 64 / KC;
+  float4 pos_i[EPL];
+#pragma unroll
+  for (int k2 = 0; k2 < EPL; ++k2) {
+    const int row = i0 + ws * RW + lane / KC + ESTEP * k2;
+    pos_i[k2] = use_e ? ra.pos(prm.ev.pos4, row < len ? row : (len > 0 ? len - 1 : 0)) : float4{0.f, 0.f, 0.f, 0.f};
+  }
+
+  for (int pass = 0; pass < 2; ++pass) {
+    for (int j0 = 0; j0 < len; j0 += KC) {
+      // ---- bf16: stage K and V rows of the chunk (zero past the event) ----
+      if constexpr (BF) {
+        constexpr int PER_ROW = D / 8;
+        const int total = H * KC * PER_ROW;
+        for (int idx = tid; idx < total; idx += 256) {
+          const int dv = idx % PER_ROW;
+          const int key = (idx / PER_ROW) % KC;
+          const int h = idx / (PER_ROW * KC);
+          const int j = j0 + key;
+          const long off = ra.off(h, j < len ? j : 0, D) + dv * 8;
+          const bf16x8 kv = j < len ? *reinterpret_cast<const bf16x8*>(kg + off) : VecOf<bf16>::zero();
+          const bf16x8 vv = j < len ? *reinterpret_cast<const bf16x8*>(vg + off) : VecOf<bf16>::zero();
+          *reinterpret_cast<bf16x8*>(Ks + (h * KC + key) * Cfg::KV_ROW + dv * 8) = kv;
+          *reinterpret_cast<bf16x8*>(Vs + (h * KC + key) * Cfg::KV_ROW + dv * 8) = vv;
+        }
+      }
+      // ---- row-owner: embedding, u.E and w~.E staged per (row, head) ----
+      if (use_e) {
+        const int key = lane % KC;
+        const int j = j0 + key;
+        const float4 pj = ra.pos(prm.ev.pos4, j < len ? j : len - 1);
+#pragma unroll
+        for (int k2 = 0; k2 < EPL; ++k2) {
+          const int il = ws * RW + lane / KC + ESTEP * k2;
+          write_embedding<T, C>(Es + (il * KC + key) * Cfg::E_ROW, pos_i[k2], pj, prm.freq);
+        }
+        wave_lds_sync();
+#pragma unroll
+        for (int ri = 0; ri < RW; ++ri) {
+          const int il = ws * RW + ri;
+#pragma unroll
+          for (int s = 0; s < NS; ++s) {
+            CFrag<T, C> ef;
+            ef.load(Es + (il * KC + 16 * s + n) * Cfg::E_ROW, g);
+            float* slot = Sf + (il * HP + n) * SLOT_F;
+            if (attn) {
+              const f32x4 ue = mma_c<C>(ef, uf[ri], zero4());
+              if (n < H) *reinterpret_cast<f32x4*>(slot + 16 * s + 4 * g) = ue;
+            }
+            if (act) {
+              const f32x4 we = mma_c<C>(ef, wf[ri], zero4());
+              if (n < H) *reinterpret_cast<f32x4*>(slot + Cfg::U_ROW + 16 * s + 4 * g) = we;
+            }
+          }
+        }
+      }
+      __syncthreads();
+
+      // ---- head-owner: P, dP (and in pass 2 dS, dq) ----
+#pragma unroll
+      for (int hl = 0; hl < HW; ++hl) {
+        const int h = ws * HW + hl;
+        if (h >= H) continue;
+        f32x4 S[NS], P_[NS];
+        const float* slot = Sf + (n * HP + h) * SLOT_F;
+#pragma unroll
+        for (int s = 0; s < NS; ++s) {
+          const f32x4 ue = attn ? *reinterpret_cast<const f32x4*>(slot + 16 * s + 4 * g) : zero4();
+          const f32x4 we = act ? *reinterpret_cast<const f32x4*>(slot + Cfg::U_ROW + 16 * s + 4 * g) : zero4();
+          KFrag<T, D> kf, vf;
+          if constexpr (BF) {
+            kf.load(Ks + (h * KC + 16 * s + n) * Cfg::KV_ROW, g);
+            vf.load(Vs + (h * KC + 16 * s + n) * Cfg::KV_ROW, g);
+          } else {
+            int key = j0 + 16 * s + n;
+            key = key < len ? key : len - 1;
+            kf.load(kg + ra.off(h, key, D), g);
+            vf.load(vg + ra.off(h, key, D), g);
+          }
+          S[s] = mma_k<D>(kf, qf[hl], ue);
+          P_[s] = mma_k<D>(vf, dof[hl], we);
+          unsigned vm = 0;
+#pragma unroll
+          for (int r = 0; r < 4; ++r) vm |= (j0 + 16 * s + 4 * g + r < len ? 1u : 0u) << r;
+          finish_p_dp(S[s], P_[s], lse2[hl], dobv[hl], vm);
+        }
+        // S now holds P, P_ holds dP.
+        if (pass == 0) {
+#pragma unroll
+          for (int s = 0; s < NS; ++s)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+              nsum[hl] = __builtin_fmaf(S[s][r], P_[s][r], nsum[hl]);
+              zsum[hl] += S[s][r];
+            }
+        } else {
+          f32x4 dS[NS];
+#pragma unroll
+          for (int s = 0; s < NS; ++s)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+              dS[s][r] = S[s][r] * (P_[s][r] - dval[hl]);
+              sig[hl] += dS[s][r];
+            }
+          JFrag<T, NS> dsf, pf;
+          dsf.from_tiles(dS);
+          pf.from_tiles(S);
+#pragma unroll
+          for (int dt = 0; dt < D / 16; ++dt) {
+            JFrag<T, NS> kt;
+            if constexpr (BF) {
+              kt.load_tr(Ks + h * KC * Cfg::KV_ROW, Cfg::KV_ROW, 16 * dt, g, n);
+            } else {
+#pragma unroll
+              for (int s = 0; s < NS; ++s)
+#pragma unroll
+                for (int r = 0; r < 4; ++r) {
+                  const int j = j0 + 16 * s + 4 * g + r;
+                  kt.v[4 * s + r] = j < len ? kg[ra.off(h, j, D) + 16 * dt + n] : 0.f;
+                }
+            }
+            dQ[hl][dt] = mma_j(kt, dsf, dQ[hl][dt]);
+          }
+          if (use_e) {
+            wave_lds_sync();  // the slot's u.E / w~.E were read above
+            T* tslot = St + (n * HP + h) * SLOT_T;
+            pf.store_keys(tslot, g);
+            dsf.store_keys(tslot + Cfg::P_ROW, g);
+          }
+        }
+      }
+      __syncthreads();
+
+      // ---- row-owner (pass 2): H += E^T dS, G += E^T P ----
+      if (pass == 1 && use_e) {
+#pragma unroll
+        for (int ri = 0; ri < RW; ++ri) {
+          const int il = ws * RW + ri;
+          JFrag<T, NS> pf, dsf;
+          if (n < H) {
+            const T* tslot = St + (il * HP + n) * SLOT_T;
+            pf.load_keys(tslot, g);
+            dsf.load_keys(tslot + Cfg::P_ROW, g);
+          } else {
+            pf.zero();
+            dsf.zero();
+          }
+#pragma unroll
+          for (int ct = 0; ct < C / 16; ++ct) {
+            JFrag<T, NS> ef;
+            ef.load_tr(Es + il * KC * Cfg::E_ROW, Cfg::E_ROW, 16 * ct, g, n);
+            if (attn) Hacc[ri][ct] = mma_j(ef, dsf, Hacc[ri][ct]);
+            if (act) Gacc[ri][ct] = mma_j(ef, pf, Gacc[ri][ct]);
+          }
+        }
+      }
+      __syncthreads();
+    }
+    if (pass == 0) {
+#pragma unroll
+      for (int hl = 0; hl < HW; ++hl) {
+        const int h = ws * HW + hl;
+        const float nn = group_allsum(nsum[hl]);
+        const float zz = group_allsum(zsum[hl]);
+        dval[hl] = zz > 0.f ? nn / zz : 0.f;
+        if (g == 0 && h < H && row_ok) prm.dsum[ra.vec(h, my_row)] = dval[hl];
+      }
+    }
+  }
+
+  // ---- epilogue: dq = scale (dQ + W H + sigma b) ----
+#pragma unroll
+  for (int hl = 0; hl < HW; ++hl) {
+    sig[hl] = group_allsum(sig[hl]);
+    const int h = ws * HW + hl;
+    if (prm.rowsum && g == 0 && h < H && row_ok) prm.rowsum[ra.vec(h, my_row)] = sig[hl];
+  }
+  T* dqg = reinterpret_cast<T*>(prm.dq);
+#pragma unroll
+  for (int dt = 0; dt < D / 16; ++dt) {
+    if (attn) {
+#pragma unroll
+      for (int ri = 0; ri < RW; ++ri) {
+        const int il = ws * RW + ri;
+        f32x4 acc = zero4();
+#pragma unroll
+        for (int ct = 0; ct < C / 16; ++ct)
+#pragma unroll
+          for (int sp = 0; sp < 4; ++sp)
+            acc = mfma_f32(prm.weight[(16 * dt + n) * C + 16 * ct + 4 * g + sp], Hacc[ri][ct][sp], acc);
+        if (n < H) *reinterpret_cast<f32x4*>(Sf + (il * HP + n) * SLOT_F + 4 * g) = acc;
+      }
+      __syncthreads();
+    }
+#pragma unroll
+    for (int hl = 0; hl < HW; ++hl) {
+      const int h = ws * HW + hl;
+      if (h >= H) continue;
+      f32x4 o = dQ[hl][dt];
+      if (attn) {
+        o = o + *reinterpret_cast<const f32x4*>(Sf + (n * HP + h) * SLOT_F + 4 * g);
+        if (prm.bias) {
+#pragma unroll
+          for (int r = 0; r < 4; ++r) o[r] = __builtin_fmaf(sig[hl], prm.bias[16 * dt + 4 * g + r], o[r]);
+        }
+      }
+      o = o * prm.scale;
+      if (row_ok) store4<T>(dqg + ra.off(h, my_row, D) + 16 * dt + 4 * g, o);
+    }
+    if (attn) __syncthreads();
+  }
+
+  // ---- dW / db partials of this block: sum over its rows and heads ----
+  if (use_e) {
+    // dW[d, c] += sum_(row, head) A[d, (row, head)] B[(row, head), c] on fp32
+    // MFMA: a step covers heads 4s + g of one row; A = qt (resp. dO) with d
+    // on the lanes, B = H (resp. G) with c on the lanes, read back from LDS
+    // one 16-channel tile at a time as [row][head][c].
+    f32x4 dw[D / 16][C / 16];
+    float dbl[D / 16];
+#pragma unroll
+    for (int dt = 0; dt < D / 16; ++dt) {
+      dbl[dt] = 0.f;
+#pragma unroll
+      for (int ct = 0; ct < C / 16; ++ct) dw[dt][ct] = zero4();
+    }
+#pragma unroll
+    for (int ct = 0; ct < C / 16; ++ct) {
+#pragma unroll
+      for (int ri = 0; ri < RW; ++ri) {
+        const int il = ws * RW + ri;
+        float* slot = Sf + (il * HP + n) * SLOT_F;
+        if (n < H) {
+          *reinterpret_cast<f32x4*>(slot + 4 * g) = Hacc[ri][ct];
+          *reinterpret_cast<f32x4*>(slot + 20 + 4 * g) = Gacc[ri][ct];
+        }
+      }
+      __syncthreads();
+#pragma unroll
+      for (int ri = 0; ri < RW; ++ri) {
+        const int il = ws * RW + ri;
+        const int row = i0 + il;
+        const bool rok = row < len;
+#pragma unroll
+        for (int s4 = 0; s4 < HP / 4; ++s4) {
+          const int h = 4 * s4 + g;
+          const bool ok = rok && h < H;
+          const float* slot = Sf + (il * HP + h) * SLOT_F;
+          const float bh = (attn && ok) ? slot[n] : 0.f;
+          const float bg = (act && ok) ? slot[20 + n] : 0.f;
+#pragma unroll
+          for (int dt = 0; dt < D / 16; ++dt) {
+            const int d = 16 * dt + n;
+            const float aq = (attn && ok) ? (float)qg[ra.off(h, row, D) + d] * prm.scale : 0.f;
+            const float ao = (act && ok) ? (float)dog[ra.off(h, row, D) + d] : 0.f;
+            if (ct == 0) dbl[dt] += ao;
+            dw[dt][ct] = mfma_f32(aq, bh, dw[dt][ct]);
+            dw[dt][ct] = mfma_f32(ao, bg, dw[dt][ct]);
+          }
+        }
+      }
+      __syncthreads();
+    }
+    float* wr = Wred + wave * (D * C + D);
+#pragma unroll
+    for (int dt = 0; dt < D / 16; ++dt) {
+#pragma unroll
+      for (int ct = 0; ct < C / 16; ++ct)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) wr[(16 * dt + 4 * g + r) * C + 16 * ct + n] = dw[dt][ct][r];
+      const float dbs = group_allsum(dbl[dt]);
+      if (g == 0) wr[D * C + 16 * dt + n] = dbs;
+    }
+    __syncthreads();
+    float* part = prm.dw_part + (long)blockIdx.x * (D * C + D);
+    for (int e = tid; e < D * C + D; e += 256) {
+      float acc = 0.f;
+#pragma unroll
+      for (int w = 0; w < 4; ++w) acc += Wred[w * (D * C + D) + e];
+      part[e] = acc;
+    }
+  }
+
+  zero_pad_rows<T>(prm.ev, eb, ra, row0, Cfg::ROWS, D, tid, 256, dqg, prm.rowsum, 1);
+}
+
+// ---------------------------------------------------------------------------
+// Cols kernel: keys owned (lanes), query rows streamed in chunks of KC.
+// ---------------------------------------------------------------------------
+template <typename T, int HP, int D, int C, int NW, int NS>
+struct BwdColsCfg {
+  static constexpr bool BF = is_bf16<T>::value;
+  static constexpr int HW = HP / NW, TILES = 4 / NW, KEYS = 16 * TILES;
+  static constexpr int KC = 16 * NS;          // streamed rows per chunk
+  static constexpr int RWS = KC / NW;         // streamed rows per pair-owner wave
+  static constexpr int ESZ = sizeof(T);
+  static constexpr int PAD = 16 / ESZ;
+  static constexpr int QO_ROW = D + PAD;
+  static constexpr int QO_BYTES = BF ? 2 * HP * KC * QO_ROW * ESZ : 0;  // qt and dO (bf16 only)
+  static constexpr int VEC_BYTES = 3 * HP * KC * 4;                     // lse2, D, dob
+  static constexpr int E_ROW = C + PAD;
+  static constexpr int E_TILE = KC * 16 * E_ROW * ESZ;                   // [row][key][c]
+  static constexpr int UW_ROW = KC + 4;                                 // fp32 rows per (head, key)
+  static constexpr int UW_TILE = 2 * HP * 16 * UW_ROW * 4;              // u.E and w~.E
+  static constexpr int TILE_BYTES = E_TILE + UW_TILE;
+  static constexpr int LDS_BYTES = QO_BYTES + VEC_BYTES + TILES * TILE_BYTES;
+  static constexpr bool FITS = LDS_BYTES <= 160 * 1024 && HP % NW == 0 && RWS >= 4 && RWS % 4 == 0;
+};
+
+template <typename T, int HP, int D, int C, int NW, int NS>
+__global__ __launch_bounds__(256, 1) void bwd_cols_kernel(BwdParams prm) {
+  using Cfg = BwdColsCfg<T, HP, D, C, NW, NS>;
+  constexpr bool BF = Cfg::BF;
+  constexpr int HW = Cfg::HW, KC = Cfg::KC, RWS = Cfg::RWS;
+  constexpr int UWR = Cfg::UW_ROW;
+  extern __shared__ __align__(16) unsigned char smem[];
+
+  const int tid = threadIdx.x;
+  const int wave = tid >> 6, lane = tid & 63, g = lane >> 4, n = lane & 15;
+  const int tile = wave / NW, ws = wave % NW;
+
+  EventSpec ev = prm.ev;
+  ev.blkcum = prm.blkcum_cols;
+  EventBlock eb;
+  if (!locate_block(ev, blockIdx.x, eb)) return;
+  const int len = eb.len;
+  const int H = prm.H;
+  const bool attn = prm.flags & FST_ATTN_BIAS;
+  const bool act = prm.flags & FST_ACT_BIAS;
+  const bool use_e = attn || act;
+  const RowAddr ra = row_addr(ev, eb);
+  const int key0 = eb.blk * Cfg::KEYS;
+  const int j0t = key0 + 16 * tile;
+
+  T* Qs = reinterpret_cast<T*>(smem);                 // [HP][KC][QO_ROW] bf16(q*scale)
+  T* Os = Qs + HP * KC * Cfg::QO_ROW;                 // [HP][KC][QO_ROW] dO
+  float* Lv = reinterpret_cast<float*>(smem + Cfg::QO_BYTES);  // [3][HP][KC]
+  unsigned char* tbase = smem + Cfg::QO_BYTES + Cfg::VEC_BYTES + tile * Cfg::TILE_BYTES;
+  T* Es = reinterpret_cast<T*>(tbase);                               // [KC][16][E_ROW]
+  float* UWs = reinterpret_cast<float*>(tbase + Cfg::E_TILE);        // [2][HP][16][UW_ROW]
+
+  const T* __restrict__ qg = reinterpret_cast<const T*>(prm.q);
+  const T* __restrict__ kg = reinterpret_cast<const T*>(prm.k);
+  const T* __restrict__ vg = reinterpret_cast<const T*>(prm.v);
+  const T* __restrict__ dog = reinterpret_cast<const T*>(prm.dout);
+  const T* __restrict__ ug = reinterpret_cast<const T*>(prm.u);
+  const T* __restrict__ wg_ = reinterpret_cast<const T*>(prm.wt);
+
+  // ---- head-owner: own keys on lane n ----
+  const int my_key = j0t + n;
+  const bool key_ok = my_key < len;
+  KFrag<T, D> kf[HW], vf[HW];
+  f32x4 dK[HW][D / 16], dV[HW][D / 16];
+#pragma unroll
+  for (int hl = 0; hl < HW; ++hl) {
+    const int h = ws * HW + hl;
+    if (h < H && key_ok) {
+      kf[hl].load(kg + ra.off(h, my_key, D), g);
+      vf[hl].load(vg + ra.off(h, my_key, D), g);
+    } else {
+      kf[hl].zero();
+      vf[hl].zero();
+    }
+#pragma unroll
+    for (int dt = 0; dt < D / 16; ++dt) dK[hl][dt] = dV[hl][dt] = zero4();
+  }
+  // ---- pair-owner: own keys (lane % 16) x streamed rows [ws*RWS, +RWS) ----
+  const int pk = lane & 15;
+  const float4 pos_j = use_e ? ra.pos(ev.pos4, j0t + pk < len ? j0t + pk : (len > 0 ? len - 1 : 0))
+                             : float4{0.f, 0.f, 0.f, 0.f};
+
+  for (int c0 = 0; c0 < len; c0 += KC) {
+    // ---- stage the chunk's streamed rows: qt, dO (bf16), lse2, D, dob ----
+    if constexpr (BF) {
+      constexpr int PER_ROW = D / 8;
+      const int total = H * KC * PER_ROW;
+      for (int idx = tid; idx < total; idx += 256) {
+        const int dv = idx % PER_ROW;
+        const int il = (idx / PER_ROW) % KC;
+        const int h = idx / (PER_ROW * KC);
+        const int i = c0 + il;
+        bf16x8 qv = VecOf<bf16>::zero(), ov = VecOf<bf16>::zero();
+        if (i < len) {
+          const long off = ra.off(h, i, D) + dv * 8;
+          const bf16x8 raw = *reinterpret_cast<const bf16x8*>(qg + off);
+#pragma unroll
+          for (int e = 0; e < 8; ++e) qv[e] = (bf16)((float)raw[e] * prm.scale);
+          ov = *reinterpret_cast<const bf16x8*>(dog + off);
+        }
+        *reinterpret_cast<bf16x8*>(Qs + (h * KC + il) * Cfg::QO_ROW + dv * 8) = qv;
+        *reinterpret_cast<bf16x8*>(Os + (h * KC + il) * Cfg::QO_ROW + dv * 8) = ov;
+      }
+    }
+    for (int idx = tid; idx < H * KC; idx += 256) {
+      const int il = idx % KC, h = idx / KC;
+      const int i = c0 + il;
+      const bool ok = i < len;
+      Lv[idx] = ok ? prm.lse[ra.vec(h, i)] * kLog2e : 0.f;
+      Lv[HP * KC + idx] = ok ? prm.dsum[ra.vec(h, i)] : 0.f;
+      Lv[2 * HP * KC + idx] = (ok && act && prm.bias) ? prm.dob[ra.vec(h, i)] : 0.f;
+    }
+    // ---- pair-owner: E of (streamed rows, own keys), u.E and w~.E ----
+    if (use_e) {
+#pragma unroll
+      for (int k4 = 0; k4 < RWS / 4; ++k4) {
+        const int il = ws * RWS + (lane >> 4) + 4 * k4;
+        const int i = c0 + il;
+        const float4 pi = ra.pos(ev.pos4, i < len ? i : len - 1);
+        write_embedding<T, C>(Es + (il * 16 + pk) * Cfg::E_ROW, pi, pos_j, prm.freq);
+      }
+      wave_lds_sync();
+#pragma unroll
+      for (int ri = 0; ri < RWS; ++ri) {
+        const int il = ws * RWS + ri;
+        const int i = c0 + il;
+        const bool ok = i < len && n < H;
+        CFrag<T, C> ef;  // B = E_i[c, j]: lane n = key
+        ef.load(Es + (il * 16 + n) * Cfg::E_ROW, g);
+        if (attn) {
+          CFrag<T, C> uf;  // A = u_i[h, c]: lane n = head
+          if (ok)
+            uf.load(ug + ra.off(n, i, C), g);
+          else
+            uf.zero();
+          const f32x4 ue = mma_c<C>(uf, ef, zero4());  // [h = 4g + r][j = n]
+#pragma unroll
+          for (int r = 0; r < 4; ++r)
+            if (4 * g + r < H) UWs[((4 * g + r) * 16 + n) * UWR + il] = ue[r];
+        }
+        if (act) {
+          CFrag<T, C> wf;
+          if (ok)
+            wf.load(wg_ + ra.off(n, i, C), g);
+          else
+            wf.zero();
+          const f32x4 we = mma_c<C>(wf, ef, zero4());
+#pragma unroll
+          for (int r = 0; r < 4; ++r)
+            if (4 * g + r < H) UWs[HP * 16 * UWR + ((4 * g + r) * 16 + n) * UWR + il] = we[r];
+        }
+      }
+    }
+    __syncthreads();
+
+    // ---- head-owner: S = qt k^T + u.E, P, dP, dS; dv += dO^T P, dk += qt^T dS ----
+#pragma unroll
+    for (int hl = 0; hl < HW; ++hl) {
+      const int h = ws * HW + hl;
+      if (h >= H) continue;
+      f32x4 S[NS], dP[NS], dS[NS];
+#pragma unroll
+      for (int s = 0; s < NS; ++s) {
+        const float* us = UWs + (h * 16 + n) * UWR + 16 * s + 4 * g;
+        const f32x4 ue = attn ? *reinterpret_cast<const f32x4*>(us) : zero4();
+        const f32x4 we = act ? *reinterpret_cast<const f32x4*>(us + HP * 16 * UWR) : zero4();
+        KFrag<T, D> qa, oa;  // A = qt_i[d], dO_i[d]: lane n = streamed row 16s + n
+        if constexpr (BF) {
+          qa.load(Qs + (h * KC + 16 * s + n) * Cfg::QO_ROW, g);
+          oa.load(Os + (h * KC + 16 * s + n) * Cfg::QO_ROW, g);
+        } else {
+          int i = c0 + 16 * s + n;
+          i = i < len ? i : len - 1;
+          qa.load_scaled(qg + ra.off(h, i, D), g, prm.scale);
+          oa.load(dog + ra.off(h, i, D), g);
+        }
+        S[s] = mma_k<D>(qa, kf[hl], ue);
+        dP[s] = mma_k<D>(oa, vf[hl], we);
+        unsigned vm = 0;
+        f32x4 lse4, d4, dob4;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int il = 16 * s + 4 * g + r;
+          vm |= ((c0 + il < len && key_ok) ? 1u : 0u) << r;
+          lse4[r] = Lv[h * KC + il];
+          d4[r] = Lv[HP * KC + h * KC + il];
+          dob4[r] = Lv[2 * HP * KC + h * KC + il];
+        }
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const bool ok = (vm >> r) & 1u;
+          const float p = exp2f_fast(__builtin_fmaf(S[s][r], kLog2e, -lse4[r]));
+          S[s][r] = ok ? p : 0.f;
+          dP[s][r] = dP[s][r] + dob4[r];
+          dS[s][r] = S[s][r] * (dP[s][r] - d4[r]);
+        }
+      }
+      JFrag<T, NS> pf, dsf;
+      pf.from_tiles(S);
+      dsf.from_tiles(dS);
+#pragma unroll
+      for (int dt = 0; dt < D / 16; ++dt) {
+        JFrag<T, NS> ot, qt;
+        if constexpr (BF) {
+          ot.load_tr(Os + h * KC * Cfg::QO_ROW, Cfg::QO_ROW, 16 * dt, g, n);
+          qt.load_tr(Qs + h * KC * Cfg::QO_ROW, Cfg::QO_ROW, 16 * dt, g, n);
+        } else {
+#pragma unroll
+          for (int s = 0; s < NS; ++s)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+              const int i = c0 + 16 * s + 4 * g + r;
+              const bool ok = i < len;
+              const long off = ra.off(h, ok ? i : 0, D) + 16 * dt + n;
+              ot.v[4 * s + r] = ok ? (float)dog[off] : 0.f;
+              qt.v[4 * s + r] = ok ? (float)qg[off] * prm.scale : 0.f;
+            }
+        }
+        dV[hl][dt] = mma_j(ot, pf, dV[hl][dt]);
+        dK[hl][dt] = mma_j(qt, dsf, dK[hl][dt]);
+      }
+    }
+    __syncthreads();
+  }
+
+  T* dkg = reinterpret_cast<T*>(prm.dk);
+  T* dvg = reinterpret_cast<T*>(prm.dv);
+#pragma unroll
+  for (int hl = 0; hl < HW; ++hl) {
+    const int h = ws * HW + hl;
+    if (h >= H || !key_ok) continue;
+#pragma unroll
+    for (int dt = 0; dt < D / 16; ++dt) {
+      store4<T>(dkg + ra.off(h, my_key, D) + 16 * dt + 4 * g, dK[hl][dt]);
+      store4<T>(dvg + ra.off(h, my_key, D) + 16 * dt + 4 * g, dV[hl][dt]);
+    }
+  }
+  zero_pad_rows<T>(ev, eb, ra, key0, Cfg::KEYS, D, tid, 256, dkg, nullptr, 1);
+  zero_pad_rows<T>(ev, eb, ra, key0, Cfg::KEYS, D, tid, 256, dvg, nullptr, 1);
+}
+
+// ---------------------------------------------------------------------------
+// Dispatch.
+// ---------------------------------------------------------------------------
+template <template <typename, int, int, int, int, int> class Cfg, typename T, int HP, int D, int C>
+struct BwdPick {
+  template <int NW, int NS>
+  using F = Cfg<T, HP, D, C, NW, NS>;
+  static constexpr int NS = (F<1, 2>::FITS || F<2, 2>::FITS || F<4, 2>::FITS) ? 2 : 1;
+  static constexpr int NW = F<1, NS>::FITS ? 1 : (F<2, NS>::FITS ? 2 : 4);
+  using Sel = F<NW, NS>;
+  static constexpr bool OK = Sel::FITS;
+};
+
+template <typename T, int HP, int D, int C>
+int bwd_launch_t(const BwdParams& prm, int which, hipStream_t stream, int grid, bool query, int* rows) {
+  using PR = BwdPick<BwdRowsCfg, T, HP, D, C>;
+  using PC = BwdPick<BwdColsCfg, T, HP, D, C>;
+  if constexpr (!PR::OK || !PC::OK) {
+    if (query) *rows = 0;
+    return FST_EUNSUPPORTED;
+  } else {
+    if (query) {
+      *rows = which == 0 ? PR::Sel::ROWS : PC::Sel::KEYS;
+      return FST_OK;
+    }
+    const void* kern;
+    int lds;
+    if (which == 0) {
+      kern = (const void*)bwd_rows_kernel<T, HP, D, C, PR::NW, PR::NS>;
+      lds = PR::Sel::LDS_BYTES;
+    } else {
+      kern = (const void*)bwd_cols_kernel<T, HP, D, C, PC::NW, PC::NS>;
+      lds = PC::Sel::LDS_BYTES;
+    }
+    if (hipFuncSetAttribute(kern, hipFuncAttributeMaxDynamicSharedMemorySize, lds) != hipSuccess) return FST_ELAUNCH;
+    if (grid > 0) {
+      if (which == 0)
+        hipLaunchKernelGGL((bwd_rows_kernel<T, HP, D, C, PR::NW, PR::NS>), dim3(grid), dim3(256), lds, stream, prm);
+      else
+        hipLaunchKernelGGL((bwd_cols_kernel<T, HP, D, C, PC::NW, PC::NS>), dim3(grid), dim3(256), lds, stream, prm);
+    }
+    return hipGetLastError() == hipSuccess ? FST_OK : FST_ELAUNCH;
+  }
+}
+
+}  // namespace fst

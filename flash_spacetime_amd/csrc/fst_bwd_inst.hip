@@ -1,0 +1,30 @@
+// Instantiates the backward kernels for one (dtype, D) over every head
+// padding HP in {4, 8, 12, 16} and channel count C in {16, 32, 48, 64}.
+// Built once per (dtype, D) with -DFST_T, -DFST_D and -DFST_NAME.
+#include "fst_backward.hip"
+
+#if !defined(FST_T) || !defined(FST_D) || !defined(FST_NAME)
+#error "FST_T, FST_D and FST_NAME must be defined"
+#endif
+
+#define FST_CAT2(a, b) a##b
+#define FST_CAT(a, b) FST_CAT2(a, b)
+
+namespace fst {
+
+int FST_CAT(bwd_dispatch_, FST_NAME)(const BwdParams& prm, int which, int HP, int C, hipStream_t stream, int grid,
+                                     bool query, int* rows) {
+#define FST_CASE(HPV, CV) \
+  if (HP == HPV && C == CV) return bwd_launch_t<FST_T, HPV, FST_D, CV>(prm, which, stream, grid, query, rows);
+#define FST_CASES(HPV) FST_CASE(HPV, 16) FST_CASE(HPV, 32) FST_CASE(HPV, 48) FST_CASE(HPV, 64)
+  FST_CASES(4)
+  FST_CASES(8)
+  FST_CASES(12)
+  FST_CASES(16)
+#undef FST_CASES
+#undef FST_CASE
+  if (query) *rows = 0;
+  return FST_EUNSUPPORTED;
+}
+
+}  // namespace fst

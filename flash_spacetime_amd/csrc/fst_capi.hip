@@ -129,6 +129,79 @@ static int check_common(int dtype, int flags, int B, int H, int L, int T, int D,
 
 static size_t blkcum_bytes(int B) { return align_up((size_t)(B + 1) * sizeof(int32_t), 256); }
 
+typedef int (*bwd_dispatch_fn)(const BwdParams&, int, int, int, hipStream_t, int, bool, int*);
+
+static bwd_dispatch_fn bwd_table(int dtype, int D) {
+  if (dtype == FST_BF16) {
+    switch (D) {
+      case 16: return bwd_dispatch_bf16_16;
+      case 32: return bwd_dispatch_bf16_32;
+      case 48: return bwd_dispatch_bf16_48;
+      case 64: return bwd_dispatch_bf16_64;
+    }
+  } else if (dtype == FST_F32) {
+    switch (D) {
+      case 16: return bwd_dispatch_f32_16;
+      case 32: return bwd_dispatch_f32_32;
+      case 48: return bwd_dispatch_f32_48;
+      case 64: return bwd_dispatch_f32_64;
+    }
+  }
+  return nullptr;
+}
+
+// Sums the per-block dW / db partials of the rows kernel in block order.
+__global__ __launch_bounds__(256) void dw_reduce_kernel(const float* part, const int32_t* blkcum, int B, int DC, int D,
+                                                         int use_e, float* dw, float* db) {
+  const int nblk = blkcum[B];
+  for (int e = blockIdx.x * blockDim.x + threadIdx.x; e < DC + D; e += gridDim.x * blockDim.x) {
+    float acc = 0.f;
+    if (use_e)
+      for (int w = 0; w < nblk; ++w) acc += part[(long)w * (DC + D) + e];
+    if (e < DC)
+      dw[e] = acc;
+    else if (db)
+      db[e - DC] = acc;
+  }
+}
+
+struct BwdLayout {
+  int rows_r, rows_c;   // rows (keys) per workgroup of the rows / cols kernels
+  long grid_r, grid_c;
+  size_t off_bc_r, off_bc_c, off_u, off_wt, off_dob, off_dsum, off_part, total;
+};
+
+static int bwd_layout(int dtype, int flags, int B, int H, int L, int T, int D, int C, BwdLayout& lay) {
+  bwd_dispatch_fn fn = bwd_table(dtype, D);
+  BwdParams dummy;
+  std::memset(&dummy, 0, sizeof(dummy));
+  const int HP = head_padding(H);
+  if (fn(dummy, 0, HP, C, nullptr, 0, true, &lay.rows_r) != FST_OK || lay.rows_r <= 0) return FST_EUNSUPPORTED;
+  if (fn(dummy, 1, HP, C, nullptr, 0, true, &lay.rows_c) != FST_OK || lay.rows_c <= 0) return FST_EUNSUPPORTED;
+  const bool packed = flags & FST_PACKED;
+  const long rows = packed ? (long)T : (long)B * L;
+  lay.grid_r = packed ? ((long)T + lay.rows_r - 1) / lay.rows_r + B : (long)B * ((L + lay.rows_r - 1) / lay.rows_r);
+  lay.grid_c = packed ? ((long)T + lay.rows_c - 1) / lay.rows_c + B : (long)B * ((L + lay.rows_c - 1) / lay.rows_c);
+  const size_t esz = dtype == FST_BF16 ? 2 : 4;
+  size_t off = 0;
+  lay.off_bc_r = off;
+  off += blkcum_bytes(B);
+  lay.off_bc_c = off;
+  off += blkcum_bytes(B);
+  lay.off_u = off;
+  off += align_up((size_t)rows * H * C * esz, 256);
+  lay.off_wt = off;
+  off += align_up((size_t)rows * H * C * esz, 256);
+  lay.off_dob = off;
+  off += align_up((size_t)rows * H * 4, 256);
+  lay.off_dsum = off;
+  off += align_up((size_t)rows * H * 4, 256);
+  lay.off_part = off;
+  off += align_up((size_t)(lay.grid_r > 0 ? lay.grid_r : 0) * (D * C + D) * 4, 256);
+  lay.total = off;
+  return FST_OK;
+}
+
 }  // namespace fst
 
 using namespace fst;
@@ -221,14 +294,93 @@ int fst_forward(int dtype, int flags, int B, int H, int L, int T, int D, int C, 
 }
 
 size_t fst_backward_workspace_bytes(int dtype, int flags, int B, int H, int L, int T, int D, int C) {
-  return fst_forward_workspace_bytes(dtype, flags, B, H, L, T, D, C);
+  if (check_common(dtype, flags, B, H, L, T, D, C) != FST_OK) return 0;
+  BwdLayout lay;
+  if (bwd_layout(dtype, flags, B, H, L, T, D, C, lay) != FST_OK) return 0;
+  return lay.total;
 }
 
 int fst_backward(int dtype, int flags, int B, int H, int L, int T, int D, int C, const void* q, const void* k,
                  const void* v, const float* pos4, const float* weight, const float* bias, const int32_t* lens,
                  const float* lse, const void* grad_out, float scale, void* dq, void* dk, void* dv, float* dweight,
                  float* dbias, float* rowsum, void* workspace, size_t workspace_bytes, void* stream) {
-  return fail(FST_EUNSUPPORTED, "backward kernels are not built yet");
+  g_last_error[0] = 0;
+  int rc = check_common(dtype, flags, B, H, L, T, D, C);
+  if (rc != FST_OK) return rc;
+  const bool packed = flags & FST_PACKED;
+  const bool use_w = flags & (FST_ATTN_BIAS | FST_ACT_BIAS);
+  hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  const long rows_total = packed ? (long)T : (long)B * L;
+  if (!dweight) return fail(FST_EINVAL, "dweight is required");
+  if (B == 0 || rows_total == 0) {
+    hipMemsetAsync(dweight, 0, sizeof(float) * D * C, st);
+    if (dbias) hipMemsetAsync(dbias, 0, sizeof(float) * D, st);
+    return FST_OK;
+  }
+  if (!q || !k || !v || !lens || !lse || !grad_out || !dq || !dk || !dv)
+    return fail(FST_EINVAL, "null tensor pointer");
+  if (use_w && (!pos4 || !weight)) return fail(FST_EINVAL, "pos4 and weight are required when a bias flag is set");
+  if (!std::isfinite(scale)) return fail(FST_EINVAL, "scale must be finite");
+  BwdLayout lay;
+  if (bwd_layout(dtype, flags, B, H, L, T, D, C, lay) != FST_OK)
+    return fail(FST_EUNSUPPORTED, "no compiled backward for dtype=%d H=%d D=%d C=%d", dtype, H, D, C);
+  if (!workspace || workspace_bytes < lay.total)
+    return fail(FST_EWORKSPACE, "workspace of %zu bytes is smaller than the %zu required", workspace_bytes, lay.total);
+  if (lay.grid_r > 0x7fffffffL || lay.grid_c > 0x7fffffffL) return fail(FST_EUNSUPPORTED, "problem too large");
+
+  unsigned char* ws = reinterpret_cast<unsigned char*>(workspace);
+  int32_t* bc_r = reinterpret_cast<int32_t*>(ws + lay.off_bc_r);
+  int32_t* bc_c = reinterpret_cast<int32_t*>(ws + lay.off_bc_c);
+  hipLaunchKernelGGL(blkcum_kernel, dim3(1), dim3(1024), 0, st, lens, packed ? 1 : 0, B, L, T, lay.rows_r, bc_r);
+  hipLaunchKernelGGL(blkcum_kernel, dim3(1), dim3(1024), 0, st, lens, packed ? 1 : 0, B, L, T, lay.rows_c, bc_c);
+  if (hipGetLastError() != hipSuccess) return fail(FST_ELAUNCH, "work-list kernel launch failed");
+
+  BwdParams prm;
+  std::memset(&prm, 0, sizeof(prm));
+  prm.ev.lens = lens;
+  prm.ev.blkcum = bc_r;
+  prm.ev.pos4 = reinterpret_cast<const float4*>(pos4);
+  prm.ev.B = B;
+  prm.ev.H = H;
+  prm.ev.L = L;
+  prm.ev.T = T;
+  prm.ev.packed = packed ? 1 : 0;
+  prm.blkcum_cols = bc_c;
+  prm.H = H;
+  prm.flags = flags;
+  prm.scale = scale;
+  prm.q = q;
+  prm.k = k;
+  prm.v = v;
+  prm.dout = grad_out;
+  prm.weight = weight;
+  prm.bias = bias;
+  prm.lse = lse;
+  prm.u = ws + lay.off_u;
+  prm.wt = ws + lay.off_wt;
+  prm.dob = reinterpret_cast<float*>(ws + lay.off_dob);
+  prm.dsum = reinterpret_cast<float*>(ws + lay.off_dsum);
+  prm.dw_part = reinterpret_cast<float*>(ws + lay.off_part);
+  prm.dq = dq;
+  prm.dk = dk;
+  prm.dv = dv;
+  prm.rowsum = rowsum;
+  prm.dweight = dweight;
+  prm.dbias = dbias;
+  freq_table(C, prm.freq);
+
+  bwd_dispatch_fn fn = bwd_table(dtype, D);
+  const int HP = head_padding(H);
+  int dummy_rows = 0;
+  rc = fn(prm, 0, HP, C, st, (int)lay.grid_r, false, &dummy_rows);
+  if (rc != FST_OK) return fail(rc, "backward rows kernel launch failed");
+  rc = fn(prm, 1, HP, C, st, (int)lay.grid_c, false, &dummy_rows);
+  if (rc != FST_OK) return fail(rc, "backward cols kernel launch failed");
+  const int DC = D * C;
+  hipLaunchKernelGGL(dw_reduce_kernel, dim3((DC + D + 255) / 256), dim3(256), 0, st, prm.dw_part, bc_r, B, DC, D,
+                     use_w ? 1 : 0, dweight, dbias);
+  if (hipGetLastError() != hipSuccess) return fail(FST_ELAUNCH, "dW reduction launch failed");
+  return FST_OK;
 }
 
 }  // extern "C"

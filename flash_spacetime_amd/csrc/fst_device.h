@@ -319,6 +319,21 @@ __device__ __forceinline__ float pair_angle(float4 a, float4 b) {
   return kInputScale * fminf(fmaxf(sd, -kClip), kClip);
 }
 
+// The same angle evaluated in binary64 from the fp32 coordinates (the
+// differences are exact there, so only the final rounding remains). Used by
+// the fp32 kernels: near the light cone I is a difference of nearly equal
+// squares, and any fp32 evaluation of it carries an error that is large
+// relative to I; in binary64 that error is gone, so the fp32 kernels are at
+// least as accurate as the eager fp32 definition on every pair.
+__device__ __forceinline__ double pair_angle_f64(float4 a, float4 b) {
+  const double dx = (double)a.x - (double)b.x, dy = (double)a.y - (double)b.y, dz = (double)a.z - (double)b.z;
+  const double dt = ((double)a.w - (double)b.w) * 18.0;
+  const double interval = dx * dx + dy * dy + dz * dz - dt * dt;
+  const double mag = __builtin_sqrt(__builtin_fabs(interval));
+  const double sd = interval > 0.0 ? mag : (interval < 0.0 ? -mag : 0.0);
+  return 1024.0 * __builtin_fmin(__builtin_fmax(sd, -4.0), 4.0);
+}
+
 // Frequency table handed to the kernels: ghi + glo = f_c / (2 pi) split in
 // two fp32 words (the hardware sin/cos take revolutions), and whether the
 // largest angle 4096 f_c exceeds the +-256 revolution domain of v_sin_f32,
@@ -329,19 +344,23 @@ struct FreqTable {
   uint32_t reduce_mask;  // bit f set -> reduce channel pair f
 };
 
-// sin and cos of 2*pi*(x * g) for one frequency. ACCURATE adds the low word
-// of g and the rounding error of x*ghi (two FMAs) so the reduced argument is
-// good to ~1e-7 revolutions even at |x*g| ~ 650; otherwise the argument
-// carries the fp32 rounding of the product (~4e-5 rev), which is far below
-// the bf16 rounding the embedding gets next.
+// sin and cos of 2*pi*(x * g) for one frequency. ACCURATE (fp32 embedding)
+// reduces to [0, 1) revolutions and adds the low word of g and the rounding
+// error of x*ghi (two FMAs), so the argument is good to ~1e-7 revolutions
+// even at |x*g| ~ 650; otherwise (bf16 embedding) only arguments beyond the
+// +-256 revolution domain are reduced and the argument carries the fp32
+// rounding of the product (<= 1.5e-5 rev), far below the bf16 rounding the
+// embedding gets next.
 template <bool ACCURATE>
 __device__ __forceinline__ void sincos_rev(float x, float ghi, float glo, bool reduce, float& s, float& c) {
   float p = x * ghi;
   float r;
   if constexpr (ACCURATE) {
+    // Every channel is reduced to [0, 1) before the correction is added, so
+    // the correction is not lost to the ulp of a large argument.
     float e = __builtin_fmaf(x, ghi, -p);
     e = __builtin_fmaf(x, glo, e);
-    r = (reduce ? __builtin_amdgcn_fractf(p) : p) + e;
+    r = __builtin_amdgcn_fractf(p) + e;
   } else {
     r = reduce ? __builtin_amdgcn_fractf(p) : p;
   }

@@ -169,8 +169,7 @@ __global__ __launch_bounds__(256, 1) void fwd_kernel(FwdParams prm) {
 #pragma unroll
       for (int k2 = 0; k2 < EPL; ++k2) {
         const int il = ws * RW + lane / KC + ESTEP * k2;
-        const float x = pair_angle(pos_i[k2], pj);
-        write_embedding<T, C>(Es + (il * KC + key) * Cfg::E_ROW, x, prm.freq);
+        write_embedding<T, C>(Es + (il * KC + key) * Cfg::E_ROW, pos_i[k2], pj, prm.freq);
       }
       wave_lds_sync();
       if (attn) {

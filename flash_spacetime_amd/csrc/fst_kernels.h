@@ -91,6 +91,30 @@ struct FwdParams {
   FreqTable freq;
 };
 
+struct BwdParams {
+  EventSpec ev;     // rows-kernel work list in ev.blkcum
+  const int32_t* blkcum_cols;  // cols-kernel work list
+  int H, flags;
+  float scale;
+  const void *q, *k, *v, *dout;
+  const float* weight;  // [D, C]
+  const float* bias;    // [D] or null
+  const float* lse;     // [rows]
+  // scratch written by the rows kernel, read by the cols kernel
+  void* u;              // [rows, C] T
+  void* wt;             // [rows, C] T
+  float* dob;           // [rows]
+  float* dsum;          // [rows]
+  float* dw_part;       // [blocks, D, C]
+  float* db_part;       // [blocks, D]
+  // outputs
+  void *dq, *dk, *dv;
+  float* rowsum;        // nullable
+  float* dweight;
+  float* dbias;         // nullable
+  FreqTable freq;
+};
+
 template <typename T>
 struct VecOf;
 template <>
@@ -216,15 +240,28 @@ __device__ __forceinline__ void project_row(const T* x_row, long hstride, bool v
   }
 }
 
-// Pair embedding of one (row, key) into an LDS row: channel f is
-// sin(x f_f), channel C/2 + f is cos(x f_f) (reference.py:82-84 order).
+// Pair embedding of one (row i, key j) into an LDS row: channel f is
+// sin(x_ij f_f), channel C/2 + f is cos(x_ij f_f) (reference.py:75-84 order).
+// bf16 kernels evaluate the angle in fp32 (the result is rounded to bf16);
+// fp32 kernels evaluate angle and argument reduction in binary64.
 template <typename T, int C>
-__device__ __forceinline__ void write_embedding(T* erow, float x, const FreqTable& ft) {
+__device__ __forceinline__ void write_embedding(T* erow, float4 pi, float4 pj, const FreqTable& ft) {
   constexpr int F = C / 2;
   float sv[F], cv[F];
+  if constexpr (is_bf16<T>::value) {
+    const float x = pair_angle(pi, pj);
 #pragma unroll
-  for (int f = 0; f < F; ++f)
-    sincos_rev<!is_bf16<T>::value>(x, ft.ghi[f], ft.glo[f], (ft.reduce_mask >> f) & 1u, sv[f], cv[f]);
+    for (int f = 0; f < F; ++f) sincos_rev<false>(x, ft.ghi[f], ft.glo[f], (ft.reduce_mask >> f) & 1u, sv[f], cv[f]);
+  } else {
+    const double x = pair_angle_f64(pi, pj);
+#pragma unroll
+    for (int f = 0; f < F; ++f) {
+      const double rev = x * ((double)ft.ghi[f] + (double)ft.glo[f]);
+      const float r = (float)(rev - __builtin_floor(rev));
+      sv[f] = __builtin_amdgcn_sinf(r);
+      cv[f] = __builtin_amdgcn_cosf(r);
+    }
+  }
   if constexpr (is_bf16<T>::value) {
     static_assert(F % 4 == 0, "C must be a multiple of 8");
 #pragma unroll
@@ -289,5 +326,21 @@ FST_DECL_FWD(f32_32)
 FST_DECL_FWD(f32_48)
 FST_DECL_FWD(f32_64)
 #undef FST_DECL_FWD
+
+// Backward dispatch per (dtype, D) (fst_bwd_inst.hip). which = 0: rows
+// kernel, 1: cols kernel. With query set, reports rows (or keys) per
+// workgroup in *rows (0 = unsupported).
+#define FST_DECL_BWD(NAME)                                                                                   \
+  int bwd_dispatch_##NAME(const BwdParams& prm, int which, int HP, int C, hipStream_t stream, int grid, bool query, \
+                          int* rows);
+FST_DECL_BWD(bf16_16)
+FST_DECL_BWD(bf16_32)
+FST_DECL_BWD(bf16_48)
+FST_DECL_BWD(bf16_64)
+FST_DECL_BWD(f32_16)
+FST_DECL_BWD(f32_32)
+FST_DECL_BWD(f32_48)
+FST_DECL_BWD(f32_64)
+#undef FST_DECL_BWD
 
 }  // namespace fst

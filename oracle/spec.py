@@ -21,6 +21,7 @@ Two evaluators live here:
 
 from __future__ import annotations
 
+import math
 from typing import Optional, Sequence, Tuple
 
 import torch
@@ -37,17 +38,25 @@ SINEMB_N_FREQ = 10000.0
 def frequencies(c: int) -> Tensor:
     """fp32 frequency ladder `exp(-i * ln(1e4) / (c/2))`, i < c/2.
 
-    reference.py:45-56: the ladder is formed in float32 whatever the working
-    dtype (log of the fp32 constant, divided by the float c/2, times an fp32
-    arange, exponentiated in fp32); the same four fp32 steps are taken here
-    so the values agree bit for bit.
+    reference.py:45-56 forms the ladder in float32 whatever the working dtype:
+    fp32 log of 1e4, divided by the float c/2, times an fp32 arange,
+    exponentiated in fp32. The same fp32 steps are taken here, with the two
+    transcendental steps correctly rounded (evaluated in binary64, rounded
+    once to fp32). torch's vectorised fp32 exp is not correctly rounded and
+    differs between CPUs by an ulp on some entries (seen: C=64 i=11 in one
+    container, i=3 on another host); a correctly rounded ladder makes the
+    oracle machine-independent and equal to the GPU library's ladder. The
+    golden-vector test pins it bitwise to the reference wherever the
+    reference's own evaluation was correctly rounded, and to within one ulp
+    elsewhere.
     """
     if c <= 0 or c % 2:
         raise ValueError(f"channel count must be positive and even, got {c}")
     half = c / 2
-    neg_log_step = -(torch.log(torch.tensor([SINEMB_N_FREQ], dtype=torch.float32)) / half)
+    log_n = torch.tensor([math.log(SINEMB_N_FREQ)], dtype=torch.float64).float()
+    neg_log_step = -(log_n / half)
     ramp = torch.arange(half, dtype=torch.float32)
-    return torch.exp(ramp * neg_log_step)
+    return torch.exp((ramp * neg_log_step).double()).float()
 
 
 def pair_angle_rect(rows: Tensor, cols: Tensor) -> Tensor:
