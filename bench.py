@@ -1,0 +1,260 @@
+"""Benchmark of the fused spacetime-bias attention step on one MI355X.
+
+Workload (the metric's configuration): one
+forward + backward of `flash_spacetime_attention` at B=256, L=768, H=12,
+D=32, C=16 in bf16 with per-event valid lengths ~ U{16..768}. Inputs are
+synthetic and drawn from one seeded CPU generator in a fixed order
+(q, k, v, pos, W, b, lengths, dO): q, k, v, dO ~ N(0, 1); x, y, z ~
+U(-500, 500), t ~ U(0, 2e4); W ~ N(0, 1/C) and b ~ N(0, 0.02) in fp32.
+
+Prints ONE JSON line: ms/step of the whole fwd+bwd step (HIP events over K
+steps after W warm-up steps, inputs resident in HBM), peak GiB allocated
+by the step, % of the bf16 MFMA peak for the algorithmic FLOPs, per-kernel
+times of the individual launches, the MFMA roofline of the dominant kernel,
+and the CPU baseline (the oracle's eager restatement of the spec, fp32,
+fwd+bwd, timed on this host's cores on a bounded sample of events).
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W]
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+if ROOT not in sys.path:
+    sys.path.insert(0, ROOT)
+
+import torch  # noqa: E402
+
+METRIC = "fwd+bwd ms/step & peak GiB at B=256,L=768,C=16 bf16; % MFMA peak"
+B, L, H, D, C = 256, 768, 12, 32, 16
+PEAK_BF16_TFLOPS = 2500.0  # MI355X dense bf16 MFMA
+PEAK_HBM_GBS = 8000.0
+
+
+def make_inputs(device):
+    gen = torch.Generator().manual_seed(0)
+    q = torch.randn(B, H, L, D, generator=gen)
+    k = torch.randn(B, H, L, D, generator=gen)
+    v = torch.randn(B, H, L, D, generator=gen)
+    xyz = (torch.rand(B, L, 3, generator=gen) - 0.5) * 1000.0
+    t = torch.rand(B, L, 1, generator=gen) * 2e4
+    feats = torch.cat([xyz, t], -1)
+    w = torch.randn(D, C, generator=gen) / C ** 0.5
+    bias = torch.randn(D, generator=gen) * 0.02
+    lengths = torch.randint(16, L + 1, (B,), generator=gen)
+    do = torch.randn(B, H, L, D, generator=gen)
+    pad_mask = torch.arange(L)[None, :] >= lengths[:, None]  # bool key_padding_mask, True = padding
+    return dict(
+        q=q.to(device, torch.bfloat16), k=k.to(device, torch.bfloat16), v=v.to(device, torch.bfloat16),
+        feats=feats.to(device), w=w.to(device), b=bias.to(device), lengths=lengths,
+        pad_mask=pad_mask.to(device), do=do.to(device, torch.bfloat16),
+    )
+
+
+def flop_counts(lengths):
+    """Algorithmic FLOPs over valid pairs (per pair-head): fwd 4(D+C);
+    bwd 10D+8C, of which the rows kernel is credited 6D+8C (one S and dP
+    recompute, dq, H, G) and the cols kernel 4D (dk, dv)."""
+    sl2 = float((lengths.double() ** 2).sum())
+    return {
+        "fwd": H * sl2 * 4 * (D + C),
+        "bwd_rows": H * sl2 * (6 * D + 8 * C),
+        "bwd_cols": H * sl2 * 4 * D,
+        "sum_l2": sl2,
+        "dense_fwd_bwd": H * B * L * L * (4 * (D + C) + 10 * D + 8 * C),
+    }
+
+
+def time_events(fn, iters, stream):
+    start = torch.cuda.Event(enable_timing=True)
+    end = torch.cuda.Event(enable_timing=True)
+    start.record(stream)
+    for _ in range(iters):
+        fn()
+    end.record(stream)
+    end.synchronize()
+    return start.elapsed_time(end) / iters
+
+
+def kernel_times(inp, seqlens, iters=10):
+    """Average duration of each launch, timed with HIP events on the stream the
+    library launches on (torch's current stream), one phase at a time."""
+    from flash_spacetime_amd import _lib
+    from flash_spacetime_amd.forward import _Prepared
+
+    lib = _lib.load()
+    dev = inp["q"].device
+    prep = _Prepared(inp["q"], inp["k"], inp["v"], inp["feats"], inp["w"], inp["b"], seqlens, None,
+                     True, True, None)
+    dims = prep.dims()
+    stream = torch.cuda.current_stream(dev)
+    sh = stream.cuda_stream
+    out = torch.empty_like(prep.q)
+    lse = torch.empty(prep.vec_shape(), device=dev, dtype=torch.float32)
+    fws = lib.fst_forward_workspace_bytes(*dims)
+    fwork = torch.empty(fws, device=dev, dtype=torch.uint8)
+    P = _lib.ptr
+    fargs = (P(prep.q), P(prep.k), P(prep.v), P(prep.pos4), P(prep.weight), P(prep.bias), P(prep.lens),
+             prep.scale, P(out), P(lse), P(fwork), fws, sh)
+    _lib.check(lib.fst_forward_phases(_lib.FST_PHASE_WORKLIST, *dims, *fargs), "worklist")
+    do = inp["do"].contiguous()
+    dq, dk, dv = (torch.empty_like(prep.q) for _ in range(3))
+    dw = torch.empty(D, C, device=dev)
+    db = torch.empty(D, device=dev)
+    bws = lib.fst_backward_workspace_bytes(*dims)
+    bwork = torch.empty(bws, device=dev, dtype=torch.uint8)
+    bargs = (P(prep.q), P(prep.k), P(prep.v), P(prep.pos4), P(prep.weight), P(prep.bias), P(prep.lens), P(lse),
+             P(do), prep.scale, P(dq), P(dk), P(dv), P(dw), P(db), None, P(bwork), bws, sh)
+    _lib.check(lib.fst_forward_phases(_lib.FST_PHASE_FWD, *dims, *fargs), "fwd")
+    _lib.check(lib.fst_backward_phases(_lib.FST_BWD_ALL, *dims, *bargs), "bwd")
+    torch.cuda.synchronize(dev)
+    res = {}
+    res["fwd"] = time_events(lambda: lib.fst_forward_phases(_lib.FST_PHASE_FWD, *dims, *fargs), iters, stream)
+    res["bwd_rows"] = time_events(lambda: lib.fst_backward_phases(_lib.FST_PHASE_BWD_ROWS, *dims, *bargs), iters,
+                                  stream)
+    res["bwd_cols"] = time_events(lambda: lib.fst_backward_phases(_lib.FST_PHASE_BWD_COLS, *dims, *bargs), iters,
+                                  stream)
+    res["bwd_reduce"] = time_events(lambda: lib.fst_backward_phases(_lib.FST_PHASE_REDUCE, *dims, *bargs), iters,
+                                    stream)
+    res["worklist"] = time_events(lambda: lib.fst_forward_phases(_lib.FST_PHASE_WORKLIST, *dims, *fargs), iters,
+                                  stream)
+    return res
+
+
+def cpu_baseline(inp, budget_s=15.0, max_events=B):
+    """The oracle's eager restatement of the spec (materialised R, autograd
+    backward), fp32, padded events of length L with the float mask exactly as
+    the eager module runs, timed one event at a time until the time budget is
+    spent; ms/step is extrapolated to the 256 events (eager padded cost is the
+    same for every event)."""
+    import oracle
+
+    torch.set_num_threads(os.cpu_count() or 1)
+    threads = torch.get_num_threads()
+    q = inp["q"].float().cpu()
+    k = inp["k"].float().cpu()
+    v = inp["v"].float().cpu()
+    feats = inp["feats"].float().cpu()
+    w, b = inp["w"].cpu(), inp["b"].cpu()
+    do = inp["do"].float().cpu()
+    valid = ~inp["pad_mask"].cpu()
+    fmask = oracle.float_padding_mask(valid, torch.float32)
+    done, t_total = 0, 0.0
+    while done < max_events and (t_total < budget_s or done == 0):
+        sl = slice(done, done + 1)
+        leaves = [x[sl].clone().requires_grad_(True) for x in (q, k, v)]
+        wl, bl = w.clone().requires_grad_(True), b.clone().requires_grad_(True)
+        t0 = time.perf_counter()
+        out = oracle.attention(*leaves, feats[sl], wl, bl, key_padding_mask=fmask[sl])
+        out.backward(do[sl] * valid[sl][:, None, :, None])
+        t_total += time.perf_counter() - t0
+        done += 1
+    per_event_ms = 1e3 * t_total / done
+    return {
+        "value": per_event_ms * B,
+        "unit": "ms",
+        "cores": threads,
+        "kind": "port",
+        "sample": f"{done} of {B} padded events (L={L}) fwd+bwd in fp32 eager PyTorch on the CPU "
+                  f"(oracle.attention + autograd, materialised [1,L,L,D] pair tensor), {1e3 * t_total:.0f} ms "
+                  f"total, extrapolated x{B}/{done}",
+    }
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-budget-s", type=float, default=15.0)
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU: this build's hot path is single-device (events are independent; "
+              f"multi-GPU would shard events with no exchange). --gpus {args.gpus} is not run.", file=sys.stderr)
+        sys.exit(2)
+
+    from flash_spacetime_amd import flash_spacetime_attention
+    from flash_spacetime_amd.forward import lengths_from_mask
+
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    inp = make_inputs(dev)
+    seqlens = lengths_from_mask(inp["pad_mask"], L)  # the bool mask, converted once (one readback)
+    leaves = [inp[n].detach().clone().requires_grad_(True) for n in ("q", "k", "v")]
+    wl = inp["w"].clone().requires_grad_(True)
+    bl = inp["b"].clone().requires_grad_(True)
+    do = inp["do"]
+
+    def step():
+        for t in (*leaves, wl, bl):
+            t.grad = None
+        out = flash_spacetime_attention(*leaves, inp["feats"], wl, bl, seqlens)
+        out.backward(do)
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize(dev)
+    stream = torch.cuda.current_stream(dev)
+    ms = time_events(step, args.steps, stream)
+    torch.cuda.synchronize(dev)
+
+    torch.cuda.reset_peak_memory_stats(dev)
+    base = torch.cuda.memory_allocated(dev)
+    step()
+    torch.cuda.synchronize(dev)
+    peak_gib = (torch.cuda.max_memory_allocated(dev) - base) / 2 ** 30
+
+    flops = flop_counts(inp["lengths"])
+    kt = kernel_times(inp, seqlens)
+    f_total = flops["fwd"] + flops["bwd_rows"] + flops["bwd_cols"]
+    mfma_pct = 100.0 * f_total / (ms * 1e-3) / (PEAK_BF16_TFLOPS * 1e12)
+    dominant = max(("fwd", "bwd_rows", "bwd_cols"), key=lambda k_: kt[k_])
+    achieved = flops[dominant] / (kt[dominant] * 1e-3) / 1e12
+    result = {
+        "metric": METRIC,
+        "value": round(ms, 4),
+        "unit": "ms",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 4),
+        "higher_is_better": False,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded; BASELINE.json configs[2] distributions)",
+        "config": {
+            "workload": "configs[2]: flash_spacetime_attention fwd+bwd, B=256 L=768 H=12 D=32 C=16 bf16, "
+                        "valid lengths U{16..768} (bool key_padding_mask -> seqlens once), W/b fp32",
+            "B": B, "L": L, "H": H, "D": D, "C": C,
+            "valid_pairs": flops["sum_l2"],
+        },
+        "peak_gib": round(peak_gib, 4),
+        "mfma_pct_of_peak": round(mfma_pct, 3),
+        "algorithmic_tflop": round(f_total / 1e12, 4),
+        "achieved_tflops": round(f_total / (ms * 1e-3) / 1e12, 3),
+        "kernels_ms": {k_: round(v_, 4) for k_, v_ in kt.items()},
+        "roofline": {
+            "kernel": dominant,
+            "bound": "mfma",
+            "achieved": round(achieved, 3),
+            "peak": PEAK_BF16_TFLOPS,
+            "unit": "TFLOP/s",
+            "frac": round(achieved / PEAK_BF16_TFLOPS, 5),
+            "traffic": None,
+        },
+    }
+    if not args.no_cpu_baseline:
+        result["cpu_baseline"] = cpu_baseline(inp, budget_s=args.cpu_budget_s)
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -21,6 +21,14 @@ FST_ATTN_BIAS = 1
 FST_ACT_BIAS = 2
 FST_PACKED = 4
 
+FST_PHASE_WORKLIST = 1
+FST_PHASE_FWD = 2
+FST_PHASE_BWD_ROWS = 4
+FST_PHASE_BWD_COLS = 8
+FST_PHASE_REDUCE = 16
+FST_FWD_ALL = FST_PHASE_WORKLIST | FST_PHASE_FWD
+FST_BWD_ALL = FST_PHASE_WORKLIST | FST_PHASE_BWD_ROWS | FST_PHASE_BWD_COLS | FST_PHASE_REDUCE
+
 FST_OK = 0
 FST_EINVAL = -1
 FST_EUNSUPPORTED = -2
@@ -40,6 +48,15 @@ SIGNATURES = {
     "fst_backward": (
         _i,
         [_i, _i, _i, _i, _i, _i, _i, _i, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _f,
+         _vp, _vp, _vp, _vp, _vp, _vp, _vp, _sz, _vp],
+    ),
+    "fst_forward_phases": (
+        _i,
+        [_i, _i, _i, _i, _i, _i, _i, _i, _i, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _f, _vp, _vp, _vp, _sz, _vp],
+    ),
+    "fst_backward_phases": (
+        _i,
+        [_i, _i, _i, _i, _i, _i, _i, _i, _i, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _f,
          _vp, _vp, _vp, _vp, _vp, _vp, _vp, _sz, _vp],
     ),
     "fst_frequencies": (None, [_i, ctypes.POINTER(ctypes.c_float)]),

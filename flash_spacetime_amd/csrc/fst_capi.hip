@@ -165,6 +165,10 @@ __global__ __launch_bounds__(256) void dw_reduce_kernel(const float* part, const
   }
 }
 
+__global__ __launch_bounds__(256) void fill_zero_kernel(float* p, int n) {
+  for (int i = threadIdx.x; i < n; i += 256) p[i] = 0.f;
+}
+
 struct BwdLayout {
   int rows_r, rows_c;   // rows (keys) per workgroup of the rows / cols kernels
   long grid_r, grid_c;
@@ -236,10 +240,12 @@ size_t fst_forward_workspace_bytes(int dtype, int flags, int B, int H, int L, in
   return blkcum_bytes(B < 0 ? 0 : B);
 }
 
-int fst_forward(int dtype, int flags, int B, int H, int L, int T, int D, int C, const void* q, const void* k,
-                const void* v, const float* pos4, const float* weight, const float* bias, const int32_t* lens,
-                float scale, void* out, float* lse, void* workspace, size_t workspace_bytes, void* stream) {
+int fst_forward_phases(int phases, int dtype, int flags, int B, int H, int L, int T, int D, int C, const void* q,
+                       const void* k, const void* v, const float* pos4, const float* weight, const float* bias,
+                       const int32_t* lens, float scale, void* out, float* lse, void* workspace,
+                       size_t workspace_bytes, void* stream) {
   g_last_error[0] = 0;
+  if (phases & ~FST_FWD_ALL) return fail(FST_EINVAL, "unknown forward phase bits 0x%x", phases);
   int rc = check_common(dtype, flags, B, H, L, T, D, C);
   if (rc != FST_OK) return rc;
   const bool packed = flags & FST_PACKED;
@@ -264,8 +270,11 @@ int fst_forward(int dtype, int flags, int B, int H, int L, int T, int D, int C, 
 
   int32_t* blkcum = reinterpret_cast<int32_t*>(workspace);
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
-  hipLaunchKernelGGL(blkcum_kernel, dim3(1), dim3(1024), 0, st, lens, packed ? 1 : 0, B, L, T, rows, blkcum);
-  if (hipGetLastError() != hipSuccess) return fail(FST_ELAUNCH, "work-list kernel launch failed");
+  if (phases & FST_PHASE_WORKLIST) {
+    hipLaunchKernelGGL(blkcum_kernel, dim3(1), dim3(1024), 0, st, lens, packed ? 1 : 0, B, L, T, rows, blkcum);
+    if (hipGetLastError() != hipSuccess) return fail(FST_ELAUNCH, "work-list kernel launch failed");
+  }
+  if (!(phases & FST_PHASE_FWD)) return FST_OK;
 
   prm.ev.lens = lens;
   prm.ev.blkcum = blkcum;
@@ -293,6 +302,13 @@ int fst_forward(int dtype, int flags, int B, int H, int L, int T, int D, int C, 
   return FST_OK;
 }
 
+int fst_forward(int dtype, int flags, int B, int H, int L, int T, int D, int C, const void* q, const void* k,
+                const void* v, const float* pos4, const float* weight, const float* bias, const int32_t* lens,
+                float scale, void* out, float* lse, void* workspace, size_t workspace_bytes, void* stream) {
+  return fst_forward_phases(FST_FWD_ALL, dtype, flags, B, H, L, T, D, C, q, k, v, pos4, weight, bias, lens, scale,
+                            out, lse, workspace, workspace_bytes, stream);
+}
+
 size_t fst_backward_workspace_bytes(int dtype, int flags, int B, int H, int L, int T, int D, int C) {
   if (check_common(dtype, flags, B, H, L, T, D, C) != FST_OK) return 0;
   BwdLayout lay;
@@ -300,11 +316,13 @@ size_t fst_backward_workspace_bytes(int dtype, int flags, int B, int H, int L, i
   return lay.total;
 }
 
-int fst_backward(int dtype, int flags, int B, int H, int L, int T, int D, int C, const void* q, const void* k,
-                 const void* v, const float* pos4, const float* weight, const float* bias, const int32_t* lens,
-                 const float* lse, const void* grad_out, float scale, void* dq, void* dk, void* dv, float* dweight,
-                 float* dbias, float* rowsum, void* workspace, size_t workspace_bytes, void* stream) {
+int fst_backward_phases(int phases, int dtype, int flags, int B, int H, int L, int T, int D, int C, const void* q,
+                        const void* k, const void* v, const float* pos4, const float* weight, const float* bias,
+                        const int32_t* lens, const float* lse, const void* grad_out, float scale, void* dq, void* dk,
+                        void* dv, float* dweight, float* dbias, float* rowsum, void* workspace,
+                        size_t workspace_bytes, void* stream) {
   g_last_error[0] = 0;
+  if (phases & ~FST_BWD_ALL) return fail(FST_EINVAL, "unknown backward phase bits 0x%x", phases);
   int rc = check_common(dtype, flags, B, H, L, T, D, C);
   if (rc != FST_OK) return rc;
   const bool packed = flags & FST_PACKED;
@@ -313,8 +331,11 @@ int fst_backward(int dtype, int flags, int B, int H, int L, int T, int D, int C,
   const long rows_total = packed ? (long)T : (long)B * L;
   if (!dweight) return fail(FST_EINVAL, "dweight is required");
   if (B == 0 || rows_total == 0) {
-    hipMemsetAsync(dweight, 0, sizeof(float) * D * C, st);
-    if (dbias) hipMemsetAsync(dbias, 0, sizeof(float) * D, st);
+    if (phases & FST_PHASE_REDUCE) {
+      hipLaunchKernelGGL(fill_zero_kernel, dim3(1), dim3(256), 0, st, dweight, D * C);
+      if (dbias) hipLaunchKernelGGL(fill_zero_kernel, dim3(1), dim3(256), 0, st, dbias, D);
+      if (hipGetLastError() != hipSuccess) return fail(FST_ELAUNCH, "zero fill launch failed");
+    }
     return FST_OK;
   }
   if (!q || !k || !v || !lens || !lse || !grad_out || !dq || !dk || !dv)
@@ -331,9 +352,11 @@ int fst_backward(int dtype, int flags, int B, int H, int L, int T, int D, int C,
   unsigned char* ws = reinterpret_cast<unsigned char*>(workspace);
   int32_t* bc_r = reinterpret_cast<int32_t*>(ws + lay.off_bc_r);
   int32_t* bc_c = reinterpret_cast<int32_t*>(ws + lay.off_bc_c);
-  hipLaunchKernelGGL(blkcum_kernel, dim3(1), dim3(1024), 0, st, lens, packed ? 1 : 0, B, L, T, lay.rows_r, bc_r);
-  hipLaunchKernelGGL(blkcum_kernel, dim3(1), dim3(1024), 0, st, lens, packed ? 1 : 0, B, L, T, lay.rows_c, bc_c);
-  if (hipGetLastError() != hipSuccess) return fail(FST_ELAUNCH, "work-list kernel launch failed");
+  if (phases & FST_PHASE_WORKLIST) {
+    hipLaunchKernelGGL(blkcum_kernel, dim3(1), dim3(1024), 0, st, lens, packed ? 1 : 0, B, L, T, lay.rows_r, bc_r);
+    hipLaunchKernelGGL(blkcum_kernel, dim3(1), dim3(1024), 0, st, lens, packed ? 1 : 0, B, L, T, lay.rows_c, bc_c);
+    if (hipGetLastError() != hipSuccess) return fail(FST_ELAUNCH, "work-list kernel launch failed");
+  }
 
   BwdParams prm;
   std::memset(&prm, 0, sizeof(prm));
@@ -372,15 +395,29 @@ int fst_backward(int dtype, int flags, int B, int H, int L, int T, int D, int C,
   bwd_dispatch_fn fn = bwd_table(dtype, D);
   const int HP = head_padding(H);
   int dummy_rows = 0;
-  rc = fn(prm, 0, HP, C, st, (int)lay.grid_r, false, &dummy_rows);
-  if (rc != FST_OK) return fail(rc, "backward rows kernel launch failed");
-  rc = fn(prm, 1, HP, C, st, (int)lay.grid_c, false, &dummy_rows);
-  if (rc != FST_OK) return fail(rc, "backward cols kernel launch failed");
-  const int DC = D * C;
-  hipLaunchKernelGGL(dw_reduce_kernel, dim3((DC + D + 255) / 256), dim3(256), 0, st, prm.dw_part, bc_r, B, DC, D,
-                     use_w ? 1 : 0, dweight, dbias);
-  if (hipGetLastError() != hipSuccess) return fail(FST_ELAUNCH, "dW reduction launch failed");
+  if (phases & FST_PHASE_BWD_ROWS) {
+    rc = fn(prm, 0, HP, C, st, (int)lay.grid_r, false, &dummy_rows);
+    if (rc != FST_OK) return fail(rc, "backward rows kernel launch failed");
+  }
+  if (phases & FST_PHASE_BWD_COLS) {
+    rc = fn(prm, 1, HP, C, st, (int)lay.grid_c, false, &dummy_rows);
+    if (rc != FST_OK) return fail(rc, "backward cols kernel launch failed");
+  }
+  if (phases & FST_PHASE_REDUCE) {
+    const int DC = D * C;
+    hipLaunchKernelGGL(dw_reduce_kernel, dim3((DC + D + 255) / 256), dim3(256), 0, st, prm.dw_part, bc_r, B, DC, D,
+                       use_w ? 1 : 0, dweight, dbias);
+    if (hipGetLastError() != hipSuccess) return fail(FST_ELAUNCH, "dW reduction launch failed");
+  }
   return FST_OK;
+}
+
+int fst_backward(int dtype, int flags, int B, int H, int L, int T, int D, int C, const void* q, const void* k,
+                 const void* v, const float* pos4, const float* weight, const float* bias, const int32_t* lens,
+                 const float* lse, const void* grad_out, float scale, void* dq, void* dk, void* dv, float* dweight,
+                 float* dbias, float* rowsum, void* workspace, size_t workspace_bytes, void* stream) {
+  return fst_backward_phases(FST_BWD_ALL, dtype, flags, B, H, L, T, D, C, q, k, v, pos4, weight, bias, lens, lse,
+                             grad_out, scale, dq, dk, dv, dweight, dbias, rowsum, workspace, workspace_bytes, stream);
 }
 
 }  // extern "C"

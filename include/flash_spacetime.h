@@ -43,6 +43,20 @@ enum fst_flags {
   FST_PACKED = 4     /* packed [T, H, D] layout with cu_seqlens              */
 };
 
+/* Phases of one operator call, for callers that time or schedule them
+ * separately (the one-shot entry points run all of them, in this order).
+ * The work list (per-event row-block prefix sums) is written into the
+ * workspace by the first phase and read by the later ones. */
+enum fst_phase {
+  FST_PHASE_WORKLIST = 1, /* per-event row blocks -> workspace (tiny kernel)   */
+  FST_PHASE_FWD = 2,      /* forward kernel                                   */
+  FST_PHASE_BWD_ROWS = 4, /* backward rows kernel: D, dq, H, G, dW/db partials */
+  FST_PHASE_BWD_COLS = 8, /* backward cols kernel: dk, dv                     */
+  FST_PHASE_REDUCE = 16,  /* ordered sum of the dW / db partials              */
+  FST_FWD_ALL = FST_PHASE_WORKLIST | FST_PHASE_FWD,
+  FST_BWD_ALL = FST_PHASE_WORKLIST | FST_PHASE_BWD_ROWS | FST_PHASE_BWD_COLS | FST_PHASE_REDUCE
+};
+
 enum fst_status {
   FST_OK = 0,
   FST_EINVAL = -1,       /* bad argument (shape, pointer, flag)             */
@@ -71,6 +85,15 @@ int fst_forward(int dtype, int flags, int B, int H, int L, int T, int D, int C,
                 float scale, void* out, float* lse, void* workspace,
                 size_t workspace_bytes, void* stream);
 
+/* fst_forward restricted to the given phases (FST_PHASE_WORKLIST,
+ * FST_PHASE_FWD). Survey's split launcher fst_fwd; no reference counterpart
+ * beyond forward.py:306-331 (the launch itself). */
+int fst_forward_phases(int phases, int dtype, int flags, int B, int H, int L, int T, int D,
+                       int C, const void* q, const void* k, const void* v,
+                       const float* pos4, const float* weight, const float* bias,
+                       const int32_t* lens, float scale, void* out, float* lse,
+                       void* workspace, size_t workspace_bytes, void* stream);
+
 /* Scratch bytes fst_backward needs. */
 size_t fst_backward_workspace_bytes(int dtype, int flags, int B, int H, int L, int T,
                                     int D, int C);
@@ -88,6 +111,19 @@ int fst_backward(int dtype, int flags, int B, int H, int L, int T, int D, int C,
                  const float* lse, const void* grad_out, float scale, void* dq,
                  void* dk, void* dv, float* dweight, float* dbias, float* rowsum,
                  void* workspace, size_t workspace_bytes, void* stream);
+
+/* fst_backward restricted to the given phases (FST_PHASE_WORKLIST,
+ * FST_PHASE_BWD_ROWS, FST_PHASE_BWD_COLS, FST_PHASE_REDUCE): the rows and cols
+ * kernels are the counterparts of the reference's two Triton launches
+ * (backward.py:589-598), the reduce phase of its dW/db epilogue
+ * (backward.py:607-622). */
+int fst_backward_phases(int phases, int dtype, int flags, int B, int H, int L, int T, int D,
+                        int C, const void* q, const void* k, const void* v,
+                        const float* pos4, const float* weight, const float* bias,
+                        const int32_t* lens, const float* lse, const void* grad_out,
+                        float scale, void* dq, void* dk, void* dv, float* dweight,
+                        float* dbias, float* rowsum, void* workspace,
+                        size_t workspace_bytes, void* stream);
 
 /* The fp32 frequency ladder exp(-i ln(1e4) / (C/2)), i < C/2, that the kernels
  * embed with, written to out[0 .. C/2). Counterpart of sinusoidal_frequencies
