@@ -150,19 +150,35 @@ static bwd_dispatch_fn bwd_table(int dtype, int D) {
   return nullptr;
 }
 
-// Sums the per-block dW / db partials of the rows kernel in block order.
-__global__ __launch_bounds__(256) void dw_reduce_kernel(const float* part, const int32_t* blkcum, int B, int DC, int D,
-                                                         int use_e, float* dw, float* db) {
+// dW / db from the per-block partials of the rows kernel, in two fixed-order
+// stages so the result does not depend on scheduling: stage 1 sums runs of
+// kRedSeg consecutive blocks per column (coalesced over the columns), stage
+// 2 sums the run totals in order.
+constexpr int kRedSeg = 64;
+
+__global__ __launch_bounds__(256) void dw_reduce_seg_kernel(const float* part, const int32_t* blkcum, int B,
+                                                            int ncol, float* seg) {
   const int nblk = blkcum[B];
-  for (int e = blockIdx.x * blockDim.x + threadIdx.x; e < DC + D; e += gridDim.x * blockDim.x) {
-    float acc = 0.f;
-    if (use_e)
-      for (int w = 0; w < nblk; ++w) acc += part[(long)w * (DC + D) + e];
-    if (e < DC)
-      dw[e] = acc;
-    else if (db)
-      db[e - DC] = acc;
-  }
+  const int col = blockIdx.x * 256 + threadIdx.x;
+  if (col >= ncol) return;
+  const long w0 = (long)blockIdx.y * kRedSeg;
+  const long w1 = w0 + kRedSeg < nblk ? w0 + kRedSeg : nblk;
+  float acc = 0.f;
+  for (long w = w0; w < w1; ++w) acc += part[w * ncol + col];
+  seg[(long)blockIdx.y * ncol + col] = acc;
+}
+
+__global__ __launch_bounds__(256) void dw_reduce_final_kernel(const float* seg, int nseg, int DC, int D, int use_e,
+                                                              float* dw, float* db) {
+  const int e = blockIdx.x * 256 + threadIdx.x;
+  if (e >= DC + D) return;
+  float acc = 0.f;
+  if (use_e)
+    for (int s = 0; s < nseg; ++s) acc += seg[(long)s * (DC + D) + e];
+  if (e < DC)
+    dw[e] = acc;
+  else if (db)
+    db[e - DC] = acc;
 }
 
 __global__ __launch_bounds__(256) void fill_zero_kernel(float* p, int n) {
@@ -172,7 +188,8 @@ __global__ __launch_bounds__(256) void fill_zero_kernel(float* p, int n) {
 struct BwdLayout {
   int rows_r, rows_c;   // rows (keys) per workgroup of the rows / cols kernels
   long grid_r, grid_c;
-  size_t off_bc_r, off_bc_c, off_u, off_wt, off_dob, off_dsum, off_part, total;
+  size_t off_bc_r, off_bc_c, off_u, off_wt, off_dob, off_dsum, off_part, off_seg, total;
+  long nseg;  // stage-1 runs of the dW reduction
 };
 
 static int bwd_layout(int dtype, int flags, int B, int H, int L, int T, int D, int C, BwdLayout& lay) {
@@ -202,6 +219,9 @@ static int bwd_layout(int dtype, int flags, int B, int H, int L, int T, int D, i
   off += align_up((size_t)rows * H * 4, 256);
   lay.off_part = off;
   off += align_up((size_t)(lay.grid_r > 0 ? lay.grid_r : 0) * (D * C + D) * 4, 256);
+  lay.nseg = lay.grid_r > 0 ? (lay.grid_r + kRedSeg - 1) / kRedSeg : 0;
+  lay.off_seg = off;
+  off += align_up((size_t)lay.nseg * (D * C + D) * 4, 256);
   lay.total = off;
   return FST_OK;
 }
@@ -405,8 +425,14 @@ int fst_backward_phases(int phases, int dtype, int flags, int B, int H, int L, i
   }
   if (phases & FST_PHASE_REDUCE) {
     const int DC = D * C;
-    hipLaunchKernelGGL(dw_reduce_kernel, dim3((DC + D + 255) / 256), dim3(256), 0, st, prm.dw_part, bc_r, B, DC, D,
-                       use_w ? 1 : 0, dweight, dbias);
+    const int ncol = DC + D;
+    float* seg = reinterpret_cast<float*>(ws + lay.off_seg);
+    if (lay.nseg > 65535) return fail(FST_EUNSUPPORTED, "problem too large for the dW reduction");
+    if (use_w && lay.nseg > 0)
+      hipLaunchKernelGGL(dw_reduce_seg_kernel, dim3((ncol + 255) / 256, (unsigned)lay.nseg), dim3(256), 0, st,
+                         prm.dw_part, bc_r, B, ncol, seg);
+    hipLaunchKernelGGL(dw_reduce_final_kernel, dim3((ncol + 255) / 256), dim3(256), 0, st, seg, (int)lay.nseg, DC,
+                       D, use_w ? 1 : 0, dweight, dbias);
     if (hipGetLastError() != hipSuccess) return fail(FST_ELAUNCH, "dW reduction launch failed");
   }
   return FST_OK;
