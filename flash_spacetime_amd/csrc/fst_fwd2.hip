@@ -1,0 +1,439 @@
+// Forward kernel of flash-spacetime attention for gfx950, bf16 operands.
+//
+// Spec: reference.py:106-167; fused algebra: forward.py:5-22. For every
+// query row i, head h and key j of one event:
+//   s_ij = qt_i . k_j + [A] u_i . E_ij         (u = bf16(qt @ W), qt = q*scale)
+//   p_ij = softmax_j(s_ij)
+//   out_i = sum_j p_ij v_j + [V] (W (sum_j p_ij E_ij) + b)
+//
+// One workgroup = one 16-row tile of one event, four waves. Wave w is
+//  * head-owner of heads [w HW, (w+1) HW): S^T_h = K_h Qt_h^T + (u.E)^T and
+//    O^T_h += V_h^T P^T_h on 16x16 MFMA tiles with the 16 rows on the lanes,
+//    the online softmax, and the row sums l = 1^T P^T (an all-ones MFMA
+//    operand, so l is the sum of the very bf16 P that weights V);
+//  * row-owner of rows 4w .. 4w+3: u of its rows (fp32 MFMA projection), the
+//    embedding E of its rows x the chunk's keys, computed directly in the
+//    operand layout of the u.E product (UE^T_i = E_i U_i^T, heads on the
+//    lanes) and kept in LDS for A^T_i += E_i^T P_i^T (A = sum_j p_ij E_ij).
+// The roles meet in LDS: u.E goes row-owner -> head-owner (fp32), P and the
+// rescale factors head-owner -> row-owner; E is private to the wave that
+// computed it. Two barriers per key chunk.
+//
+// K and V come from global memory in row-major operand layout; V^T is made
+// on the matrix core (identity product). Keys past the event are clamped to
+// the last valid key for loads and masked to -inf in the last chunk only.
+// The softmax reference m is raised only when a row's chunk maximum exceeds
+// it by more than 2^8 (log2 domain), so O, l and A are rescaled rarely.
+#include "fst_tile.h"
+
+namespace fst {
+
+template <int HP, int D, int C, int KC>
+struct Fwd2Cfg {
+  static constexpr int HW = HP / 4;  // heads per wave
+  static constexpr int NS = KC / 16;  // 16-key subtiles per chunk
+  static constexpr int NCT = C / 16;  // channel steps
+  static constexpr int E_BYTES = ETile<C, KC>::BYTES;
+  static constexpr int STAGE_BYTES = (KC / 4) * 16 * 16 * 16;  // fp32 u.E of KC keys per (row, head)
+  static constexpr int SCAL_BYTES = 16 * 17 * 4;
+  static constexpr int LDS_BYTES = E_BYTES + STAGE_BYTES + SCAL_BYTES;
+  static constexpr bool FITS = LDS_BYTES <= 80 * 1024 && HP % 4 == 0 && (KC == 16 || KC == 32);
+};
+
+constexpr float kRescaleLog2 = 8.f;
+
+template <int HP, int D, int C, int KC>
+__global__ __launch_bounds__(256, 2) void fwd2_kernel(FwdParams prm) {
+  using Cfg = Fwd2Cfg<HP, D, C, KC>;
+  using ET = ETile<C, KC>;
+  using DT = DTiles<D>;
+  constexpr int HW = Cfg::HW, NS = Cfg::NS, NCT = Cfg::NCT, NQ = DT::NQ;
+  extern __shared__ __align__(16) unsigned char smem[];
+  bf16* Es = reinterpret_cast<bf16*>(smem);
+  unsigned char* stage = smem + Cfg::E_BYTES;
+  unsigned char* scal = stage + Cfg::STAGE_BYTES;
+
+  const int tid = threadIdx.x;
+  const int w = tid >> 6, lane = tid & 63, g = lane >> 4, n = lane & 15;
+
+  EventBlock eb;
+  if (!tile_block(prm.ev, xcd_remap(blockIdx.x, gridDim.x), eb)) return;
+  const int len = eb.len;
+  const int H = prm.H;
+  const bool attn = prm.flags & FST_ATTN_BIAS;
+  const bool act = prm.flags & FST_ACT_BIAS;
+  const bool use_e = attn || act;
+  const RowAddr ra = row_addr(prm.ev, eb);
+  const int i0 = eb.blk * 16;
+  const int last = len - 1;
+  bf16* outg = reinterpret_cast<bf16*>(prm.out);
+  if (i0 >= len) {  // a tile of padding rows only
+    zero_tile_rows<bf16, D>(prm.ev, ra, i0, len, H, tid, outg, prm.lse);
+    return;
+  }
+
+  const bf16* __restrict__ qg = reinterpret_cast<const bf16*>(prm.q);
+  const bf16* __restrict__ kg = reinterpret_cast<const bf16*>(prm.k);
+  const bf16* __restrict__ vg = reinterpret_cast<const bf16*>(prm.v);
+  const bf16x4 id = ident_x16(g, n);
+
+  // ---- head-owner state (lane n = row i0 + n) ----
+  const int my_row = i0 + n;
+  const bool row_ok = my_row < len;
+  KFrag<bf16, D> qf[HW];
+  f32x4 O[HW][NQ], lacc[HW];
+  float mref[HW];
+#pragma unroll
+  for (int hl = 0; hl < HW; ++hl) {
+    const int h = w * HW + hl;
+    if (h < H && row_ok)
+      qf[hl].load_scaled(qg + ra.off(h, my_row, D), g, prm.scale);
+    else
+      qf[hl].zero();
+#pragma unroll
+    for (int q = 0; q < NQ; ++q) O[hl][q] = zero4();
+    lacc[hl] = zero4();
+    mref[hl] = -INFINITY;
+  }
+  JFrag<bf16, NS> ones;
+#pragma unroll
+  for (int e = 0; e < 4 * NS; ++e) ones.v[e] = (bf16)1.f;
+
+  // ---- row-owner state: rows i0 + 4w + r, heads on lane n ----
+  bf16x4 uf[4][NCT];
+  f32x4 AE[4][NCT];
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const int row = i0 + 4 * w + r;
+    if (attn) {
+      const bool ok = row < len && n < H;
+      f32x4 acc[NCT];
+#pragma unroll
+      for (int ct = 0; ct < NCT; ++ct) {
+        // u^T[slot][h] = sum_d W[d][channel(slot)] qt[h][d] on fp32 MFMA.
+        constexpr int Qd = D / 4;
+        f32x4 a = zero4();
+        const bf16* xr = qg + ra.off(0, ok ? row : 0, D) + n * ra.hs * D + Qd * g;
+#pragma unroll
+        for (int s = 0; s < Qd; ++s) {
+          const float xv = ok ? (float)xr[s] * prm.scale : 0.f;
+          a = mfma_f32(prm.weight[(Qd * g + s) * C + slot_channel<C>(16 * ct + n)], xv, a);
+        }
+        acc[ct] = a;
+      }
+#pragma unroll
+      for (int ct = 0; ct < NCT; ++ct) uf[r][ct] = pack4(acc[ct]);
+    } else {
+#pragma unroll
+      for (int ct = 0; ct < NCT; ++ct) uf[r][ct] = bf16x4{};
+    }
+#pragma unroll
+    for (int ct = 0; ct < NCT; ++ct) AE[r][ct] = zero4();
+  }
+  // Angle lane assignment: lane (g, n) evaluates row i0 + 4w + g against key
+  // j0 + 16 s + n; the four rows are then gathered into every lane group.
+  float4 pos_i = float4{0.f, 0.f, 0.f, 0.f};
+  float fa[NCT], fb[NCT];
+  if (use_e) {
+    const int row = i0 + 4 * w + g;
+    pos_i = ra.pos(prm.ev.pos4, row < len ? row : last);
+#pragma unroll
+    for (int ct = 0; ct < NCT; ++ct) {
+      fa[ct] = 1024.f * prm.freq.ghi[8 * ct + 2 * g];
+      fb[ct] = 1024.f * prm.freq.ghi[8 * ct + 2 * g + 1];
+    }
+  }
+
+  // Buffer views of this event's K, V and positions. Row r of head h sits at
+  // element (r ts + h hs) D from the event's base; a chunk advances the
+  // scalar offset by KC ts D elements.
+  const long ebase = ra.off(0, 0, D);
+  const int rowb = (int)(ra.ts * D * 2);  // bytes per key row
+  const unsigned ebytes = (unsigned)((prm.ev.packed ? (long)len * ra.ts : (long)H * ra.hs) * D * 2);
+  const Buf kbuf(kg + ebase, ebytes), vbuf(vg + ebase, ebytes);
+  const Buf pbuf(prm.ev.pos4 + ra.pos_base, (unsigned)len * 16u);
+  int kvo[HW];  // lane offset of head hl, key n (bytes)
+#pragma unroll
+  for (int hl = 0; hl < HW; ++hl)
+    kvo[hl] = (int)((w * HW + hl) * ra.hs * D * 2) + n * rowb + kfrag_goff<D>(g);
+
+  // Operands of the chunk in flight: K, V rows of the wave's heads and the
+  // key positions. Loads for chunk j0 + KC are issued as soon as the
+  // head-owner has consumed those of chunk j0; keys are clamped to the event.
+  KFrag<bf16, D> kf[HW][NS], vf[HW][NS];
+  float4 pj[NS];
+  auto issue = [&](int jn) {
+    const bool full = jn + KC <= len;
+#pragma unroll
+    for (int hl = 0; hl < HW; ++hl) {
+      if (w * HW + hl >= H) continue;
+#pragma unroll
+      for (int s = 0; s < NS; ++s) {
+        if (full) {
+          load_kfrag<D>(kf[hl][s], kbuf, kvo[hl] + 16 * s * rowb, jn * rowb);
+          load_kfrag<D>(vf[hl][s], vbuf, kvo[hl] + 16 * s * rowb, jn * rowb);
+        } else {
+          const int key = min(jn + 16 * s + n, last);
+          load_kfrag<D>(kf[hl][s], kbuf, kvo[hl] + (key - n) * rowb, 0);
+          load_kfrag<D>(vf[hl][s], vbuf, kvo[hl] + (key - n) * rowb, 0);
+        }
+      }
+    }
+    if (use_e) {
+#pragma unroll
+      for (int s = 0; s < NS; ++s) pj[s] = pbuf.ldf4(min(jn + 16 * s + n, last) * 16, 0);
+    }
+  };
+  issue(0);
+
+  auto chunk = [&](int j0, auto tail_tag) {
+    constexpr bool TAIL = decltype(tail_tag)::value;
+
+    // ---- row-owner: E of rows 4w..4w+3 x KC keys; u.E staged ----
+    if (use_e) {
+      float xg[NS][4];
+#pragma unroll
+      for (int s = 0; s < NS; ++s) group_gather(pair_angle_unit(pos_i, pj[s]), xg[s]);
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+#pragma unroll
+        for (int s = 0; s < NS; ++s) {
+          bf16x4 ef[NCT];
+#pragma unroll
+          for (int ct = 0; ct < NCT; ++ct) {
+            ef[ct] = embed_step<C>(xg[s][r], fa[ct], fb[ct], ct);
+            if (act) ET::store(Es, 4 * w + r, ct, 16 * s + n, g, ef[ct]);
+          }
+          if (attn) {
+            f32x4 ue = zero4();
+#pragma unroll
+            for (int ct = 0; ct < NCT; ++ct) ue = mfma_x16(ef[ct], uf[r][ct], ue);
+            *reinterpret_cast<f32x4*>(stage + stage_off(4 * s + g, 4 * w + r, n)) = ue;
+          }
+        }
+    }
+    __syncthreads();  // u.E staged
+
+    // ---- head-owner: logits, online softmax, P V (phase by phase over the
+    // wave's heads, so the heads' dependency chains overlap) ----
+    f32x4 S[HW][NS];
+#pragma unroll
+    for (int hl = 0; hl < HW; ++hl) {
+      if (w * HW + hl >= H) {
+#pragma unroll
+        for (int s = 0; s < NS; ++s) S[hl][s] = zero4();
+        continue;
+      }
+#pragma unroll
+      for (int s = 0; s < NS; ++s) {
+        const f32x4 init =
+            attn ? *reinterpret_cast<const f32x4*>(stage + stage_off(4 * s + g, n, w * HW + hl)) : zero4();
+        S[hl][s] = mma_k<D>(kf[hl][s], qf[hl], init);
+        if constexpr (TAIL) {
+#pragma unroll
+          for (int r = 0; r < 4; ++r)
+            if (j0 + 16 * s + 4 * g + r >= len) S[hl][s][r] = -INFINITY;
+        }
+      }
+    }
+    float mx[HW], alpha[HW];
+    bool need_any = false;
+#pragma unroll
+    for (int hl = 0; hl < HW; ++hl) {
+      float m = S[hl][0][0];
+#pragma unroll
+      for (int s = 0; s < NS; ++s)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) m = fmaxf(m, S[hl][s][r]);
+      mx[hl] = m;
+    }
+#pragma unroll
+    for (int hl = 0; hl < HW; ++hl) {
+      mx[hl] = group_allmax(mx[hl]) * kLog2e;
+      alpha[hl] = 1.f;
+      need_any |= (w * HW + hl < H) && mx[hl] > mref[hl] + kRescaleLog2;
+    }
+    if (__builtin_amdgcn_ballot_w64(need_any)) {
+#pragma unroll
+      for (int hl = 0; hl < HW; ++hl) {
+        const float mnew = mx[hl] > mref[hl] + kRescaleLog2 ? mx[hl] : mref[hl];
+        alpha[hl] = exp2f_fast(mref[hl] - mnew);
+        mref[hl] = mnew;
+#pragma unroll
+        for (int q = 0; q < NQ; ++q) O[hl][q] = O[hl][q] * alpha[hl];
+        lacc[hl] = lacc[hl] * alpha[hl];
+      }
+    }
+    JFrag<bf16, NS> pf[HW];
+#pragma unroll
+    for (int hl = 0; hl < HW; ++hl) {
+      const float mb = mref[hl];
+#pragma unroll
+      for (int s = 0; s < NS; ++s)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) S[hl][s][r] = exp2f_fast(__builtin_fmaf(S[hl][s][r], kLog2e, -mb));
+      pf[hl].from_tiles(S[hl]);
+    }
+#pragma unroll
+    for (int hl = 0; hl < HW; ++hl) {
+      if (w * HW + hl >= H) continue;
+      lacc[hl] = mma_j(ones, pf[hl], lacc[hl]);
+#pragma unroll
+      for (int q = 0; q < NQ; ++q) {
+        JFrag<bf16, NS> vt;
+        if constexpr (NS == 2)
+          vt.v = cat8(transpose_x16(DT::part(vf[hl][0], q), id), transpose_x16(DT::part(vf[hl][1], q), id));
+        else
+          vt.v = transpose_x16(DT::part(vf[hl][0], q), id);
+        O[hl][q] = mma_j(vt, pf[hl], O[hl][q]);
+      }
+    }
+    if (act) {
+      // P for the row-owner: keys 16s + 4g .. +3 of slot (row n, head h).
+#pragma unroll
+      for (int hl = 0; hl < HW; ++hl) {
+        const int h = w * HW + hl;
+        if (h >= H) continue;
+#pragma unroll
+        for (int s = 0; s < NS; ++s) {
+          bf16x4 pv;
+#pragma unroll
+          for (int r = 0; r < 4; ++r) pv[r] = pf[hl].v[4 * s + r];
+          *reinterpret_cast<bf16x4*>(stage + stage_off(2 * s + (g >> 1), n, h) + 8 * (g & 1)) = pv;
+        }
+        if (g == 0) *reinterpret_cast<float*>(scal + scal_off(n, h)) = alpha[hl];
+      }
+    }
+    if (j0 + KC < len) issue(j0 + KC);
+    __syncthreads();  // P and rescale factors staged
+
+    // ---- row-owner: A = alpha A + E^T P ----
+    if (act) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int il = 4 * w + r;
+        const float alpha = n < H ? *reinterpret_cast<const float*>(scal + scal_off(il, n)) : 1.f;
+        JFrag<bf16, NS> pr;
+        if (n < H) {
+#pragma unroll
+          for (int s = 0; s < NS; ++s) {
+            const bf16x4 pv =
+                *reinterpret_cast<const bf16x4*>(stage + stage_off(2 * s + (g >> 1), il, n) + 8 * (g & 1));
+#pragma unroll
+            for (int e = 0; e < 4; ++e) pr.v[4 * s + e] = pv[e];
+          }
+        } else {
+          pr.zero();
+        }
+        if (__builtin_amdgcn_ballot_w64(alpha != 1.f)) {
+#pragma unroll
+          for (int ct = 0; ct < NCT; ++ct) AE[r][ct] = AE[r][ct] * alpha;
+        }
+#pragma unroll
+        for (int ct = 0; ct < NCT; ++ct) {
+          JFrag<bf16, NS> et;
+          if constexpr (NS == 2)
+            et.v = cat8(ET::load_tr(Es, il, ct, 0, g, n), ET::load_tr(Es, il, ct, 16, g, n));
+          else
+            et.v = ET::load_tr(Es, il, ct, 0, g, n);
+          AE[r][ct] = mma_j(et, pr, AE[r][ct]);
+        }
+      }
+    }
+  };
+
+  int j0 = 0;
+  for (; j0 + KC <= len; j0 += KC) chunk(j0, std::false_type{});
+  if (j0 < len) chunk(j0, std::true_type{});
+
+  // ---- epilogue ----
+  float inv_l[HW];
+#pragma unroll
+  for (int hl = 0; hl < HW; ++hl) {
+    const float l = lacc[hl][0];
+    inv_l[hl] = 1.f / l;
+    const int h = w * HW + hl;
+    if (g == 0 && row_ok && h < H) prm.lse[ra.vec(h, my_row)] = mref[hl] * kLn2 + __logf(l);
+  }
+
+  // One head-dim tile per round: the row-owner forms o2^T_i[d, h] =
+  // sum_slot W[d, channel(slot)] A^T_i[slot, h] on fp32 MFMA (lane n of the
+  // A operand is the tile's feature dmap(q, n/4, n%4)) and stages it; the
+  // head-owner forms out = (O + o2) / l + b in place.
+#pragma unroll
+  for (int q = 0; q < NQ; ++q) {
+    if (act) {
+      __syncthreads();  // previous round (or the last chunk) done with the stage
+      const int dn = DT::dmap(q, n >> 2, n & 3);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        f32x4 acc = zero4();
+#pragma unroll
+        for (int ct = 0; ct < NCT; ++ct)
+#pragma unroll
+          for (int sp = 0; sp < 4; ++sp)
+            acc = mfma_f32(prm.weight[dn * C + slot_channel<C>(16 * ct + 4 * g + sp)], AE[r][ct][sp], acc);
+        *reinterpret_cast<f32x4*>(stage + stage_off(g, 4 * w + r, n)) = acc;
+      }
+      __syncthreads();
+    }
+#pragma unroll
+    for (int hl = 0; hl < HW; ++hl) {
+      f32x4 o = O[hl][q];
+      if (act) o = o + *reinterpret_cast<const f32x4*>(stage + stage_off(g, n, w * HW + hl));
+      o = o * inv_l[hl];
+      if (act && prm.bias) {
+#pragma unroll
+        for (int r = 0; r < 4; ++r) o[r] += prm.bias[DT::dmap(q, g, r)];
+      }
+      O[hl][q] = o;
+    }
+  }
+  if (row_ok) {
+#pragma unroll
+    for (int hl = 0; hl < HW; ++hl) {
+      const int h = w * HW + hl;
+      if (h >= H) continue;
+      bf16* orow = outg + ra.off(h, my_row, D);
+      if constexpr (DT::X32) {
+#pragma unroll
+        for (int t = 0; t < NQ / 2; ++t)
+          *reinterpret_cast<bf16x8*>(orow + DT::dmap(2 * t, g, 0)) = cat8(pack4(O[hl][2 * t]), pack4(O[hl][2 * t + 1]));
+      } else {
+#pragma unroll
+        for (int q = 0; q < NQ; ++q) *reinterpret_cast<bf16x4*>(orow + DT::dmap(q, g, 0)) = pack4(O[hl][q]);
+      }
+    }
+  }
+
+  zero_tile_rows<bf16, D>(prm.ev, ra, i0, len, H, tid, outg, prm.lse);
+}
+
+template <int HP, int D, int C>
+struct Fwd2Pick {
+  // 32-key chunks where the register plan of 16 heads x 32 keys fits (no
+  // spills at HP <= 12, C = 16); 16-key chunks otherwise.
+  static constexpr int KC = (Fwd2Cfg<HP, D, C, 32>::FITS && HP <= 12 && C <= 16 && D <= 32) ? 32 : 16;
+  using Cfg = Fwd2Cfg<HP, D, C, KC>;
+  static constexpr bool OK = Cfg::FITS;
+};
+
+template <int HP, int D, int C>
+int fwd2_launch_t(const FwdParams& prm, hipStream_t stream, int grid) {
+  using P = Fwd2Pick<HP, D, C>;
+  if constexpr (!P::OK) {
+    return FST_EUNSUPPORTED;
+  } else {
+    auto kern = fwd2_kernel<HP, D, C, P::KC>;
+    if (hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, P::Cfg::LDS_BYTES) !=
+        hipSuccess)
+      return FST_ELAUNCH;
+    // The grid is rounded up to a multiple of 8 for the XCD remapping;
+    // logical blocks past the work list exit at once.
+    const int g8 = (grid + 7) & ~7;
+    if (grid > 0) hipLaunchKernelGGL(kern, dim3(g8), dim3(256), P::Cfg::LDS_BYTES, stream, prm);
+    return hipGetLastError() == hipSuccess ? FST_OK : FST_ELAUNCH;
+  }
+}
+
+}  // namespace fst

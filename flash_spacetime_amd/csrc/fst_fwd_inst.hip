@@ -3,6 +3,7 @@
 // Built once per (dtype, D) with -DFST_T=<bf16|float> -DFST_D=<D>
 // -DFST_NAME=<dtype>_<D> so the instances compile in parallel.
 #include "fst_forward.hip"
+#include "fst_fwd2.hip"
 
 #if !defined(FST_T) || !defined(FST_D) || !defined(FST_NAME)
 #error "FST_T, FST_D and FST_NAME must be defined"
@@ -15,13 +16,23 @@ namespace fst {
 
 int FST_CAT(fwd_dispatch_, FST_NAME)(const FwdParams& prm, int HP, int C, hipStream_t stream, int grid, bool query,
                                      int* rows) {
-#define FST_CASE(HPV, CV)                                         \
-  if (HP == HPV && C == CV) {                                     \
-    if (query) {                                                  \
-      *rows = fwd_rows_t<FST_T, HPV, FST_D, CV>();                \
-      return *rows ? FST_OK : FST_EUNSUPPORTED;                   \
-    }                                                             \
-    return fwd_launch_t<FST_T, HPV, FST_D, CV>(prm, stream, grid); \
+  // bf16 runs the 16-row-tile kernel (fst_fwd2.hip) wherever its LDS plan
+  // fits; fp32 and the remaining shapes run fst_forward.hip.
+#define FST_CASE(HPV, CV)                                                       \
+  if (HP == HPV && C == CV) {                                                   \
+    if constexpr (is_bf16<FST_T>::value && Fwd2Pick<HPV, FST_D, CV>::OK) {      \
+      if (query) {                                                              \
+        *rows = 16;                                                             \
+        return FST_OK;                                                          \
+      }                                                                         \
+      return fwd2_launch_t<HPV, FST_D, CV>(prm, stream, grid);                  \
+    } else {                                                                    \
+      if (query) {                                                              \
+        *rows = fwd_rows_t<FST_T, HPV, FST_D, CV>();                            \
+        return *rows ? FST_OK : FST_EUNSUPPORTED;                               \
+      }                                                                         \
+      return fwd_launch_t<FST_T, HPV, FST_D, CV>(prm, stream, grid);            \
+    }                                                                           \
   }
 #define FST_CASES(HPV) FST_CASE(HPV, 16) FST_CASE(HPV, 32) FST_CASE(HPV, 48) FST_CASE(HPV, 64)
   FST_CASES(4)

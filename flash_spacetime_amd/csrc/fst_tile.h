@@ -1,0 +1,266 @@
+// Building blocks of the second-generation gfx950 kernels (one 16-row tile
+// per workgroup, four waves, operands straight from global memory).
+//
+// Layout conventions are those of fst_device.h (lane = 16 g + n, MFMA A / B /
+// C layouts). On top of them:
+//  * Channel slots. The C embedding channels of a pair are contracted in
+//    16-slot steps ct (16x16x16 bf16). Slot k = 16 ct + 4 g + e of lane group
+//    g holds, for e = 0, 1, sin(x f) and for e = 2, 3, cos(x f) of frequency
+//    f = 8 ct + 2 g + (e & 1), so every lane evaluates two sin/cos pairs per
+//    step from one angle. `slot_channel` maps a slot to the spec's channel
+//    index (sin channels first, then cos: reference.py:82-84); the weight is
+//    read through it wherever a slot meets W, so the permutation never shows
+//    outside the kernels.
+//  * Transposes on the matrix core. An operand tile held as A (lane n = row,
+//    slots = four columns of group g) multiplied by the identity gives the
+//    tile in C layout with the roles swapped (lane n = column, registers =
+//    rows 4g .. 4g+3), which is again an A / B operand of a 16x16x16 step
+//    after packing to bf16. The values are bf16 inputs times 1 plus zeros,
+//    so the transpose is exact.
+//  * LDS layouts are swizzled so that every access pattern below touches 64
+//    distinct banks per pass (gfx950: 64 banks of 4 bytes).
+#pragma once
+
+#include <type_traits>
+
+#include "fst_kernels.h"
+
+namespace fst {
+
+typedef unsigned u32x2 __attribute__((ext_vector_type(2)));
+typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
+
+// Hardware workgroup w of a grid of G (a multiple of 8) runs logical block
+// (w % 8) * (G / 8) + w / 8: workgroups are dealt to the eight XCDs round
+// robin, so each XCD gets a contiguous range of logical blocks and an event's
+// row blocks share one L2.
+__device__ __forceinline__ int xcd_remap(int w, int G) { return (w & 7) * (G >> 3) + (w >> 3); }
+
+// Natural channel index of channel slot k (see the header comment).
+template <int C>
+__host__ __device__ constexpr int slot_channel(int k) {
+  const int ct = k >> 4, g = (k >> 2) & 3, e = k & 3;
+  const int f = 8 * ct + 2 * g + (e & 1);
+  return e < 2 ? f : C / 2 + f;
+}
+
+// Frequencies whose largest angle 4096 f / (2 pi) leaves the +-256 revolution
+// domain of v_sin_f32 / v_cos_f32: f_k > 0.3927, i.e. the first C / 16 of the
+// ladder exp(-k ln(1e4) / (C/2)). They sit in channel step 0.
+template <int C>
+struct EmbedSteps {
+  static constexpr int NCT = C / 16;
+  static constexpr int NRED = C / 16;
+  // In step 0, lane group 0 holds frequencies 0 and 1, group 1 holds 2 and 3.
+  static constexpr bool RA = NRED >= 1;  // frequency 2g needs reduction for some g
+  static constexpr bool RB = NRED >= 2;  // frequency 2g + 1 needs reduction for some g
+};
+
+
+// clip(sign(I) sqrt|I|, -4, 4) for I = |p_i - p_j|^2 - (18 (t_i - t_j))^2:
+// the spec's pair angle (reference.py:75-81) without its factor 1024, which
+// the frequencies carry (a power of two, so no rounding moves).
+__device__ __forceinline__ float pair_angle_unit(float4 a, float4 b) {
+  const float dx = a.x - b.x, dy = a.y - b.y, dz = a.z - b.z;
+  const float dt = (a.w - b.w) * kTimeScale;
+  const float interval = __builtin_fmaf(dx, dx, __builtin_fmaf(dy, dy, __builtin_fmaf(dz, dz, -dt * dt)));
+  const float mag = __builtin_amdgcn_sqrtf(fabsf(interval));
+  return __builtin_amdgcn_fmed3f(__builtin_copysignf(mag, interval), -kClip, kClip);
+}
+
+// x of every lane group, gathered into every lane: out[r] = x of lane group r
+// (same n). v_permlane32_swap exchanges lanes 32-63 of its first operand with
+// lanes 0-31 of its second, v_permlane16_swap the odd 16-lane rows of the
+// first with the even rows of the second.
+__device__ __forceinline__ void group_gather(float x, float out[4]) {
+  const unsigned u = __float_as_uint(x);
+  const auto a = __builtin_amdgcn_permlane32_swap(u, u, false, false);  // x_{g&1}, x_{2+(g&1)}
+  const auto b = __builtin_amdgcn_permlane16_swap(a[0], a[0], false, false);
+  const auto c = __builtin_amdgcn_permlane16_swap(a[1], a[1], false, false);
+  out[0] = __uint_as_float(b[0]);
+  out[1] = __uint_as_float(b[1]);
+  out[2] = __uint_as_float(c[0]);
+  out[3] = __uint_as_float(c[1]);
+}
+
+// The four embedding slots of lane group g in channel step ct for one pair
+// angle x (unit angle): {sin x fa, sin x fb, cos x fa, cos x fb}, fa and fb
+// the lane's frequencies times 1024 / (2 pi) (revolutions per unit angle).
+// RA / RB reduce the argument to [0, 1) revolutions first (the channels of
+// step 0 whose frequency can leave the +-256 revolution domain).
+template <bool RA, bool RB>
+__device__ __forceinline__ bf16x4 embed_slots(float x, float fa, float fb) {
+  float pa = x * fa, pb = x * fb;
+  if constexpr (RA) pa = __builtin_amdgcn_fractf(pa);
+  if constexpr (RB) pb = __builtin_amdgcn_fractf(pb);
+  bf16x4 e;
+  e[0] = (bf16)__builtin_amdgcn_sinf(pa);
+  e[1] = (bf16)__builtin_amdgcn_sinf(pb);
+  e[2] = (bf16)__builtin_amdgcn_cosf(pa);
+  e[3] = (bf16)__builtin_amdgcn_cosf(pb);
+  return e;
+}
+
+template <int C>
+__device__ __forceinline__ bf16x4 embed_step(float x, float fa, float fb, int ct) {
+  if (ct == 0) return embed_slots<EmbedSteps<C>::RA, EmbedSteps<C>::RB>(x, fa, fb);
+  return embed_slots<false, false>(x, fa, fb);
+}
+
+// Identity operand of a 16x16x16 step: lane (g, n) slot e = [4 g + e == n].
+__device__ __forceinline__ bf16x4 ident_x16(int g, int n) {
+  bf16x4 id;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) id[e] = (bf16)((4 * g + e == n) ? 1.f : 0.f);
+  return id;
+}
+
+__device__ __forceinline__ bf16x4 pack4(const f32x4& c) {
+  bf16x4 o;
+#pragma unroll
+  for (int r = 0; r < 4; ++r) o[r] = (bf16)c[r];
+  return o;
+}
+
+// Transpose of a 16x16 tile held as an A operand (lane n = row m, slots =
+// columns 4g .. 4g+3): lane n now holds column n, slots = rows 4g .. 4g+3.
+__device__ __forceinline__ bf16x4 transpose_x16(bf16x4 a, bf16x4 id) { return pack4(mfma_x16(a, id, zero4())); }
+
+// Lower / upper four slots of a 16x16x32 operand.
+__device__ __forceinline__ bf16x4 lo4(const bf16x8& v) { return __builtin_shufflevector(v, v, 0, 1, 2, 3); }
+__device__ __forceinline__ bf16x4 hi4(const bf16x8& v) { return __builtin_shufflevector(v, v, 4, 5, 6, 7); }
+__device__ __forceinline__ bf16x8 cat8(const bf16x4& a, const bf16x4& b) {
+  return __builtin_shufflevector(a, b, 0, 1, 2, 3, 4, 5, 6, 7);
+}
+
+// Head-dim tiles of an operand loaded as KFrag<bf16, D> (lane n = row, group
+// g holds the feature slots of fst_device.h) after transposing: tile q holds
+// feature dmap(q, g', r) in register r of lane group g' of the product it is
+// contracted into. 16x16x32 fragments (D % 32 == 0) split each 32-feature
+// step t into its lower and upper four slots (tiles 2t, 2t+1); 16x16x16
+// fragments map one to one.
+template <int D>
+struct DTiles {
+  static constexpr bool X32 = (D % 32) == 0;
+  static constexpr int NQ = D / 16;
+  static __device__ __forceinline__ int dmap(int q, int g, int r) {
+    if constexpr (X32) return 32 * (q >> 1) + 8 * g + 4 * (q & 1) + r;
+    else return 16 * q + 4 * g + r;
+  }
+  // A-operand half tile q of a fragment (16 rows x 16 features).
+  static __device__ __forceinline__ bf16x4 part(const KFrag<bf16, D>& f, int q) {
+    if constexpr (X32) return (q & 1) ? hi4(f.x32[q >> 1]) : lo4(f.x32[q >> 1]);
+    else return f.x16[q];
+  }
+};
+
+// ---------------------------------------------------------------------------
+// Work items of the 16-row tile kernels. Padded events map directly: logical
+// block w is tile w % nb of event w / nb (nb = ceil(L / 16)), so a tile wholly
+// past its event's length only zeroes its rows. Packed events have no padding
+// and use the per-event prefix sums of tiles.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ bool tile_block(const EventSpec& ev, int w, EventBlock& eb) {
+  if (ev.packed) return locate_block(ev, w, eb);
+  const int nb = (ev.L + 15) >> 4;
+  const int b = w / nb;
+  if (b >= ev.B) return false;
+  eb.b = b;
+  eb.blk = w - b * nb;
+  event_range(ev, b, eb.tok0, eb.len);
+  return true;
+}
+
+// Zero rows [max(i0, len), min(i0 + 16, L)) of a padded event for every head
+// (pad-row contract: forward.py:19-22), 16 bytes per store; `vec` gets zeros
+// at the same (head, row) positions when not null.
+template <typename T, int D>
+__device__ __forceinline__ void zero_tile_rows(const EventSpec& ev, const RowAddr& ra, int i0, int len, int H,
+                                               int tid, T* out, float* vec) {
+  if (ev.packed) return;
+  const int first = i0 > len ? i0 : len;
+  const int end = i0 + 16 < ev.L ? i0 + 16 : ev.L;
+  if (first >= end) return;
+  const int nr = end - first;
+  constexpr int CH = D * (int)sizeof(T) / 16;
+  for (int idx = tid; idx < H * nr * CH; idx += 256) {
+    const int c = idx % CH, r = (idx / CH) % nr, h = idx / (CH * nr);
+    *reinterpret_cast<u32x4*>(out + ra.off(h, first + r, D) + c * (16 / (int)sizeof(T))) = u32x4{0u, 0u, 0u, 0u};
+  }
+  if (vec)
+    for (int idx = tid; idx < H * nr; idx += 256) vec[ra.vec(idx / nr, first + idx % nr)] = 0.f;
+}
+
+// ---------------------------------------------------------------------------
+// Buffer loads. One resource per tensor and event (base = the event's first
+// element, range = its bytes); a lane's offset within the event is fixed and
+// the key chunk moves through the scalar offset, so the chunk loop spends no
+// vector instructions on addresses. Offsets past the range read as zero.
+// ---------------------------------------------------------------------------
+struct Buf {
+  __amdgpu_buffer_rsrc_t r;
+  __device__ __forceinline__ Buf(const void* base, unsigned bytes)
+      : r(__builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000)) {}
+  __device__ __forceinline__ bf16x8 ld128(int voff, int soff) const {
+    return __builtin_bit_cast(bf16x8, __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0));
+  }
+  __device__ __forceinline__ bf16x4 ld64(int voff, int soff) const {
+    return __builtin_bit_cast(bf16x4, __builtin_amdgcn_raw_buffer_load_b64(r, voff, soff, 0));
+  }
+  __device__ __forceinline__ float4 ldf4(int voff, int soff) const {
+    return __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0));
+  }
+};
+
+// Byte offset of lane group g's part of a KFrag<bf16, D> row, and the loader:
+// 16x16x32 steps t at 64 t + 16 g, 16x16x16 steps at 32 t + 8 g.
+template <int D>
+__device__ __forceinline__ int kfrag_goff(int g) {
+  return (D % 32 == 0) ? 16 * g : 8 * g;
+}
+template <int D>
+__device__ __forceinline__ void load_kfrag(KFrag<bf16, D>& f, const Buf& b, int voff, int soff) {
+#pragma unroll
+  for (int t = 0; t < KFrag<bf16, D>::N32; ++t) f.x32[t] = b.ld128(voff + 64 * t, soff);
+#pragma unroll
+  for (int t = 0; t < KFrag<bf16, D>::N16; ++t) f.x16[t] = b.ld64(voff + 32 * t, soff);
+}
+
+// ---------------------------------------------------------------------------
+// LDS layouts.
+// ---------------------------------------------------------------------------
+
+// Embedding tile: [row 16][ct][key KC][16 slots] bf16. The four 8-byte blocks
+// (slot groups) of key j are stored in the order b ^ (2 * ((j >> 3) & 1)):
+// writes of 16 keys x 2 lane groups and transposing reads of 8 keys x 4
+// blocks then each cover 256 distinct bytes.
+template <int C, int KC>
+struct ETile {
+  static constexpr int NCT = C / 16;
+  static constexpr int BYTES = 16 * NCT * KC * 16 * 2;
+  static __device__ __forceinline__ int off(int row, int ct, int key, int blk) {
+    return (((row * NCT + ct) * KC + key) << 4) + ((blk ^ (((key >> 3) & 1) << 1)) << 2);
+  }
+  static __device__ __forceinline__ void store(bf16* e, int row, int ct, int key, int g, bf16x4 v) {
+    *reinterpret_cast<bf16x4*>(e + off(row, ct, key, g)) = v;
+  }
+  // Four consecutive keys kb + 4g .. kb + 4g + 3 of channel slot 16 ct + n,
+  // through the transposing read (source lane s of the group supplies key
+  // kb + 4g + s / 4, block s % 4).
+  static __device__ __forceinline__ bf16x4 load_tr(const bf16* e, int row, int ct, int kb, int g, int n) {
+    const bf16* p = e + off(row, ct, kb + 4 * g + (n >> 2), n & 3);
+    return __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4*)(p));
+  }
+};
+
+// Exchange slots between the row-major and head-major roles: 16-byte chunk c
+// of slot (row i, head h) at ((c * 16 + i) * 16 + (h ^ i)) * 16 bytes. With
+// the head index on the lanes (fixed row) or the row index on the lanes
+// (fixed head) a pass of 16 lanes writes or reads 16 distinct 16-byte bank
+// groups. Heads are padded to 16 slots.
+__device__ __forceinline__ int stage_off(int c, int i, int h) { return (((c << 4) + i) << 8) + ((h ^ i) << 4); }
+
+// Per-(row, head) scalars (rescale factors): [head][17].
+__device__ __forceinline__ int scal_off(int i, int h) { return (h * 17 + i) << 2; }
+
+}  // namespace fst
