@@ -1,0 +1,841 @@
+// Backward kernels of flash-spacetime attention for gfx950, bf16 operands.
+//
+// Gradients of the spec (reference.py:106-167) in the fused form of
+// backward.py:3-32. With qt = bf16(q*scale), u = bf16(qt W), w~ = bf16(dO W),
+// dob = dO.b:
+//   s_ij  = qt_i.k_j + [A] u_i.E_ij,          P_ij = exp(s_ij - lse_i)
+//   dP_ij = dO_i.v_j + [V] (w~_i.E_ij + dob_i)
+//   D_i   = sum_j P_ij dP_ij / sum_j P_ij     (from the same P and dP as dS)
+//   dS_ij = P_ij (dP_ij - D_i)
+//   dq_i  = scale (sum_j dS_ij k_j + [A] (W H_i + sigma_i b))
+//   dk_j  = sum_i dS_ij qt_i,      dv_j = sum_i P_ij dO_i
+//   dW    = [A] sum qt (x) H + [V] sum dO (x) G,  H_i = sum_j dS_ij E_ij,
+//           G_i = sum_j P_ij E_ij,  sigma_i = sum_j dS_ij,  db = [V] sum dO
+//
+// Rows kernel (one 16-row tile per workgroup, roles as in the forward): a
+// single pass over the keys. D is formed online: after chunk t the running
+// D_t = N_t / Z_t (N = sum P dP, Z = sum P over the keys seen) replaces
+// D_{t-1}, and the accumulators built with the old value are corrected with
+// the sums of P they lack, dQ -= (D_t - D_{t-1}) sum P k and H -= (D_t -
+// D_{t-1}) G, before chunk t adds P (dP - D_t) terms. At the end every
+// accumulator equals its value for D = N / Z over all keys, the same N and Z
+// that give sigma = N - D Z; a fully peaked row (all mass on one key) has
+// D_t = dP of that key from its chunk on, so its dS vanishes as in the
+// two-pass form (backward.py:371-407). It writes qt, u, w~ and D - dob for
+// the cols kernel and a per-tile dW / db partial.
+//
+// Cols kernel (one 16-key tile per workgroup, rows streamed): S = Qt K^T and
+// dP = dO V^T with the keys on the lanes, dV^T += dO^T P and dK^T += Qt^T dS
+// (Qt^T, dO^T transposed on the matrix core). The row-owner part forms
+// u_i E_i^T and w~_i E_i^T for the streamed rows with the heads on the
+// registers; four consecutive rows of a lane are regrouped in registers so
+// that the exchange to the head-owners is one 16-byte write and read per
+// (row group, head, key).
+//
+// Both kernels write every output exactly once in a fixed order (no atomics),
+// so results are bitwise reproducible.
+#include "fst_tile.h"
+
+#ifndef FST_ROWS_HB
+#define FST_ROWS_HB 1
+#endif
+
+namespace fst {
+
+// Four consecutive rows' values of a [rows, H] fp32 vector (rows clamped to
+// the event, invalid rows -> fill): one 16-byte load when rows are adjacent
+// (padded layout), four loads otherwise.
+__device__ __forceinline__ f32x4 load_rows4(const Buf& b, const RowAddr& ra, int h, int r0, int len, float fill,
+                                            float mult) {
+  f32x4 v;
+  if (ra.ts == 1 && r0 + 3 < len) {
+    const float4 t = b.ldf4((int)(ra.vec(h, r0) - ra.base_row) * 4, 0);
+    v = f32x4{t.x, t.y, t.z, t.w} * mult;
+  } else {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int row = r0 + r;
+      v[r] = row < len ? b.ldf((int)(ra.vec(h, row) - ra.base_row) * 4, 0) * mult : fill;
+    }
+  }
+  return v;
+}
+
+// ---------------------------------------------------------------------------
+// Rows kernel.
+// ---------------------------------------------------------------------------
+template <int HP, int D, int C, int KC>
+struct Rows2Cfg {
+  static constexpr int HW = HP / 4, NS = KC / 16, NCT = C / 16;
+  static constexpr int E_BYTES = ETile<C, KC>::BYTES;
+  static constexpr int REGION = (KC / 4) * 16 * HP * 16;  // one fp32 term of KC keys per (row, head)
+  static constexpr int SCAL_BYTES = 16 * 17 * 4;
+  static constexpr int MAIN = E_BYTES + 2 * REGION + SCAL_BYTES;
+  static constexpr int DW_BYTES = 4 * (D * C + D) * 4;   // epilogue: per-wave dW / db partials
+  static constexpr int HG_BYTES = 2 * 16 * HP * 16 * 4;  // epilogue: one channel step of H and G
+  static constexpr int EPI = DW_BYTES + HG_BYTES;
+  static constexpr int LDS_BYTES = MAIN > EPI ? MAIN : EPI;
+  static constexpr bool FITS = LDS_BYTES <= 80 * 1024 && HP % 4 == 0;
+};
+
+template <int HP, int D, int C, int KC, int HB>
+__global__ __launch_bounds__(256, 2) void bwd_rows2_kernel(BwdParams prm) {
+  using Cfg = Rows2Cfg<HP, D, C, KC>;
+  using ET = ETile<C, KC>;
+  using DT = DTiles<D>;
+  constexpr int HW = Cfg::HW, NS = Cfg::NS, NCT = Cfg::NCT, NQ = DT::NQ;
+  constexpr int DCW = D * C + D;
+  extern __shared__ __align__(16) unsigned char smem[];
+  bf16* Es = reinterpret_cast<bf16*>(smem);
+  unsigned char* stU = smem + Cfg::E_BYTES;  // u.E, then P
+  unsigned char* stW = stU + Cfg::REGION;    // w~.E + dob, then dS
+  unsigned char* scal = stW + Cfg::REGION;   // increments of D
+
+  const int tid = threadIdx.x;
+  const int w = tid >> 6, lane = tid & 63, g = lane >> 4, n = lane & 15;
+  const int wl = xcd_remap(blockIdx.x, gridDim.x);
+
+  EventBlock eb;
+  if (!tile_block(prm.ev, wl, eb)) return;
+  const int len = eb.len;
+  const int H = prm.H;
+  const bool attn = prm.flags & FST_ATTN_BIAS;
+  const bool act = prm.flags & FST_ACT_BIAS;
+  const bool use_e = attn || act;
+  const bool use_b = act && prm.bias;
+  const RowAddr ra = row_addr(prm.ev, eb);
+  const int i0 = eb.blk * 16;
+  const int last = len - 1;
+  bf16* dqg = reinterpret_cast<bf16*>(prm.dq);
+  // The dW / db partial goes to slot blkcum[b] + tile of the work list (an
+  // empty padded event owns one slot, written as zeros); tiles of padding
+  // rows past an event's last tile own none.
+  const int nbv = len > 0 ? (len + 15) / 16 : (prm.ev.packed ? 0 : 1);
+  float* part = eb.blk < nbv ? prm.dw_part + (long)(prm.ev.blkcum[eb.b] + eb.blk) * DCW : nullptr;
+  if (i0 >= len) {
+    zero_tile_rows<bf16, D>(prm.ev, ra, i0, len, H, tid, dqg, prm.rowsum);
+    if (part)
+      for (int e = tid; e < DCW; e += 256) part[e] = 0.f;
+    return;
+  }
+
+  const bf16* __restrict__ qg = reinterpret_cast<const bf16*>(prm.q);
+  const bf16* __restrict__ kg = reinterpret_cast<const bf16*>(prm.k);
+  const bf16* __restrict__ vg = reinterpret_cast<const bf16*>(prm.v);
+  const bf16* __restrict__ dog = reinterpret_cast<const bf16*>(prm.dout);
+  const bf16x4 id = ident_x16(g, n);
+
+  // ---- head-owner state (lane n = row i0 + n) ----
+  const int my_row = i0 + n;
+  const bool row_ok = my_row < len;
+  KFrag<bf16, D> qf[HW], dof[HW];
+  f32x4 dQ[HW][NQ], A2[HW][NQ];
+  float lse2[HW], dobv[HW], Nn[HW], Zz[HW], Dc[HW];
+  bf16* qtg = reinterpret_cast<bf16*>(prm.qt);
+#pragma unroll
+  for (int hl = 0; hl < HW; ++hl) {
+    const int h = w * HW + hl;
+    const bool ok = h < H && row_ok;
+    if (ok) {
+      qf[hl].load_scaled(qg + ra.off(h, my_row, D), g, prm.scale);
+      dof[hl].load(dog + ra.off(h, my_row, D), g);
+      // qt for the cols kernel: the same bf16 values the logits use.
+      bf16* qd = qtg + ra.off(h, my_row, D);
+#pragma unroll
+      for (int t = 0; t < KFrag<bf16, D>::N32; ++t) *reinterpret_cast<bf16x8*>(qd + 32 * t + 8 * g) = qf[hl].x32[t];
+#pragma unroll
+      for (int t = 0; t < KFrag<bf16, D>::N16; ++t) *reinterpret_cast<bf16x4*>(qd + 16 * t + 4 * g) = qf[hl].x16[t];
+    } else {
+      qf[hl].zero();
+      dof[hl].zero();
+    }
+    // Invalid rows get lse = +inf, so their P (and dS) are exactly zero.
+    lse2[hl] = ok ? prm.lse[ra.vec(h, my_row)] * kLog2e : INFINITY;
+    float pb = 0.f;
+    if (use_b && ok) {
+#pragma unroll
+      for (int t = 0; t < KFrag<bf16, D>::N32; ++t)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) pb = __builtin_fmaf((float)dof[hl].x32[t][e], prm.bias[32 * t + 8 * g + e], pb);
+#pragma unroll
+      for (int t = 0; t < KFrag<bf16, D>::N16; ++t)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) pb = __builtin_fmaf((float)dof[hl].x16[t][e], prm.bias[16 * t + 4 * g + e], pb);
+    }
+    dobv[hl] = group_allsum(pb);
+    Nn[hl] = Zz[hl] = Dc[hl] = 0.f;
+#pragma unroll
+    for (int q = 0; q < NQ; ++q) dQ[hl][q] = A2[hl][q] = zero4();
+  }
+
+  // ---- row-owner state: rows i0 + 4w + r, heads on lane n ----
+  bf16x4 uf[4][NCT], wf[4][NCT];
+  f32x4 Hacc[4][NCT], Gacc[4][NCT];
+  bf16* ug = reinterpret_cast<bf16*>(prm.u);
+  bf16* wtg = reinterpret_cast<bf16*>(prm.wt);
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const int row = i0 + 4 * w + r;
+    const bool ok = row < len && n < H;
+    const long xo = ra.off(0, row < len ? row : last, D);
+    if (attn) {
+      project_slots<D, C>(qg + xo, ra.hs * D, ok, prm.scale, prm.weight, g, n, uf[r]);
+      if (ok)
+#pragma unroll
+        for (int ct = 0; ct < NCT; ++ct) *reinterpret_cast<bf16x4*>(ug + ra.off(n, row, C) + 16 * ct + 4 * g) = uf[r][ct];
+    }
+    if (act) {
+      project_slots<D, C>(dog + xo, ra.hs * D, ok, 1.f, prm.weight, g, n, wf[r]);
+      if (ok)
+#pragma unroll
+        for (int ct = 0; ct < NCT; ++ct) *reinterpret_cast<bf16x4*>(wtg + ra.off(n, row, C) + 16 * ct + 4 * g) = wf[r][ct];
+    }
+#pragma unroll
+    for (int ct = 0; ct < NCT; ++ct) Hacc[r][ct] = Gacc[r][ct] = zero4();
+  }
+  float4 pos_i = float4{0.f, 0.f, 0.f, 0.f};
+  float fa[NCT], fb[NCT];
+  if (use_e) {
+    const int row = i0 + 4 * w + g;
+    pos_i = ra.pos(prm.ev.pos4, row < len ? row : last);
+#pragma unroll
+    for (int ct = 0; ct < NCT; ++ct) {
+      fa[ct] = 1024.f * prm.freq.ghi[8 * ct + 2 * g];
+      fb[ct] = 1024.f * prm.freq.ghi[8 * ct + 2 * g + 1];
+    }
+  }
+
+  // ---- operand stream: K, V rows of the wave's heads, key positions ----
+  const long ebase = ra.off(0, 0, D);
+  const int rowb = (int)(ra.ts * D * 2);
+  const unsigned ebytes = (unsigned)((prm.ev.packed ? (long)len * ra.ts : (long)H * ra.hs) * D * 2);
+  const Buf kbuf(kg + ebase, ebytes), vbuf(vg + ebase, ebytes);
+  const Buf pbuf(prm.ev.pos4 + ra.pos_base, (unsigned)len * 16u);
+  int kvo[HW];
+#pragma unroll
+  for (int hl = 0; hl < HW; ++hl) kvo[hl] = (int)((w * HW + hl) * ra.hs * D * 2) + n * rowb + kfrag_goff<D>(g);
+  KFrag<bf16, D> kf[HW][NS], vf[HW][NS];
+  float4 pj[NS];
+  auto issue = [&](int jn) __attribute__((always_inline)) {
+    const bool full = jn + KC <= len;
+#pragma unroll
+    for (int hl = 0; hl < HW; ++hl) {
+      if (w * HW + hl >= H) continue;
+#pragma unroll
+      for (int s = 0; s < NS; ++s) {
+        const int voff = full ? kvo[hl] + 16 * s * rowb : kvo[hl] + (min(jn + 16 * s + n, last) - n) * rowb;
+        const int soff = full ? jn * rowb : 0;
+        load_kfrag<D>(kf[hl][s], kbuf, voff, soff);
+        load_kfrag<D>(vf[hl][s], vbuf, voff, soff);
+      }
+    }
+    if (use_e) {
+#pragma unroll
+      for (int s = 0; s < NS; ++s) pj[s] = pbuf.ldf4(min(jn + 16 * s + n, last) * 16, 0);
+    }
+  };
+  issue(0);
+
+  auto chunk = [&](int j0, auto tail_tag) __attribute__((always_inline)) {
+    constexpr bool TAIL = decltype(tail_tag)::value;
+    // ---- row-owner: E, u.E and w~.E of rows 4w..4w+3 ----
+    if (use_e) {
+      float xg[NS][4];
+#pragma unroll
+      for (int s = 0; s < NS; ++s) group_gather(pair_angle_unit(pos_i, pj[s]), xg[s]);
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+#pragma unroll
+        for (int s = 0; s < NS; ++s) {
+          bf16x4 ef[NCT];
+#pragma unroll
+          for (int ct = 0; ct < NCT; ++ct) {
+            ef[ct] = embed_step<C>(xg[s][r], fa[ct], fb[ct], ct);
+            ET::store(Es, 4 * w + r, ct, 16 * s + n, g, ef[ct]);
+          }
+          if (n < HP) {
+            if (attn) {
+              f32x4 ue = zero4();
+#pragma unroll
+              for (int ct = 0; ct < NCT; ++ct) ue = mfma_x16(ef[ct], uf[r][ct], ue);
+              *reinterpret_cast<f32x4*>(stU + hslot_off<HP>(4 * s + g, 4 * w + r, n)) = ue;
+            }
+            if (act) {
+              f32x4 we = zero4();
+#pragma unroll
+              for (int ct = 0; ct < NCT; ++ct) we = mfma_x16(ef[ct], wf[r][ct], we);
+              *reinterpret_cast<f32x4*>(stW + hslot_off<HP>(4 * s + g, 4 * w + r, n)) = we;
+            }
+          }
+        }
+    }
+    __syncthreads();  // u.E, w~.E staged
+
+    // ---- head-owner: P, dP, online D, dS, dQ (phase by phase over batches
+    // of HB heads, so the heads' dependency chains overlap) ----
+#pragma unroll
+    for (int hb = 0; hb < HW; hb += HB) {
+      constexpr int NB = HB;
+      f32x4 S[NB][NS], dP[NB][NS];
+#pragma unroll
+      for (int b = 0; b < NB; ++b) {
+        const int hl = hb + b;
+        const int h = w * HW + hl;
+#pragma unroll
+        for (int s = 0; s < NS; ++s) {
+          if (hl >= HW || h >= H) {
+            S[b][s] = dP[b][s] = zero4();
+            continue;
+          }
+          const f32x4 ui = attn ? *reinterpret_cast<const f32x4*>(stU + hslot_off<HP>(4 * s + g, n, h)) : zero4();
+          const f32x4 wi = act ? *reinterpret_cast<const f32x4*>(stW + hslot_off<HP>(4 * s + g, n, h)) : zero4();
+          S[b][s] = mma_k<D>(kf[hl][s], qf[hl], ui);
+          dP[b][s] = mma_k<D>(vf[hl][s], dof[hl], wi);
+        }
+      }
+      float nt[NB], zt[NB];
+#pragma unroll
+      for (int b = 0; b < NB; ++b) {
+        const int hl = hb + b < HW ? hb + b : HW - 1;
+        float a = 0.f, z = 0.f;
+#pragma unroll
+        for (int s = 0; s < NS; ++s)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            float p = exp2f_fast(__builtin_fmaf(S[b][s][r], kLog2e, -lse2[hl]));
+            if constexpr (TAIL) p = (j0 + 16 * s + 4 * g + r < len) ? p : 0.f;
+            const float dp = dP[b][s][r] + dobv[hl];
+            S[b][s][r] = p;
+            dP[b][s][r] = dp;
+            a = __builtin_fmaf(p, dp, a);
+            z += p;
+          }
+        nt[b] = a;
+        zt[b] = z;
+      }
+      float dD[NB];
+#pragma unroll
+      for (int b = 0; b < NB; ++b) {
+        const int hl = hb + b;
+        if (hl >= HW) continue;
+        Nn[hl] += group_allsum(nt[b]);
+        Zz[hl] += group_allsum(zt[b]);
+        const float dn = Zz[hl] > 0.f ? Nn[hl] / Zz[hl] : 0.f;
+        dD[b] = dn - Dc[hl];
+        Dc[hl] = dn;
+      }
+      JFrag<bf16, NS> pf[NB], dsf[NB];
+#pragma unroll
+      for (int b = 0; b < NB; ++b) {
+        const int hl = hb + b;
+        if (hl >= HW) continue;
+#pragma unroll
+        for (int s = 0; s < NS; ++s)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) dP[b][s][r] = S[b][s][r] * (dP[b][s][r] - Dc[hl]);
+        pf[b].from_tiles(S[b]);
+        dsf[b].from_tiles(dP[b]);
+      }
+#pragma unroll
+      for (int b = 0; b < NB; ++b) {
+        const int hl = hb + b;
+        if (hl >= HW || w * HW + hl >= H) continue;
+#pragma unroll
+        for (int q = 0; q < NQ; ++q) {
+          JFrag<bf16, NS> kt;
+          if constexpr (NS == 2)
+            kt.v = cat8(transpose_x16(DT::part(kf[hl][0], q), id), transpose_x16(DT::part(kf[hl][1], q), id));
+          else
+            kt.v = transpose_x16(DT::part(kf[hl][0], q), id);
+          dQ[hl][q] = dQ[hl][q] - dD[b] * A2[hl][q];
+          A2[hl][q] = mma_j(kt, pf[b], A2[hl][q]);
+          dQ[hl][q] = mma_j(kt, dsf[b], dQ[hl][q]);
+        }
+      }
+      if (use_e) {
+        // P and dS for the row-owner (keys 16s + 4g .. +3 of slot (row n,
+        // head h)), and the increment of D.
+#pragma unroll
+        for (int b = 0; b < NB; ++b) {
+          const int hl = hb + b;
+          const int h = w * HW + hl;
+          if (hl >= HW || h >= H) continue;
+#pragma unroll
+          for (int s = 0; s < NS; ++s) {
+            bf16x4 pv, dv;
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+              pv[r] = pf[b].v[4 * s + r];
+              dv[r] = dsf[b].v[4 * s + r];
+            }
+            const int so = hslot_off<HP>(2 * s + (g >> 1), n, h) + 8 * (g & 1);
+            *reinterpret_cast<bf16x4*>(stU + so) = pv;
+            *reinterpret_cast<bf16x4*>(stW + so) = dv;
+          }
+          if (g == 0) *reinterpret_cast<float*>(scal + scal_off(n, h)) = dD[b];
+        }
+      }
+    }
+    if (j0 + KC < len) issue(j0 + KC);
+    __syncthreads();  // P, dS and D increments staged
+
+    // ---- row-owner: H -= dD G; H += E^T dS; G += E^T P ----
+    if (use_e) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int il = 4 * w + r;
+        const bool hv = n < H;
+        const float dd = hv ? *reinterpret_cast<const float*>(scal + scal_off(il, n)) : 0.f;
+        JFrag<bf16, NS> pr, dr;
+        if (hv) {
+#pragma unroll
+          for (int s = 0; s < NS; ++s) {
+            const int so = hslot_off<HP>(2 * s + (g >> 1), il, n) + 8 * (g & 1);
+            const bf16x4 pv = *reinterpret_cast<const bf16x4*>(stU + so);
+            const bf16x4 dv = *reinterpret_cast<const bf16x4*>(stW + so);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              pr.v[4 * s + e] = pv[e];
+              dr.v[4 * s + e] = dv[e];
+            }
+          }
+        } else {
+          pr.zero();
+          dr.zero();
+        }
+#pragma unroll
+        for (int ct = 0; ct < NCT; ++ct) {
+          JFrag<bf16, NS> et;
+          if constexpr (NS == 2)
+            et.v = cat8(ET::load_tr(Es, il, ct, 0, g, n), ET::load_tr(Es, il, ct, 16, g, n));
+          else
+            et.v = ET::load_tr(Es, il, ct, 0, g, n);
+          if (attn) {
+            Hacc[r][ct] = Hacc[r][ct] - dd * Gacc[r][ct];
+            Hacc[r][ct] = mma_j(et, dr, Hacc[r][ct]);
+          }
+          Gacc[r][ct] = mma_j(et, pr, Gacc[r][ct]);
+        }
+      }
+    }
+  };
+
+  int j0 = 0;
+  for (; j0 + KC <= len; j0 += KC) chunk(j0, std::false_type{});
+  if (j0 < len) chunk(j0, std::true_type{});
+
+  // ---- epilogue: sigma, D, dq = scale (dQ + W H + sigma b) ----
+  float sig[HW];
+#pragma unroll
+  for (int hl = 0; hl < HW; ++hl) {
+    sig[hl] = Nn[hl] - Dc[hl] * Zz[hl];
+    const int h = w * HW + hl;
+    if (g == 0 && row_ok && h < H) {
+      prm.dsum[ra.vec(h, my_row)] = Dc[hl] - dobv[hl];  // the cols kernel's dS = P (dP~ - (D - dob))
+      if (prm.rowsum) prm.rowsum[ra.vec(h, my_row)] = sig[hl];
+    }
+  }
+#pragma unroll
+  for (int q = 0; q < NQ; ++q) {
+    if (attn) {
+      __syncthreads();  // the stage is free (last chunk, or previous round)
+      const int dn = DT::dmap(q, n >> 2, n & 3);
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        f32x4 acc = zero4();
+#pragma unroll
+        for (int ct = 0; ct < NCT; ++ct)
+#pragma unroll
+          for (int sp = 0; sp < 4; ++sp)
+            acc = mfma_f32(prm.weight[dn * C + slot_channel<C>(16 * ct + 4 * g + sp)], Hacc[r][ct][sp], acc);
+        if (n < HP) *reinterpret_cast<f32x4*>(stU + hslot_off<HP>(g, 4 * w + r, n)) = acc;
+      }
+      __syncthreads();
+    }
+#pragma unroll
+    for (int hl = 0; hl < HW; ++hl) {
+      const int h = w * HW + hl;
+      f32x4 o = dQ[hl][q];
+      if (attn && h < H) {
+        o = o + *reinterpret_cast<const f32x4*>(stU + hslot_off<HP>(g, n, h));
+        if (prm.bias) {
+#pragma unroll
+          for (int r = 0; r < 4; ++r) o[r] = __builtin_fmaf(sig[hl], prm.bias[DT::dmap(q, g, r)], o[r]);
+        }
+      }
+      dQ[hl][q] = o * prm.scale;
+    }
+  }
+  if (row_ok) {
+#pragma unroll
+    for (int hl = 0; hl < HW; ++hl) {
+      const int h = w * HW + hl;
+      if (h >= H) continue;
+      bf16* orow = dqg + ra.off(h, my_row, D);
+      if constexpr (DT::X32) {
+#pragma unroll
+        for (int t = 0; t < NQ / 2; ++t)
+          *reinterpret_cast<bf16x8*>(orow + DT::dmap(2 * t, g, 0)) =
+              cat8(pack4(dQ[hl][2 * t]), pack4(dQ[hl][2 * t + 1]));
+      } else {
+#pragma unroll
+        for (int q = 0; q < NQ; ++q) *reinterpret_cast<bf16x4*>(orow + DT::dmap(q, g, 0)) = pack4(dQ[hl][q]);
+      }
+    }
+  }
+
+  // ---- dW / db partial of this tile: sum over its rows and heads ----
+  // dW[d, channel(slot)] += sum_(row, head) A[d, (row, head)] B[(row, head), slot]
+  // on fp32 MFMA: A = qt (resp. dO) with d on the lanes, B = H (resp. G) with
+  // the slot on the lanes, staged one channel step at a time as
+  // [row][head][16 slots].
+  __syncthreads();
+  float* Wred = reinterpret_cast<float*>(smem);
+  float* HGs = Wred + 4 * DCW;
+  if (use_e) {
+    f32x4 dw[NQ][NCT];
+    float dbl[NQ];
+#pragma unroll
+    for (int q = 0; q < NQ; ++q) {
+      dbl[q] = 0.f;
+#pragma unroll
+      for (int ct = 0; ct < NCT; ++ct) dw[q][ct] = zero4();
+    }
+#pragma unroll
+    for (int ct = 0; ct < NCT; ++ct) {
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int il = 4 * w + r;
+        if (n < HP) {
+          *reinterpret_cast<f32x4*>(HGs + (il * HP + n) * 16 + 4 * g) = Hacc[r][ct];
+          *reinterpret_cast<f32x4*>(HGs + 16 * HP * 16 + (il * HP + n) * 16 + 4 * g) = Gacc[r][ct];
+        }
+      }
+      __syncthreads();
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const int il = 4 * w + r;
+        const int row = i0 + il;
+        const bool rok = row < len;
+#pragma unroll
+        for (int s4 = 0; s4 < HP / 4; ++s4) {
+          const int h = 4 * s4 + g;
+          const bool ok = rok && h < H;
+          const float bh = (attn && ok) ? HGs[(il * HP + h) * 16 + n] : 0.f;
+          const float bg = (act && ok) ? HGs[16 * HP * 16 + (il * HP + h) * 16 + n] : 0.f;
+#pragma unroll
+          for (int q = 0; q < NQ; ++q) {
+            const int d = 16 * q + n;
+            const float aq = (attn && ok) ? (float)qg[ra.off(h, row, D) + d] * prm.scale : 0.f;
+            const float ao = (act && ok) ? (float)dog[ra.off(h, row, D) + d] : 0.f;
+            if (ct == 0) dbl[q] += ao;
+            dw[q][ct] = mfma_f32(aq, bh, dw[q][ct]);
+            dw[q][ct] = mfma_f32(ao, bg, dw[q][ct]);
+          }
+        }
+      }
+      __syncthreads();
+    }
+    float* wr = Wred + w * DCW;
+#pragma unroll
+    for (int q = 0; q < NQ; ++q) {
+#pragma unroll
+      for (int ct = 0; ct < NCT; ++ct)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) wr[(16 * q + 4 * g + r) * C + slot_channel<C>(16 * ct + n)] = dw[q][ct][r];
+      const float dbs = group_allsum(dbl[q]);
+      if (g == 0) wr[D * C + 16 * q + n] = dbs;
+    }
+    __syncthreads();
+    for (int e = tid; e < DCW; e += 256) part[e] = Wred[e] + Wred[DCW + e] + Wred[2 * DCW + e] + Wred[3 * DCW + e];
+  } else {
+    for (int e = tid; e < DCW; e += 256) part[e] = 0.f;
+  }
+
+  zero_tile_rows<bf16, D>(prm.ev, ra, i0, len, H, tid, dqg, prm.rowsum);
+}
+
+// ---------------------------------------------------------------------------
+// Cols kernel.
+// ---------------------------------------------------------------------------
+template <int HP, int D, int C, int RC>
+struct Cols2Cfg {
+  static constexpr int HW = HP / 4, NS = RC / 16, NCT = C / 16;
+  static constexpr int RG = RC / 4;     // row groups per chunk
+  static constexpr int RGW = RC / 16;   // row groups per row-owner wave
+  static constexpr int REGION = RG * HP * 16 * 16;  // one fp32 term: [row group][head][key] x 4 rows
+  static constexpr int LDS_BYTES = 2 * REGION;
+  static constexpr bool FITS = LDS_BYTES <= 80 * 1024 && HP % 4 == 0;
+};
+
+template <int HP, int D, int C, int RC>
+__global__ __launch_bounds__(256, 2) void bwd_cols2_kernel(BwdParams prm) {
+  using Cfg = Cols2Cfg<HP, D, C, RC>;
+  using DT = DTiles<D>;
+  constexpr int HW = Cfg::HW, NS = Cfg::NS, NCT = Cfg::NCT, NQ = DT::NQ, RGW = Cfg::RGW;
+  extern __shared__ __align__(16) unsigned char smem[];
+  unsigned char* stU = smem;                 // u.E
+  unsigned char* stW = smem + Cfg::REGION;   // w~.E
+
+  const int tid = threadIdx.x;
+  const int w = tid >> 6, lane = tid & 63, g = lane >> 4, n = lane & 15;
+
+  EventSpec ev = prm.ev;
+  ev.blkcum = prm.blkcum_cols;
+  EventBlock eb;
+  if (!tile_block(ev, xcd_remap(blockIdx.x, gridDim.x), eb)) return;
+  const int len = eb.len;
+  const int H = prm.H;
+  const bool attn = prm.flags & FST_ATTN_BIAS;
+  const bool act = prm.flags & FST_ACT_BIAS;
+  const bool use_e = attn || act;
+  const RowAddr ra = row_addr(ev, eb);
+  const int k0 = eb.blk * 16;
+  const int last = len - 1;
+  bf16* dkg = reinterpret_cast<bf16*>(prm.dk);
+  bf16* dvg = reinterpret_cast<bf16*>(prm.dv);
+  if (k0 >= len) {
+    zero_tile_rows<bf16, D>(ev, ra, k0, len, H, tid, dkg, nullptr);
+    zero_tile_rows<bf16, D>(ev, ra, k0, len, H, tid, dvg, nullptr);
+    return;
+  }
+  const bf16x4 id = ident_x16(g, n);
+
+  // ---- head-owner state (lane n = key k0 + n) ----
+  const int my_key = k0 + n;
+  const bool key_ok = my_key < len;
+  const int kc = key_ok ? my_key : last;
+  KFrag<bf16, D> kf[HW], vf[HW];
+  f32x4 dK[HW][NQ], dV[HW][NQ];
+  const bf16* __restrict__ kg = reinterpret_cast<const bf16*>(prm.k);
+  const bf16* __restrict__ vg = reinterpret_cast<const bf16*>(prm.v);
+#pragma unroll
+  for (int hl = 0; hl < HW; ++hl) {
+    const int h = w * HW + hl;
+    if (h < H) {
+      kf[hl].load(kg + ra.off(h, kc, D), g);
+      vf[hl].load(vg + ra.off(h, kc, D), g);
+    } else {
+      kf[hl].zero();
+      vf[hl].zero();
+    }
+#pragma unroll
+    for (int q = 0; q < NQ; ++q) dK[hl][q] = dV[hl][q] = zero4();
+  }
+
+  // ---- row-owner: streamed rows 4 (RGW w + q') + r of each chunk ----
+  float4 pos_k = float4{0.f, 0.f, 0.f, 0.f};
+  float fa[NCT], fb[NCT];
+  if (use_e) {
+    pos_k = ra.pos(ev.pos4, kc);
+#pragma unroll
+    for (int ct = 0; ct < NCT; ++ct) {
+      fa[ct] = 1024.f * prm.freq.ghi[8 * ct + 2 * g];
+      fb[ct] = 1024.f * prm.freq.ghi[8 * ct + 2 * g + 1];
+    }
+  }
+
+  // ---- operand stream: qt and dO rows of the wave's heads, per-row scalars,
+  // u / w~ rows and row positions ----
+  const long ebase = ra.off(0, 0, D);
+  const int rowb = (int)(ra.ts * D * 2);
+  const unsigned ebytes = (unsigned)((ev.packed ? (long)len * ra.ts : (long)H * ra.hs) * D * 2);
+  const Buf qbuf(reinterpret_cast<const bf16*>(prm.qt) + ebase, ebytes);
+  const Buf obuf(reinterpret_cast<const bf16*>(prm.dout) + ebase, ebytes);
+  const unsigned vbytes = (unsigned)((ev.packed ? (long)len * ra.ts : (long)H * ra.hs) * 4);
+  const Buf lbuf(prm.lse + ra.base_row, vbytes), dbuf(prm.dsum + ra.base_row, vbytes);
+  const long cbase = ra.off(0, 0, C);
+  const unsigned cbytes = (unsigned)((ev.packed ? (long)len * ra.ts : (long)H * ra.hs) * C * 2);
+  const Buf ubuf(reinterpret_cast<const bf16*>(prm.u) + cbase, cbytes),
+      wbuf(reinterpret_cast<const bf16*>(prm.wt) + cbase, cbytes);
+  const Buf pbuf(ev.pos4 + ra.pos_base, (unsigned)len * 16u);
+  int qvo[HW];
+#pragma unroll
+  for (int hl = 0; hl < HW; ++hl) qvo[hl] = (int)((w * HW + hl) * ra.hs * D * 2) + n * rowb + kfrag_goff<D>(g);
+
+  KFrag<bf16, D> qr[HW][NS], orw[HW][NS];
+  f32x4 lse2[HW][NS], dsv[HW][NS];
+  float4 prow[RGW];
+  auto issue = [&](int in) __attribute__((always_inline)) {
+    const bool full = in + RC <= len;
+#pragma unroll
+    for (int hl = 0; hl < HW; ++hl) {
+      const int h = w * HW + hl;
+      if (h >= H) continue;
+#pragma unroll
+      for (int s = 0; s < NS; ++s) {
+        const int voff = full ? qvo[hl] + 16 * s * rowb : qvo[hl] + (min(in + 16 * s + n, last) - n) * rowb;
+        const int soff = full ? in * rowb : 0;
+        load_kfrag<D>(qr[hl][s], qbuf, voff, soff);
+        load_kfrag<D>(orw[hl][s], obuf, voff, soff);
+        const int r0 = in + 16 * s + 4 * g;
+        lse2[hl][s] = load_rows4(lbuf, ra, h, r0, len, INFINITY, kLog2e);
+        dsv[hl][s] = load_rows4(dbuf, ra, h, r0, len, 0.f, 1.f);
+      }
+    }
+    if (use_e) {
+#pragma unroll
+      for (int q2 = 0; q2 < RGW; ++q2) prow[q2] = pbuf.ldf4(min(in + 4 * (RGW * w + q2) + g, last) * 16, 0);
+    }
+  };
+  issue(0);
+
+  auto chunk = [&](int i0c, auto tail_tag) __attribute__((always_inline)) {
+    constexpr bool TAIL = decltype(tail_tag)::value;
+    // ---- row-owner: u_i E_i^T and w~_i E_i^T for its row groups ----
+    if (use_e) {
+#pragma unroll
+      for (int q2 = 0; q2 < RGW; ++q2) {
+        const int rg = RGW * w + q2;
+        float xg[4];
+        group_gather(pair_angle_unit(prow[q2], pos_k), xg);
+        f32x4 ue[4], we[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int row = min(i0c + 4 * rg + r, last);
+          bf16x4 ef[NCT];
+#pragma unroll
+          for (int ct = 0; ct < NCT; ++ct) ef[ct] = embed_step<C>(xg[r], fa[ct], fb[ct], ct);
+          const int co = (int)(ra.off(n, row, C) - cbase) * 2 + 8 * g;
+          ue[r] = we[r] = zero4();
+#pragma unroll
+          for (int ct = 0; ct < NCT; ++ct) {
+            if (attn) ue[r] = mfma_x16(ubuf.ld64(co + 32 * ct, 0), ef[ct], ue[r]);
+            if (act) we[r] = mfma_x16(wbuf.ld64(co + 32 * ct, 0), ef[ct], we[r]);
+          }
+        }
+        // lane (g, key n) holds heads 4g + e of rows r: regroup by head.
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int h = 4 * g + e;
+          if (h >= HP) continue;
+          const int so = ((rg * HP + h) * 16 + n) * 16;
+          if (attn) *reinterpret_cast<f32x4*>(stU + so) = f32x4{ue[0][e], ue[1][e], ue[2][e], ue[3][e]};
+          if (act) *reinterpret_cast<f32x4*>(stW + so) = f32x4{we[0][e], we[1][e], we[2][e], we[3][e]};
+        }
+      }
+    }
+    __syncthreads();  // u.E, w~.E staged
+
+    // ---- head-owner: P, dS, dV^T += dO^T P, dK^T += Qt^T dS ----
+    f32x4 S[HW][NS], dP[HW][NS];
+#pragma unroll
+    for (int hl = 0; hl < HW; ++hl) {
+      const int h = w * HW + hl;
+#pragma unroll
+      for (int s = 0; s < NS; ++s) {
+        if (h >= H) {
+          S[hl][s] = dP[hl][s] = zero4();
+          continue;
+        }
+        const int so = (((4 * s + g) * HP + h) * 16 + n) * 16;
+        const f32x4 ui = attn ? *reinterpret_cast<const f32x4*>(stU + so) : zero4();
+        const f32x4 wi = act ? *reinterpret_cast<const f32x4*>(stW + so) : zero4();
+        S[hl][s] = mma_k<D>(qr[hl][s], kf[hl], ui);
+        dP[hl][s] = mma_k<D>(orw[hl][s], vf[hl], wi);
+      }
+    }
+    JFrag<bf16, NS> pf[HW], dsf[HW];
+#pragma unroll
+    for (int hl = 0; hl < HW; ++hl) {
+#pragma unroll
+      for (int s = 0; s < NS; ++s)
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          // Rows past the event carry lse = +inf: P = 0 there.
+          const float p = exp2f_fast(__builtin_fmaf(S[hl][s][r], kLog2e, -lse2[hl][s][r]));
+          S[hl][s][r] = p;
+          dP[hl][s][r] = p * (dP[hl][s][r] - dsv[hl][s][r]);
+        }
+      pf[hl].from_tiles(S[hl]);
+      dsf[hl].from_tiles(dP[hl]);
+    }
+#pragma unroll
+    for (int hl = 0; hl < HW; ++hl) {
+      if (w * HW + hl >= H) continue;
+#pragma unroll
+      for (int q = 0; q < NQ; ++q) {
+        JFrag<bf16, NS> ot, qt;
+        if constexpr (NS == 2) {
+          ot.v = cat8(transpose_x16(DT::part(orw[hl][0], q), id), transpose_x16(DT::part(orw[hl][1], q), id));
+          qt.v = cat8(transpose_x16(DT::part(qr[hl][0], q), id), transpose_x16(DT::part(qr[hl][1], q), id));
+        } else {
+          ot.v = transpose_x16(DT::part(orw[hl][0], q), id);
+          qt.v = transpose_x16(DT::part(qr[hl][0], q), id);
+        }
+        dV[hl][q] = mma_j(ot, pf[hl], dV[hl][q]);
+        dK[hl][q] = mma_j(qt, dsf[hl], dK[hl][q]);
+      }
+    }
+    (void)TAIL;
+    if (i0c + RC < len) issue(i0c + RC);
+    __syncthreads();  // the stage is read; the next chunk may overwrite it
+  };
+
+  int i0c = 0;
+  for (; i0c + RC <= len; i0c += RC) chunk(i0c, std::false_type{});
+  if (i0c < len) chunk(i0c, std::true_type{});
+
+  // ---- store dk, dv (lane n = key, 8 consecutive features per lane group) ----
+  if (key_ok) {
+#pragma unroll
+    for (int hl = 0; hl < HW; ++hl) {
+      const int h = w * HW + hl;
+      if (h >= H) continue;
+      bf16* krow = dkg + ra.off(h, my_key, D);
+      bf16* vrow = dvg + ra.off(h, my_key, D);
+      if constexpr (DT::X32) {
+#pragma unroll
+        for (int t = 0; t < NQ / 2; ++t) {
+          *reinterpret_cast<bf16x8*>(krow + DT::dmap(2 * t, g, 0)) = cat8(pack4(dK[hl][2 * t]), pack4(dK[hl][2 * t + 1]));
+          *reinterpret_cast<bf16x8*>(vrow + DT::dmap(2 * t, g, 0)) = cat8(pack4(dV[hl][2 * t]), pack4(dV[hl][2 * t + 1]));
+        }
+      } else {
+#pragma unroll
+        for (int q = 0; q < NQ; ++q) {
+          *reinterpret_cast<bf16x4*>(krow + DT::dmap(q, g, 0)) = pack4(dK[hl][q]);
+          *reinterpret_cast<bf16x4*>(vrow + DT::dmap(q, g, 0)) = pack4(dV[hl][q]);
+        }
+      }
+    }
+  }
+  zero_tile_rows<bf16, D>(ev, ra, k0, len, H, tid, dkg, nullptr);
+  zero_tile_rows<bf16, D>(ev, ra, k0, len, H, tid, dvg, nullptr);
+}
+
+// ---------------------------------------------------------------------------
+// Dispatch.
+// ---------------------------------------------------------------------------
+template <int HP, int D, int C>
+struct Bwd2Pick {
+  static constexpr int KC = 16;  // keys per rows-kernel chunk
+  static constexpr int HB = FST_ROWS_HB;  // heads per phase batch of the rows kernel
+  static constexpr int RC = 16;  // rows per cols-kernel chunk
+  static constexpr bool OK = Rows2Cfg<HP, D, C, KC>::FITS && Cols2Cfg<HP, D, C, RC>::FITS;
+};
+
+template <int HP, int D, int C>
+int bwd2_launch_t(const BwdParams& prm, int which, hipStream_t stream, int grid) {
+  using P = Bwd2Pick<HP, D, C>;
+  if constexpr (!P::OK) {
+    return FST_EUNSUPPORTED;
+  } else {
+    const int g8 = (grid + 7) & ~7;
+    if (which == 0) {
+      auto kern = bwd_rows2_kernel<HP, D, C, P::KC, P::HB>;
+      constexpr int lds = Rows2Cfg<HP, D, C, P::KC>::LDS_BYTES;
+      if (hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, lds) != hipSuccess)
+        return FST_ELAUNCH;
+      if (grid > 0) hipLaunchKernelGGL(kern, dim3(g8), dim3(256), lds, stream, prm);
+    } else {
+      auto kern = bwd_cols2_kernel<HP, D, C, P::RC>;
+      constexpr int lds = Cols2Cfg<HP, D, C, P::RC>::LDS_BYTES;
+      if (hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, lds) != hipSuccess)
+        return FST_ELAUNCH;
+      if (grid > 0) hipLaunchKernelGGL(kern, dim3(g8), dim3(256), lds, stream, prm);
+    }
+    return hipGetLastError() == hipSuccess ? FST_OK : FST_ELAUNCH;
+  }
+}
+
+}  // namespace fst

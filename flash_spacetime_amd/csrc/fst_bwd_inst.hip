@@ -2,6 +2,7 @@
 // padding HP in {4, 8, 12, 16} and channel count C in {16, 32, 48, 64}.
 // Built once per (dtype, D) with -DFST_T, -DFST_D and -DFST_NAME.
 #include "fst_backward.hip"
+#include "fst_bwd2.hip"
 
 #if !defined(FST_T) || !defined(FST_D) || !defined(FST_NAME)
 #error "FST_T, FST_D and FST_NAME must be defined"
@@ -14,8 +15,20 @@ namespace fst {
 
 int FST_CAT(bwd_dispatch_, FST_NAME)(const BwdParams& prm, int which, int HP, int C, hipStream_t stream, int grid,
                                      bool query, int* rows) {
-#define FST_CASE(HPV, CV) \
-  if (HP == HPV && C == CV) return bwd_launch_t<FST_T, HPV, FST_D, CV>(prm, which, stream, grid, query, rows);
+  // bf16 runs the 16-row / 16-key tile kernels (fst_bwd2.hip) wherever their
+  // LDS plan fits; fp32 and the remaining shapes run fst_backward.hip.
+#define FST_CASE(HPV, CV)                                                      \
+  if (HP == HPV && C == CV) {                                                  \
+    if constexpr (is_bf16<FST_T>::value && Bwd2Pick<HPV, FST_D, CV>::OK) {     \
+      if (query) {                                                             \
+        *rows = 16;                                                            \
+        return FST_OK;                                                         \
+      }                                                                        \
+      return bwd2_launch_t<HPV, FST_D, CV>(prm, which, stream, grid);          \
+    } else {                                                                   \
+      return bwd_launch_t<FST_T, HPV, FST_D, CV>(prm, which, stream, grid, query, rows); \
+    }                                                                          \
+  }
 #define FST_CASES(HPV) FST_CASE(HPV, 16) FST_CASE(HPV, 32) FST_CASE(HPV, 48) FST_CASE(HPV, 64)
   FST_CASES(4)
   FST_CASES(8)

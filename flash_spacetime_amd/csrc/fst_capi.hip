@@ -188,7 +188,7 @@ __global__ __launch_bounds__(256) void fill_zero_kernel(float* p, int n) {
 struct BwdLayout {
   int rows_r, rows_c;   // rows (keys) per workgroup of the rows / cols kernels
   long grid_r, grid_c;
-  size_t off_bc_r, off_bc_c, off_u, off_wt, off_dob, off_dsum, off_part, off_seg, total;
+  size_t off_bc_r, off_bc_c, off_u, off_wt, off_qt, off_dob, off_dsum, off_part, off_seg, total;
   long nseg;  // stage-1 runs of the dW reduction
 };
 
@@ -213,6 +213,8 @@ static int bwd_layout(int dtype, int flags, int B, int H, int L, int T, int D, i
   off += align_up((size_t)rows * H * C * esz, 256);
   lay.off_wt = off;
   off += align_up((size_t)rows * H * C * esz, 256);
+  lay.off_qt = off;
+  if (dtype == FST_BF16) off += align_up((size_t)rows * H * D * esz, 256);
   lay.off_dob = off;
   off += align_up((size_t)rows * H * 4, 256);
   lay.off_dsum = off;
@@ -401,6 +403,7 @@ int fst_backward_phases(int phases, int dtype, int flags, int B, int H, int L, i
   prm.lse = lse;
   prm.u = ws + lay.off_u;
   prm.wt = ws + lay.off_wt;
+  prm.qt = ws + lay.off_qt;
   prm.dob = reinterpret_cast<float*>(ws + lay.off_dob);
   prm.dsum = reinterpret_cast<float*>(ws + lay.off_dsum);
   prm.dw_part = reinterpret_cast<float*>(ws + lay.off_part);

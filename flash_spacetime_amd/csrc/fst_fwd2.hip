@@ -162,7 +162,7 @@ __global__ __launch_bounds__(256, 2) void fwd2_kernel(FwdParams prm) {
   // head-owner has consumed those of chunk j0; keys are clamped to the event.
   KFrag<bf16, D> kf[HW][NS], vf[HW][NS];
   float4 pj[NS];
-  auto issue = [&](int jn) {
+  auto issue = [&](int jn) __attribute__((always_inline)) {
     const bool full = jn + KC <= len;
 #pragma unroll
     for (int hl = 0; hl < HW; ++hl) {
@@ -186,7 +186,7 @@ __global__ __launch_bounds__(256, 2) void fwd2_kernel(FwdParams prm) {
   };
   issue(0);
 
-  auto chunk = [&](int j0, auto tail_tag) {
+  auto chunk = [&](int j0, auto tail_tag) __attribute__((always_inline)) {
     constexpr bool TAIL = decltype(tail_tag)::value;
 
     // ---- row-owner: E of rows 4w..4w+3 x KC keys; u.E staged ----

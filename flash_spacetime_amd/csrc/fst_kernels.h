@@ -103,6 +103,7 @@ struct BwdParams {
   // scratch written by the rows kernel, read by the cols kernel
   void* u;              // [rows, C] T
   void* wt;             // [rows, C] T
+  void* qt;             // [rows, D] T: bf16(q * scale) (written by the bf16 rows kernel)
   float* dob;           // [rows]
   float* dsum;          // [rows]
   float* dw_part;       // [blocks, D, C]

@@ -191,6 +191,27 @@ __device__ __forceinline__ void zero_tile_rows(const EventSpec& ev, const RowAdd
     for (int idx = tid; idx < H * nr; idx += 256) vec[ra.vec(idx / nr, first + idx % nr)] = 0.f;
 }
 
+// u = bf16(x @ W[:, channel(slot)]) for the heads of one row, x = row * mult
+// (q * scale or dO): fp32 MFMA with the head on lane n (heads >= H or an
+// invalid row give zeros); lane (g, n = h) receives slots 16 ct + 4 g .. +3.
+// xrow points at head 0 of the row, hstride is the element stride of heads.
+template <int D, int C>
+__device__ __forceinline__ void project_slots(const bf16* xrow, long hstride, bool ok, float mult,
+                                              const float* __restrict__ W, int g, int n, bf16x4* out) {
+  constexpr int Qd = D / 4;
+  float xv[Qd];
+  const bf16* p = xrow + (ok ? n * hstride : 0) + Qd * g;
+#pragma unroll
+  for (int s = 0; s < Qd; ++s) xv[s] = ok ? (float)p[s] * mult : 0.f;
+#pragma unroll
+  for (int ct = 0; ct < C / 16; ++ct) {
+    f32x4 a = zero4();
+#pragma unroll
+    for (int s = 0; s < Qd; ++s) a = mfma_f32(W[(Qd * g + s) * C + slot_channel<C>(16 * ct + n)], xv[s], a);
+    out[ct] = pack4(a);
+  }
+}
+
 // ---------------------------------------------------------------------------
 // Buffer loads. One resource per tensor and event (base = the event's first
 // element, range = its bytes); a lane's offset within the event is fixed and
@@ -209,6 +230,9 @@ struct Buf {
   }
   __device__ __forceinline__ float4 ldf4(int voff, int soff) const {
     return __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0));
+  }
+  __device__ __forceinline__ float ldf(int voff, int soff) const {
+    return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, voff, soff, 0));
   }
 };
 
@@ -259,6 +283,18 @@ struct ETile {
 // (fixed head) a pass of 16 lanes writes or reads 16 distinct 16-byte bank
 // groups. Heads are padded to 16 slots.
 __device__ __forceinline__ int stage_off(int c, int i, int h) { return (((c << 4) + i) << 8) + ((h ^ i) << 4); }
+
+// The same exchange with heads padded only to HP: 16-byte chunk c of slot
+// (row i, head h) at ((c * 16 + i) * HP + (h + (i >> SH)) % HP) * 16 bytes;
+// the rotation by i >> SH keeps both access patterns on 16 distinct 16-byte
+// bank groups for HP in {4, 8, 12, 16}. h must be < HP.
+template <int HP>
+__device__ __forceinline__ int hslot_off(int c, int i, int h) {
+  constexpr int SH = HP == 8 ? 1 : (HP == 16 ? 0 : 2);
+  int hh = h + (i >> SH);
+  hh = hh >= HP ? hh - HP : hh;
+  return (((c << 4) + i) * HP + hh) << 4;
+}
 
 // Per-(row, head) scalars (rescale factors): [head][17].
 __device__ __forceinline__ int scal_off(int i, int h) { return (h * 17 + i) << 2; }

@@ -73,9 +73,12 @@ def test_workspace_queries():
     fwd = lib.fst_forward_workspace_bytes(_lib.FST_BF16, 3, 256, 12, 768, 0, 32, 16)
     assert fwd >= 257 * 4 and fwd % 256 == 0
     bwd = lib.fst_backward_workspace_bytes(_lib.FST_BF16, 3, 256, 12, 768, 0, 32, 16)
-    # u and w~ ([rows, H, C] bf16) dominate the backward scratch: O(B L C).
+    # u, w~ ([rows, H, C]) and qt ([rows, H, D], bf16 only) dominate the
+    # backward scratch: linear in the number of rows, nothing O(L^2).
     rows_h = 256 * 768 * 12
-    assert 2 * rows_h * 16 * 2 <= bwd < 3 * rows_h * 16 * 2 + 64 * 2 ** 20
+    assert rows_h * (2 * 16 + 32) * 2 <= bwd < rows_h * (2 * 16 + 32) * 2 + 64 * 2 ** 20
+    f32 = lib.fst_backward_workspace_bytes(_lib.FST_F32, 3, 256, 12, 768, 0, 32, 16)
+    assert 2 * rows_h * 16 * 4 <= f32 < 2 * rows_h * 16 * 4 + 64 * 2 ** 20
     packed = lib.fst_backward_workspace_bytes(_lib.FST_BF16, 3 | _lib.FST_PACKED, 4096, 12, 0, 973765, 32, 16)
     assert packed > 0
     assert lib.fst_backward_workspace_bytes(_lib.FST_BF16, 3, 4, 17, 64, 0, 32, 16) == 0
