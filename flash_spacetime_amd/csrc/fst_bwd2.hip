@@ -42,20 +42,22 @@
 
 namespace fst {
 
-// Four consecutive rows' values of a [rows, H] fp32 vector (rows clamped to
-// the event, invalid rows -> fill): one 16-byte load when rows are adjacent
-// (padded layout), four loads otherwise.
+// Four consecutive rows' values of a [rows, H] fp32 vector, times mult.
+// `full` (uniform) says all four rows lie in the event: then adjacent rows
+// (padded layout) take one 16-byte load; otherwise rows past the event give
+// `fill` and rows are loaded one by one.
 __device__ __forceinline__ f32x4 load_rows4(const Buf& b, const RowAddr& ra, int h, int r0, int len, float fill,
-                                            float mult) {
+                                            float mult, bool full) {
   f32x4 v;
-  if (ra.ts == 1 && r0 + 3 < len) {
+  if (full && ra.ts == 1) {
     const float4 t = b.ldf4((int)(ra.vec(h, r0) - ra.base_row) * 4, 0);
     v = f32x4{t.x, t.y, t.z, t.w} * mult;
   } else {
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const int row = r0 + r;
-      v[r] = row < len ? b.ldf((int)(ra.vec(h, row) - ra.base_row) * 4, 0) * mult : fill;
+      const float x = b.ldf((int)(ra.vec(h, row < len ? row : len - 1) - ra.base_row) * 4, 0) * mult;
+      v[r] = row < len ? x : fill;
     }
   }
   return v;
@@ -78,7 +80,7 @@ struct Rows2Cfg {
   static constexpr bool FITS = LDS_BYTES <= 80 * 1024 && HP % 4 == 0;
 };
 
-template <int HP, int D, int C, int KC, int HB>
+template <int HP, int D, int C, int KC, int HB, int FL>
 __global__ __launch_bounds__(256, 2) void bwd_rows2_kernel(BwdParams prm) {
   using Cfg = Rows2Cfg<HP, D, C, KC>;
   using ET = ETile<C, KC>;
@@ -92,15 +94,16 @@ __global__ __launch_bounds__(256, 2) void bwd_rows2_kernel(BwdParams prm) {
   unsigned char* scal = stW + Cfg::REGION;   // increments of D
 
   const int tid = threadIdx.x;
-  const int w = tid >> 6, lane = tid & 63, g = lane >> 4, n = lane & 15;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63, g = lane >> 4, n = lane & 15;
   const int wl = xcd_remap(blockIdx.x, gridDim.x);
 
   EventBlock eb;
   if (!tile_block(prm.ev, wl, eb)) return;
   const int len = eb.len;
   const int H = prm.H;
-  const bool attn = prm.flags & FST_ATTN_BIAS;
-  const bool act = prm.flags & FST_ACT_BIAS;
+  // FL >= 0: the bias flags fixed at compile time; -1: read at run time.
+  const bool attn = FL >= 0 ? (FL & FST_ATTN_BIAS) != 0 : (prm.flags & FST_ATTN_BIAS) != 0;
+  const bool act = FL >= 0 ? (FL & FST_ACT_BIAS) != 0 : (prm.flags & FST_ACT_BIAS) != 0;
   const bool use_e = attn || act;
   const bool use_b = act && prm.bias;
   const RowAddr ra = row_addr(prm.ev, eb);
@@ -568,7 +571,7 @@ struct Cols2Cfg {
   static constexpr bool FITS = LDS_BYTES <= 80 * 1024 && HP % 4 == 0;
 };
 
-template <int HP, int D, int C, int RC>
+template <int HP, int D, int C, int RC, int FL>
 __global__ __launch_bounds__(256, 2) void bwd_cols2_kernel(BwdParams prm) {
   using Cfg = Cols2Cfg<HP, D, C, RC>;
   using DT = DTiles<D>;
@@ -578,7 +581,7 @@ __global__ __launch_bounds__(256, 2) void bwd_cols2_kernel(BwdParams prm) {
   unsigned char* stW = smem + Cfg::REGION;   // w~.E
 
   const int tid = threadIdx.x;
-  const int w = tid >> 6, lane = tid & 63, g = lane >> 4, n = lane & 15;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63, g = lane >> 4, n = lane & 15;
 
   EventSpec ev = prm.ev;
   ev.blkcum = prm.blkcum_cols;
@@ -586,8 +589,9 @@ __global__ __launch_bounds__(256, 2) void bwd_cols2_kernel(BwdParams prm) {
   if (!tile_block(ev, xcd_remap(blockIdx.x, gridDim.x), eb)) return;
   const int len = eb.len;
   const int H = prm.H;
-  const bool attn = prm.flags & FST_ATTN_BIAS;
-  const bool act = prm.flags & FST_ACT_BIAS;
+  // FL >= 0: the bias flags fixed at compile time; -1: read at run time.
+  const bool attn = FL >= 0 ? (FL & FST_ATTN_BIAS) != 0 : (prm.flags & FST_ATTN_BIAS) != 0;
+  const bool act = FL >= 0 ? (FL & FST_ACT_BIAS) != 0 : (prm.flags & FST_ACT_BIAS) != 0;
   const bool use_e = attn || act;
   const RowAddr ra = row_addr(ev, eb);
   const int k0 = eb.blk * 16;
@@ -669,8 +673,8 @@ __global__ __launch_bounds__(256, 2) void bwd_cols2_kernel(BwdParams prm) {
         load_kfrag<D>(qr[hl][s], qbuf, voff, soff);
         load_kfrag<D>(orw[hl][s], obuf, voff, soff);
         const int r0 = in + 16 * s + 4 * g;
-        lse2[hl][s] = load_rows4(lbuf, ra, h, r0, len, INFINITY, kLog2e);
-        dsv[hl][s] = load_rows4(dbuf, ra, h, r0, len, 0.f, 1.f);
+        lse2[hl][s] = load_rows4(lbuf, ra, h, r0, len, INFINITY, kLog2e, full);
+        dsv[hl][s] = load_rows4(dbuf, ra, h, r0, len, 0.f, 1.f, full);
       }
     }
     if (use_e) {
@@ -822,13 +826,14 @@ int bwd2_launch_t(const BwdParams& prm, int which, hipStream_t stream, int grid)
   } else {
     const int g8 = (grid + 7) & ~7;
     if (which == 0) {
-      auto kern = bwd_rows2_kernel<HP, D, C, P::KC, P::HB>;
+      auto kern = (prm.flags & 3) == 3 ? bwd_rows2_kernel<HP, D, C, P::KC, P::HB, 3>
+                                       : bwd_rows2_kernel<HP, D, C, P::KC, P::HB, -1>;
       constexpr int lds = Rows2Cfg<HP, D, C, P::KC>::LDS_BYTES;
       if (hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, lds) != hipSuccess)
         return FST_ELAUNCH;
       if (grid > 0) hipLaunchKernelGGL(kern, dim3(g8), dim3(256), lds, stream, prm);
     } else {
-      auto kern = bwd_cols2_kernel<HP, D, C, P::RC>;
+      auto kern = (prm.flags & 3) == 3 ? bwd_cols2_kernel<HP, D, C, P::RC, 3> : bwd_cols2_kernel<HP, D, C, P::RC, -1>;
       constexpr int lds = Cols2Cfg<HP, D, C, P::RC>::LDS_BYTES;
       if (hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, lds) != hipSuccess)
         return FST_ELAUNCH;

@@ -195,11 +195,8 @@ template <>
 struct JFrag<bf16, 2> {
   bf16x8 v;
   __device__ __forceinline__ void from_tiles(const f32x4* s) {
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      v[r] = (bf16)s[0][r];
-      v[4 + r] = (bf16)s[1][r];
-    }
+    v = __builtin_shufflevector(__builtin_convertvector(s[0], bf16x4), __builtin_convertvector(s[1], bf16x4), 0, 1,
+                                2, 3, 4, 5, 6, 7);
   }
   __device__ __forceinline__ void zero() {
 #pragma unroll
@@ -241,10 +238,7 @@ struct JFrag<bf16, 2> {
 template <>
 struct JFrag<bf16, 1> {
   bf16x4 v;
-  __device__ __forceinline__ void from_tiles(const f32x4* s) {
-#pragma unroll
-    for (int r = 0; r < 4; ++r) v[r] = (bf16)s[0][r];
-  }
+  __device__ __forceinline__ void from_tiles(const f32x4* s) { v = __builtin_convertvector(s[0], bf16x4); }
   __device__ __forceinline__ void zero() {
 #pragma unroll
     for (int t = 0; t < 4; ++t) v[t] = (bf16)0.f;

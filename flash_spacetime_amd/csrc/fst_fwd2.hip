@@ -42,7 +42,7 @@ struct Fwd2Cfg {
 
 constexpr float kRescaleLog2 = 8.f;
 
-template <int HP, int D, int C, int KC>
+template <int HP, int D, int C, int KC, int FL>
 __global__ __launch_bounds__(256, 2) void fwd2_kernel(FwdParams prm) {
   using Cfg = Fwd2Cfg<HP, D, C, KC>;
   using ET = ETile<C, KC>;
@@ -54,14 +54,15 @@ __global__ __launch_bounds__(256, 2) void fwd2_kernel(FwdParams prm) {
   unsigned char* scal = stage + Cfg::STAGE_BYTES;
 
   const int tid = threadIdx.x;
-  const int w = tid >> 6, lane = tid & 63, g = lane >> 4, n = lane & 15;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63, g = lane >> 4, n = lane & 15;
 
   EventBlock eb;
   if (!tile_block(prm.ev, xcd_remap(blockIdx.x, gridDim.x), eb)) return;
   const int len = eb.len;
   const int H = prm.H;
-  const bool attn = prm.flags & FST_ATTN_BIAS;
-  const bool act = prm.flags & FST_ACT_BIAS;
+  // FL >= 0: the bias flags fixed at compile time; -1: read at run time.
+  const bool attn = FL >= 0 ? (FL & FST_ATTN_BIAS) != 0 : (prm.flags & FST_ATTN_BIAS) != 0;
+  const bool act = FL >= 0 ? (FL & FST_ACT_BIAS) != 0 : (prm.flags & FST_ACT_BIAS) != 0;
   const bool use_e = attn || act;
   const RowAddr ra = row_addr(prm.ev, eb);
   const int i0 = eb.blk * 16;
@@ -424,7 +425,9 @@ int fwd2_launch_t(const FwdParams& prm, hipStream_t stream, int grid) {
   if constexpr (!P::OK) {
     return FST_EUNSUPPORTED;
   } else {
-    auto kern = fwd2_kernel<HP, D, C, P::KC>;
+    // Both bias flags (the operators' default) run an instance with the flags
+    // fixed at compile time; other combinations read them at run time.
+    auto kern = (prm.flags & 3) == 3 ? fwd2_kernel<HP, D, C, P::KC, 3> : fwd2_kernel<HP, D, C, P::KC, -1>;
     if (hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, P::Cfg::LDS_BYTES) !=
         hipSuccess)
       return FST_ELAUNCH;

@@ -83,6 +83,8 @@ __device__ __forceinline__ void group_gather(float x, float out[4]) {
   out[3] = __uint_as_float(c[1]);
 }
 
+__device__ __forceinline__ bf16x4 pack4(const f32x4& c) { return __builtin_convertvector(c, bf16x4); }
+
 // The four embedding slots of lane group g in channel step ct for one pair
 // angle x (unit angle): {sin x fa, sin x fb, cos x fa, cos x fb}, fa and fb
 // the lane's frequencies times 1024 / (2 pi) (revolutions per unit angle).
@@ -93,12 +95,9 @@ __device__ __forceinline__ bf16x4 embed_slots(float x, float fa, float fb) {
   float pa = x * fa, pb = x * fb;
   if constexpr (RA) pa = __builtin_amdgcn_fractf(pa);
   if constexpr (RB) pb = __builtin_amdgcn_fractf(pb);
-  bf16x4 e;
-  e[0] = (bf16)__builtin_amdgcn_sinf(pa);
-  e[1] = (bf16)__builtin_amdgcn_sinf(pb);
-  e[2] = (bf16)__builtin_amdgcn_cosf(pa);
-  e[3] = (bf16)__builtin_amdgcn_cosf(pb);
-  return e;
+  const f32x4 e{__builtin_amdgcn_sinf(pa), __builtin_amdgcn_sinf(pb), __builtin_amdgcn_cosf(pa),
+                 __builtin_amdgcn_cosf(pb)};
+  return __builtin_convertvector(e, bf16x4);
 }
 
 template <int C>
@@ -115,12 +114,6 @@ __device__ __forceinline__ bf16x4 ident_x16(int g, int n) {
   return id;
 }
 
-__device__ __forceinline__ bf16x4 pack4(const f32x4& c) {
-  bf16x4 o;
-#pragma unroll
-  for (int r = 0; r < 4; ++r) o[r] = (bf16)c[r];
-  return o;
-}
 
 // Transpose of a 16x16 tile held as an A operand (lane n = row m, slots =
 // columns 4g .. 4g+3): lane n now holds column n, slots = rows 4g .. 4g+3.
