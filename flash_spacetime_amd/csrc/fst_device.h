@@ -63,6 +63,18 @@ __device__ __forceinline__ f32x4 mfma_f32(float a, float b, f32x4 c) {
 
 __device__ __forceinline__ f32x4 zero4() { return f32x4{0.f, 0.f, 0.f, 0.f}; }
 
+// fp32 quad -> bf16 quad (round to nearest even) as two v_cvt_pk_bf16_f32.
+// Converted pairwise through 32-bit words: converting the quad directly is
+// split into single conversions plus permutes by the instruction selector
+// when the result feeds an MFMA operand.
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef unsigned u32x2v __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ bf16x4 pack4(const f32x4& c) {
+  const unsigned lo = __builtin_bit_cast(unsigned, __builtin_convertvector(f32x2{c[0], c[1]}, bf16x2));
+  const unsigned hi = __builtin_bit_cast(unsigned, __builtin_convertvector(f32x2{c[2], c[3]}, bf16x2));
+  return __builtin_bit_cast(bf16x4, u32x2v{lo, hi});
+}
+
 // ---------------------------------------------------------------------------
 // Cross-lane reductions over the four lane groups (lanes n, n+16, n+32,
 // n+48) with the gfx950 row-swap instructions; every lane ends with the
@@ -195,8 +207,7 @@ template <>
 struct JFrag<bf16, 2> {
   bf16x8 v;
   __device__ __forceinline__ void from_tiles(const f32x4* s) {
-    v = __builtin_shufflevector(__builtin_convertvector(s[0], bf16x4), __builtin_convertvector(s[1], bf16x4), 0, 1,
-                                2, 3, 4, 5, 6, 7);
+    v = __builtin_shufflevector(pack4(s[0]), pack4(s[1]), 0, 1, 2, 3, 4, 5, 6, 7);
   }
   __device__ __forceinline__ void zero() {
 #pragma unroll
@@ -238,7 +249,7 @@ struct JFrag<bf16, 2> {
 template <>
 struct JFrag<bf16, 1> {
   bf16x4 v;
-  __device__ __forceinline__ void from_tiles(const f32x4* s) { v = __builtin_convertvector(s[0], bf16x4); }
+  __device__ __forceinline__ void from_tiles(const f32x4* s) { v = pack4(s[0]); }
   __device__ __forceinline__ void zero() {
 #pragma unroll
     for (int t = 0; t < 4; ++t) v[t] = (bf16)0.f;

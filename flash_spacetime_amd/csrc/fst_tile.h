@@ -83,7 +83,6 @@ __device__ __forceinline__ void group_gather(float x, float out[4]) {
   out[3] = __uint_as_float(c[1]);
 }
 
-__device__ __forceinline__ bf16x4 pack4(const f32x4& c) { return __builtin_convertvector(c, bf16x4); }
 
 // The four embedding slots of lane group g in channel step ct for one pair
 // angle x (unit angle): {sin x fa, sin x fb, cos x fa, cos x fb}, fa and fb
@@ -97,7 +96,7 @@ __device__ __forceinline__ bf16x4 embed_slots(float x, float fa, float fb) {
   if constexpr (RB) pb = __builtin_amdgcn_fractf(pb);
   const f32x4 e{__builtin_amdgcn_sinf(pa), __builtin_amdgcn_sinf(pb), __builtin_amdgcn_cosf(pa),
                  __builtin_amdgcn_cosf(pb)};
-  return __builtin_convertvector(e, bf16x4);
+  return pack4(e);
 }
 
 template <int C>
