@@ -232,12 +232,17 @@ __global__ __launch_bounds__(256, 2) void bwd_rows2_kernel(BwdParams prm) {
         load_kfrag<D>(vf[hl][s], vbuf, voff, soff);
       }
     }
+  };
+  // Key positions run one chunk further ahead: they are needed first thing
+  // in a chunk.
+  auto issue_pos = [&](int jn) __attribute__((always_inline)) {
     if (use_e) {
 #pragma unroll
       for (int s = 0; s < NS; ++s) pj[s] = pbuf.ldf4(min(jn + 16 * s + n, last) * 16, 0);
     }
   };
   issue(0);
+  issue_pos(0);
 
   auto chunk = [&](int j0, auto tail_tag) __attribute__((always_inline)) {
     constexpr bool TAIL = decltype(tail_tag)::value;
@@ -246,6 +251,7 @@ __global__ __launch_bounds__(256, 2) void bwd_rows2_kernel(BwdParams prm) {
       float xg[NS][4];
 #pragma unroll
       for (int s = 0; s < NS; ++s) group_gather(pair_angle_unit(pos_i, pj[s]), xg[s]);
+      if (j0 + KC < len) issue_pos(j0 + KC);
 #pragma unroll
       for (int r = 0; r < 4; ++r)
 #pragma unroll
@@ -677,12 +683,31 @@ __global__ __launch_bounds__(256, 2) void bwd_cols2_kernel(BwdParams prm) {
         dsv[hl][s] = load_rows4(dbuf, ra, h, r0, len, 0.f, 1.f, full);
       }
     }
+  };
+  // Row positions and the u / w~ rows of the row-owner part run one chunk
+  // further ahead: they are needed first thing in a chunk.
+  bf16x4 ur[RGW][4][NCT], wr[RGW][4][NCT];
+  auto issue_rows = [&](int in) __attribute__((always_inline)) {
     if (use_e) {
 #pragma unroll
-      for (int q2 = 0; q2 < RGW; ++q2) prow[q2] = pbuf.ldf4(min(in + 4 * (RGW * w + q2) + g, last) * 16, 0);
+      for (int q2 = 0; q2 < RGW; ++q2) {
+        const int rg = RGW * w + q2;
+        prow[q2] = pbuf.ldf4(min(in + 4 * rg + g, last) * 16, 0);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int row = min(in + 4 * rg + r, last);
+          const int co = (int)(ra.off(n, row, C) - cbase) * 2 + 8 * g;
+#pragma unroll
+          for (int ct = 0; ct < NCT; ++ct) {
+            if (attn) ur[q2][r][ct] = ubuf.ld64(co + 32 * ct, 0);
+            if (act) wr[q2][r][ct] = wbuf.ld64(co + 32 * ct, 0);
+          }
+        }
+      }
     }
   };
   issue(0);
+  issue_rows(0);
 
   auto chunk = [&](int i0c, auto tail_tag) __attribute__((always_inline)) {
     constexpr bool TAIL = decltype(tail_tag)::value;
@@ -696,16 +721,14 @@ __global__ __launch_bounds__(256, 2) void bwd_cols2_kernel(BwdParams prm) {
         f32x4 ue[4], we[4];
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-          const int row = min(i0c + 4 * rg + r, last);
           bf16x4 ef[NCT];
 #pragma unroll
           for (int ct = 0; ct < NCT; ++ct) ef[ct] = embed_step<C>(xg[r], fa[ct], fb[ct], ct);
-          const int co = (int)(ra.off(n, row, C) - cbase) * 2 + 8 * g;
           ue[r] = we[r] = zero4();
 #pragma unroll
           for (int ct = 0; ct < NCT; ++ct) {
-            if (attn) ue[r] = mfma_x16(ubuf.ld64(co + 32 * ct, 0), ef[ct], ue[r]);
-            if (act) we[r] = mfma_x16(wbuf.ld64(co + 32 * ct, 0), ef[ct], we[r]);
+            if (attn) ue[r] = mfma_x16(ur[q2][r][ct], ef[ct], ue[r]);
+            if (act) we[r] = mfma_x16(wr[q2][r][ct], ef[ct], we[r]);
           }
         }
         // lane (g, key n) holds heads 4g + e of rows r: regroup by head.
@@ -719,6 +742,7 @@ __global__ __launch_bounds__(256, 2) void bwd_cols2_kernel(BwdParams prm) {
         }
       }
     }
+    if (i0c + RC < len) issue_rows(i0c + RC);
     __syncthreads();  // u.E, w~.E staged
 
     // ---- head-owner: P, dS, dV^T += dO^T P, dK^T += Qt^T dS ----

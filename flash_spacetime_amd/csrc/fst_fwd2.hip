@@ -180,12 +180,17 @@ __global__ __launch_bounds__(256, 2) void fwd2_kernel(FwdParams prm) {
         }
       }
     }
+  };
+  // Key positions run one chunk further ahead: they are needed first thing
+  // in a chunk.
+  auto issue_pos = [&](int jn) __attribute__((always_inline)) {
     if (use_e) {
 #pragma unroll
       for (int s = 0; s < NS; ++s) pj[s] = pbuf.ldf4(min(jn + 16 * s + n, last) * 16, 0);
     }
   };
   issue(0);
+  issue_pos(0);
 
   auto chunk = [&](int j0, auto tail_tag) __attribute__((always_inline)) {
     constexpr bool TAIL = decltype(tail_tag)::value;
@@ -195,6 +200,7 @@ __global__ __launch_bounds__(256, 2) void fwd2_kernel(FwdParams prm) {
       float xg[NS][4];
 #pragma unroll
       for (int s = 0; s < NS; ++s) group_gather(pair_angle_unit(pos_i, pj[s]), xg[s]);
+      if (j0 + KC < len) issue_pos(j0 + KC);
 #pragma unroll
       for (int r = 0; r < 4; ++r)
 #pragma unroll
