@@ -216,14 +216,14 @@ __global__ __launch_bounds__(256, 2) void bwd_rows2_kernel(BwdParams prm) {
   const Buf pbuf(prm.ev.pos4 + ra.pos_base, (unsigned)len * 16u);
   int kvo[HW];
 #pragma unroll
-  for (int hl = 0; hl < HW; ++hl) kvo[hl] = (int)((w * HW + hl) * ra.hs * D * 2) + n * rowb + kfrag_goff<D>(g);
+  for (int hl = 0; hl < HW; ++hl)
+    kvo[hl] = (int)(min(w * HW + hl, H - 1) * ra.hs * D * 2) + n * rowb + kfrag_goff<D>(g);
   KFrag<bf16, D> kf[HW][NS], vf[HW][NS];
   float4 pj[NS];
   auto issue = [&](int jn) __attribute__((always_inline)) {
     const bool full = jn + KC <= len;
 #pragma unroll
     for (int hl = 0; hl < HW; ++hl) {
-      if (w * HW + hl >= H) continue;
 #pragma unroll
       for (int s = 0; s < NS; ++s) {
         const int voff = full ? kvo[hl] + 16 * s * rowb : kvo[hl] + (min(jn + 16 * s + n, last) - n) * rowb;
@@ -292,7 +292,7 @@ __global__ __launch_bounds__(256, 2) void bwd_rows2_kernel(BwdParams prm) {
         const int h = w * HW + hl;
 #pragma unroll
         for (int s = 0; s < NS; ++s) {
-          if (hl >= HW || h >= H) {
+          if (hl >= HW) {
             S[b][s] = dP[b][s] = zero4();
             continue;
           }
@@ -348,7 +348,7 @@ __global__ __launch_bounds__(256, 2) void bwd_rows2_kernel(BwdParams prm) {
 #pragma unroll
       for (int b = 0; b < NB; ++b) {
         const int hl = hb + b;
-        if (hl >= HW || w * HW + hl >= H) continue;
+        if (hl >= HW) continue;
 #pragma unroll
         for (int q = 0; q < NQ; ++q) {
           JFrag<bf16, NS> kt;
@@ -368,7 +368,7 @@ __global__ __launch_bounds__(256, 2) void bwd_rows2_kernel(BwdParams prm) {
         for (int b = 0; b < NB; ++b) {
           const int hl = hb + b;
           const int h = w * HW + hl;
-          if (hl >= HW || h >= H) continue;
+          if (hl >= HW) continue;
 #pragma unroll
           for (int s = 0; s < NS; ++s) {
             bf16x4 pv, dv;
@@ -621,14 +621,10 @@ __global__ __launch_bounds__(256, 2) void bwd_cols2_kernel(BwdParams prm) {
   const bf16* __restrict__ vg = reinterpret_cast<const bf16*>(prm.v);
 #pragma unroll
   for (int hl = 0; hl < HW; ++hl) {
-    const int h = w * HW + hl;
-    if (h < H) {
-      kf[hl].load(kg + ra.off(h, kc, D), g);
-      vf[hl].load(vg + ra.off(h, kc, D), g);
-    } else {
-      kf[hl].zero();
-      vf[hl].zero();
-    }
+    // Padded heads (h >= H) compute on head H-1's data and are never stored.
+    const int hq = min(w * HW + hl, H - 1);
+    kf[hl].load(kg + ra.off(hq, kc, D), g);
+    vf[hl].load(vg + ra.off(hq, kc, D), g);
 #pragma unroll
     for (int q = 0; q < NQ; ++q) dK[hl][q] = dV[hl][q] = zero4();
   }
@@ -661,7 +657,8 @@ __global__ __launch_bounds__(256, 2) void bwd_cols2_kernel(BwdParams prm) {
   const Buf pbuf(ev.pos4 + ra.pos_base, (unsigned)len * 16u);
   int qvo[HW];
 #pragma unroll
-  for (int hl = 0; hl < HW; ++hl) qvo[hl] = (int)((w * HW + hl) * ra.hs * D * 2) + n * rowb + kfrag_goff<D>(g);
+  for (int hl = 0; hl < HW; ++hl)
+    qvo[hl] = (int)(min(w * HW + hl, H - 1) * ra.hs * D * 2) + n * rowb + kfrag_goff<D>(g);
 
   KFrag<bf16, D> qr[HW][NS], orw[HW][NS];
   f32x4 lse2[HW][NS], dsv[HW][NS];
@@ -670,8 +667,7 @@ __global__ __launch_bounds__(256, 2) void bwd_cols2_kernel(BwdParams prm) {
     const bool full = in + RC <= len;
 #pragma unroll
     for (int hl = 0; hl < HW; ++hl) {
-      const int h = w * HW + hl;
-      if (h >= H) continue;
+      const int h = min(w * HW + hl, H - 1);
 #pragma unroll
       for (int s = 0; s < NS; ++s) {
         const int voff = full ? qvo[hl] + 16 * s * rowb : qvo[hl] + (min(in + 16 * s + n, last) - n) * rowb;
@@ -752,10 +748,6 @@ __global__ __launch_bounds__(256, 2) void bwd_cols2_kernel(BwdParams prm) {
       const int h = w * HW + hl;
 #pragma unroll
       for (int s = 0; s < NS; ++s) {
-        if (h >= H) {
-          S[hl][s] = dP[hl][s] = zero4();
-          continue;
-        }
         const int so = (((4 * s + g) * HP + h) * 16 + n) * 16;
         const f32x4 ui = attn ? *reinterpret_cast<const f32x4*>(stU + so) : zero4();
         const f32x4 wi = act ? *reinterpret_cast<const f32x4*>(stW + so) : zero4();
@@ -780,7 +772,6 @@ __global__ __launch_bounds__(256, 2) void bwd_cols2_kernel(BwdParams prm) {
     }
 #pragma unroll
     for (int hl = 0; hl < HW; ++hl) {
-      if (w * HW + hl >= H) continue;
 #pragma unroll
       for (int q = 0; q < NQ; ++q) {
         JFrag<bf16, NS> ot, qt;

@@ -86,9 +86,11 @@ __global__ __launch_bounds__(256, 2) void fwd2_kernel(FwdParams prm) {
   float mref[HW];
 #pragma unroll
   for (int hl = 0; hl < HW; ++hl) {
-    const int h = w * HW + hl;
-    if (h < H && row_ok)
-      qf[hl].load_scaled(qg + ra.off(h, my_row, D), g, prm.scale);
+    // Padded heads (h >= H) compute on head H-1's data and are never stored,
+    // so the chunk loop needs no per-head branches.
+    const int hq = min(w * HW + hl, H - 1);
+    if (row_ok)
+      qf[hl].load_scaled(qg + ra.off(hq, my_row, D), g, prm.scale);
     else
       qf[hl].zero();
 #pragma unroll
@@ -156,7 +158,7 @@ __global__ __launch_bounds__(256, 2) void fwd2_kernel(FwdParams prm) {
   int kvo[HW];  // lane offset of head hl, key n (bytes)
 #pragma unroll
   for (int hl = 0; hl < HW; ++hl)
-    kvo[hl] = (int)((w * HW + hl) * ra.hs * D * 2) + n * rowb + kfrag_goff<D>(g);
+    kvo[hl] = (int)(min(w * HW + hl, H - 1) * ra.hs * D * 2) + n * rowb + kfrag_goff<D>(g);
 
   // Operands of the chunk in flight: K, V rows of the wave's heads and the
   // key positions. Loads for chunk j0 + KC are issued as soon as the
@@ -167,7 +169,6 @@ __global__ __launch_bounds__(256, 2) void fwd2_kernel(FwdParams prm) {
     const bool full = jn + KC <= len;
 #pragma unroll
     for (int hl = 0; hl < HW; ++hl) {
-      if (w * HW + hl >= H) continue;
 #pragma unroll
       for (int s = 0; s < NS; ++s) {
         if (full) {
@@ -226,11 +227,6 @@ __global__ __launch_bounds__(256, 2) void fwd2_kernel(FwdParams prm) {
     f32x4 S[HW][NS];
 #pragma unroll
     for (int hl = 0; hl < HW; ++hl) {
-      if (w * HW + hl >= H) {
-#pragma unroll
-        for (int s = 0; s < NS; ++s) S[hl][s] = zero4();
-        continue;
-      }
 #pragma unroll
       for (int s = 0; s < NS; ++s) {
         const f32x4 init =
@@ -243,6 +239,9 @@ __global__ __launch_bounds__(256, 2) void fwd2_kernel(FwdParams prm) {
         }
       }
     }
+    // A row's reference m moves only when some key of the chunk exceeds it by
+    // more than 2^8; each lane tests its own keys, and only then is the row
+    // maximum formed across the lane groups.
     float mx[HW], alpha[HW];
     bool need_any = false;
 #pragma unroll
@@ -252,17 +251,14 @@ __global__ __launch_bounds__(256, 2) void fwd2_kernel(FwdParams prm) {
       for (int s = 0; s < NS; ++s)
 #pragma unroll
         for (int r = 0; r < 4; ++r) m = fmaxf(m, S[hl][s][r]);
-      mx[hl] = m;
-    }
-#pragma unroll
-    for (int hl = 0; hl < HW; ++hl) {
-      mx[hl] = group_allmax(mx[hl]) * kLog2e;
+      mx[hl] = m * kLog2e;
       alpha[hl] = 1.f;
-      need_any |= (w * HW + hl < H) && mx[hl] > mref[hl] + kRescaleLog2;
+      need_any |= mx[hl] > mref[hl] + kRescaleLog2;
     }
     if (__builtin_amdgcn_ballot_w64(need_any)) {
 #pragma unroll
       for (int hl = 0; hl < HW; ++hl) {
+        mx[hl] = group_allmax(mx[hl]);
         const float mnew = mx[hl] > mref[hl] + kRescaleLog2 ? mx[hl] : mref[hl];
         alpha[hl] = exp2f_fast(mref[hl] - mnew);
         mref[hl] = mnew;
@@ -283,7 +279,6 @@ __global__ __launch_bounds__(256, 2) void fwd2_kernel(FwdParams prm) {
     }
 #pragma unroll
     for (int hl = 0; hl < HW; ++hl) {
-      if (w * HW + hl >= H) continue;
       lacc[hl] = mma_j(ones, pf[hl], lacc[hl]);
 #pragma unroll
       for (int q = 0; q < NQ; ++q) {
@@ -300,7 +295,6 @@ __global__ __launch_bounds__(256, 2) void fwd2_kernel(FwdParams prm) {
 #pragma unroll
       for (int hl = 0; hl < HW; ++hl) {
         const int h = w * HW + hl;
-        if (h >= H) continue;
 #pragma unroll
         for (int s = 0; s < NS; ++s) {
           bf16x4 pv;
