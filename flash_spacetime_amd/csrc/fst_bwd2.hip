@@ -21,8 +21,10 @@
 // accumulator equals its value for D = N / Z over all keys, the same N and Z
 // that give sigma = N - D Z; a fully peaked row (all mass on one key) has
 // D_t = dP of that key from its chunk on, so its dS vanishes as in the
-// two-pass form (backward.py:371-407). It writes qt, u, w~ and D - dob for
-// the cols kernel and a per-tile dW / db partial.
+// two-pass form (backward.py:371-407). The row constant dob never enters a
+// pair: with dP~ = dP - dob, D - dob = sum P dP~ / sum P and dS = P (dP~ -
+// (D - dob)), so the kernel forms D - dob directly. It writes qt, u, w~ and
+// D - dob for the cols kernel and a per-tile dW / db partial.
 //
 // Cols kernel (one 16-key tile per workgroup, rows streamed): S = Qt K^T and
 // dP = dO V^T with the keys on the lanes, dV^T += dO^T P and dK^T += Qt^T dS
@@ -105,7 +107,6 @@ __global__ __launch_bounds__(256, 2) void bwd_rows2_kernel(BwdParams prm) {
   const bool attn = FL >= 0 ? (FL & FST_ATTN_BIAS) != 0 : (prm.flags & FST_ATTN_BIAS) != 0;
   const bool act = FL >= 0 ? (FL & FST_ACT_BIAS) != 0 : (prm.flags & FST_ACT_BIAS) != 0;
   const bool use_e = attn || act;
-  const bool use_b = act && prm.bias;
   const RowAddr ra = row_addr(prm.ev, eb);
   const int i0 = eb.blk * 16;
   const int last = len - 1;
@@ -133,7 +134,7 @@ __global__ __launch_bounds__(256, 2) void bwd_rows2_kernel(BwdParams prm) {
   const bool row_ok = my_row < len;
   KFrag<bf16, D> qf[HW], dof[HW];
   f32x4 dQ[HW][NQ], A2[HW][NQ];
-  float lse2[HW], dobv[HW], Nn[HW], Zz[HW], Dc[HW];
+  float lse2[HW], Nn[HW], Zz[HW], Dc[HW];  // Dc: the running D - dob
   bf16* qtg = reinterpret_cast<bf16*>(prm.qt);
 #pragma unroll
   for (int hl = 0; hl < HW; ++hl) {
@@ -154,18 +155,6 @@ __global__ __launch_bounds__(256, 2) void bwd_rows2_kernel(BwdParams prm) {
     }
     // Invalid rows get lse = +inf, so their P (and dS) are exactly zero.
     lse2[hl] = ok ? prm.lse[ra.vec(h, my_row)] * kLog2e : INFINITY;
-    float pb = 0.f;
-    if (use_b && ok) {
-#pragma unroll
-      for (int t = 0; t < KFrag<bf16, D>::N32; ++t)
-#pragma unroll
-        for (int e = 0; e < 8; ++e) pb = __builtin_fmaf((float)dof[hl].x32[t][e], prm.bias[32 * t + 8 * g + e], pb);
-#pragma unroll
-      for (int t = 0; t < KFrag<bf16, D>::N16; ++t)
-#pragma unroll
-        for (int e = 0; e < 4; ++e) pb = __builtin_fmaf((float)dof[hl].x16[t][e], prm.bias[16 * t + 4 * g + e], pb);
-    }
-    dobv[hl] = group_allsum(pb);
     Nn[hl] = Zz[hl] = Dc[hl] = 0.f;
 #pragma unroll
     for (int q = 0; q < NQ; ++q) dQ[hl][q] = A2[hl][q] = zero4();
@@ -313,10 +302,8 @@ __global__ __launch_bounds__(256, 2) void bwd_rows2_kernel(BwdParams prm) {
           for (int r = 0; r < 4; ++r) {
             float p = exp2f_fast(__builtin_fmaf(S[b][s][r], kLog2e, -lse2[hl]));
             if constexpr (TAIL) p = (j0 + 16 * s + 4 * g + r < len) ? p : 0.f;
-            const float dp = dP[b][s][r] + dobv[hl];
             S[b][s][r] = p;
-            dP[b][s][r] = dp;
-            a = __builtin_fmaf(p, dp, a);
+            a = __builtin_fmaf(p, dP[b][s][r], a);
             z += p;
           }
         nt[b] = a;
@@ -329,7 +316,7 @@ __global__ __launch_bounds__(256, 2) void bwd_rows2_kernel(BwdParams prm) {
         if (hl >= HW) continue;
         Nn[hl] += group_allsum(nt[b]);
         Zz[hl] += group_allsum(zt[b]);
-        const float dn = Zz[hl] > 0.f ? Nn[hl] / Zz[hl] : 0.f;
+        const float dn = Zz[hl] > 0.f ? Nn[hl] * __builtin_amdgcn_rcpf(Zz[hl]) : 0.f;
         dD[b] = dn - Dc[hl];
         Dc[hl] = dn;
       }
@@ -393,24 +380,21 @@ __global__ __launch_bounds__(256, 2) void bwd_rows2_kernel(BwdParams prm) {
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const int il = 4 * w + r;
-        const bool hv = n < H;
-        const float dd = hv ? *reinterpret_cast<const float*>(scal + scal_off(il, n)) : 0.f;
+        // Lanes of padded heads (n >= H) read some other slot of the row:
+        // finite values whose columns of H and G are never used.
+        const int hn = n < HP ? n : HP - 1;
+        const float dd = *reinterpret_cast<const float*>(scal + scal_off(il, n));
         JFrag<bf16, NS> pr, dr;
-        if (hv) {
 #pragma unroll
-          for (int s = 0; s < NS; ++s) {
-            const int so = hslot_off<HP>(2 * s + (g >> 1), il, n) + 8 * (g & 1);
-            const bf16x4 pv = *reinterpret_cast<const bf16x4*>(stU + so);
-            const bf16x4 dv = *reinterpret_cast<const bf16x4*>(stW + so);
+        for (int s = 0; s < NS; ++s) {
+          const int so = hslot_off<HP>(2 * s + (g >> 1), il, hn) + 8 * (g & 1);
+          const bf16x4 pv = *reinterpret_cast<const bf16x4*>(stU + so);
+          const bf16x4 dv = *reinterpret_cast<const bf16x4*>(stW + so);
 #pragma unroll
-            for (int e = 0; e < 4; ++e) {
-              pr.v[4 * s + e] = pv[e];
-              dr.v[4 * s + e] = dv[e];
-            }
+          for (int e = 0; e < 4; ++e) {
+            pr.v[4 * s + e] = pv[e];
+            dr.v[4 * s + e] = dv[e];
           }
-        } else {
-          pr.zero();
-          dr.zero();
         }
 #pragma unroll
         for (int ct = 0; ct < NCT; ++ct) {
@@ -440,7 +424,7 @@ __global__ __launch_bounds__(256, 2) void bwd_rows2_kernel(BwdParams prm) {
     sig[hl] = Nn[hl] - Dc[hl] * Zz[hl];
     const int h = w * HW + hl;
     if (g == 0 && row_ok && h < H) {
-      prm.dsum[ra.vec(h, my_row)] = Dc[hl] - dobv[hl];  // the cols kernel's dS = P (dP~ - (D - dob))
+      prm.dsum[ra.vec(h, my_row)] = Dc[hl];  // D - dob: the cols kernel's dS = P (dP~ - (D - dob))
       if (prm.rowsum) prm.rowsum[ra.vec(h, my_row)] = sig[hl];
     }
   }
@@ -572,7 +556,7 @@ struct Cols2Cfg {
   static constexpr int HW = HP / 4, NS = RC / 16, NCT = C / 16;
   static constexpr int RG = RC / 4;     // row groups per chunk
   static constexpr int RGW = RC / 16;   // row groups per row-owner wave
-  static constexpr int REGION = RG * HP * 16 * 16;  // one fp32 term: [row group][head][key] x 4 rows
+  static constexpr int REGION = RG * 16 * 16 * 16;  // one fp32 term: [row group][16 heads][key] x 4 rows
   static constexpr int LDS_BYTES = 2 * REGION;
   static constexpr bool FITS = LDS_BYTES <= 80 * 1024 && HP % 4 == 0;
 };
@@ -730,9 +714,7 @@ __global__ __launch_bounds__(256, 2) void bwd_cols2_kernel(BwdParams prm) {
         // lane (g, key n) holds heads 4g + e of rows r: regroup by head.
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-          const int h = 4 * g + e;
-          if (h >= HP) continue;
-          const int so = ((rg * HP + h) * 16 + n) * 16;
+          const int so = ((rg * 16 + 4 * g + e) * 16 + n) * 16;
           if (attn) *reinterpret_cast<f32x4*>(stU + so) = f32x4{ue[0][e], ue[1][e], ue[2][e], ue[3][e]};
           if (act) *reinterpret_cast<f32x4*>(stW + so) = f32x4{we[0][e], we[1][e], we[2][e], we[3][e]};
         }
@@ -748,7 +730,7 @@ __global__ __launch_bounds__(256, 2) void bwd_cols2_kernel(BwdParams prm) {
       const int h = w * HW + hl;
 #pragma unroll
       for (int s = 0; s < NS; ++s) {
-        const int so = (((4 * s + g) * HP + h) * 16 + n) * 16;
+        const int so = (((4 * s + g) * 16 + h) * 16 + n) * 16;
         const f32x4 ui = attn ? *reinterpret_cast<const f32x4*>(stU + so) : zero4();
         const f32x4 wi = act ? *reinterpret_cast<const f32x4*>(stW + so) : zero4();
         S[hl][s] = mma_k<D>(qr[hl][s], kf[hl], ui);

@@ -313,18 +313,17 @@ __global__ __launch_bounds__(256, 2) void fwd2_kernel(FwdParams prm) {
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const int il = 4 * w + r;
-        const float alpha = n < H ? *reinterpret_cast<const float*>(scal + scal_off(il, n)) : 1.f;
+        // Lanes of padded heads (n >= H) read slots nobody wrote this chunk:
+        // their columns of A are never used, and alpha is taken as 1 there.
+        const float al = *reinterpret_cast<const float*>(scal + scal_off(il, n));
+        const float alpha = n < H ? al : 1.f;
         JFrag<bf16, NS> pr;
-        if (n < H) {
 #pragma unroll
-          for (int s = 0; s < NS; ++s) {
-            const bf16x4 pv =
-                *reinterpret_cast<const bf16x4*>(stage + stage_off(2 * s + (g >> 1), il, n) + 8 * (g & 1));
+        for (int s = 0; s < NS; ++s) {
+          const bf16x4 pv =
+              *reinterpret_cast<const bf16x4*>(stage + stage_off(2 * s + (g >> 1), il, n) + 8 * (g & 1));
 #pragma unroll
-            for (int e = 0; e < 4; ++e) pr.v[4 * s + e] = pv[e];
-          }
-        } else {
-          pr.zero();
+          for (int e = 0; e < 4; ++e) pr.v[4 * s + e] = pv[e];
         }
         if (__builtin_amdgcn_ballot_w64(alpha != 1.f)) {
 #pragma unroll
