@@ -44,27 +44,6 @@
 
 namespace fst {
 
-// Four consecutive rows' values of a [rows, H] fp32 vector, times mult.
-// `full` (uniform) says all four rows lie in the event: then adjacent rows
-// (padded layout) take one 16-byte load; otherwise rows past the event give
-// `fill` and rows are loaded one by one.
-__device__ __forceinline__ f32x4 load_rows4(const Buf& b, const RowAddr& ra, int h, int r0, int len, float fill,
-                                            float mult, bool full) {
-  f32x4 v;
-  if (full && ra.ts == 1) {
-    const float4 t = b.ldf4((int)(ra.vec(h, r0) - ra.base_row) * 4, 0);
-    v = f32x4{t.x, t.y, t.z, t.w} * mult;
-  } else {
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int row = r0 + r;
-      const float x = b.ldf((int)(ra.vec(h, row < len ? row : len - 1) - ra.base_row) * 4, 0) * mult;
-      v[r] = row < len ? x : fill;
-    }
-  }
-  return v;
-}
-
 // ---------------------------------------------------------------------------
 // Rows kernel.
 // ---------------------------------------------------------------------------
@@ -557,7 +536,8 @@ struct Cols2Cfg {
   static constexpr int RG = RC / 4;     // row groups per chunk
   static constexpr int RGW = RC / 16;   // row groups per row-owner wave
   static constexpr int REGION = RG * 16 * 16 * 16;  // one fp32 term: [row group][16 heads][key] x 4 rows
-  static constexpr int LDS_BYTES = 2 * REGION;
+  static constexpr int SCAL_BYTES = 2 * RC * 16 * 4;  // lse * log2(e) and D - dob: [term][head][row]
+  static constexpr int LDS_BYTES = 2 * REGION + SCAL_BYTES;
   static constexpr bool FITS = LDS_BYTES <= 80 * 1024 && HP % 4 == 0;
 };
 
@@ -569,6 +549,7 @@ __global__ __launch_bounds__(256, 2) void bwd_cols2_kernel(BwdParams prm) {
   extern __shared__ __align__(16) unsigned char smem[];
   unsigned char* stU = smem;                 // u.E
   unsigned char* stW = smem + Cfg::REGION;   // w~.E
+  float* rsc = reinterpret_cast<float*>(smem + 2 * Cfg::REGION);  // per-row scalars of the chunk
 
   const int tid = threadIdx.x;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63, g = lane >> 4, n = lane & 15;
@@ -645,7 +626,14 @@ __global__ __launch_bounds__(256, 2) void bwd_cols2_kernel(BwdParams prm) {
     qvo[hl] = (int)(min(w * HW + hl, H - 1) * ra.hs * D * 2) + n * rowb + kfrag_goff<D>(g);
 
   KFrag<bf16, D> qr[HW][NS], orw[HW][NS];
-  f32x4 lse2[HW][NS], dsv[HW][NS];
+  // Per-row scalars (lse * log2 e and D - dob) of the next chunk: thread t
+  // loads item t of the chunk's RC x H values of each (coalesced), and writes
+  // it to LDS at the start of that chunk; the head-owners read four rows at a
+  // time (one 16-byte broadcast read).
+  float sc_l = INFINITY, sc_d = 0.f;
+  const int sc_h = ev.packed ? tid % H : tid / RC;
+  const int sc_r = ev.packed ? tid / H : tid % RC;
+  const bool sc_ok = tid < RC * H;
   float4 prow[RGW];
   auto issue = [&](int in) __attribute__((always_inline)) {
     const bool full = in + RC <= len;
@@ -658,10 +646,14 @@ __global__ __launch_bounds__(256, 2) void bwd_cols2_kernel(BwdParams prm) {
         const int soff = full ? in * rowb : 0;
         load_kfrag<D>(qr[hl][s], qbuf, voff, soff);
         load_kfrag<D>(orw[hl][s], obuf, voff, soff);
-        const int r0 = in + 16 * s + 4 * g;
-        lse2[hl][s] = load_rows4(lbuf, ra, h, r0, len, INFINITY, kLog2e, full);
-        dsv[hl][s] = load_rows4(dbuf, ra, h, r0, len, 0.f, 1.f, full);
       }
+    }
+    {
+      const int row = in + sc_r;
+      const int vo = (int)(ra.vec(sc_h, min(row, last)) - ra.base_row) * 4;
+      const float l = lbuf.ldf(vo, 0), d = dbuf.ldf(vo, 0);
+      sc_l = (sc_ok && row < len) ? l * kLog2e : INFINITY;  // rows past the event: P = 0
+      sc_d = d;
     }
   };
   // Row positions and the u / w~ rows of the row-owner part run one chunk
@@ -691,6 +683,10 @@ __global__ __launch_bounds__(256, 2) void bwd_cols2_kernel(BwdParams prm) {
 
   auto chunk = [&](int i0c, auto tail_tag) __attribute__((always_inline)) {
     constexpr bool TAIL = decltype(tail_tag)::value;
+    if (sc_ok) {
+      rsc[sc_h * RC + sc_r] = sc_l;
+      rsc[16 * RC + sc_h * RC + sc_r] = sc_d;
+    }
     // ---- row-owner: u_i E_i^T and w~_i E_i^T for its row groups ----
     if (use_e) {
 #pragma unroll
@@ -740,15 +736,19 @@ __global__ __launch_bounds__(256, 2) void bwd_cols2_kernel(BwdParams prm) {
     JFrag<bf16, NS> pf[HW], dsf[HW];
 #pragma unroll
     for (int hl = 0; hl < HW; ++hl) {
+      const int h = min(w * HW + hl, H - 1);
 #pragma unroll
-      for (int s = 0; s < NS; ++s)
+      for (int s = 0; s < NS; ++s) {
+        const f32x4 lse2 = *reinterpret_cast<const f32x4*>(rsc + h * RC + 16 * s + 4 * g);
+        const f32x4 dsv = *reinterpret_cast<const f32x4*>(rsc + 16 * RC + h * RC + 16 * s + 4 * g);
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
           // Rows past the event carry lse = +inf: P = 0 there.
-          const float p = exp2f_fast(__builtin_fmaf(S[hl][s][r], kLog2e, -lse2[hl][s][r]));
+          const float p = exp2f_fast(__builtin_fmaf(S[hl][s][r], kLog2e, -lse2[r]));
           S[hl][s][r] = p;
-          dP[hl][s][r] = p * (dP[hl][s][r] - dsv[hl][s][r]);
+          dP[hl][s][r] = p * (dP[hl][s][r] - dsv[r]);
         }
+      }
       pf[hl].from_tiles(S[hl]);
       dsf[hl].from_tiles(dP[hl]);
     }
