@@ -41,6 +41,9 @@
 #ifndef FST_ROWS_HB
 #define FST_ROWS_HB 1
 #endif
+#ifndef FST_ROWS_KC
+#define FST_ROWS_KC 16
+#endif
 
 namespace fst {
 
@@ -76,10 +79,8 @@ __global__ __launch_bounds__(256, 2) void bwd_rows2_kernel(BwdParams prm) {
 
   const int tid = threadIdx.x;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63, g = lane >> 4, n = lane & 15;
-  const int wl = xcd_remap(blockIdx.x, gridDim.x);
-
   EventBlock eb;
-  if (!tile_block(prm.ev, wl, eb)) return;
+  if (!tile_block(prm.ev, blockIdx.x, eb)) return;
   const int len = eb.len;
   const int H = prm.H;
   // FL >= 0: the bias flags fixed at compile time; -1: read at run time.
@@ -557,7 +558,7 @@ __global__ __launch_bounds__(256, 2) void bwd_cols2_kernel(BwdParams prm) {
   EventSpec ev = prm.ev;
   ev.blkcum = prm.blkcum_cols;
   EventBlock eb;
-  if (!tile_block(ev, xcd_remap(blockIdx.x, gridDim.x), eb)) return;
+  if (!tile_block(ev, blockIdx.x, eb)) return;
   const int len = eb.len;
   const int H = prm.H;
   // FL >= 0: the bias flags fixed at compile time; -1: read at run time.
@@ -809,7 +810,7 @@ __global__ __launch_bounds__(256, 2) void bwd_cols2_kernel(BwdParams prm) {
 // ---------------------------------------------------------------------------
 template <int HP, int D, int C>
 struct Bwd2Pick {
-  static constexpr int KC = 16;  // keys per rows-kernel chunk
+  static constexpr int KC = FST_ROWS_KC;  // keys per rows-kernel chunk
   static constexpr int HB = FST_ROWS_HB;  // heads per phase batch of the rows kernel
   static constexpr int RC = 16;  // rows per cols-kernel chunk
   static constexpr bool OK = Rows2Cfg<HP, D, C, KC>::FITS && Cols2Cfg<HP, D, C, RC>::FITS;

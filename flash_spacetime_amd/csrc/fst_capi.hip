@@ -96,6 +96,58 @@ __global__ __launch_bounds__(1024) void blkcum_kernel(const int32_t* lens, int p
   }
 }
 
+// Padded schedule of the tile kernels: the events ordered by decreasing valid
+// length (ties by index), one workgroup, bitonic sort in LDS. Past 8192
+// events, or lengths of 2^18 and more, the identity order is used.
+constexpr int kSortMax = 8192;
+
+__global__ __launch_bounds__(1024) void sort_events_kernel(const int32_t* lens, int B, int L, int32_t* perm) {
+  extern __shared__ int keys[];
+  const int t = threadIdx.x;
+  if (B > kSortMax || L >= (1 << 18)) {
+    for (int i = t; i < B; i += 1024) perm[i] = i;
+    return;
+  }
+  int p2 = 1;
+  while (p2 < B) p2 <<= 1;
+  for (int i = t; i < p2; i += 1024) {
+    int key = -1;
+    if (i < B) {
+      int l = lens[i];
+      l = l < 0 ? 0 : (l > L ? L : l);
+      key = (l << 13) | (kSortMax - 1 - i);
+    }
+    keys[i] = key;
+  }
+  for (int k = 2; k <= p2; k <<= 1)
+    for (int j = k >> 1; j > 0; j >>= 1) {
+      __syncthreads();
+      for (int i = t; i < p2; i += 1024) {
+        const int l = i ^ j;
+        if (l > i) {
+          const int a = keys[i], b = keys[l];
+          if ((i & k) == 0 ? (a < b) : (a > b)) {
+            keys[i] = b;
+            keys[l] = a;
+          }
+        }
+      }
+    }
+  __syncthreads();
+  for (int i = t; i < B; i += 1024) perm[i] = kSortMax - 1 - (keys[i] & (kSortMax - 1));
+}
+
+static int launch_sort(const int32_t* lens, int B, int L, int32_t* perm, hipStream_t st) {
+  int p2 = 1;
+  while (p2 < B && p2 < kSortMax) p2 <<= 1;
+  const int lds = B > kSortMax ? 0 : p2 * (int)sizeof(int);
+  if (hipFuncSetAttribute((const void*)sort_events_kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
+                          kSortMax * (int)sizeof(int)) != hipSuccess)
+    return FST_ELAUNCH;
+  hipLaunchKernelGGL(sort_events_kernel, dim3(1), dim3(1024), lds, st, lens, B, L, perm);
+  return hipGetLastError() == hipSuccess ? FST_OK : FST_ELAUNCH;
+}
+
 typedef int (*fwd_dispatch_fn)(const FwdParams&, int, int, hipStream_t, int, bool, int*);
 
 static fwd_dispatch_fn fwd_table(int dtype, int D) {
@@ -127,7 +179,8 @@ static int check_common(int dtype, int flags, int B, int H, int L, int T, int D,
   return FST_OK;
 }
 
-static size_t blkcum_bytes(int B) { return align_up((size_t)(B + 1) * sizeof(int32_t), 256); }
+// Work list of one kernel family: blkcum [B+1], then perm [B] (padded schedule).
+static size_t blkcum_bytes(int B) { return align_up((size_t)(2 * B + 1) * sizeof(int32_t), 256); }
 
 typedef int (*bwd_dispatch_fn)(const BwdParams&, int, int, int, hipStream_t, int, bool, int*);
 
@@ -201,8 +254,9 @@ static int bwd_layout(int dtype, int flags, int B, int H, int L, int T, int D, i
   if (fn(dummy, 1, HP, C, nullptr, 0, true, &lay.rows_c) != FST_OK || lay.rows_c <= 0) return FST_EUNSUPPORTED;
   const bool packed = flags & FST_PACKED;
   const long rows = packed ? (long)T : (long)B * L;
-  lay.grid_r = packed ? ((long)T + lay.rows_r - 1) / lay.rows_r + B : (long)B * ((L + lay.rows_r - 1) / lay.rows_r);
-  lay.grid_c = packed ? ((long)T + lay.rows_c - 1) / lay.rows_c + B : (long)B * ((L + lay.rows_c - 1) / lay.rows_c);
+  const long B8 = (B + 7) / 8 * 8;
+  lay.grid_r = packed ? ((long)T + lay.rows_r - 1) / lay.rows_r + B : B8 * ((L + lay.rows_r - 1) / lay.rows_r);
+  lay.grid_c = packed ? ((long)T + lay.rows_c - 1) / lay.rows_c + B : B8 * ((L + lay.rows_c - 1) / lay.rows_c);
   const size_t esz = dtype == FST_BF16 ? 2 : 4;
   size_t off = 0;
   lay.off_bc_r = off;
@@ -292,14 +346,17 @@ int fst_forward_phases(int phases, int dtype, int flags, int B, int H, int L, in
 
   int32_t* blkcum = reinterpret_cast<int32_t*>(workspace);
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
+  int32_t* perm = blkcum + (B + 1);
   if (phases & FST_PHASE_WORKLIST) {
     hipLaunchKernelGGL(blkcum_kernel, dim3(1), dim3(1024), 0, st, lens, packed ? 1 : 0, B, L, T, rows, blkcum);
     if (hipGetLastError() != hipSuccess) return fail(FST_ELAUNCH, "work-list kernel launch failed");
+    if (!packed && launch_sort(lens, B, L, perm, st) != FST_OK) return fail(FST_ELAUNCH, "schedule kernel launch failed");
   }
   if (!(phases & FST_PHASE_FWD)) return FST_OK;
 
   prm.ev.lens = lens;
   prm.ev.blkcum = blkcum;
+  prm.ev.perm = perm;
   prm.ev.pos4 = reinterpret_cast<const float4*>(pos4);
   prm.ev.B = B;
   prm.ev.H = H;
@@ -317,7 +374,9 @@ int fst_forward_phases(int phases, int dtype, int flags, int B, int H, int L, in
   prm.out = out;
   prm.lse = lse;
   freq_table(C, prm.freq);
-  const long grid = packed ? ((long)T + rows - 1) / rows + B : (long)B * ((L + rows - 1) / rows);
+  // Padded grids cover ceil(B / 8) * 8 events (the tile kernels' schedule
+  // deals events to the eight XCDs); workgroups without work exit at once.
+  const long grid = packed ? ((long)T + rows - 1) / rows + B : (long)((B + 7) / 8 * 8) * ((L + rows - 1) / rows);
   if (grid > 0x7fffffffL) return fail(FST_EUNSUPPORTED, "problem too large for one launch");
   rc = fn(prm, HP, C, st, (int)grid, false, &rows);
   if (rc != FST_OK) return fail(rc, "forward kernel launch failed (%s)", hipGetErrorString(hipGetLastError()));
@@ -378,12 +437,15 @@ int fst_backward_phases(int phases, int dtype, int flags, int B, int H, int L, i
     hipLaunchKernelGGL(blkcum_kernel, dim3(1), dim3(1024), 0, st, lens, packed ? 1 : 0, B, L, T, lay.rows_r, bc_r);
     hipLaunchKernelGGL(blkcum_kernel, dim3(1), dim3(1024), 0, st, lens, packed ? 1 : 0, B, L, T, lay.rows_c, bc_c);
     if (hipGetLastError() != hipSuccess) return fail(FST_ELAUNCH, "work-list kernel launch failed");
+    if (!packed && launch_sort(lens, B, L, bc_r + (B + 1), st) != FST_OK)
+      return fail(FST_ELAUNCH, "schedule kernel launch failed");
   }
 
   BwdParams prm;
   std::memset(&prm, 0, sizeof(prm));
   prm.ev.lens = lens;
   prm.ev.blkcum = bc_r;
+  prm.ev.perm = bc_r + (B + 1);
   prm.ev.pos4 = reinterpret_cast<const float4*>(pos4);
   prm.ev.B = B;
   prm.ev.H = H;

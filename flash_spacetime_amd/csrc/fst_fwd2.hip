@@ -57,7 +57,7 @@ __global__ __launch_bounds__(256, 2) void fwd2_kernel(FwdParams prm) {
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63, g = lane >> 4, n = lane & 15;
 
   EventBlock eb;
-  if (!tile_block(prm.ev, xcd_remap(blockIdx.x, gridDim.x), eb)) return;
+  if (!tile_block(prm.ev, blockIdx.x, eb)) return;
   const int len = eb.len;
   const int H = prm.H;
   // FL >= 0: the bias flags fixed at compile time; -1: read at run time.

@@ -11,6 +11,7 @@ namespace fst {
 struct EventSpec {
   const int32_t* lens;    // seqlens [B] (padded) or cu_seqlens [B+1] (packed)
   const int32_t* blkcum;  // [B+1] prefix sums of row blocks per event
+  const int32_t* perm;    // [B] events by decreasing length (padded tile kernels' schedule)
   const float4* pos4;     // [B*L] or [T] (x, y, z, t) fp32
   int B, H, L, T, packed;
 };

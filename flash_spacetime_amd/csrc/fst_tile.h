@@ -152,13 +152,25 @@ struct DTiles {
 // past its event's length only zeroes its rows. Packed events have no padding
 // and use the per-event prefix sums of tiles.
 // ---------------------------------------------------------------------------
+//
+// Padded schedule. Every padded event has nb tiles, so the work of an event
+// grows with its length squared while its tile count does not: events are
+// taken by decreasing length (ev.perm) and dealt to the eight XCDs in snake
+// order (ranks 8j .. 8j+7 go to XCDs 0..7 for even j, 7..0 for odd j), which
+// balances the XCDs' work and starts the longest events first. Workgroups
+// are dealt to the XCDs round robin, so hardware workgroup w runs on XCD
+// w % 8 as its (w / 8)-th tile: tile (w / 8) % nb of the XCD's (w / 8) / nb-th
+// event. The grid is 8 ceil(B / 8) nb.
 __device__ __forceinline__ bool tile_block(const EventSpec& ev, int w, EventBlock& eb) {
-  if (ev.packed) return locate_block(ev, w, eb);
+  if (ev.packed) return locate_block(ev, xcd_remap(w, gridDim.x), eb);
   const int nb = (ev.L + 15) >> 4;
-  const int b = w / nb;
-  if (b >= ev.B) return false;
+  const int x = w & 7, k = w >> 3;
+  const int j = k / nb;
+  const int r = 8 * j + ((j & 1) ? 7 - x : x);
+  if (r >= ev.B) return false;
+  const int b = ev.perm[r];
   eb.b = b;
-  eb.blk = w - b * nb;
+  eb.blk = k - j * nb;
   event_range(ev, b, eb.tok0, eb.len);
   return true;
 }
