@@ -9,8 +9,8 @@
 // One workgroup = one 16-row tile of one event, four waves. Wave w is
 //  * head-owner of heads [w HW, (w+1) HW): S^T_h = K_h Qt_h^T + (u.E)^T and
 //    O^T_h += V_h^T P^T_h on 16x16 MFMA tiles with the 16 rows on the lanes,
-//    the online softmax, and the row sums l = 1^T P^T (an all-ones MFMA
-//    operand, so l is the sum of the very bf16 P that weights V);
+//    the online softmax and its row sums l (fp32, per lane group, summed
+//    across the groups at the end);
 //  * row-owner of rows 4w .. 4w+3: u of its rows (fp32 MFMA projection), the
 //    embedding E of its rows x the chunk's keys, computed directly in the
 //    operand layout of the u.E product (UE^T_i = E_i U_i^T, heads on the
@@ -28,7 +28,7 @@
 
 namespace fst {
 
-template <int HP, int D, int C, int KC>
+template <int HP, int D, int C, int KC, int OCC>
 struct Fwd2Cfg {
   static constexpr int HW = HP / 4;  // heads per wave
   static constexpr int NS = KC / 16;  // 16-key subtiles per chunk
@@ -37,14 +37,15 @@ struct Fwd2Cfg {
   static constexpr int STAGE_BYTES = (KC / 4) * 16 * 16 * 16;  // fp32 u.E of KC keys per (row, head)
   static constexpr int SCAL_BYTES = 16 * 17 * 4;
   static constexpr int LDS_BYTES = E_BYTES + STAGE_BYTES + SCAL_BYTES;
-  static constexpr bool FITS = LDS_BYTES <= 80 * 1024 && HP % 4 == 0 && (KC == 16 || KC == 32);
+  // OCC: workgroups per CU the register and LDS plan is built for.
+  static constexpr bool FITS = LDS_BYTES <= (160 / OCC) * 1024 && HP % 4 == 0 && (KC == 16 || KC == 32);
 };
 
 constexpr float kRescaleLog2 = 8.f;
 
-template <int HP, int D, int C, int KC, int FL>
-__global__ __launch_bounds__(256, 2) void fwd2_kernel(FwdParams prm) {
-  using Cfg = Fwd2Cfg<HP, D, C, KC>;
+template <int HP, int D, int C, int KC, int OCC, int FL>
+__global__ __launch_bounds__(256, OCC) void fwd2_kernel(FwdParams prm) {
+  using Cfg = Fwd2Cfg<HP, D, C, KC, OCC>;
   using ET = ETile<C, KC>;
   using DT = DTiles<D>;
   constexpr int HW = Cfg::HW, NS = Cfg::NS, NCT = Cfg::NCT, NQ = DT::NQ;
@@ -82,7 +83,8 @@ __global__ __launch_bounds__(256, 2) void fwd2_kernel(FwdParams prm) {
   const int my_row = i0 + n;
   const bool row_ok = my_row < len;
   KFrag<bf16, D> qf[HW];
-  f32x4 O[HW][NQ], lacc[HW];
+  f32x4 O[HW][NQ];
+  float lsum[HW];  // this lane group's part of the row sum
   float mref[HW];
 #pragma unroll
   for (int hl = 0; hl < HW; ++hl) {
@@ -95,12 +97,9 @@ __global__ __launch_bounds__(256, 2) void fwd2_kernel(FwdParams prm) {
       qf[hl].zero();
 #pragma unroll
     for (int q = 0; q < NQ; ++q) O[hl][q] = zero4();
-    lacc[hl] = zero4();
+    lsum[hl] = 0.f;
     mref[hl] = -INFINITY;
   }
-  JFrag<bf16, NS> ones;
-#pragma unroll
-  for (int e = 0; e < 4 * NS; ++e) ones.v[e] = (bf16)1.f;
 
   // ---- row-owner state: rows i0 + 4w + r, heads on lane n ----
   bf16x4 uf[4][NCT];
@@ -264,22 +263,26 @@ __global__ __launch_bounds__(256, 2) void fwd2_kernel(FwdParams prm) {
         mref[hl] = mnew;
 #pragma unroll
         for (int q = 0; q < NQ; ++q) O[hl][q] = O[hl][q] * alpha[hl];
-        lacc[hl] = lacc[hl] * alpha[hl];
+        lsum[hl] *= alpha[hl];
       }
     }
     JFrag<bf16, NS> pf[HW];
 #pragma unroll
     for (int hl = 0; hl < HW; ++hl) {
       const float mb = mref[hl];
+      float ls = lsum[hl];
 #pragma unroll
       for (int s = 0; s < NS; ++s)
 #pragma unroll
-        for (int r = 0; r < 4; ++r) S[hl][s][r] = exp2f_fast(__builtin_fmaf(S[hl][s][r], kLog2e, -mb));
+        for (int r = 0; r < 4; ++r) {
+          S[hl][s][r] = exp2f_fast(__builtin_fmaf(S[hl][s][r], kLog2e, -mb));
+          ls += S[hl][s][r];
+        }
+      lsum[hl] = ls;
       pf[hl].from_tiles(S[hl]);
     }
 #pragma unroll
     for (int hl = 0; hl < HW; ++hl) {
-      lacc[hl] = mma_j(ones, pf[hl], lacc[hl]);
 #pragma unroll
       for (int q = 0; q < NQ; ++q) {
         JFrag<bf16, NS> vt;
@@ -350,7 +353,7 @@ __global__ __launch_bounds__(256, 2) void fwd2_kernel(FwdParams prm) {
   float inv_l[HW];
 #pragma unroll
   for (int hl = 0; hl < HW; ++hl) {
-    const float l = lacc[hl][0];
+    const float l = group_allsum(lsum[hl]);
     inv_l[hl] = 1.f / l;
     const int h = w * HW + hl;
     if (g == 0 && row_ok && h < H) prm.lse[ra.vec(h, my_row)] = mref[hl] * kLn2 + __logf(l);
@@ -411,10 +414,14 @@ __global__ __launch_bounds__(256, 2) void fwd2_kernel(FwdParams prm) {
 
 template <int HP, int D, int C>
 struct Fwd2Pick {
-  // 32-key chunks where the register plan of 16 heads x 32 keys fits (no
-  // spills at HP <= 12, C = 16); 16-key chunks otherwise.
-  static constexpr int KC = (Fwd2Cfg<HP, D, C, 32>::FITS && HP <= 12 && C <= 16 && D <= 32) ? 32 : 16;
-  using Cfg = Fwd2Cfg<HP, D, C, KC>;
+  // Small head layouts (HP <= 12, D <= 32, C = 16) run 16-key chunks at three
+  // workgroups per CU: measured faster than 32-key chunks at two, the extra
+  // waves hiding more latency than the shorter chunks cost. Larger layouts
+  // run two workgroups per CU with 16-key chunks.
+  static constexpr bool SMALL = HP <= 12 && D <= 32 && C <= 16;
+  static constexpr int KC = 16;
+  static constexpr int OCC = SMALL ? 3 : 2;
+  using Cfg = Fwd2Cfg<HP, D, C, KC, OCC>;
   static constexpr bool OK = Cfg::FITS;
 };
 
@@ -426,7 +433,7 @@ int fwd2_launch_t(const FwdParams& prm, hipStream_t stream, int grid) {
   } else {
     // Both bias flags (the operators' default) run an instance with the flags
     // fixed at compile time; other combinations read them at run time.
-    auto kern = (prm.flags & 3) == 3 ? fwd2_kernel<HP, D, C, P::KC, 3> : fwd2_kernel<HP, D, C, P::KC, -1>;
+    auto kern = (prm.flags & 3) == 3 ? fwd2_kernel<HP, D, C, P::KC, P::OCC, 3> : fwd2_kernel<HP, D, C, P::KC, P::OCC, -1>;
     if (hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, P::Cfg::LDS_BYTES) !=
         hipSuccess)
       return FST_ELAUNCH;

@@ -254,6 +254,32 @@ __device__ __forceinline__ void load_kfrag(KFrag<bf16, D>& f, const Buf& b, int 
   for (int t = 0; t < KFrag<bf16, D>::N16; ++t) f.x16[t] = b.ld64(voff + 32 * t, soff);
 }
 
+// K / V (or streamed) rows staged through LDS by the wave that uses them:
+// buffer loads write LDS directly, so nothing occupies VGPRs while the next
+// chunk is in flight. A KFrag<bf16, D> of 16 rows (D % 32 == 0) takes D / 32
+// blocks of 1 KB; lane l's 16 bytes of block t sit at 16 l. The LDS base of
+// a load must be wave-uniform.
+template <int D>
+struct LdsFrag {
+  static_assert(D % 32 == 0, "LDS-staged fragments need 16-byte lane parts");
+  static constexpr int NP = D / 32;
+  static constexpr int BYTES = NP * 1024;
+  static __device__ __forceinline__ void load(const Buf& b, unsigned char* dst, int voff, int soff) {
+#pragma unroll
+    for (int t = 0; t < NP; ++t)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(b.r, (__attribute__((address_space(3))) void*)(dst + t * 1024), 16,
+                                               voff + 64 * t, soff, 0, 0);
+  }
+  static __device__ __forceinline__ void read(KFrag<bf16, D>& f, const unsigned char* src, int lane) {
+#pragma unroll
+    for (int t = 0; t < NP; ++t) f.x32[t] = *reinterpret_cast<const bf16x8*>(src + t * 1024 + 16 * lane);
+  }
+};
+
+// Completion of this wave's outstanding buffer loads (including loads into
+// LDS), ordered against every later memory access of the wave.
+__device__ __forceinline__ void wait_vmem() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+
 // ---------------------------------------------------------------------------
 // LDS layouts.
 // ---------------------------------------------------------------------------
