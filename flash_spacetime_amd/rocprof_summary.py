@@ -27,9 +27,13 @@ import os
 from collections import defaultdict
 
 CALIB_TAG = "MulFunctor"           # torch's elementwise multiply kernel
-PHASES = {"fwd_kernel": "fwd", "bwd_rows_kernel": "bwd_rows", "bwd_cols_kernel": "bwd_cols",
+# Kernel-name fragments of each phase: the bf16 kernels (fwd2/bwd_rows2/bwd_cols2)
+# and the fp32 ones (fwd/bwd_rows/bwd_cols) share a phase.
+PHASES = {"fwd2_kernel": "fwd", "fwd_kernel": "fwd",
+          "bwd_rows2_kernel": "bwd_rows", "bwd_rows_kernel": "bwd_rows",
+          "bwd_cols2_kernel": "bwd_cols", "bwd_cols_kernel": "bwd_cols",
           "dw_reduce_seg_kernel": "bwd_reduce_seg", "dw_reduce_final_kernel": "bwd_reduce_final",
-          "blkcum_kernel": "worklist"}
+          "blkcum_kernel": "worklist", "sort_events_kernel": "worklist_sort"}
 
 
 def _find(directory: str, suffix: str) -> str:
@@ -103,7 +107,7 @@ def main():
     lines = ["| kernel | launches | avg duration (us) | FETCH_SIZE (KiB) | WRITE_SIZE (KiB) | HBM bytes / launch "
              "(scaled) | grid | VGPR | AGPR | LDS (B) |",
              "|---|---|---|---|---|---|---|---|---|---|"]
-    for ph in ("fwd", "bwd_rows", "bwd_cols", "bwd_reduce_seg", "bwd_reduce_final", "worklist"):
+    for ph in ("fwd", "bwd_rows", "bwd_cols", "bwd_reduce_seg", "bwd_reduce_final", "worklist", "worklist_sort"):
         if ph not in stats:
             continue
         fk, wk = fetch.get(ph), write.get(ph)
