@@ -210,8 +210,12 @@ __global__ __launch_bounds__(256, 2) void bwd_rows2_kernel(BwdParams prm) {
       for (int s = 0; s < NS; ++s) pj[s] = pbuf.ldf4(min(jn + 16 * s + n, last) * 16, 0);
     }
   };
-  issue(0);
+  // Every chunk issues the same loads in the same order (positions, then K
+  // and V; past the last chunk they reread clamped keys), so the wait at the
+  // top of a chunk covers the positions only and E is formed while K and V
+  // are still in flight.
   issue_pos(0);
+  issue(0);
 
   auto chunk = [&](int j0, auto tail_tag) __attribute__((always_inline)) {
     constexpr bool TAIL = decltype(tail_tag)::value;
@@ -220,7 +224,7 @@ __global__ __launch_bounds__(256, 2) void bwd_rows2_kernel(BwdParams prm) {
       float xg[NS][4];
 #pragma unroll
       for (int s = 0; s < NS; ++s) group_gather(pair_angle_unit(pos_i, pj[s]), xg[s]);
-      if (j0 + KC < len) issue_pos(j0 + KC);
+      issue_pos(j0 + KC);
 #pragma unroll
       for (int r = 0; r < 4; ++r)
 #pragma unroll
@@ -352,7 +356,7 @@ __global__ __launch_bounds__(256, 2) void bwd_rows2_kernel(BwdParams prm) {
         }
       }
     }
-    if (j0 + KC < len) issue(j0 + KC);
+    issue(j0 + KC);
     __syncthreads();  // P, dS and D increments staged
 
     // ---- row-owner: H -= dD G; H += E^T dS; G += E^T P ----
@@ -631,10 +635,13 @@ __global__ __launch_bounds__(256, 2) void bwd_cols2_kernel(BwdParams prm) {
   // loads item t of the chunk's RC x H values of each (coalesced), and writes
   // it to LDS at the start of that chunk; the head-owners read four rows at a
   // time (one 16-byte broadcast read).
-  float sc_l = INFINITY, sc_d = 0.f;
+  // The raw values are kept until the chunk's scalars are written, so the
+  // loads are not waited for where they are issued.
+  float sc_lraw = 0.f, sc_draw = 0.f;
   const int sc_h = ev.packed ? tid % H : tid / RC;
   const int sc_r = ev.packed ? tid / H : tid % RC;
   const bool sc_ok = tid < RC * H;
+  const int sc_hc = min(sc_h, H - 1);
   float4 prow[RGW];
   auto issue = [&](int in) __attribute__((always_inline)) {
     const bool full = in + RC <= len;
@@ -650,11 +657,9 @@ __global__ __launch_bounds__(256, 2) void bwd_cols2_kernel(BwdParams prm) {
       }
     }
     {
-      const int row = in + sc_r;
-      const int vo = (int)(ra.vec(sc_h, min(row, last)) - ra.base_row) * 4;
-      const float l = lbuf.ldf(vo, 0), d = dbuf.ldf(vo, 0);
-      sc_l = (sc_ok && row < len) ? l * kLog2e : INFINITY;  // rows past the event: P = 0
-      sc_d = d;
+      const int vo = (int)(ra.vec(sc_hc, min(in + sc_r, last)) - ra.base_row) * 4;
+      sc_lraw = lbuf.ldf(vo, 0);
+      sc_draw = dbuf.ldf(vo, 0);
     }
   };
   // Row positions and the u / w~ rows of the row-owner part run one chunk
@@ -679,15 +684,14 @@ __global__ __launch_bounds__(256, 2) void bwd_cols2_kernel(BwdParams prm) {
       }
     }
   };
-  issue(0);
+  // Every chunk issues the same loads in the same order (the row-owner's
+  // rows, then the head-owner's; past the last chunk they reread clamped
+  // rows), so each phase waits only for the loads it uses.
   issue_rows(0);
+  issue(0);
 
   auto chunk = [&](int i0c, auto tail_tag) __attribute__((always_inline)) {
     constexpr bool TAIL = decltype(tail_tag)::value;
-    if (sc_ok) {
-      rsc[sc_h * RC + sc_r] = sc_l;
-      rsc[16 * RC + sc_h * RC + sc_r] = sc_d;
-    }
     // ---- row-owner: u_i E_i^T and w~_i E_i^T for its row groups ----
     if (use_e) {
 #pragma unroll
@@ -717,8 +721,12 @@ __global__ __launch_bounds__(256, 2) void bwd_cols2_kernel(BwdParams prm) {
         }
       }
     }
-    if (i0c + RC < len) issue_rows(i0c + RC);
-    __syncthreads();  // u.E, w~.E staged
+    issue_rows(i0c + RC);
+    if (sc_ok) {
+      rsc[sc_h * RC + sc_r] = i0c + sc_r < len ? sc_lraw * kLog2e : INFINITY;  // rows past the event: P = 0
+      rsc[16 * RC + sc_h * RC + sc_r] = sc_draw;
+    }
+    __syncthreads();  // u.E, w~.E and the row scalars staged
 
     // ---- head-owner: P, dS, dV^T += dO^T P, dK^T += Qt^T dS ----
     f32x4 S[HW][NS], dP[HW][NS];
@@ -770,7 +778,7 @@ __global__ __launch_bounds__(256, 2) void bwd_cols2_kernel(BwdParams prm) {
       }
     }
     (void)TAIL;
-    if (i0c + RC < len) issue(i0c + RC);
+    issue(i0c + RC);
     __syncthreads();  // the stage is read; the next chunk may overwrite it
   };
 

@@ -162,6 +162,10 @@ __global__ __launch_bounds__(256, OCC) void fwd2_kernel(FwdParams prm) {
   // Operands of the chunk in flight: K, V rows of the wave's heads and the
   // key positions. Loads for chunk j0 + KC are issued as soon as the
   // head-owner has consumed those of chunk j0; keys are clamped to the event.
+  // Every chunk issues the same loads in the same order (positions, then K
+  // and V; past the last chunk they reread clamped keys), so the wait at the
+  // top of a chunk covers the positions only and E is formed while K and V
+  // are still in flight.
   KFrag<bf16, D> kf[HW][NS], vf[HW][NS];
   float4 pj[NS];
   auto issue = [&](int jn) __attribute__((always_inline)) {
@@ -170,14 +174,10 @@ __global__ __launch_bounds__(256, OCC) void fwd2_kernel(FwdParams prm) {
     for (int hl = 0; hl < HW; ++hl) {
 #pragma unroll
       for (int s = 0; s < NS; ++s) {
-        if (full) {
-          load_kfrag<D>(kf[hl][s], kbuf, kvo[hl] + 16 * s * rowb, jn * rowb);
-          load_kfrag<D>(vf[hl][s], vbuf, kvo[hl] + 16 * s * rowb, jn * rowb);
-        } else {
-          const int key = min(jn + 16 * s + n, last);
-          load_kfrag<D>(kf[hl][s], kbuf, kvo[hl] + (key - n) * rowb, 0);
-          load_kfrag<D>(vf[hl][s], vbuf, kvo[hl] + (key - n) * rowb, 0);
-        }
+        const int voff = full ? kvo[hl] + 16 * s * rowb : kvo[hl] + (min(jn + 16 * s + n, last) - n) * rowb;
+        const int soff = full ? jn * rowb : 0;
+        load_kfrag<D>(kf[hl][s], kbuf, voff, soff);
+        load_kfrag<D>(vf[hl][s], vbuf, voff, soff);
       }
     }
   };
@@ -189,8 +189,8 @@ __global__ __launch_bounds__(256, OCC) void fwd2_kernel(FwdParams prm) {
       for (int s = 0; s < NS; ++s) pj[s] = pbuf.ldf4(min(jn + 16 * s + n, last) * 16, 0);
     }
   };
-  issue(0);
   issue_pos(0);
+  issue(0);
 
   auto chunk = [&](int j0, auto tail_tag) __attribute__((always_inline)) {
     constexpr bool TAIL = decltype(tail_tag)::value;
@@ -200,7 +200,7 @@ __global__ __launch_bounds__(256, OCC) void fwd2_kernel(FwdParams prm) {
       float xg[NS][4];
 #pragma unroll
       for (int s = 0; s < NS; ++s) group_gather(pair_angle_unit(pos_i, pj[s]), xg[s]);
-      if (j0 + KC < len) issue_pos(j0 + KC);
+      issue_pos(j0 + KC);
 #pragma unroll
       for (int r = 0; r < 4; ++r)
 #pragma unroll
@@ -308,7 +308,7 @@ __global__ __launch_bounds__(256, OCC) void fwd2_kernel(FwdParams prm) {
         if (g == 0) *reinterpret_cast<float*>(scal + scal_off(n, h)) = alpha[hl];
       }
     }
-    if (j0 + KC < len) issue(j0 + KC);
+    issue(j0 + KC);
     __syncthreads();  // P and rescale factors staged
 
     // ---- row-owner: A = alpha A + E^T P ----
