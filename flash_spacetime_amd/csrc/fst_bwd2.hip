@@ -56,7 +56,8 @@ struct Rows2Cfg {
   static constexpr int E_BYTES = ETile<C, KC>::BYTES;
   static constexpr int REGION = (KC / 4) * 16 * HP * 16;  // one fp32 term of KC keys per (row, head)
   static constexpr int SCAL_BYTES = 16 * 17 * 4;
-  static constexpr int MAIN = E_BYTES + 2 * REGION + SCAL_BYTES;
+  static constexpr int TRASH_BYTES = 64 * 16;  // sink for the stores of padded-head lanes
+  static constexpr int MAIN = E_BYTES + 2 * REGION + SCAL_BYTES + TRASH_BYTES;
   static constexpr int DW_BYTES = 4 * (D * C + D) * 4;   // epilogue: per-wave dW / db partials
   static constexpr int HG_BYTES = 2 * 16 * HP * 16 * 4;  // epilogue: one channel step of H and G
   static constexpr int EPI = DW_BYTES + HG_BYTES;
@@ -76,6 +77,7 @@ __global__ __launch_bounds__(256, 2) void bwd_rows2_kernel(BwdParams prm) {
   unsigned char* stU = smem + Cfg::E_BYTES;  // u.E, then P
   unsigned char* stW = stU + Cfg::REGION;    // w~.E + dob, then dS
   unsigned char* scal = stW + Cfg::REGION;   // increments of D
+  const int trash = Cfg::E_BYTES + 2 * Cfg::REGION + Cfg::SCAL_BYTES + 16 * (threadIdx.x & 63);
 
   const int tid = threadIdx.x;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63, g = lane >> 4, n = lane & 15;
@@ -143,8 +145,12 @@ __global__ __launch_bounds__(256, 2) void bwd_rows2_kernel(BwdParams prm) {
   // ---- row-owner state: rows i0 + 4w + r, heads on lane n ----
   bf16x4 uf[4][NCT], wf[4][NCT];
   f32x4 Hacc[4][NCT], Gacc[4][NCT];
-  bf16* ug = reinterpret_cast<bf16*>(prm.u);
-  bf16* wtg = reinterpret_cast<bf16*>(prm.wt);
+  // u and w~ of the row group go to the cols kernel's scratch; rows past the
+  // event are written as zeros, so every row of a group the cols kernel
+  // reads is defined.
+  const long uwg = ((long)prm.ev.blkcum[eb.b] + eb.blk) * 4 + w;
+  bf16* ug = reinterpret_cast<bf16*>(prm.u) + uwg * uw_group_elems(H, NCT);
+  bf16* wtg = reinterpret_cast<bf16*>(prm.wt) + uwg * uw_group_elems(H, NCT);
 #pragma unroll
   for (int r = 0; r < 4; ++r) {
     const int row = i0 + 4 * w + r;
@@ -152,15 +158,17 @@ __global__ __launch_bounds__(256, 2) void bwd_rows2_kernel(BwdParams prm) {
     const long xo = ra.off(0, row < len ? row : last, D);
     if (attn) {
       project_slots<D, C>(qg + xo, ra.hs * D, ok, prm.scale, prm.weight, g, n, uf[r]);
-      if (ok)
+      if (n < H)
 #pragma unroll
-        for (int ct = 0; ct < NCT; ++ct) *reinterpret_cast<bf16x4*>(ug + ra.off(n, row, C) + 16 * ct + 4 * g) = uf[r][ct];
+        for (int ct = 0; ct < NCT; ++ct)
+          *reinterpret_cast<bf16x4*>(ug + uw_off(r >> 1, ct, n, g, r & 1, H, NCT)) = uf[r][ct];
     }
     if (act) {
       project_slots<D, C>(dog + xo, ra.hs * D, ok, 1.f, prm.weight, g, n, wf[r]);
-      if (ok)
+      if (n < H)
 #pragma unroll
-        for (int ct = 0; ct < NCT; ++ct) *reinterpret_cast<bf16x4*>(wtg + ra.off(n, row, C) + 16 * ct + 4 * g) = wf[r][ct];
+        for (int ct = 0; ct < NCT; ++ct)
+          *reinterpret_cast<bf16x4*>(wtg + uw_off(r >> 1, ct, n, g, r & 1, H, NCT)) = wf[r][ct];
     }
 #pragma unroll
     for (int ct = 0; ct < NCT; ++ct) Hacc[r][ct] = Gacc[r][ct] = zero4();
@@ -235,19 +243,20 @@ __global__ __launch_bounds__(256, 2) void bwd_rows2_kernel(BwdParams prm) {
             ef[ct] = embed_step<C>(xg[s][r], fa[ct], fb[ct], ct);
             ET::store(Es, 4 * w + r, ct, 16 * s + n, g, ef[ct]);
           }
-          if (n < HP) {
-            if (attn) {
-              f32x4 ue = zero4();
+          // Lanes of heads past HP have no slot: they store into the sink,
+          // which keeps the phase free of branches.
+          const int so = hslot_off<HP>(4 * s + g, 4 * w + r, n);
+          if (attn) {
+            f32x4 ue = zero4();
 #pragma unroll
-              for (int ct = 0; ct < NCT; ++ct) ue = mfma_x16(ef[ct], uf[r][ct], ue);
-              *reinterpret_cast<f32x4*>(stU + hslot_off<HP>(4 * s + g, 4 * w + r, n)) = ue;
-            }
-            if (act) {
-              f32x4 we = zero4();
+            for (int ct = 0; ct < NCT; ++ct) ue = mfma_x16(ef[ct], uf[r][ct], ue);
+            *reinterpret_cast<f32x4*>(smem + (n < HP ? Cfg::E_BYTES + so : trash)) = ue;
+          }
+          if (act) {
+            f32x4 we = zero4();
 #pragma unroll
-              for (int ct = 0; ct < NCT; ++ct) we = mfma_x16(ef[ct], wf[r][ct], we);
-              *reinterpret_cast<f32x4*>(stW + hslot_off<HP>(4 * s + g, 4 * w + r, n)) = we;
-            }
+            for (int ct = 0; ct < NCT; ++ct) we = mfma_x16(ef[ct], wf[r][ct], we);
+            *reinterpret_cast<f32x4*>(smem + (n < HP ? Cfg::E_BYTES + Cfg::REGION + so : trash)) = we;
           }
         }
     }
@@ -279,7 +288,7 @@ __global__ __launch_bounds__(256, 2) void bwd_rows2_kernel(BwdParams prm) {
 #pragma unroll
       for (int b = 0; b < NB; ++b) {
         const int hl = hb + b < HW ? hb + b : HW - 1;
-        float a = 0.f, z = 0.f;
+        float a = -0.f, z = -0.f;
 #pragma unroll
         for (int s = 0; s < NS; ++s)
 #pragma unroll
@@ -352,7 +361,7 @@ __global__ __launch_bounds__(256, 2) void bwd_rows2_kernel(BwdParams prm) {
             *reinterpret_cast<bf16x4*>(stU + so) = pv;
             *reinterpret_cast<bf16x4*>(stW + so) = dv;
           }
-          if (g == 0) *reinterpret_cast<float*>(scal + scal_off(n, h)) = dD[b];
+          *reinterpret_cast<float*>(scal + scal_off(n, h)) = dD[b];  // the same value from every lane group
         }
       }
     }
@@ -620,8 +629,12 @@ __global__ __launch_bounds__(256, 2) void bwd_cols2_kernel(BwdParams prm) {
   const Buf obuf(reinterpret_cast<const bf16*>(prm.dout) + ebase, ebytes);
   const unsigned vbytes = (unsigned)((ev.packed ? (long)len * ra.ts : (long)H * ra.hs) * 4);
   const Buf lbuf(prm.lse + ra.base_row, vbytes), dbuf(prm.dsum + ra.base_row, vbytes);
-  const long cbase = ra.off(0, 0, C);
-  const unsigned cbytes = (unsigned)((ev.packed ? (long)len * ra.ts : (long)H * ra.hs) * C * 2);
+  // u / w~ in the row-group layout the rows kernel writes (uw_off): the
+  // event's groups start at 4 x its first tile in the rows work list.
+  const long ggrp = uw_group_elems(H, NCT);
+  const long cbase = (long)prm.ev.blkcum[eb.b] * 4 * ggrp;
+  const int glast = (len - 1) >> 2;  // last row group of the event
+  const unsigned cbytes = (unsigned)((long)(glast + 1) * ggrp * 2);
   const Buf ubuf(reinterpret_cast<const bf16*>(prm.u) + cbase, cbytes),
       wbuf(reinterpret_cast<const bf16*>(prm.wt) + cbase, cbytes);
   const Buf pbuf(ev.pos4 + ra.pos_base, (unsigned)len * 16u);
@@ -671,16 +684,25 @@ __global__ __launch_bounds__(256, 2) void bwd_cols2_kernel(BwdParams prm) {
       for (int q2 = 0; q2 < RGW; ++q2) {
         const int rg = RGW * w + q2;
         prow[q2] = pbuf.ldf4(min(in + 4 * rg + g, last) * 16, 0);
+        // Groups past the event reread its last group: their rows carry
+        // P = 0 (lse = +inf) in the head-owner part.
+        const int go = (int)(min((in >> 2) + rg, glast) * ggrp);
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const int row = min(in + 4 * rg + r, last);
-          const int co = (int)(ra.off(n, row, C) - cbase) * 2 + 8 * g;
+        for (int half = 0; half < 2; ++half)
 #pragma unroll
           for (int ct = 0; ct < NCT; ++ct) {
-            if (attn) ur[q2][r][ct] = ubuf.ld64(co + 32 * ct, 0);
-            if (act) wr[q2][r][ct] = wbuf.ld64(co + 32 * ct, 0);
+            const int co = (go + uw_off(half, ct, n, g, 0, H, NCT)) * 2;
+            if (attn) {
+              const bf16x8 v = ubuf.ld128(co, 0);
+              ur[q2][2 * half][ct] = lo4(v);
+              ur[q2][2 * half + 1][ct] = hi4(v);
+            }
+            if (act) {
+              const bf16x8 v = wbuf.ld128(co, 0);
+              wr[q2][2 * half][ct] = lo4(v);
+              wr[q2][2 * half + 1][ct] = hi4(v);
+            }
           }
-        }
       }
     }
   };

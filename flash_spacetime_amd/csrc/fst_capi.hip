@@ -263,10 +263,13 @@ static int bwd_layout(int dtype, int flags, int B, int H, int L, int T, int D, i
   off += blkcum_bytes(B);
   lay.off_bc_c = off;
   off += blkcum_bytes(B);
+  // u and w~ hold whole 16-row tiles of each event (the bf16 kernels' row-group
+  // layout): at most B ceil(L / 16) tiles padded, T / 16 + B packed.
+  const long rows_uw = packed ? ((long)(T + 15) / 16 + B) * 16 : (long)B * ((L + 15) / 16) * 16;
   lay.off_u = off;
-  off += align_up((size_t)rows * H * C * esz, 256);
+  off += align_up((size_t)(rows_uw > rows ? rows_uw : rows) * H * C * esz, 256);
   lay.off_wt = off;
-  off += align_up((size_t)rows * H * C * esz, 256);
+  off += align_up((size_t)(rows_uw > rows ? rows_uw : rows) * H * C * esz, 256);
   lay.off_qt = off;
   if (dtype == FST_BF16) off += align_up((size_t)rows * H * D * esz, 256);
   lay.off_dob = off;

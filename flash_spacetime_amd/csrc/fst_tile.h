@@ -217,6 +217,22 @@ __device__ __forceinline__ void project_slots(const bf16* xrow, long hstride, bo
 }
 
 // ---------------------------------------------------------------------------
+// Layout of the u / w~ scratch the rows kernel writes for the cols kernel.
+// Rows are grouped by four ("row group" = a quarter of a 16-row tile; the
+// groups of an event start at 4 x its first tile in the rows work list).
+// Within a group, for each half (rows 0-1 / 2-3), channel step ct, head h and
+// lane group g, the 8 values (row 2 half + rb, slot 16 ct + 4 g + e) sit
+// together, rb = 0..1, e = 0..3. A cols-kernel lane (g, head n) then reads two
+// rows of its four slots with one 16-byte load, and the 64 lanes of the load
+// read one contiguous run; a row-major [rows, H, C] layout would put the
+// heads of one row an entire head plane apart.
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ long uw_group_elems(int H, int NCT) { return 64L * NCT * H; }
+__device__ __forceinline__ int uw_off(int half, int ct, int h, int g, int rb, int H, int NCT) {
+  return (((half * NCT + ct) * H + h) * 4 + g) * 8 + rb * 4;
+}
+
+// ---------------------------------------------------------------------------
 // Buffer loads. One resource per tensor and event (base = the event's first
 // element, range = its bytes); a lane's offset within the event is fixed and
 // the key chunk moves through the scalar offset, so the chunk loop spends no
