@@ -151,20 +151,22 @@ __global__ __launch_bounds__(256, 2) void bwd_rows2_kernel(BwdParams prm) {
   const long uwg = ((long)prm.ev.blkcum[eb.b] + eb.blk) * 4 + w;
   bf16* ug = reinterpret_cast<bf16*>(prm.u) + uwg * uw_group_elems(H, NCT);
   bf16* wtg = reinterpret_cast<bf16*>(prm.wt) + uwg * uw_group_elems(H, NCT);
+  WSlots<D, C> wv;
+  if (use_e) wv.load(prm.weight, g, n);
 #pragma unroll
   for (int r = 0; r < 4; ++r) {
     const int row = i0 + 4 * w + r;
     const bool ok = row < len && n < H;
     const long xo = ra.off(0, row < len ? row : last, D);
     if (attn) {
-      project_slots<D, C>(qg + xo, ra.hs * D, ok, prm.scale, prm.weight, g, n, uf[r]);
+      project_slots<D, C>(qg + xo, ra.hs * D, ok, prm.scale, wv, g, n, uf[r]);
       if (n < H)
 #pragma unroll
         for (int ct = 0; ct < NCT; ++ct)
           *reinterpret_cast<bf16x4*>(ug + uw_off(r >> 1, ct, n, g, r & 1, H, NCT)) = uf[r][ct];
     }
     if (act) {
-      project_slots<D, C>(dog + xo, ra.hs * D, ok, 1.f, prm.weight, g, n, wf[r]);
+      project_slots<D, C>(dog + xo, ra.hs * D, ok, 1.f, wv, g, n, wf[r]);
       if (n < H)
 #pragma unroll
         for (int ct = 0; ct < NCT; ++ct)

@@ -104,27 +104,15 @@ __global__ __launch_bounds__(256, OCC) void fwd2_kernel(FwdParams prm) {
   // ---- row-owner state: rows i0 + 4w + r, heads on lane n ----
   bf16x4 uf[4][NCT];
   f32x4 AE[4][NCT];
+  WSlots<D, C> wv;
+  if (attn) wv.load(prm.weight, g, n);
 #pragma unroll
   for (int r = 0; r < 4; ++r) {
     const int row = i0 + 4 * w + r;
     if (attn) {
+      // u^T[slot][h] = sum_d W[d][channel(slot)] qt[h][d] on fp32 MFMA.
       const bool ok = row < len && n < H;
-      f32x4 acc[NCT];
-#pragma unroll
-      for (int ct = 0; ct < NCT; ++ct) {
-        // u^T[slot][h] = sum_d W[d][channel(slot)] qt[h][d] on fp32 MFMA.
-        constexpr int Qd = D / 4;
-        f32x4 a = zero4();
-        const bf16* xr = qg + ra.off(0, ok ? row : 0, D) + n * ra.hs * D + Qd * g;
-#pragma unroll
-        for (int s = 0; s < Qd; ++s) {
-          const float xv = ok ? (float)xr[s] * prm.scale : 0.f;
-          a = mfma_f32(prm.weight[(Qd * g + s) * C + slot_channel<C>(16 * ct + n)], xv, a);
-        }
-        acc[ct] = a;
-      }
-#pragma unroll
-      for (int ct = 0; ct < NCT; ++ct) uf[r][ct] = pack4(acc[ct]);
+      project_slots<D, C>(qg + ra.off(0, row < len ? row : last, D), ra.hs * D, ok, prm.scale, wv, g, n, uf[r]);
     } else {
 #pragma unroll
       for (int ct = 0; ct < NCT; ++ct) uf[r][ct] = bf16x4{};

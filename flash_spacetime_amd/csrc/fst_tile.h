@@ -195,23 +195,51 @@ __device__ __forceinline__ void zero_tile_rows(const EventSpec& ev, const RowAdd
     for (int idx = tid; idx < H * nr; idx += 256) vec[ra.vec(idx / nr, first + idx % nr)] = 0.f;
 }
 
+// The W operand of project_slots: lane (g, n) holds W[Qd g + s][channel(16
+// ct + n)], loaded once and shared by every row a kernel projects.
+template <int D, int C>
+struct WSlots {
+  float v[D / 4][C / 16];
+  __device__ __forceinline__ void load(const float* __restrict__ W, int g, int n) {
+#pragma unroll
+    for (int s = 0; s < D / 4; ++s)
+#pragma unroll
+      for (int ct = 0; ct < C / 16; ++ct) v[s][ct] = W[((D / 4) * g + s) * C + slot_channel<C>(16 * ct + n)];
+  }
+};
+
 // u = bf16(x @ W[:, channel(slot)]) for the heads of one row, x = row * mult
 // (q * scale or dO): fp32 MFMA with the head on lane n (heads >= H or an
 // invalid row give zeros); lane (g, n = h) receives slots 16 ct + 4 g .. +3.
 // xrow points at head 0 of the row, hstride is the element stride of heads.
 template <int D, int C>
 __device__ __forceinline__ void project_slots(const bf16* xrow, long hstride, bool ok, float mult,
-                                              const float* __restrict__ W, int g, int n, bf16x4* out) {
+                                              const WSlots<D, C>& wv, int g, int n, bf16x4* out) {
   constexpr int Qd = D / 4;
   float xv[Qd];
+  // Features Qd g .. Qd g + Qd - 1 of head n's row in 8- or 16-byte loads
+  // (a row holds D bf16, so they are aligned); a lane with !ok reads head 0.
   const bf16* p = xrow + (ok ? n * hstride : 0) + Qd * g;
+  if constexpr (Qd % 8 == 0) {
 #pragma unroll
-  for (int s = 0; s < Qd; ++s) xv[s] = ok ? (float)p[s] * mult : 0.f;
+    for (int t = 0; t < Qd / 8; ++t) {
+      const bf16x8 v = *reinterpret_cast<const bf16x8*>(p + 8 * t);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) xv[8 * t + e] = ok ? (float)v[e] * mult : 0.f;
+    }
+  } else {
+#pragma unroll
+    for (int t = 0; t < Qd / 4; ++t) {
+      const bf16x4 v = *reinterpret_cast<const bf16x4*>(p + 4 * t);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) xv[4 * t + e] = ok ? (float)v[e] * mult : 0.f;
+    }
+  }
 #pragma unroll
   for (int ct = 0; ct < C / 16; ++ct) {
     f32x4 a = zero4();
 #pragma unroll
-    for (int s = 0; s < Qd; ++s) a = mfma_f32(W[(Qd * g + s) * C + slot_channel<C>(16 * ct + n)], xv[s], a);
+    for (int s = 0; s < Qd; ++s) a = mfma_f32(wv.v[s][ct], xv[s], a);
     out[ct] = pack4(a);
   }
 }
