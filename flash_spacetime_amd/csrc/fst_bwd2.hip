@@ -58,9 +58,13 @@ struct Rows2Cfg {
   static constexpr int SCAL_BYTES = 16 * 17 * 4;
   static constexpr int TRASH_BYTES = 64 * 16;  // sink for the stores of padded-head lanes
   static constexpr int MAIN = E_BYTES + 2 * REGION + SCAL_BYTES + TRASH_BYTES;
-  static constexpr int DW_BYTES = 4 * (D * C + D) * 4;   // epilogue: per-wave dW / db partials
-  static constexpr int HG_BYTES = 2 * 16 * HP * 16 * 4;  // epilogue: one channel step of H and G
-  static constexpr int EPI = DW_BYTES + HG_BYTES;
+  // Epilogue: the tile's qt (or dO) rows, then per-wave dW / db partials in
+  // the same bytes; one channel step of H (or G) after them.
+  static constexpr int DW_BYTES = 4 * (D * C + D) * 4;
+  static constexpr int XS_BYTES = 16 * HP * D * 2;
+  static constexpr int X_DW = DW_BYTES > XS_BYTES ? DW_BYTES : XS_BYTES;
+  static constexpr int HG_BYTES = 16 * HP * 16 * 4;
+  static constexpr int EPI = X_DW + HG_BYTES;
   static constexpr int LDS_BYTES = MAIN > EPI ? MAIN : EPI;
   static constexpr bool FITS = LDS_BYTES <= 80 * 1024 && HP % 4 == 0;
 };
@@ -474,12 +478,14 @@ __global__ __launch_bounds__(256, 2) void bwd_rows2_kernel(BwdParams prm) {
 
   // ---- dW / db partial of this tile: sum over its rows and heads ----
   // dW[d, channel(slot)] += sum_(row, head) A[d, (row, head)] B[(row, head), slot]
-  // on fp32 MFMA: A = qt (resp. dO) with d on the lanes, B = H (resp. G) with
-  // the slot on the lanes, staged one channel step at a time as
-  // [row][head][16 slots].
+  // on fp32 MFMA: A = qt (then dO) with d on the lanes, read from the tile's
+  // rows staged by the head-owners ([row][head][D], zeros for invalid rows
+  // and heads); B = H (then G) with the slot on the lanes, staged one channel
+  // step at a time as [row][head][16 slots].
   __syncthreads();
-  float* Wred = reinterpret_cast<float*>(smem);
-  float* HGs = Wred + 4 * DCW;
+  float* Wred = reinterpret_cast<float*>(smem);  // after the products, over Xs
+  bf16* Xs = reinterpret_cast<bf16*>(smem);
+  float* HGs = reinterpret_cast<float*>(smem + Cfg::X_DW);
   if (use_e) {
     f32x4 dw[NQ][NCT];
     float dbl[NQ];
@@ -490,39 +496,37 @@ __global__ __launch_bounds__(256, 2) void bwd_rows2_kernel(BwdParams prm) {
       for (int ct = 0; ct < NCT; ++ct) dw[q][ct] = zero4();
     }
 #pragma unroll
-    for (int ct = 0; ct < NCT; ++ct) {
+    for (int op = 0; op < 2; ++op) {
+      if (!(op == 0 ? attn : act)) continue;
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int il = 4 * w + r;
-        if (n < HP) {
-          *reinterpret_cast<f32x4*>(HGs + (il * HP + n) * 16 + 4 * g) = Hacc[r][ct];
-          *reinterpret_cast<f32x4*>(HGs + 16 * HP * 16 + (il * HP + n) * 16 + 4 * g) = Gacc[r][ct];
-        }
+      for (int hl = 0; hl < HW; ++hl) {
+        const int h = w * HW + hl;
+        if (h < HP) (op == 0 ? qf[hl] : dof[hl]).store(Xs + (n * HP + h) * D, g);
       }
-      __syncthreads();
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int il = 4 * w + r;
-        const int row = i0 + il;
-        const bool rok = row < len;
+      for (int ct = 0; ct < NCT; ++ct) {
 #pragma unroll
-        for (int s4 = 0; s4 < HP / 4; ++s4) {
-          const int h = 4 * s4 + g;
-          const bool ok = rok && h < H;
-          const float bh = (attn && ok) ? HGs[(il * HP + h) * 16 + n] : 0.f;
-          const float bg = (act && ok) ? HGs[16 * HP * 16 + (il * HP + h) * 16 + n] : 0.f;
+        for (int r = 0; r < 4; ++r)
+          if (n < HP)
+            *reinterpret_cast<f32x4*>(HGs + ((4 * w + r) * HP + n) * 16 + 4 * g) = op == 0 ? Hacc[r][ct] : Gacc[r][ct];
+        __syncthreads();
 #pragma unroll
-          for (int q = 0; q < NQ; ++q) {
-            const int d = 16 * q + n;
-            const float aq = (attn && ok) ? (float)qg[ra.off(h, row, D) + d] * prm.scale : 0.f;
-            const float ao = (act && ok) ? (float)dog[ra.off(h, row, D) + d] : 0.f;
-            if (ct == 0) dbl[q] += ao;
-            dw[q][ct] = mfma_f32(aq, bh, dw[q][ct]);
-            dw[q][ct] = mfma_f32(ao, bg, dw[q][ct]);
+        for (int r = 0; r < 4; ++r) {
+          const int il = 4 * w + r;
+#pragma unroll
+          for (int s4 = 0; s4 < HP / 4; ++s4) {
+            const int h = 4 * s4 + g;
+            const float b = HGs[(il * HP + h) * 16 + n];
+#pragma unroll
+            for (int q = 0; q < NQ; ++q) {
+              const float a = (float)Xs[(il * HP + h) * D + 16 * q + n];
+              if (op == 1 && ct == 0) dbl[q] += a;
+              dw[q][ct] = mfma_f32(a, b, dw[q][ct]);
+            }
           }
         }
+        __syncthreads();
       }
-      __syncthreads();
     }
     float* wr = Wred + w * DCW;
 #pragma unroll

@@ -141,6 +141,13 @@ struct KFrag<bf16, K> {
 #pragma unroll
     for (int t = 0; t < N16; ++t) x16[t] = *reinterpret_cast<const bf16x4*>(p + 16 * t + 4 * g);
   }
+  // The inverse of load: this lane's slots back to element 0 of its row.
+  __device__ __forceinline__ void store(bf16* p, int g) const {
+#pragma unroll
+    for (int t = 0; t < N32; ++t) *reinterpret_cast<bf16x8*>(p + 32 * t + 8 * g) = x32[t];
+#pragma unroll
+    for (int t = 0; t < N16; ++t) *reinterpret_cast<bf16x4*>(p + 16 * t + 4 * g) = x16[t];
+  }
   // bf16(float(p[k]) * scale): the reference's q * scale before the cast.
   __device__ __forceinline__ void load_scaled(const bf16* p, int g, float scale) {
     load(p, g);

@@ -105,7 +105,9 @@ def test_backward_matches_oracle_fp32(shape, flags, masked):
 
 
 @pytest.mark.parametrize("shape", [(2, 96, 12, 32, 16), (2, 33, 4, 32, 32), (1, 64, 16, 48, 48),
-                                   (1, 130, 8, 64, 64)], ids=lambda s: "x".join(map(str, s)))
+                                   (1, 130, 8, 64, 64), (1, 70, 12, 64, 64), (1, 50, 16, 48, 64),
+                                   (1, 50, 16, 64, 48), (1, 40, 16, 64, 64)],
+                         ids=lambda s: "x".join(map(str, s)))
 @pytest.mark.parametrize("flags", FLAGS[:3], ids=["attn1act1", "attn1act0", "attn0act1"])
 @pytest.mark.parametrize("pos", ["normal", "detector"])
 def test_backward_bf16_relative(shape, flags, pos):
