@@ -35,7 +35,7 @@ struct Fwd2Cfg {
   static constexpr int NCT = C / 16;  // channel steps
   static constexpr int E_BYTES = ETile<C, KC>::BYTES;
   static constexpr int STAGE_BYTES = (KC / 4) * 16 * 16 * 16;  // fp32 u.E of KC keys per (row, head)
-  static constexpr int SCAL_BYTES = 16 * 17 * 4;
+  static constexpr int SCAL_BYTES = 16 * 17 * 4 + 16;  // rescale factors, then one flag per wave
   static constexpr int LDS_BYTES = E_BYTES + STAGE_BYTES + SCAL_BYTES;
   // OCC: workgroups per CU the register and LDS plan is built for.
   static constexpr bool FITS = LDS_BYTES <= (160 / OCC) * 1024 && HP % 4 == 0 && (KC == 16 || KC == 32);
@@ -53,6 +53,7 @@ __global__ __launch_bounds__(256, OCC) void fwd2_kernel(FwdParams prm) {
   bf16* Es = reinterpret_cast<bf16*>(smem);
   unsigned char* stage = smem + Cfg::E_BYTES;
   unsigned char* scal = stage + Cfg::STAGE_BYTES;
+  int* rflag = reinterpret_cast<int*>(scal + 16 * 17 * 4);  // wave w rescaled its heads this chunk
 
   const int tid = threadIdx.x;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63, g = lane >> 4, n = lane & 15;
@@ -227,25 +228,29 @@ __global__ __launch_bounds__(256, OCC) void fwd2_kernel(FwdParams prm) {
       }
     }
     // A row's reference m moves only when some key of the chunk exceeds it by
-    // more than 2^8; each lane tests its own keys, and only then is the row
-    // maximum formed across the lane groups.
+    // more than 2^8; each lane compares its own logits with the threshold,
+    // and only then is the row maximum formed across the lane groups.
     float mx[HW], alpha[HW];
     bool need_any = false;
 #pragma unroll
     for (int hl = 0; hl < HW; ++hl) {
-      float m = S[hl][0][0];
+      const float thr = (mref[hl] + kRescaleLog2) * kLn2;
 #pragma unroll
       for (int s = 0; s < NS; ++s)
 #pragma unroll
-        for (int r = 0; r < 4; ++r) m = fmaxf(m, S[hl][s][r]);
-      mx[hl] = m * kLog2e;
+        for (int r = 0; r < 4; ++r) need_any |= S[hl][s][r] > thr;
       alpha[hl] = 1.f;
-      need_any |= mx[hl] > mref[hl] + kRescaleLog2;
     }
-    if (__builtin_amdgcn_ballot_w64(need_any)) {
+    const bool rescale = __builtin_amdgcn_ballot_w64(need_any) != 0;
+    if (rescale) {
 #pragma unroll
       for (int hl = 0; hl < HW; ++hl) {
-        mx[hl] = group_allmax(mx[hl]);
+        float m = S[hl][0][0];
+#pragma unroll
+        for (int s = 0; s < NS; ++s)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) m = fmaxf(m, S[hl][s][r]);
+        mx[hl] = group_allmax(m * kLog2e);
         const float mnew = mx[hl] > mref[hl] + kRescaleLog2 ? mx[hl] : mref[hl];
         alpha[hl] = exp2f_fast(mref[hl] - mnew);
         mref[hl] = mnew;
@@ -293,21 +298,35 @@ __global__ __launch_bounds__(256, OCC) void fwd2_kernel(FwdParams prm) {
           for (int r = 0; r < 4; ++r) pv[r] = pf[hl].v[4 * s + r];
           *reinterpret_cast<bf16x4*>(stage + stage_off(2 * s + (g >> 1), n, h) + 8 * (g & 1)) = pv;
         }
-        if (g == 0) *reinterpret_cast<float*>(scal + scal_off(n, h)) = alpha[hl];
+        // Only a wave that rescaled writes its factors (the same value from
+        // every lane group); its flag tells the row-owners to read them.
+        if (rescale) *reinterpret_cast<float*>(scal + scal_off(n, h)) = alpha[hl];
       }
+      rflag[w] = rescale ? 1 : 0;
     }
     issue(j0 + KC);
     __syncthreads();  // P and rescale factors staged
 
     // ---- row-owner: A = alpha A + E^T P ----
     if (act) {
+      const int4 fl = *reinterpret_cast<const int4*>(rflag);
+      if (__builtin_amdgcn_readfirstlane(fl.x | fl.y | fl.z | fl.w)) {
+        // Rare: some head-owner moved its reference m this chunk. (The empty
+        // volatile asm keeps this a branch rather than selects.)
+        __asm__ volatile("");
+        const int ow = n / HW;  // the wave that owns head n
+        const bool fresh = n < H && (ow == 0 ? fl.x : ow == 1 ? fl.y : ow == 2 ? fl.z : fl.w) != 0;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const float al = *reinterpret_cast<const float*>(scal + scal_off(4 * w + r, n));
+          const float alpha = fresh ? al : 1.f;
+#pragma unroll
+          for (int ct = 0; ct < NCT; ++ct) AE[r][ct] = AE[r][ct] * alpha;
+        }
+      }
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         const int il = 4 * w + r;
-        // Lanes of padded heads (n >= H) read slots nobody wrote this chunk:
-        // their columns of A are never used, and alpha is taken as 1 there.
-        const float al = *reinterpret_cast<const float*>(scal + scal_off(il, n));
-        const float alpha = n < H ? al : 1.f;
         JFrag<bf16, NS> pr;
 #pragma unroll
         for (int s = 0; s < NS; ++s) {
@@ -315,10 +334,6 @@ __global__ __launch_bounds__(256, OCC) void fwd2_kernel(FwdParams prm) {
               *reinterpret_cast<const bf16x4*>(stage + stage_off(2 * s + (g >> 1), il, n) + 8 * (g & 1));
 #pragma unroll
           for (int e = 0; e < 4; ++e) pr.v[4 * s + e] = pv[e];
-        }
-        if (__builtin_amdgcn_ballot_w64(alpha != 1.f)) {
-#pragma unroll
-          for (int ct = 0; ct < NCT; ++ct) AE[r][ct] = AE[r][ct] * alpha;
         }
 #pragma unroll
         for (int ct = 0; ct < NCT; ++ct) {
