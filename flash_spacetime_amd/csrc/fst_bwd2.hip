@@ -54,10 +54,9 @@ template <int HP, int D, int C, int KC>
 struct Rows2Cfg {
   static constexpr int HW = HP / 4, NS = KC / 16, NCT = C / 16;
   static constexpr int E_BYTES = ETile<C, KC>::BYTES;
-  static constexpr int REGION = (KC / 4) * 16 * HP * 16;  // one fp32 term of KC keys per (row, head)
+  static constexpr int REGION = (KC / 4) * 16 * 16 * 16;  // one fp32 term of KC keys per (row, 16 head slots)
   static constexpr int SCAL_BYTES = 16 * 17 * 4;
-  static constexpr int TRASH_BYTES = 64 * 16;  // sink for the stores of padded-head lanes
-  static constexpr int MAIN = E_BYTES + 2 * REGION + SCAL_BYTES + TRASH_BYTES;
+  static constexpr int MAIN = E_BYTES + 2 * REGION + SCAL_BYTES;
   // Epilogue: the tile's qt (or dO) rows, then per-wave dW / db partials in
   // the same bytes; one channel step of H (or G) after them.
   static constexpr int DW_BYTES = 4 * (D * C + D) * 4;
@@ -81,7 +80,6 @@ __global__ __launch_bounds__(256, 2) void bwd_rows2_kernel(BwdParams prm) {
   unsigned char* stU = smem + Cfg::E_BYTES;  // u.E, then P
   unsigned char* stW = stU + Cfg::REGION;    // w~.E + dob, then dS
   unsigned char* scal = stW + Cfg::REGION;   // increments of D
-  const int trash = Cfg::E_BYTES + 2 * Cfg::REGION + Cfg::SCAL_BYTES + 16 * (threadIdx.x & 63);
 
   const int tid = threadIdx.x;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63, g = lane >> 4, n = lane & 15;
@@ -249,20 +247,19 @@ __global__ __launch_bounds__(256, 2) void bwd_rows2_kernel(BwdParams prm) {
             ef[ct] = embed_step<C>(xg[s][r], fa[ct], fb[ct], ct);
             ET::store(Es, 4 * w + r, ct, 16 * s + n, g, ef[ct]);
           }
-          // Lanes of heads past HP have no slot: they store into the sink,
-          // which keeps the phase free of branches.
-          const int so = hslot_off<HP>(4 * s + g, 4 * w + r, n);
+          // Lanes of heads past HP fill padding slots nobody reads.
+          const int so = stage_off(4 * s + g, 4 * w + r, n);
           if (attn) {
             f32x4 ue = zero4();
 #pragma unroll
             for (int ct = 0; ct < NCT; ++ct) ue = mfma_x16(ef[ct], uf[r][ct], ue);
-            *reinterpret_cast<f32x4*>(smem + (n < HP ? Cfg::E_BYTES + so : trash)) = ue;
+            *reinterpret_cast<f32x4*>(stU + so) = ue;
           }
           if (act) {
             f32x4 we = zero4();
 #pragma unroll
             for (int ct = 0; ct < NCT; ++ct) we = mfma_x16(ef[ct], wf[r][ct], we);
-            *reinterpret_cast<f32x4*>(smem + (n < HP ? Cfg::E_BYTES + Cfg::REGION + so : trash)) = we;
+            *reinterpret_cast<f32x4*>(stW + so) = we;
           }
         }
     }
@@ -284,8 +281,8 @@ __global__ __launch_bounds__(256, 2) void bwd_rows2_kernel(BwdParams prm) {
             S[b][s] = dP[b][s] = zero4();
             continue;
           }
-          const f32x4 ui = attn ? *reinterpret_cast<const f32x4*>(stU + hslot_off<HP>(4 * s + g, n, h)) : zero4();
-          const f32x4 wi = act ? *reinterpret_cast<const f32x4*>(stW + hslot_off<HP>(4 * s + g, n, h)) : zero4();
+          const f32x4 ui = attn ? *reinterpret_cast<const f32x4*>(stU + stage_off(4 * s + g, n, h)) : zero4();
+          const f32x4 wi = act ? *reinterpret_cast<const f32x4*>(stW + stage_off(4 * s + g, n, h)) : zero4();
           S[b][s] = mma_k<D>(kf[hl][s], qf[hl], ui);
           dP[b][s] = mma_k<D>(vf[hl][s], dof[hl], wi);
         }
@@ -363,7 +360,7 @@ __global__ __launch_bounds__(256, 2) void bwd_rows2_kernel(BwdParams prm) {
               pv[r] = pf[b].v[4 * s + r];
               dv[r] = dsf[b].v[4 * s + r];
             }
-            const int so = hslot_off<HP>(2 * s + (g >> 1), n, h) + 8 * (g & 1);
+            const int so = half_off(2 * s + (g >> 1), n, h, g & 1);
             *reinterpret_cast<bf16x4*>(stU + so) = pv;
             *reinterpret_cast<bf16x4*>(stW + so) = dv;
           }
@@ -386,7 +383,7 @@ __global__ __launch_bounds__(256, 2) void bwd_rows2_kernel(BwdParams prm) {
         JFrag<bf16, NS> pr, dr;
 #pragma unroll
         for (int s = 0; s < NS; ++s) {
-          const int so = hslot_off<HP>(2 * s + (g >> 1), il, hn) + 8 * (g & 1);
+          const int so = half_off(2 * s + (g >> 1), il, hn, g & 1);
           const bf16x4 pv = *reinterpret_cast<const bf16x4*>(stU + so);
           const bf16x4 dv = *reinterpret_cast<const bf16x4*>(stW + so);
 #pragma unroll
@@ -440,7 +437,7 @@ __global__ __launch_bounds__(256, 2) void bwd_rows2_kernel(BwdParams prm) {
 #pragma unroll
           for (int sp = 0; sp < 4; ++sp)
             acc = mfma_f32(prm.weight[dn * C + slot_channel<C>(16 * ct + 4 * g + sp)], Hacc[r][ct][sp], acc);
-        if (n < HP) *reinterpret_cast<f32x4*>(stU + hslot_off<HP>(g, 4 * w + r, n)) = acc;
+        *reinterpret_cast<f32x4*>(stU + stage_off(g, 4 * w + r, n)) = acc;
       }
       __syncthreads();
     }
@@ -449,7 +446,7 @@ __global__ __launch_bounds__(256, 2) void bwd_rows2_kernel(BwdParams prm) {
       const int h = w * HW + hl;
       f32x4 o = dQ[hl][q];
       if (attn && h < H) {
-        o = o + *reinterpret_cast<const f32x4*>(stU + hslot_off<HP>(g, n, h));
+        o = o + *reinterpret_cast<const f32x4*>(stU + stage_off(g, n, h));
         if (prm.bias) {
 #pragma unroll
           for (int r = 0; r < 4; ++r) o[r] = __builtin_fmaf(sig[hl], prm.bias[DT::dmap(q, g, r)], o[r]);

@@ -296,7 +296,7 @@ __global__ __launch_bounds__(256, OCC) void fwd2_kernel(FwdParams prm) {
           bf16x4 pv;
 #pragma unroll
           for (int r = 0; r < 4; ++r) pv[r] = pf[hl].v[4 * s + r];
-          *reinterpret_cast<bf16x4*>(stage + stage_off(2 * s + (g >> 1), n, h) + 8 * (g & 1)) = pv;
+          *reinterpret_cast<bf16x4*>(stage + half_off(2 * s + (g >> 1), n, h, g & 1)) = pv;
         }
         // Only a wave that rescaled writes its factors (the same value from
         // every lane group); its flag tells the row-owners to read them.
@@ -331,7 +331,7 @@ __global__ __launch_bounds__(256, OCC) void fwd2_kernel(FwdParams prm) {
 #pragma unroll
         for (int s = 0; s < NS; ++s) {
           const bf16x4 pv =
-              *reinterpret_cast<const bf16x4*>(stage + stage_off(2 * s + (g >> 1), il, n) + 8 * (g & 1));
+              *reinterpret_cast<const bf16x4*>(stage + half_off(2 * s + (g >> 1), il, n, g & 1));
 #pragma unroll
           for (int e = 0; e < 4; ++e) pr.v[4 * s + e] = pv[e];
         }

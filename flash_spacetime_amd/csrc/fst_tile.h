@@ -329,15 +329,16 @@ __device__ __forceinline__ void wait_vmem() { asm volatile("s_waitcnt vmcnt(0)" 
 // ---------------------------------------------------------------------------
 
 // Embedding tile: [row 16][ct][key KC][16 slots] bf16. The four 8-byte blocks
-// (slot groups) of key j are stored in the order b ^ (2 * ((j >> 3) & 1)):
-// writes of 16 keys x 2 lane groups and transposing reads of 8 keys x 4
-// blocks then each cover 256 distinct bytes.
+// (slot groups) of key j are stored in the order b ^ ((j >> 2) & 3): an
+// 8-byte write pass (16 keys of one block, 32 bytes apart) then covers the 32
+// banks of a pass once, and a transposing read of 8 keys x 4 blocks covers
+// 256 contiguous bytes.
 template <int C, int KC>
 struct ETile {
   static constexpr int NCT = C / 16;
   static constexpr int BYTES = 16 * NCT * KC * 16 * 2;
   static __device__ __forceinline__ int off(int row, int ct, int key, int blk) {
-    return (((row * NCT + ct) * KC + key) << 4) + ((blk ^ (((key >> 3) & 1) << 1)) << 2);
+    return (((row * NCT + ct) * KC + key) << 4) + ((blk ^ ((key >> 2) & 3)) << 2);
   }
   static __device__ __forceinline__ void store(bf16* e, int row, int ct, int key, int g, bf16x4 v) {
     *reinterpret_cast<bf16x4*>(e + off(row, ct, key, g)) = v;
@@ -354,20 +355,15 @@ struct ETile {
 // Exchange slots between the row-major and head-major roles: 16-byte chunk c
 // of slot (row i, head h) at ((c * 16 + i) * 16 + (h ^ i)) * 16 bytes. With
 // the head index on the lanes (fixed row) or the row index on the lanes
-// (fixed head) a pass of 16 lanes writes or reads 16 distinct 16-byte bank
-// groups. Heads are padded to 16 slots.
+// (fixed head) the lanes of one LDS pass (8 per 16-byte write, 16 per
+// 16-byte read) hit distinct banks. Heads are padded to 16 slots.
 __device__ __forceinline__ int stage_off(int c, int i, int h) { return (((c << 4) + i) << 8) + ((h ^ i) << 4); }
 
-// The same exchange with heads padded only to HP: 16-byte chunk c of slot
-// (row i, head h) at ((c * 16 + i) * HP + (h + (i >> SH)) % HP) * 16 bytes;
-// the rotation by i >> SH keeps both access patterns on 16 distinct 16-byte
-// bank groups for HP in {4, 8, 12, 16}. h must be < HP.
-template <int HP>
-__device__ __forceinline__ int hslot_off(int c, int i, int h) {
-  constexpr int SH = HP == 8 ? 1 : (HP == 16 ? 0 : 2);
-  int hh = h + (i >> SH);
-  hh = hh >= HP ? hh - HP : hh;
-  return (((c << 4) + i) * HP + hh) << 4;
+// One 8-byte half of such a slot (P and dS, bf16): half `half` of lane group
+// g & 1, swapped when (h ^ i) >= 8, so that the 16 lanes of one 8-byte write
+// pass (rows on the lanes) cover the 32 banks of a pass exactly once.
+__device__ __forceinline__ int half_off(int c, int i, int h, int half) {
+  return stage_off(c, i, h) + ((half ^ (((h ^ i) >> 3) & 1)) << 3);
 }
 
 // Per-(row, head) scalars (rescale factors): [head][17].
