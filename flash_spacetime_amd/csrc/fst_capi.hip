@@ -217,17 +217,27 @@ __global__ __launch_bounds__(256) void dw_reduce_seg_kernel(const float* part, c
   const long w0 = (long)blockIdx.y * kRedSeg;
   const long w1 = w0 + kRedSeg < nblk ? w0 + kRedSeg : nblk;
   float acc = 0.f;
+#pragma unroll 8
   for (long w = w0; w < w1; ++w) acc += part[w * ncol + col];
   seg[(long)blockIdx.y * ncol + col] = acc;
 }
 
+// Stage 2: a workgroup per 64 columns; thread (q, c) sums runs q, q + 4, ...
+// of column c, and the four partial sums are added in the order q = 0..3.
 __global__ __launch_bounds__(256) void dw_reduce_final_kernel(const float* seg, int nseg, int DC, int D, int use_e,
                                                               float* dw, float* db) {
-  const int e = blockIdx.x * 256 + threadIdx.x;
-  if (e >= DC + D) return;
+  __shared__ float part[4][64];
+  const int c = threadIdx.x & 63, q = threadIdx.x >> 6;
+  const int e = blockIdx.x * 64 + c;
   float acc = 0.f;
-  if (use_e)
-    for (int s = 0; s < nseg; ++s) acc += seg[(long)s * (DC + D) + e];
+  if (use_e && e < DC + D) {
+#pragma unroll 8
+    for (int s = q; s < nseg; s += 4) acc += seg[(long)s * (DC + D) + e];
+  }
+  part[q][c] = acc;
+  __syncthreads();
+  if (q != 0 || e >= DC + D) return;
+  acc = ((part[0][c] + part[1][c]) + part[2][c]) + part[3][c];
   if (e < DC)
     dw[e] = acc;
   else if (db)
@@ -499,7 +509,7 @@ int fst_backward_phases(int phases, int dtype, int flags, int B, int H, int L, i
     if (use_w && lay.nseg > 0)
       hipLaunchKernelGGL(dw_reduce_seg_kernel, dim3((ncol + 255) / 256, (unsigned)lay.nseg), dim3(256), 0, st,
                          prm.dw_part, bc_r, B, ncol, seg);
-    hipLaunchKernelGGL(dw_reduce_final_kernel, dim3((ncol + 255) / 256), dim3(256), 0, st, seg, (int)lay.nseg, DC,
+    hipLaunchKernelGGL(dw_reduce_final_kernel, dim3((ncol + 63) / 64), dim3(256), 0, st, seg, (int)lay.nseg, DC,
                        D, use_w ? 1 : 0, dweight, dbias);
     if (hipGetLastError() != hipSuccess) return fail(FST_ELAUNCH, "dW reduction launch failed");
   }
