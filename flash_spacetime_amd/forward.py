@@ -52,6 +52,20 @@ def lengths_from_mask(mask: Tensor, length: int) -> Tensor:
     return seqlens
 
 
+def _valid_from_mask(mask: Tensor, length: int) -> Tensor:
+    """`[B, L]` bool validity (True = valid token) of a padding mask."""
+    if mask.dim() != 2 or mask.shape[1] != length:
+        raise ValueError(f"key_padding_mask must be [B, L={length}], got {tuple(mask.shape)}")
+    return ~mask if mask.dtype == torch.bool else (mask == 0)
+
+
+def _is_front_packed(valid: Tensor) -> bool:
+    """Whether every event's valid tokens form a prefix (one device readback)."""
+    seqlens = valid.sum(1, dtype=torch.int32)
+    prefix = torch.arange(valid.shape[1], device=valid.device)[None, :] < seqlens[:, None]
+    return bool(torch.equal(prefix, valid))
+
+
 def _resolve_lengths(seqlens: Optional[Tensor], key_padding_mask: Optional[Tensor], batch: int,
                      length: int) -> Tensor:
     if key_padding_mask is not None and seqlens is not None:
@@ -271,14 +285,50 @@ def flash_spacetime_attention(
 
     Semantics of `spacetime_attention_reference` on valid rows; padding rows
     of the output are exactly zero. The 7th argument is the `[B]` integer
-    tensor of valid lengths; a front-packed `[B, L]` padding mask may be
-    given instead, positionally or as `key_padding_mask=`.
+    tensor of valid lengths; a `[B, L]` padding mask (bool, True = padding,
+    or the 0 / -inf float mask) may be given instead, positionally or as
+    `key_padding_mask=`. A front-packed mask becomes lengths (one readback);
+    a mask with holes runs the packed kernels on the gathered valid tokens.
     """
-    if key_padding_mask is not None:
-        seqlens = _resolve_lengths(seqlens, key_padding_mask, q.shape[0], q.shape[2])
+    mask = key_padding_mask
+    if mask is None and seqlens is not None and seqlens.dim() == 2:
+        mask = seqlens
+        seqlens = None
+    if mask is not None:
+        if seqlens is not None:
+            raise ValueError("pass either seqlens or key_padding_mask, not both")
+        valid = _valid_from_mask(mask, q.shape[2])
+        if not _is_front_packed(valid):
+            return _attention_scattered(q, k, v, feats, weight, bias, valid, scale, use_attn_bias,
+                                        use_activation_bias)
+        seqlens = valid.sum(1, dtype=torch.int32)
     return _FlashSpacetimeAttention.apply(
         q, k, v, feats, weight, bias, seqlens, scale, use_attn_bias, use_activation_bias, None
     )
+
+
+def _attention_scattered(q, k, v, feats, weight, bias, valid, scale, use_attn_bias, use_activation_bias):
+    """A padding mask whose valid tokens are not a prefix of each event.
+
+    The spec's semantics (reference.py:106-167: padding keys masked out,
+    padding rows zero in the kernel's contract) depend only on which tokens
+    are valid and on their features, not on their slots: the valid tokens of
+    every event are gathered in order into the packed layout, run through the
+    packed kernels, and the rows scattered back (padding rows zero). The
+    gather and scatter are torch index operations on the device and reading
+    the token count back is one host synchronisation.
+    """
+    b, h, length, d = q.shape
+    if feats.dim() != 3 or feats.shape[:2] != (b, length):
+        raise ValueError(f"feats must be [B, L, F>=4], got {tuple(feats.shape)}")
+    counts = valid.sum(1, dtype=torch.int32)
+    cu = torch.zeros(b + 1, dtype=torch.int32, device=q.device)
+    cu[1:] = torch.cumsum(counts, 0, dtype=torch.int32)
+    rows = lambda x: x.transpose(1, 2)[valid]  # [T, H, D], events and tokens in order
+    out = flash_spacetime_attention_varlen(rows(q), rows(k), rows(v), feats[valid], weight, bias, cu, scale,
+                                           use_attn_bias, use_activation_bias)
+    full = out.new_zeros(b, length, h, d).index_put((valid,), out)
+    return full.transpose(1, 2).contiguous()
 
 
 def flash_spacetime_attention_varlen(
@@ -288,7 +338,7 @@ def flash_spacetime_attention_varlen(
     feats: Tensor,
     weight: Tensor,
     bias: Optional[Tensor],
-    cu_seqlens: Tensor,
+    cu_seqlens: Optional[Tensor] = None,
     scale: Optional[float] = None,
     use_attn_bias: bool = True,
     use_activation_bias: bool = True,
@@ -299,7 +349,28 @@ def flash_spacetime_attention_varlen(
     `cu_seqlens` (`[B+1]` token offsets, cu[0] = 0, cu[-1] = T) -- the values
     layout of a jagged NestedTensor. No padding exists and event lengths are
     unbounded; nothing is read back to the host.
+
+    q, k and v may instead be `torch.nested` jagged tensors `[B, j, H, D]`
+    (feats jagged `[B, j, F]` or its `[T, F]` values): the events are then
+    the nested tensor's, `cu_seqlens` may be omitted (or must equal its
+    offsets), and the output is a jagged tensor with the same offsets.
     """
+    if q.is_nested:
+        if not (k.is_nested and v.is_nested):
+            raise ValueError("q, k and v must all be nested tensors, or none of them")
+        if q.layout != torch.jagged or q.dim() != 4:
+            raise ValueError("nested q, k, v must be jagged [B, j, H, D] tensors (torch.jagged layout)")
+        offsets = q.offsets()
+        if cu_seqlens is None:
+            cu_seqlens = offsets
+        fv = feats.values() if feats.is_nested else feats
+        out = _FlashSpacetimeAttention.apply(
+            q.values(), k.values(), v.values(), fv, weight, bias, None, scale, use_attn_bias,
+            use_activation_bias, cu_seqlens
+        )
+        return torch.nested.nested_tensor_from_jagged(out, offsets)
+    if cu_seqlens is None:
+        raise ValueError("cu_seqlens is required for dense packed inputs")
     return _FlashSpacetimeAttention.apply(
         q, k, v, feats, weight, bias, None, scale, use_attn_bias, use_activation_bias, cu_seqlens
     )

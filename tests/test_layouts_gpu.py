@@ -1,0 +1,143 @@
+"""GPU tests of the input formats the build adds to the reference's API.
+
+* `torch.nested` jagged q / k / v (and feats) for the packed operator: the
+  result and every gradient are bitwise those of the dense packed call on the
+  same values and offsets.
+* Padding masks whose valid tokens are not a prefix of each event (the
+  reference accepts front-packed lengths only): valid rows and all gradients
+  against the float64 oracle evaluated with the same mask (`pair_mask`, the
+  spec's one-sided key mask), padding rows exactly zero.
+"""
+
+import pytest
+import torch
+
+import oracle
+from tests._cases import FLAGS, make_packed, make_padded, rel_err, seed_of
+
+pytestmark = pytest.mark.gpu
+
+if torch.cuda.is_available():
+    from flash_spacetime_amd import flash_spacetime_attention, flash_spacetime_attention_varlen
+
+
+def _holey_mask(batch: int, length: int, seed: int) -> torch.Tensor:
+    """[B, L] validity with holes: ~60 % valid, every event non-empty, one
+    event fully valid and one with a single valid token in the middle."""
+    gen = torch.Generator().manual_seed(seed)
+    valid = torch.rand(batch, length, generator=gen) < 0.6
+    valid[:, length // 2] = True
+    valid[0] = True
+    if batch > 1:
+        valid[-1] = False
+        valid[-1, length // 3] = True
+    return valid
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16], ids=["fp32", "bf16"])
+@pytest.mark.parametrize("flags", FLAGS[:3], ids=["attn1act1", "attn1act0", "attn0act1"])
+def test_holey_mask_matches_oracle(dtype, flags):
+    shape = (3, 70, 4, 32, 16)
+    case = make_padded(*shape, seed=seed_of("holes", dtype, flags), masked=False)
+    valid = _holey_mask(shape[0], shape[1], seed_of("holes-mask", dtype, flags))
+    # The reference is evaluated on the dtype-rounded inputs, which isolates
+    # the kernel's own error from input quantisation.
+    for key in ("q", "k", "v", "weight", "bias"):
+        case[key] = case[key].to(dtype).double()
+    names = {"q": "q", "k": "k", "v": "v", "W": "weight", "b": "bias"}
+    dev = "cuda"
+    leaves = {n: case[c].to(dev, dtype).requires_grad_(True) for n, c in names.items()}
+    out = flash_spacetime_attention(
+        leaves["q"], leaves["k"], leaves["v"], case["feats"].to(dev), leaves["W"], leaves["b"],
+        key_padding_mask=~valid.to(dev), use_attn_bias=flags[0], use_activation_bias=flags[1],
+    )
+    vm = valid[:, None, :, None].expand(out.shape)
+    gw = torch.randn(out.shape, dtype=torch.float64, generator=torch.Generator().manual_seed(3)) * vm
+    (out.double() * gw.to(dev)).sum().backward()
+
+    ref_leaves = {n: case[c].clone().requires_grad_(True) for n, c in names.items()}
+    ref = oracle.attention(
+        ref_leaves["q"], ref_leaves["k"], ref_leaves["v"], case["feats"], ref_leaves["W"], ref_leaves["b"],
+        key_padding_mask=oracle.float_padding_mask(valid, torch.float64),
+        use_attn_bias=flags[0], use_activation_bias=flags[1],
+    )
+    (ref * gw).sum().backward()
+
+    got = out.detach().cpu()
+    assert (got[~vm] == 0).all(), "padding rows must be exactly zero"
+    tol = 2e-2 if dtype == torch.bfloat16 else 1e-4
+    err = rel_err(got * vm, ref.detach() * vm)
+    assert err <= tol, f"output: relative error {err:.3e}"
+    # fp32 gradients: 1e-3, the bound the fp32 large-logit test also uses
+    # (sums over the event of E-weighted terms).
+    gtol = 2e-2 if dtype == torch.bfloat16 else 1e-3
+    keys = ["q", "k", "v"] + (["W"] if (flags[0] or flags[1]) else []) + (["b"] if flags[1] else [])
+    if flags[0] and not flags[1]:
+        # b enters only through the row-constant logit term qt.b: db = 0
+        # (backward.py:616-622); the float64 oracle's value is rounding noise.
+        assert leaves["b"].grad is None or (leaves["b"].grad == 0).all()
+        assert ref_leaves["b"].grad.abs().max().item() < 1e-9
+    for key in keys:
+        g = leaves[key].grad
+        assert g is not None and torch.isfinite(g).all(), key
+        err = rel_err(g, ref_leaves[key].grad)
+        assert err <= gtol, f"grad {key}: relative error {err:.3e}"
+
+
+def test_front_packed_mask_keeps_the_lengths_path():
+    """A front-packed mask and its lengths give bitwise the same result; a mask
+    with holes agrees with the same events packed by hand."""
+    shape = (3, 40, 4, 32, 16)
+    case = make_padded(*shape, seed=seed_of("mask-paths"))
+    dev = "cuda"
+    g = {k: case[k].to(dev, torch.bfloat16) for k in ("q", "k", "v", "weight", "bias")}
+    feats = case["feats"].to(dev)
+    valid = oracle.valid_row_mask(3, 40, case["seqlens"]).to(dev)
+    base = flash_spacetime_attention(g["q"], g["k"], g["v"], feats, g["weight"], g["bias"],
+                                     case["seqlens"].to(dev))
+    by_mask = flash_spacetime_attention(g["q"], g["k"], g["v"], feats, g["weight"], g["bias"],
+                                        key_padding_mask=~valid)
+    assert torch.equal(base, by_mask)
+
+    holey = _holey_mask(3, 40, seed_of("mask-paths-holes")).to(dev)
+    out = flash_spacetime_attention(g["q"], g["k"], g["v"], feats, g["weight"], g["bias"],
+                                    key_padding_mask=~holey)
+    counts = holey.sum(1).tolist()
+    cu = torch.tensor([0] + torch.tensor(counts).cumsum(0).tolist(), dtype=torch.int32, device=dev)
+    rows = lambda x: x.transpose(1, 2)[holey]
+    packed = flash_spacetime_attention_varlen(rows(g["q"]), rows(g["k"]), rows(g["v"]), feats[holey],
+                                              g["weight"], g["bias"], cu)
+    assert torch.equal(out.transpose(1, 2)[holey], packed)
+    assert (out.transpose(1, 2)[~holey] == 0).all()
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16], ids=["fp32", "bf16"])
+def test_nested_inputs_match_dense_packed(dtype):
+    lengths = [17, 64, 1, 200, 33]
+    case = make_packed(lengths, 4, 32, 16, seed_of("nested", dtype))
+    dev = "cuda"
+    cu = case["cu"].to(dev)
+    gw = torch.randn(case["q"].shape, generator=torch.Generator().manual_seed(5)).to(dev, dtype)
+
+    def run(nested: bool):
+        leaves = {k: case[k].to(dev, dtype).requires_grad_(True) for k in ("q", "k", "v")}
+        w = case["weight"].to(dev, dtype).requires_grad_(True)
+        b = case["bias"].to(dev, dtype).requires_grad_(True)
+        feats = case["feats"].to(dev)
+        if nested:
+            offs = cu.long()
+            nt = {k: torch.nested.nested_tensor_from_jagged(x, offs) for k, x in leaves.items()}
+            fnt = torch.nested.nested_tensor_from_jagged(feats, offs)
+            out_nt = flash_spacetime_attention_varlen(nt["q"], nt["k"], nt["v"], fnt, w, b)
+            assert out_nt.is_nested and torch.equal(out_nt.offsets(), offs)
+            out = out_nt.values()
+        else:
+            out = flash_spacetime_attention_varlen(leaves["q"], leaves["k"], leaves["v"], feats, w, b, cu)
+        (out.float() * gw.float()).sum().backward()
+        return out.detach(), [leaves[k].grad for k in ("q", "k", "v")] + [w.grad, b.grad]
+
+    out_d, grads_d = run(False)
+    out_n, grads_n = run(True)
+    assert torch.equal(out_d, out_n)
+    for a, b in zip(grads_d, grads_n):
+        assert torch.equal(a, b)
