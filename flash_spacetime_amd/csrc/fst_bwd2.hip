@@ -552,21 +552,56 @@ struct Cols2Cfg {
   static constexpr int HW = HP / 4, NS = RC / 16, NCT = C / 16;
   static constexpr int RG = RC / 4;     // row groups per chunk
   static constexpr int RGW = RC / 16;   // row groups per row-owner wave
-  static constexpr int REGION = RG * 16 * 16 * 16;  // one fp32 term: [row group][16 heads][key] x 4 rows
+  static constexpr int REGION = RG * HP * 16 * 16;  // one fp32 term: [row group][HP heads][key] x 4 rows
   static constexpr int SCAL_BYTES = 2 * RC * 16 * 4;  // lse * log2(e) and D - dob: [term][head][row]
-  static constexpr int LDS_BYTES = 2 * REGION + SCAL_BYTES;
+  static constexpr int BASE_BYTES = 2 * REGION + SCAL_BYTES;
+  // QL: the chunk's qt and dO rows are staged in LDS (QoTile), so both their
+  // row-major and transposed operand fragments are LDS reads; otherwise they
+  // stream through registers and are transposed on the matrix core.
+  static constexpr int QO_BYTES = 2 * HP * (D / 32) * 1024;
+  static constexpr bool QL = D % 32 == 0 && RC == 16 && BASE_BYTES + QO_BYTES <= 80 * 1024;
+  static constexpr int LDS_BYTES = BASE_BYTES + (QL ? QO_BYTES : 0);
   static constexpr bool FITS = LDS_BYTES <= 80 * 1024 && HP % 4 == 0;
+  // Workgroups per CU the register plan is built for: three for the small
+  // head layouts whose staged tiles fit a third of the LDS.
+  static constexpr int OCC = (QL && HP <= 12 && D <= 32 && C <= 16 && LDS_BYTES <= 160 * 1024 / 3) ? 3 : 2;
+};
+
+// qt / dO rows of one 16-row chunk in LDS: per (tensor, head, 32-feature part)
+// a 1 KB block of 16 rows x 4 16-byte quarters, quarter c of row r at slot
+// 4 r + (c ^ ((r >> 2) & 3)). A 16-byte read of quarter g by the 16 rows of
+// a lane group, and the transposing 8-byte read of 4 rows x 4 quarters, both
+// hit distinct banks. One direct-to-LDS load (lane l -> slot l) fills a block.
+struct QoTile {
+  static __device__ __forceinline__ int slot(int r, int c) { return 4 * r + (c ^ ((r >> 2) & 3)); }
+  // Row-major fragment part (row n, features 8g .. 8g + 7 of the part).
+  static __device__ __forceinline__ bf16x8 row_frag(const unsigned char* blk, int g, int n) {
+    return *reinterpret_cast<const bf16x8*>(blk + 16 * slot(n, g));
+  }
+  // Transposed 16x16 operand of 16-feature slice q of the part (q & 1 picks
+  // the half of each quarter): lane (g, n) receives rows 4g .. 4g + 3 of the
+  // feature the row-major fragment's slice q holds in slot n (DTiles::dmap).
+  // Source lane s of the group supplies row 4g + s / 4, features 8 (s % 4) +
+  // 4 (q & 1) .. +3 of the part.
+  static __device__ __forceinline__ bf16x4 tr_frag(const unsigned char* blk, int q, int g, int n) {
+    const int r = 4 * g + (n >> 2);
+    const unsigned char* p = blk + 16 * slot(r, n & 3) + 8 * (q & 1);
+    return __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4*)(p));
+  }
 };
 
 template <int HP, int D, int C, int RC, int FL>
-__global__ __launch_bounds__(256, 2) void bwd_cols2_kernel(BwdParams prm) {
+__global__ __launch_bounds__(256, (Cols2Cfg<HP, D, C, RC>::OCC)) void bwd_cols2_kernel(BwdParams prm) {
   using Cfg = Cols2Cfg<HP, D, C, RC>;
   using DT = DTiles<D>;
   constexpr int HW = Cfg::HW, NS = Cfg::NS, NCT = Cfg::NCT, NQ = DT::NQ, RGW = Cfg::RGW;
+  constexpr bool QL = Cfg::QL;
+  constexpr int NP = D / 32;  // 32-feature parts of a row (QL)
   extern __shared__ __align__(16) unsigned char smem[];
   unsigned char* stU = smem;                 // u.E
   unsigned char* stW = smem + Cfg::REGION;   // w~.E
   float* rsc = reinterpret_cast<float*>(smem + 2 * Cfg::REGION);  // per-row scalars of the chunk
+  unsigned char* qo = smem + Cfg::BASE_BYTES;  // QL: [qt, dO][head][part] QoTile blocks
 
   const int tid = threadIdx.x;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63, g = lane >> 4, n = lane & 15;
@@ -646,7 +681,7 @@ __global__ __launch_bounds__(256, 2) void bwd_cols2_kernel(BwdParams prm) {
   for (int hl = 0; hl < HW; ++hl)
     qvo[hl] = (int)(min(w * HW + hl, H - 1) * ra.hs * D * 2) + n * rowb + kfrag_goff<D>(g);
 
-  KFrag<bf16, D> qr[HW][NS], orw[HW][NS];
+  KFrag<bf16, D> qr[QL ? 1 : HW][NS], orw[QL ? 1 : HW][NS];
   // Per-row scalars (lse * log2 e and D - dob) of the next chunk: thread t
   // loads item t of the chunk's RC x H values of each (coalesced), and writes
   // it to LDS at the start of that chunk; the head-owners read four rows at a
@@ -659,17 +694,41 @@ __global__ __launch_bounds__(256, 2) void bwd_cols2_kernel(BwdParams prm) {
   const bool sc_ok = tid < RC * H;
   const int sc_hc = min(sc_h, H - 1);
   float4 prow[RGW];
+  // QL: the wave's heads' qt and dO rows of a chunk go straight to LDS, lane
+  // l of a block load fetching the quarter QoTile keeps in slot l; rows past
+  // the event are clamped to its last row.
+  const int qo_r = lane >> 2, qo_c = (lane & 3) ^ ((qo_r >> 2) & 3);
+  auto issue_qo = [&](int in) __attribute__((always_inline)) {
+    if constexpr (QL) {
+      const bool full = in + RC <= len;
+      const int rel = full ? qo_r * rowb : (min(in + qo_r, last)) * rowb;
+      const int soff = full ? in * rowb : 0;
+#pragma unroll
+      for (int hl = 0; hl < HW; ++hl) {
+        const int h = w * HW + hl;
+        const int voff = (int)(min(h, H - 1) * ra.hs * D * 2) + rel + 16 * qo_c;
+#pragma unroll
+        for (int t = 0; t < NP; ++t) {
+          __builtin_amdgcn_raw_ptr_buffer_load_lds(qbuf.r, (__attribute__((address_space(3))) void*)(qo + ((0 * HP + h) * NP + t) * 1024),
+                                                   16, voff + 64 * t, soff, 0, 0);
+          __builtin_amdgcn_raw_ptr_buffer_load_lds(obuf.r, (__attribute__((address_space(3))) void*)(qo + ((1 * HP + h) * NP + t) * 1024),
+                                                   16, voff + 64 * t, soff, 0, 0);
+        }
+      }
+    }
+  };
   auto issue = [&](int in) __attribute__((always_inline)) {
-    const bool full = in + RC <= len;
+    if constexpr (!QL) {
+      const bool full = in + RC <= len;
 #pragma unroll
-    for (int hl = 0; hl < HW; ++hl) {
-      const int h = min(w * HW + hl, H - 1);
+      for (int hl = 0; hl < HW; ++hl) {
 #pragma unroll
-      for (int s = 0; s < NS; ++s) {
-        const int voff = full ? qvo[hl] + 16 * s * rowb : qvo[hl] + (min(in + 16 * s + n, last) - n) * rowb;
-        const int soff = full ? in * rowb : 0;
-        load_kfrag<D>(qr[hl][s], qbuf, voff, soff);
-        load_kfrag<D>(orw[hl][s], obuf, voff, soff);
+        for (int s = 0; s < NS; ++s) {
+          const int voff = full ? qvo[hl] + 16 * s * rowb : qvo[hl] + (min(in + 16 * s + n, last) - n) * rowb;
+          const int soff = full ? in * rowb : 0;
+          load_kfrag<D>(qr[hl][s], qbuf, voff, soff);
+          load_kfrag<D>(orw[hl][s], obuf, voff, soff);
+        }
       }
     }
     {
@@ -717,6 +776,7 @@ __global__ __launch_bounds__(256, 2) void bwd_cols2_kernel(BwdParams prm) {
 
   auto chunk = [&](int i0c, auto tail_tag) __attribute__((always_inline)) {
     constexpr bool TAIL = decltype(tail_tag)::value;
+    issue_qo(i0c);  // lands during the row-owner part
     // ---- row-owner: u_i E_i^T and w~_i E_i^T for its row groups ----
     if (use_e) {
 #pragma unroll
@@ -740,18 +800,23 @@ __global__ __launch_bounds__(256, 2) void bwd_cols2_kernel(BwdParams prm) {
         // lane (g, key n) holds heads 4g + e of rows r: regroup by head.
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-          const int so = ((rg * 16 + 4 * g + e) * 16 + n) * 16;
-          if (attn) *reinterpret_cast<f32x4*>(stU + so) = f32x4{ue[0][e], ue[1][e], ue[2][e], ue[3][e]};
-          if (act) *reinterpret_cast<f32x4*>(stW + so) = f32x4{we[0][e], we[1][e], we[2][e], we[3][e]};
+          // Heads past HP (lane groups g >= HP / 4) have no slot.
+          const int so = ((rg * HP + 4 * g + e) * 16 + n) * 16;
+          if (4 * g < HP) {
+            if (attn) *reinterpret_cast<f32x4*>(stU + so) = f32x4{ue[0][e], ue[1][e], ue[2][e], ue[3][e]};
+            if (act) *reinterpret_cast<f32x4*>(stW + so) = f32x4{we[0][e], we[1][e], we[2][e], we[3][e]};
+          }
         }
       }
     }
-    issue_rows(i0c + RC);
+    if constexpr (!QL) issue_rows(i0c + RC);
     if (sc_ok) {
       rsc[sc_h * RC + sc_r] = i0c + sc_r < len ? sc_lraw * kLog2e : INFINITY;  // rows past the event: P = 0
       rsc[16 * RC + sc_h * RC + sc_r] = sc_draw;
     }
-    __syncthreads();  // u.E, w~.E and the row scalars staged
+    if constexpr (QL) wait_vmem();  // this wave's direct-to-LDS rows have landed
+    __syncthreads();  // u.E, w~.E, the row scalars (and the qt / dO rows) staged
+    if constexpr (QL) issue_rows(i0c + RC);
 
     // ---- head-owner: P, dS, dV^T += dO^T P, dK^T += Qt^T dS ----
     f32x4 S[HW][NS], dP[HW][NS];
@@ -760,11 +825,22 @@ __global__ __launch_bounds__(256, 2) void bwd_cols2_kernel(BwdParams prm) {
       const int h = w * HW + hl;
 #pragma unroll
       for (int s = 0; s < NS; ++s) {
-        const int so = (((4 * s + g) * 16 + h) * 16 + n) * 16;
+        const int so = (((4 * s + g) * HP + h) * 16 + n) * 16;
         const f32x4 ui = attn ? *reinterpret_cast<const f32x4*>(stU + so) : zero4();
         const f32x4 wi = act ? *reinterpret_cast<const f32x4*>(stW + so) : zero4();
-        S[hl][s] = mma_k<D>(qr[hl][s], kf[hl], ui);
-        dP[hl][s] = mma_k<D>(orw[hl][s], vf[hl], wi);
+        if constexpr (QL) {
+          KFrag<bf16, D> qf, of;
+#pragma unroll
+          for (int t = 0; t < NP; ++t) {
+            qf.x32[t] = QoTile::row_frag(qo + ((0 * HP + h) * NP + t) * 1024, g, n);
+            of.x32[t] = QoTile::row_frag(qo + ((1 * HP + h) * NP + t) * 1024, g, n);
+          }
+          S[hl][s] = mma_k<D>(qf, kf[hl], ui);
+          dP[hl][s] = mma_k<D>(of, vf[hl], wi);
+        } else {
+          S[hl][s] = mma_k<D>(qr[hl][s], kf[hl], ui);
+          dP[hl][s] = mma_k<D>(orw[hl][s], vf[hl], wi);
+        }
       }
     }
     JFrag<bf16, NS> pf[HW], dsf[HW];
@@ -791,7 +867,11 @@ __global__ __launch_bounds__(256, 2) void bwd_cols2_kernel(BwdParams prm) {
 #pragma unroll
       for (int q = 0; q < NQ; ++q) {
         JFrag<bf16, NS> ot, qt;
-        if constexpr (NS == 2) {
+        if constexpr (QL) {
+          const int h = w * HW + hl;
+          ot.v = QoTile::tr_frag(qo + ((1 * HP + h) * NP + (q >> 1)) * 1024, q, g, n);
+          qt.v = QoTile::tr_frag(qo + ((0 * HP + h) * NP + (q >> 1)) * 1024, q, g, n);
+        } else if constexpr (NS == 2) {
           ot.v = cat8(transpose_x16(DT::part(orw[hl][0], q), id), transpose_x16(DT::part(orw[hl][1], q), id));
           qt.v = cat8(transpose_x16(DT::part(qr[hl][0], q), id), transpose_x16(DT::part(qr[hl][1], q), id));
         } else {
