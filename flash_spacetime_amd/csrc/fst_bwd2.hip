@@ -567,28 +567,6 @@ struct Cols2Cfg {
   static constexpr int OCC = (QL && HP <= 12 && D <= 32 && C <= 16 && LDS_BYTES <= 160 * 1024 / 3) ? 3 : 2;
 };
 
-// qt / dO rows of one 16-row chunk in LDS: per (tensor, head, 32-feature part)
-// a 1 KB block of 16 rows x 4 16-byte quarters, quarter c of row r at slot
-// 4 r + (c ^ ((r >> 2) & 3)). A 16-byte read of quarter g by the 16 rows of
-// a lane group, and the transposing 8-byte read of 4 rows x 4 quarters, both
-// hit distinct banks. One direct-to-LDS load (lane l -> slot l) fills a block.
-struct QoTile {
-  static __device__ __forceinline__ int slot(int r, int c) { return 4 * r + (c ^ ((r >> 2) & 3)); }
-  // Row-major fragment part (row n, features 8g .. 8g + 7 of the part).
-  static __device__ __forceinline__ bf16x8 row_frag(const unsigned char* blk, int g, int n) {
-    return *reinterpret_cast<const bf16x8*>(blk + 16 * slot(n, g));
-  }
-  // Transposed 16x16 operand of 16-feature slice q of the part (q & 1 picks
-  // the half of each quarter): lane (g, n) receives rows 4g .. 4g + 3 of the
-  // feature the row-major fragment's slice q holds in slot n (DTiles::dmap).
-  // Source lane s of the group supplies row 4g + s / 4, features 8 (s % 4) +
-  // 4 (q & 1) .. +3 of the part.
-  static __device__ __forceinline__ bf16x4 tr_frag(const unsigned char* blk, int q, int g, int n) {
-    const int r = 4 * g + (n >> 2);
-    const unsigned char* p = blk + 16 * slot(r, n & 3) + 8 * (q & 1);
-    return __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4*)(p));
-  }
-};
 
 template <int HP, int D, int C, int RC, int FL>
 __global__ __launch_bounds__(256, (Cols2Cfg<HP, D, C, RC>::OCC)) void bwd_cols2_kernel(BwdParams prm) {
