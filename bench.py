@@ -14,7 +14,7 @@ times of the individual launches, the MFMA roofline of the dominant kernel,
 and the CPU baseline (the oracle's eager restatement of the spec, fp32,
 fwd+bwd, timed on this host's cores on a bounded sample of events).
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W]
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload cfg2|cfg3|cfg4|cfg4-fp32]
 """
 
 from __future__ import annotations
@@ -82,7 +82,7 @@ def time_events(fn, iters, stream):
     return start.elapsed_time(end) / iters
 
 
-def kernel_times(inp, seqlens, iters=10):
+def kernel_times(inp, seqlens, iters=10, cu=None):
     """Average duration of each launch, timed with HIP events on the stream the
     library launches on (torch's current stream), one phase at a time."""
     from flash_spacetime_amd import _lib
@@ -91,7 +91,8 @@ def kernel_times(inp, seqlens, iters=10):
     lib = _lib.load()
     dev = inp["q"].device
     prep = _Prepared(inp["q"], inp["k"], inp["v"], inp["feats"], inp["w"], inp["b"], seqlens, None,
-                     True, True, None)
+                     True, True, cu)
+    d_, c_ = inp["w"].shape
     dims = prep.dims()
     stream = torch.cuda.current_stream(dev)
     sh = stream.cuda_stream
@@ -105,8 +106,8 @@ def kernel_times(inp, seqlens, iters=10):
     _lib.check(lib.fst_forward_phases(_lib.FST_PHASE_WORKLIST, *dims, *fargs), "worklist")
     do = inp["do"].contiguous()
     dq, dk, dv = (torch.empty_like(prep.q) for _ in range(3))
-    dw = torch.empty(D, C, device=dev)
-    db = torch.empty(D, device=dev)
+    dw = torch.empty(d_, c_, device=dev)
+    db = torch.empty(d_, device=dev)
     bws = lib.fst_backward_workspace_bytes(*dims)
     bwork = torch.empty(bws, device=dev, dtype=torch.uint8)
     bargs = (P(prep.q), P(prep.k), P(prep.v), P(prep.pos4), P(prep.weight), P(prep.bias), P(prep.lens), P(lse),
@@ -192,6 +193,92 @@ def cpu_baseline(inp, budget_s=15.0, max_events=B):
     }
 
 
+WORKLOADS = {
+    "cfg3": "configs[3]: flash_spacetime_attention_varlen fwd+bwd, 4096 packed events, lengths "
+            "round(lognormal(5, 1)) in [1, 3000] with 1% of length 1, H=12 D=32 C=16 bf16",
+    "cfg4": "configs[4]: flash_spacetime_attention fwd+bwd, B=8 L=4096 (no padding) H=8 D=64 C=64, "
+            "q and k x30, bf16",
+    "cfg4-fp32": "configs[4]: flash_spacetime_attention fwd+bwd, B=8 L=4096 (no padding) H=8 D=64 C=64, "
+                 "q and k x30, fp32",
+}
+
+
+def run_other_workload(name, steps, warmup):
+    """One JSON line for a non-headline BASELINE configuration: ms/step of the
+    fwd+bwd step through the operators, per-kernel times and the MFMA fraction
+    of the algorithmic FLOPs (fp32 runs are priced at the fp32 matrix peak)."""
+    from flash_spacetime_amd import flash_spacetime_attention, flash_spacetime_attention_varlen
+
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    gen = torch.Generator().manual_seed(3 if name == "cfg3" else 4)
+    rn = lambda *s_: torch.randn(*s_, generator=gen)
+    if name == "cfg3":
+        import math
+        h, d, c, n_ev = 12, 32, 16, 4096
+        lens = torch.exp(5.0 + torch.randn(n_ev, generator=gen, dtype=torch.float64)).round().clamp(1, 3000).long()
+        lens[torch.randperm(n_ev, generator=gen)[: math.ceil(0.01 * n_ev)]] = 1
+        total = int(lens.sum())
+        dtype = torch.bfloat16
+        shape = (total, h, d)
+        xyz = (torch.rand(total, 3, generator=gen) - 0.5) * 1000.0
+        t = torch.rand(total, 1, generator=gen) * 2e4
+        cu = torch.zeros(n_ev + 1, dtype=torch.int32)
+        cu[1:] = torch.cumsum(lens, 0)
+        cu = cu.to(dev)
+        scale_qk = 1.0
+    else:
+        h, d, c, bsz, length = 8, 64, 64, 8, 4096
+        lens = torch.full((bsz,), length, dtype=torch.long)
+        dtype = torch.float32 if name == "cfg4-fp32" else torch.bfloat16
+        shape = (bsz, h, length, d)
+        xyz = (torch.rand(bsz, length, 3, generator=gen) - 0.5) * 1000.0
+        t = torch.rand(bsz, length, 1, generator=gen) * 2e4
+        cu = None
+        scale_qk = 30.0
+    q = (rn(*shape) * scale_qk).to(dev, dtype)
+    k = (rn(*shape) * scale_qk).to(dev, dtype)
+    v = rn(*shape).to(dev, dtype)
+    feats = torch.cat([xyz, t], -1).to(dev)
+    w = (rn(d, c) / c ** 0.5).to(dev)
+    bias = (rn(d) * 0.02).to(dev)
+    do = rn(*shape).to(dev, dtype)
+    seqlens = None if cu is not None else lens.to(dev, torch.int32)
+    leaves = [x.detach().clone().requires_grad_(True) for x in (q, k, v)]
+    wl, bl = w.clone().requires_grad_(True), bias.clone().requires_grad_(True)
+
+    def step():
+        for t_ in (*leaves, wl, bl):
+            t_.grad = None
+        if cu is not None:
+            out = flash_spacetime_attention_varlen(*leaves, feats, wl, bl, cu)
+        else:
+            out = flash_spacetime_attention(*leaves, feats, wl, bl, seqlens)
+        out.backward(do)
+
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize(dev)
+    stream = torch.cuda.current_stream(dev)
+    ms = time_events(step, steps, stream)
+    torch.cuda.synchronize(dev)
+    inp = dict(q=q, k=k, v=v, feats=feats, w=w, b=bias, do=do)
+    kt = kernel_times(inp, seqlens, cu=cu)
+    sl2 = float((lens.double() ** 2).sum())
+    f_total = h * sl2 * (4 * (d + c) + 10 * d + 8 * c)
+    peak = PEAK_BF16_TFLOPS if dtype == torch.bfloat16 else 157.3
+    print(json.dumps({
+        "metric": f"fwd+bwd ms/step at {name}", "value": round(ms, 4), "unit": "ms", "n_gpus": 1,
+        "steps": steps, "warmup": warmup, "ms_per_step": round(ms, 4), "higher_is_better": False,
+        "scaling": "weak", "vs_baseline": None, "dtype": "bf16" if dtype == torch.bfloat16 else "fp32",
+        "data": "synthetic (seeded; BASELINE.json distributions)",
+        "config": {"workload": WORKLOADS[name], "valid_pairs": sl2},
+        "mfma_pct_of_peak": round(100.0 * f_total / (ms * 1e-3) / (peak * 1e12), 3),
+        "algorithmic_tflop": round(f_total / 1e12, 4),
+        "kernels_ms": {k_: round(v_, 4) for k_, v_ in kt.items()},
+    }), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -202,11 +289,17 @@ def main():
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="after the bench, run a known-size fp32 copy kernel (1 GiB read + 1 GiB written) "
                          "that rocprof counter runs use to scale FETCH_SIZE / WRITE_SIZE")
+    ap.add_argument("--workload", default="cfg2", choices=["cfg2", *WORKLOADS],
+                    help="cfg2 (default) is the metric's configuration; the others print a line of their own")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this build's hot path is single-device (events are independent; "
               f"multi-GPU would shard events with no exchange). --gpus {args.gpus} is not run.", file=sys.stderr)
         sys.exit(2)
+
+    if args.workload != "cfg2":
+        run_other_workload(args.workload, args.steps, args.warmup)
+        return
 
     from flash_spacetime_amd import flash_spacetime_attention
     from flash_spacetime_amd.forward import lengths_from_mask
