@@ -113,69 +113,39 @@ __global__ __launch_bounds__(256, 2) void bwd_rows2_kernel(BwdParams prm) {
   const bf16* __restrict__ dog = reinterpret_cast<const bf16*>(prm.dout);
   const bf16x4 id = ident_x16(g, n);
 
+  // The prologue issues every load it needs (the tile's q and dO, lse, W,
+  // the projected rows, positions, then the first chunk's operands) before
+  // its first store: a store between two loads that may alias it would make
+  // the second wait for the first, one round trip per row.
+
   // ---- head-owner state (lane n = row i0 + n) ----
   const int my_row = i0 + n;
   const bool row_ok = my_row < len;
   KFrag<bf16, D> qf[HW], dof[HW];
   f32x4 dQ[HW][NQ], A2[HW][NQ];
   float lse2[HW], Nn[HW], Zz[HW], Dc[HW];  // Dc: the running D - dob
-  bf16* qtg = reinterpret_cast<bf16*>(prm.qt);
+  // Loads from a clamped row and head, without branches, so that no load
+  // waits for the one before it; invalid rows and heads are zeroed below.
+  const int rc = row_ok ? my_row : last;
 #pragma unroll
   for (int hl = 0; hl < HW; ++hl) {
-    const int h = w * HW + hl;
-    const bool ok = h < H && row_ok;
-    if (ok) {
-      qf[hl].load_scaled(qg + ra.off(h, my_row, D), g, prm.scale);
-      dof[hl].load(dog + ra.off(h, my_row, D), g);
-      // qt for the cols kernel: the same bf16 values the logits use.
-      bf16* qd = qtg + ra.off(h, my_row, D);
-#pragma unroll
-      for (int t = 0; t < KFrag<bf16, D>::N32; ++t) *reinterpret_cast<bf16x8*>(qd + 32 * t + 8 * g) = qf[hl].x32[t];
-#pragma unroll
-      for (int t = 0; t < KFrag<bf16, D>::N16; ++t) *reinterpret_cast<bf16x4*>(qd + 16 * t + 4 * g) = qf[hl].x16[t];
-    } else {
-      qf[hl].zero();
-      dof[hl].zero();
-    }
-    // Invalid rows get lse = +inf, so their P (and dS) are exactly zero.
-    lse2[hl] = ok ? prm.lse[ra.vec(h, my_row)] * kLog2e : INFINITY;
-    Nn[hl] = Zz[hl] = Dc[hl] = 0.f;
-#pragma unroll
-    for (int q = 0; q < NQ; ++q) dQ[hl][q] = A2[hl][q] = zero4();
+    const int hc = min(w * HW + hl, H - 1);
+    qf[hl].load(qg + ra.off(hc, rc, D), g);
+    dof[hl].load(dog + ra.off(hc, rc, D), g);
+    lse2[hl] = prm.lse[ra.vec(hc, rc)];
   }
 
   // ---- row-owner state: rows i0 + 4w + r, heads on lane n ----
-  bf16x4 uf[4][NCT], wf[4][NCT];
-  f32x4 Hacc[4][NCT], Gacc[4][NCT];
-  // u and w~ of the row group go to the cols kernel's scratch; rows past the
-  // event are written as zeros, so every row of a group the cols kernel
-  // reads is defined.
-  const long uwg = ((long)prm.ev.blkcum[eb.b] + eb.blk) * 4 + w;
-  bf16* ug = reinterpret_cast<bf16*>(prm.u) + uwg * uw_group_elems(H, NCT);
-  bf16* wtg = reinterpret_cast<bf16*>(prm.wt) + uwg * uw_group_elems(H, NCT);
   WSlots<D, C> wv;
   if (use_e) wv.load(prm.weight, g, n);
+  SlotRow<D> xq[4], xd[4];
 #pragma unroll
   for (int r = 0; r < 4; ++r) {
     const int row = i0 + 4 * w + r;
     const bool ok = row < len && n < H;
     const long xo = ra.off(0, row < len ? row : last, D);
-    if (attn) {
-      project_slots<D, C>(qg + xo, ra.hs * D, ok, prm.scale, wv, g, n, uf[r]);
-      if (n < H)
-#pragma unroll
-        for (int ct = 0; ct < NCT; ++ct)
-          *reinterpret_cast<bf16x4*>(ug + uw_off(r >> 1, ct, n, g, r & 1, H, NCT)) = uf[r][ct];
-    }
-    if (act) {
-      project_slots<D, C>(dog + xo, ra.hs * D, ok, 1.f, wv, g, n, wf[r]);
-      if (n < H)
-#pragma unroll
-        for (int ct = 0; ct < NCT; ++ct)
-          *reinterpret_cast<bf16x4*>(wtg + uw_off(r >> 1, ct, n, g, r & 1, H, NCT)) = wf[r][ct];
-    }
-#pragma unroll
-    for (int ct = 0; ct < NCT; ++ct) Hacc[r][ct] = Gacc[r][ct] = zero4();
+    if (attn) xq[r].load(qg + xo, ra.hs * D, ok, g, n);
+    if (act) xd[r].load(dog + xo, ra.hs * D, ok, g, n);
   }
   float4 pos_i = float4{0.f, 0.f, 0.f, 0.f};
   float fa[NCT], fb[NCT];
@@ -228,6 +198,61 @@ __global__ __launch_bounds__(256, 2) void bwd_rows2_kernel(BwdParams prm) {
   // are still in flight.
   issue_pos(0);
   issue(0);
+
+  // ---- prologue stores ----
+  bf16* qtg = reinterpret_cast<bf16*>(prm.qt);
+#pragma unroll
+  for (int hl = 0; hl < HW; ++hl) {
+    const int h = w * HW + hl;
+    const bool ok = h < H && row_ok;
+    if (ok) {
+      qf[hl].scale_by(prm.scale);
+    } else {
+      qf[hl].zero();
+      dof[hl].zero();
+    }
+    // Invalid rows get lse = +inf, so their P (and dS) are exactly zero.
+    lse2[hl] = ok ? lse2[hl] * kLog2e : INFINITY;
+    if (ok) {
+      // qt for the cols kernel: the same bf16 values the logits use.
+      bf16* qd = qtg + ra.off(h, my_row, D);
+#pragma unroll
+      for (int t = 0; t < KFrag<bf16, D>::N32; ++t) *reinterpret_cast<bf16x8*>(qd + 32 * t + 8 * g) = qf[hl].x32[t];
+#pragma unroll
+      for (int t = 0; t < KFrag<bf16, D>::N16; ++t) *reinterpret_cast<bf16x4*>(qd + 16 * t + 4 * g) = qf[hl].x16[t];
+    }
+    Nn[hl] = Zz[hl] = Dc[hl] = 0.f;
+#pragma unroll
+    for (int q = 0; q < NQ; ++q) dQ[hl][q] = A2[hl][q] = zero4();
+  }
+  bf16x4 uf[4][NCT], wf[4][NCT];
+  f32x4 Hacc[4][NCT], Gacc[4][NCT];
+  // u and w~ of the row group go to the cols kernel's scratch; rows past the
+  // event are written as zeros, so every row of a group the cols kernel
+  // reads is defined.
+  const long uwg = ((long)prm.ev.blkcum[eb.b] + eb.blk) * 4 + w;
+  bf16* ug = reinterpret_cast<bf16*>(prm.u) + uwg * uw_group_elems(H, NCT);
+  bf16* wtg = reinterpret_cast<bf16*>(prm.wt) + uwg * uw_group_elems(H, NCT);
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const bool ok = i0 + 4 * w + r < len && n < H;
+    if (attn) {
+      project_row<D, C>(xq[r], ok, prm.scale, wv, uf[r]);
+      if (n < H)
+#pragma unroll
+        for (int ct = 0; ct < NCT; ++ct)
+          *reinterpret_cast<bf16x4*>(ug + uw_off(r >> 1, ct, n, g, r & 1, H, NCT)) = uf[r][ct];
+    }
+    if (act) {
+      project_row<D, C>(xd[r], ok, 1.f, wv, wf[r]);
+      if (n < H)
+#pragma unroll
+        for (int ct = 0; ct < NCT; ++ct)
+          *reinterpret_cast<bf16x4*>(wtg + uw_off(r >> 1, ct, n, g, r & 1, H, NCT)) = wf[r][ct];
+    }
+#pragma unroll
+    for (int ct = 0; ct < NCT; ++ct) Hacc[r][ct] = Gacc[r][ct] = zero4();
+  }
 
   auto chunk = [&](int j0, auto tail_tag) __attribute__((always_inline)) {
     constexpr bool TAIL = decltype(tail_tag)::value;
@@ -414,6 +439,21 @@ __global__ __launch_bounds__(256, 2) void bwd_rows2_kernel(BwdParams prm) {
   if (j0 < len) chunk(j0, std::true_type{});
 
   // ---- epilogue: sigma, D, dq = scale (dQ + W H + sigma b) ----
+  // W (d on the lanes, the slots of H on the k index) and b, loaded before
+  // the first barrier.
+  float wdq[NQ][NCT][4], bq[NQ][4];
+  if (attn) {
+#pragma unroll
+    for (int q = 0; q < NQ; ++q) {
+      const int dn = DT::dmap(q, n >> 2, n & 3);
+#pragma unroll
+      for (int ct = 0; ct < NCT; ++ct)
+#pragma unroll
+        for (int sp = 0; sp < 4; ++sp) wdq[q][ct][sp] = prm.weight[dn * C + slot_channel<C>(16 * ct + 4 * g + sp)];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) bq[q][r] = prm.bias ? prm.bias[DT::dmap(q, g, r)] : 0.f;
+    }
+  }
   float sig[HW];
 #pragma unroll
   for (int hl = 0; hl < HW; ++hl) {
@@ -428,15 +468,13 @@ __global__ __launch_bounds__(256, 2) void bwd_rows2_kernel(BwdParams prm) {
   for (int q = 0; q < NQ; ++q) {
     if (attn) {
       __syncthreads();  // the stage is free (last chunk, or previous round)
-      const int dn = DT::dmap(q, n >> 2, n & 3);
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         f32x4 acc = zero4();
 #pragma unroll
         for (int ct = 0; ct < NCT; ++ct)
 #pragma unroll
-          for (int sp = 0; sp < 4; ++sp)
-            acc = mfma_f32(prm.weight[dn * C + slot_channel<C>(16 * ct + 4 * g + sp)], Hacc[r][ct][sp], acc);
+          for (int sp = 0; sp < 4; ++sp) acc = mfma_f32(wdq[q][ct][sp], Hacc[r][ct][sp], acc);
         *reinterpret_cast<f32x4*>(stU + stage_off(g, 4 * w + r, n)) = acc;
       }
       __syncthreads();
@@ -447,10 +485,8 @@ __global__ __launch_bounds__(256, 2) void bwd_rows2_kernel(BwdParams prm) {
       f32x4 o = dQ[hl][q];
       if (attn && h < H) {
         o = o + *reinterpret_cast<const f32x4*>(stU + stage_off(g, n, h));
-        if (prm.bias) {
 #pragma unroll
-          for (int r = 0; r < 4; ++r) o[r] = __builtin_fmaf(sig[hl], prm.bias[DT::dmap(q, g, r)], o[r]);
-        }
+        for (int r = 0; r < 4; ++r) o[r] = __builtin_fmaf(sig[hl], bq[q][r], o[r]);
       }
       dQ[hl][q] = o * prm.scale;
     }

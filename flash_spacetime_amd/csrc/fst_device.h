@@ -148,9 +148,8 @@ struct KFrag<bf16, K> {
 #pragma unroll
     for (int t = 0; t < N16; ++t) *reinterpret_cast<bf16x4*>(p + 16 * t + 4 * g) = x16[t];
   }
-  // bf16(float(p[k]) * scale): the reference's q * scale before the cast.
-  __device__ __forceinline__ void load_scaled(const bf16* p, int g, float scale) {
-    load(p, g);
+  // bf16(float(x) * scale): the reference's q * scale before the cast.
+  __device__ __forceinline__ void scale_by(float scale) {
 #pragma unroll
     for (int t = 0; t < N32; ++t)
 #pragma unroll
@@ -159,6 +158,10 @@ struct KFrag<bf16, K> {
     for (int t = 0; t < N16; ++t)
 #pragma unroll
       for (int e = 0; e < 4; ++e) x16[t][e] = (bf16)((float)x16[t][e] * scale);
+  }
+  __device__ __forceinline__ void load_scaled(const bf16* p, int g, float scale) {
+    load(p, g);
+    scale_by(scale);
   }
 };
 

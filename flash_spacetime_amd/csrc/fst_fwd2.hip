@@ -87,39 +87,27 @@ __global__ __launch_bounds__(256, OCC) void fwd2_kernel(FwdParams prm) {
   f32x4 O[HW][NQ];
   float lsum[HW];  // this lane group's part of the row sum
   float mref[HW];
+  // The prologue's loads (q, W, the projected rows, positions, then the
+  // first chunk's operands) are all issued before the first of them is used,
+  // from clamped rows and without branches, so none waits for another.
 #pragma unroll
   for (int hl = 0; hl < HW; ++hl) {
     // Padded heads (h >= H) compute on head H-1's data and are never stored,
     // so the chunk loop needs no per-head branches.
     const int hq = min(w * HW + hl, H - 1);
-    if (row_ok)
-      qf[hl].load_scaled(qg + ra.off(hq, my_row, D), g, prm.scale);
-    else
-      qf[hl].zero();
-#pragma unroll
-    for (int q = 0; q < NQ; ++q) O[hl][q] = zero4();
-    lsum[hl] = 0.f;
-    mref[hl] = -INFINITY;
+    qf[hl].load(qg + ra.off(hq, row_ok ? my_row : last, D), g);
   }
 
   // ---- row-owner state: rows i0 + 4w + r, heads on lane n ----
-  bf16x4 uf[4][NCT];
-  f32x4 AE[4][NCT];
   WSlots<D, C> wv;
-  if (attn) wv.load(prm.weight, g, n);
+  SlotRow<D> xq[4];
+  if (attn) {
+    wv.load(prm.weight, g, n);
 #pragma unroll
-  for (int r = 0; r < 4; ++r) {
-    const int row = i0 + 4 * w + r;
-    if (attn) {
-      // u^T[slot][h] = sum_d W[d][channel(slot)] qt[h][d] on fp32 MFMA.
-      const bool ok = row < len && n < H;
-      project_slots<D, C>(qg + ra.off(0, row < len ? row : last, D), ra.hs * D, ok, prm.scale, wv, g, n, uf[r]);
-    } else {
-#pragma unroll
-      for (int ct = 0; ct < NCT; ++ct) uf[r][ct] = bf16x4{};
+    for (int r = 0; r < 4; ++r) {
+      const int row = i0 + 4 * w + r;
+      xq[r].load(qg + ra.off(0, row < len ? row : last, D), ra.hs * D, row < len && n < H, g, n);
     }
-#pragma unroll
-    for (int ct = 0; ct < NCT; ++ct) AE[r][ct] = zero4();
   }
   // Angle lane assignment: lane (g, n) evaluates row i0 + 4w + g against key
   // j0 + 16 s + n; the four rows are then gathered into every lane group.
@@ -180,6 +168,32 @@ __global__ __launch_bounds__(256, OCC) void fwd2_kernel(FwdParams prm) {
   };
   issue_pos(0);
   issue(0);
+
+#pragma unroll
+  for (int hl = 0; hl < HW; ++hl) {
+    if (row_ok)
+      qf[hl].scale_by(prm.scale);
+    else
+      qf[hl].zero();
+#pragma unroll
+    for (int q = 0; q < NQ; ++q) O[hl][q] = zero4();
+    lsum[hl] = 0.f;
+    mref[hl] = -INFINITY;
+  }
+  bf16x4 uf[4][NCT];
+  f32x4 AE[4][NCT];
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    if (attn) {
+      // u^T[slot][h] = sum_d W[d][channel(slot)] qt[h][d] on fp32 MFMA.
+      project_row<D, C>(xq[r], i0 + 4 * w + r < len && n < H, prm.scale, wv, uf[r]);
+    } else {
+#pragma unroll
+      for (int ct = 0; ct < NCT; ++ct) uf[r][ct] = bf16x4{};
+    }
+#pragma unroll
+    for (int ct = 0; ct < NCT; ++ct) AE[r][ct] = zero4();
+  }
 
   auto chunk = [&](int j0, auto tail_tag) __attribute__((always_inline)) {
     constexpr bool TAIL = decltype(tail_tag)::value;

@@ -208,40 +208,49 @@ struct WSlots {
   }
 };
 
+// One row's operand of a projection: features Qd g .. Qd g + Qd - 1 of head
+// n's row in 8- or 16-byte loads (a row holds D bf16, so they are aligned); a
+// lane with !ok reads head 0. Loading is apart from projecting so a kernel
+// can issue the loads of all its rows before the first product waits on one.
+template <int D>
+struct SlotRow {
+  static constexpr int Qd = D / 4, VW = Qd % 8 == 0 ? 8 : 4, NV = Qd / VW;
+  using V = std::conditional_t<VW == 8, bf16x8, bf16x4>;
+  V x[NV];
+  __device__ __forceinline__ void load(const bf16* xrow, long hstride, bool ok, int g, int n) {
+    const bf16* p = xrow + (ok ? n * hstride : 0) + Qd * g;
+#pragma unroll
+    for (int t = 0; t < NV; ++t) x[t] = *reinterpret_cast<const V*>(p + VW * t);
+  }
+};
+
 // u = bf16(x @ W[:, channel(slot)]) for the heads of one row, x = row * mult
 // (q * scale or dO): fp32 MFMA with the head on lane n (heads >= H or an
 // invalid row give zeros); lane (g, n = h) receives slots 16 ct + 4 g .. +3.
-// xrow points at head 0 of the row, hstride is the element stride of heads.
 template <int D, int C>
-__device__ __forceinline__ void project_slots(const bf16* xrow, long hstride, bool ok, float mult,
-                                              const WSlots<D, C>& wv, int g, int n, bf16x4* out) {
-  constexpr int Qd = D / 4;
-  float xv[Qd];
-  // Features Qd g .. Qd g + Qd - 1 of head n's row in 8- or 16-byte loads
-  // (a row holds D bf16, so they are aligned); a lane with !ok reads head 0.
-  const bf16* p = xrow + (ok ? n * hstride : 0) + Qd * g;
-  if constexpr (Qd % 8 == 0) {
+__device__ __forceinline__ void project_row(const SlotRow<D>& xr, bool ok, float mult, const WSlots<D, C>& wv,
+                                            bf16x4* out) {
+  constexpr int VW = SlotRow<D>::VW;
+  float xv[D / 4];
 #pragma unroll
-    for (int t = 0; t < Qd / 8; ++t) {
-      const bf16x8 v = *reinterpret_cast<const bf16x8*>(p + 8 * t);
-#pragma unroll
-      for (int e = 0; e < 8; ++e) xv[8 * t + e] = ok ? (float)v[e] * mult : 0.f;
-    }
-  } else {
-#pragma unroll
-    for (int t = 0; t < Qd / 4; ++t) {
-      const bf16x4 v = *reinterpret_cast<const bf16x4*>(p + 4 * t);
-#pragma unroll
-      for (int e = 0; e < 4; ++e) xv[4 * t + e] = ok ? (float)v[e] * mult : 0.f;
-    }
-  }
+  for (int s = 0; s < D / 4; ++s) xv[s] = ok ? (float)xr.x[s / VW][s % VW] * mult : 0.f;
 #pragma unroll
   for (int ct = 0; ct < C / 16; ++ct) {
     f32x4 a = zero4();
 #pragma unroll
-    for (int s = 0; s < Qd; ++s) a = mfma_f32(wv.v[s][ct], xv[s], a);
+    for (int s = 0; s < D / 4; ++s) a = mfma_f32(wv.v[s][ct], xv[s], a);
     out[ct] = pack4(a);
   }
+}
+
+// Load and project one row; xrow points at head 0 of the row, hstride is the
+// element stride of heads.
+template <int D, int C>
+__device__ __forceinline__ void project_slots(const bf16* xrow, long hstride, bool ok, float mult,
+                                              const WSlots<D, C>& wv, int g, int n, bf16x4* out) {
+  SlotRow<D> xr;
+  xr.load(xrow, hstride, ok, g, n);
+  project_row<D, C>(xr, ok, mult, wv, out);
 }
 
 // ---------------------------------------------------------------------------
