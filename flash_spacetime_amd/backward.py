@@ -17,19 +17,30 @@ import torch
 from torch import Tensor
 
 from . import _lib
-from .forward import _Prepared
+from .forward import _Prepared, _vec_in_layout
+
+
+def _same_layout(a: Tensor, b: Tensor) -> bool:
+    return all(sa == sb for sa, sb, n in zip(a.stride(), b.stride(), a.shape) if n > 1)
 
 
 def _run_backward(dims, q, k, v, pos4, w32, b32, lens, lse, grad_out, scale, vec_shape,
                   rowsum: Optional[Tensor] = None):
     lib = _lib.load()
     _lib.require_gpu(grad_out)
-    do = grad_out.to(q.dtype).contiguous()
-    if do.shape != q.shape:
+    if grad_out.shape != q.shape:
         raise ValueError(f"grad_out must have the shape of the output {tuple(q.shape)}")
+    # grad_out, dq, dk and dv share q's layout (contiguous, or token-major
+    # when the flags say so): empty_like keeps a dense view's strides.
+    do = grad_out.to(q.dtype)
+    if not _same_layout(do, q):
+        do = torch.empty_like(q).copy_(do)
     dq = torch.empty_like(q)
     dk = torch.empty_like(k)
     dv = torch.empty_like(v)
+    rs = rowsum
+    if rowsum is not None and not _same_layout(rowsum, lse):
+        rs = torch.empty_like(lse)
     dw = torch.empty(w32.shape, device=q.device, dtype=torch.float32)
     db = torch.empty(q.shape[-1], device=q.device, dtype=torch.float32) if b32 is not None else None
     ws_bytes = lib.fst_backward_workspace_bytes(*dims)
@@ -39,10 +50,12 @@ def _run_backward(dims, q, k, v, pos4, w32, b32, lens, lse, grad_out, scale, vec
             *dims,
             _lib.ptr(q), _lib.ptr(k), _lib.ptr(v), _lib.ptr(pos4), _lib.ptr(w32), _lib.ptr(b32),
             _lib.ptr(lens), _lib.ptr(lse), _lib.ptr(do), scale,
-            _lib.ptr(dq), _lib.ptr(dk), _lib.ptr(dv), _lib.ptr(dw), _lib.ptr(db), _lib.ptr(rowsum),
+            _lib.ptr(dq), _lib.ptr(dk), _lib.ptr(dv), _lib.ptr(dw), _lib.ptr(db), _lib.ptr(rs),
             _lib.ptr(ws), ws_bytes, _lib.stream_handle(q.device),
         )
     _lib.check(rc, "flash_spacetime_backward")
+    if rs is not rowsum:
+        rowsum.copy_(rs)
     return dq, dk, dv, dw, db
 
 
@@ -79,7 +92,7 @@ def flash_spacetime_backward(
                      use_activation_bias, cu_seqlens)
     dq, dk, dv, dw, db = _run_backward(
         prep.dims(), prep.q, prep.k, prep.v, prep.pos4, prep.weight, prep.bias, prep.lens,
-        lse.to(torch.float32).contiguous(), grad_out, prep.scale, prep.vec_shape(), rowsum,
+        _vec_in_layout(lse, prep.token_major), grad_out, prep.scale, prep.vec_shape(), rowsum,
     )
     return (
         dq,

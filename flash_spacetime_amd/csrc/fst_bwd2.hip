@@ -162,7 +162,7 @@ __global__ __launch_bounds__(256, 2) void bwd_rows2_kernel(BwdParams prm) {
   // ---- operand stream: K, V rows of the wave's heads, key positions ----
   const long ebase = ra.off(0, 0, D);
   const int rowb = (int)(ra.ts * D * 2);
-  const unsigned ebytes = (unsigned)((prm.ev.packed ? (long)len * ra.ts : (long)H * ra.hs) * D * 2);
+  const unsigned ebytes = (unsigned)((prm.ev.tokmajor ? (long)len * ra.ts : (long)H * ra.hs) * D * 2);
   const Buf kbuf(kg + ebase, ebytes), vbuf(vg + ebase, ebytes);
   const Buf pbuf(prm.ev.pos4 + ra.pos_base, (unsigned)len * 16u);
   int kvo[HW];
@@ -237,14 +237,14 @@ __global__ __launch_bounds__(256, 2) void bwd_rows2_kernel(BwdParams prm) {
   for (int r = 0; r < 4; ++r) {
     const bool ok = i0 + 4 * w + r < len && n < H;
     if (attn) {
-      project_row<D, C>(xq[r], ok, prm.scale, wv, uf[r]);
+      project_loaded<D, C>(xq[r], ok, prm.scale, wv, uf[r]);
       if (n < H)
 #pragma unroll
         for (int ct = 0; ct < NCT; ++ct)
           *reinterpret_cast<bf16x4*>(ug + uw_off(r >> 1, ct, n, g, r & 1, H, NCT)) = uf[r][ct];
     }
     if (act) {
-      project_row<D, C>(xd[r], ok, 1.f, wv, wf[r]);
+      project_loaded<D, C>(xd[r], ok, 1.f, wv, wf[r]);
       if (n < H)
 #pragma unroll
         for (int ct = 0; ct < NCT; ++ct)
@@ -676,10 +676,10 @@ __global__ __launch_bounds__(256, (Cols2Cfg<HP, D, C, RC>::OCC)) void bwd_cols2_
   // u / w~ rows and row positions ----
   const long ebase = ra.off(0, 0, D);
   const int rowb = (int)(ra.ts * D * 2);
-  const unsigned ebytes = (unsigned)((ev.packed ? (long)len * ra.ts : (long)H * ra.hs) * D * 2);
+  const unsigned ebytes = (unsigned)((ev.tokmajor ? (long)len * ra.ts : (long)H * ra.hs) * D * 2);
   const Buf qbuf(reinterpret_cast<const bf16*>(prm.qt) + ebase, ebytes);
   const Buf obuf(reinterpret_cast<const bf16*>(prm.dout) + ebase, ebytes);
-  const unsigned vbytes = (unsigned)((ev.packed ? (long)len * ra.ts : (long)H * ra.hs) * 4);
+  const unsigned vbytes = (unsigned)((ev.tokmajor ? (long)len * ra.ts : (long)H * ra.hs) * 4);
   const Buf lbuf(prm.lse + ra.base_row, vbytes), dbuf(prm.dsum + ra.base_row, vbytes);
   // u / w~ in the row-group layout the rows kernel writes (uw_off): the
   // event's groups start at 4 x its first tile in the rows work list.
@@ -703,8 +703,8 @@ __global__ __launch_bounds__(256, (Cols2Cfg<HP, D, C, RC>::OCC)) void bwd_cols2_
   // The raw values are kept until the chunk's scalars are written, so the
   // loads are not waited for where they are issued.
   float sc_lraw = 0.f, sc_draw = 0.f;
-  const int sc_h = ev.packed ? tid % H : tid / RC;
-  const int sc_r = ev.packed ? tid / H : tid % RC;
+  const int sc_h = ev.tokmajor ? tid % H : tid / RC;
+  const int sc_r = ev.tokmajor ? tid / H : tid % RC;
   const bool sc_ok = tid < RC * H;
   const int sc_hc = min(sc_h, H - 1);
   float4 prow[RGW];

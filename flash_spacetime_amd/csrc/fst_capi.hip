@@ -171,7 +171,10 @@ static fwd_dispatch_fn fwd_table(int dtype, int D) {
 
 static int check_common(int dtype, int flags, int B, int H, int L, int T, int D, int C) {
   if (dtype != FST_BF16 && dtype != FST_F32) return fail(FST_EINVAL, "dtype must be FST_BF16 or FST_F32, got %d", dtype);
-  if (flags & ~(FST_ATTN_BIAS | FST_ACT_BIAS | FST_PACKED)) return fail(FST_EINVAL, "unknown flag bits 0x%x", flags);
+  if (flags & ~(FST_ATTN_BIAS | FST_ACT_BIAS | FST_PACKED | FST_TOKEN_MAJOR))
+    return fail(FST_EINVAL, "unknown flag bits 0x%x", flags);
+  if ((flags & FST_PACKED) && (flags & FST_TOKEN_MAJOR))
+    return fail(FST_EINVAL, "FST_TOKEN_MAJOR applies to the padded layout (packed is token-major already)");
   if (B < 0 || L < 0 || T < 0) return fail(FST_EINVAL, "negative size (B=%d, L=%d, T=%d)", B, L, T);
   if (H < 1 || H > 16) return fail(FST_EUNSUPPORTED, "heads must be in [1, 16], got %d", H);
   if (!supported_dim(D)) return fail(FST_EUNSUPPORTED, "head_dim D must be one of 16, 32, 48, 64, got %d", D);
@@ -376,6 +379,7 @@ int fst_forward_phases(int phases, int dtype, int flags, int B, int H, int L, in
   prm.ev.L = L;
   prm.ev.T = T;
   prm.ev.packed = packed ? 1 : 0;
+  prm.ev.tokmajor = (packed || (flags & FST_TOKEN_MAJOR)) ? 1 : 0;
   prm.H = H;
   prm.flags = flags;
   prm.scale = scale;
@@ -465,6 +469,7 @@ int fst_backward_phases(int phases, int dtype, int flags, int B, int H, int L, i
   prm.ev.L = L;
   prm.ev.T = T;
   prm.ev.packed = packed ? 1 : 0;
+  prm.ev.tokmajor = (packed || (flags & FST_TOKEN_MAJOR)) ? 1 : 0;
   prm.blkcum_cols = bc_c;
   prm.H = H;
   prm.flags = flags;

@@ -128,7 +128,7 @@ __global__ __launch_bounds__(256, OCC) void fwd2_kernel(FwdParams prm) {
   // scalar offset by KC ts D elements.
   const long ebase = ra.off(0, 0, D);
   const int rowb = (int)(ra.ts * D * 2);  // bytes per key row
-  const unsigned ebytes = (unsigned)((prm.ev.packed ? (long)len * ra.ts : (long)H * ra.hs) * D * 2);
+  const unsigned ebytes = (unsigned)((prm.ev.tokmajor ? (long)len * ra.ts : (long)H * ra.hs) * D * 2);
   const Buf kbuf(kg + ebase, ebytes), vbuf(vg + ebase, ebytes);
   const Buf pbuf(prm.ev.pos4 + ra.pos_base, (unsigned)len * 16u);
   int kvo[HW];  // lane offset of head hl, key n (bytes)
@@ -186,7 +186,7 @@ __global__ __launch_bounds__(256, OCC) void fwd2_kernel(FwdParams prm) {
   for (int r = 0; r < 4; ++r) {
     if (attn) {
       // u^T[slot][h] = sum_d W[d][channel(slot)] qt[h][d] on fp32 MFMA.
-      project_row<D, C>(xq[r], i0 + 4 * w + r < len && n < H, prm.scale, wv, uf[r]);
+      project_loaded<D, C>(xq[r], i0 + 4 * w + r < len && n < H, prm.scale, wv, uf[r]);
     } else {
 #pragma unroll
       for (int ct = 0; ct < NCT; ++ct) uf[r][ct] = bf16x4{};

@@ -8,12 +8,16 @@ namespace fst {
 
 // Event layout shared by every kernel: padded [B, H, L, X] with seqlens, or
 // packed [T, H, X] with cu_seqlens (forward.py:247-255, _tiles.py:80-117).
+// Padded events may also be stored token-major, [B, L, H, X] (vectors
+// [B, L, H]): the layout a [B, L, H*D] projection has before its heads are
+// split, so the heads-first views a model passes are read in place.
 struct EventSpec {
   const int32_t* lens;    // seqlens [B] (padded) or cu_seqlens [B+1] (packed)
   const int32_t* blkcum;  // [B+1] prefix sums of row blocks per event
   const int32_t* perm;    // [B] events by decreasing length (padded tile kernels' schedule)
   const float4* pos4;     // [B*L] or [T] (x, y, z, t) fp32
   int B, H, L, T, packed;
+  int tokmajor;           // rows of one token's heads are adjacent (packed, or padded token-major)
 };
 
 struct EventBlock {
@@ -71,6 +75,11 @@ __device__ __forceinline__ RowAddr row_addr(const EventSpec& ev, const EventBloc
     r.hs = 1;
     r.ts = ev.H;
     r.pos_base = eb.tok0;
+  } else if (ev.tokmajor) {
+    r.base_row = (long)eb.b * ev.L * ev.H;
+    r.hs = 1;
+    r.ts = ev.H;
+    r.pos_base = (long)eb.b * ev.L;
   } else {
     r.base_row = (long)eb.b * ev.H * ev.L;
     r.hs = ev.L;

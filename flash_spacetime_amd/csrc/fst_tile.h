@@ -228,7 +228,7 @@ struct SlotRow {
 // (q * scale or dO): fp32 MFMA with the head on lane n (heads >= H or an
 // invalid row give zeros); lane (g, n = h) receives slots 16 ct + 4 g .. +3.
 template <int D, int C>
-__device__ __forceinline__ void project_row(const SlotRow<D>& xr, bool ok, float mult, const WSlots<D, C>& wv,
+__device__ __forceinline__ void project_loaded(const SlotRow<D>& xr, bool ok, float mult, const WSlots<D, C>& wv,
                                             bf16x4* out) {
   constexpr int VW = SlotRow<D>::VW;
   float xv[D / 4];
@@ -250,7 +250,7 @@ __device__ __forceinline__ void project_slots(const bf16* xrow, long hstride, bo
                                               const WSlots<D, C>& wv, int g, int n, bf16x4* out) {
   SlotRow<D> xr;
   xr.load(xrow, hstride, ok, g, n);
-  project_row<D, C>(xr, ok, mult, wv, out);
+  project_loaded<D, C>(xr, ok, mult, wv, out);
 }
 
 // ---------------------------------------------------------------------------

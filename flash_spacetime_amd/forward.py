@@ -66,6 +66,24 @@ def _is_front_packed(valid: Tensor) -> bool:
     return bool(torch.equal(prefix, valid))
 
 
+def is_token_major(t: Tensor) -> bool:
+    """Whether a `[B, H, L, D]` tensor is the heads-first view of dense
+    `[B, L, H, D]` memory, as `split_heads` leaves a `[B, L, H*D]`
+    projection (reference.py:187-191). Such tensors are read in place; a
+    tensor that is also contiguous `[B, H, L, D]` (H == 1 or L == 1) counts
+    as heads-first."""
+    return t.dim() == 4 and not t.is_contiguous() and t.transpose(1, 2).is_contiguous()
+
+
+def _vec_in_layout(x: Tensor, token_major: bool) -> Tensor:
+    """A float32 `[B, H, L]` per-row vector (lse) stored as the kernels read it:
+    `[B, L, H]` memory when the operands are token-major."""
+    x = x.to(torch.float32)
+    if token_major:
+        return x if x.transpose(1, 2).is_contiguous() else x.transpose(1, 2).contiguous().transpose(1, 2)
+    return x.contiguous()
+
+
 def _resolve_lengths(seqlens: Optional[Tensor], key_padding_mask: Optional[Tensor], batch: int,
                      length: int) -> Tensor:
     if key_padding_mask is not None and seqlens is not None:
@@ -84,7 +102,13 @@ def _resolve_lengths(seqlens: Optional[Tensor], key_padding_mask: Optional[Tenso
 
 
 class _Prepared:
-    """Validated, contiguous kernel operands shared by forward and backward."""
+    """Validated kernel operands shared by forward and backward.
+
+    Padded q, k, v that are all heads-first views of `[B, L, H, D]` memory
+    (`is_token_major`) are used in place and the library is told so
+    (FST_TOKEN_MAJOR); the outputs, gradients and lse then come back as the
+    same kind of view. Anything else is made contiguous `[B, H, L, D]`, as
+    the reference does (forward.py:274)."""
 
     def __init__(self, q, k, v, feats, weight, bias, seqlens, scale, use_attn_bias,
                  use_activation_bias, cu_seqlens):
@@ -131,10 +155,15 @@ class _Prepared:
         self.heads, self.dim, self.channels = heads, dim, c
         self.dtype = _DTYPES[q.dtype]
         self.scale = float(dim ** -0.5 if scale is None else scale)
+        self.token_major = not self.packed and all(is_token_major(t) for t in (q, k, v))
         self.flags = ((_lib.FST_ATTN_BIAS if use_attn_bias else 0)
                       | (_lib.FST_ACT_BIAS if use_activation_bias else 0)
-                      | (_lib.FST_PACKED if self.packed else 0))
-        self.q, self.k, self.v = (t.contiguous() for t in (q, k, v))
+                      | (_lib.FST_PACKED if self.packed else 0)
+                      | (_lib.FST_TOKEN_MAJOR if self.token_major else 0))
+        if self.token_major:
+            self.q, self.k, self.v = q, k, v
+        else:
+            self.q, self.k, self.v = (t.contiguous() for t in (q, k, v))
         self.pos4 = feats[..., :4].to(torch.float32).contiguous()
         self.weight = weight.detach().to(torch.float32).contiguous()
         self.bias = bias.detach().to(torch.float32).contiguous() if bias is not None else None
@@ -150,11 +179,18 @@ class _Prepared:
             return (self.tokens, self.heads)
         return (self.batch, self.heads, self.length)
 
+    def empty_vec(self) -> Tensor:
+        """A float32 per-row vector (lse, rowsum) in the operands' layout."""
+        if self.token_major:
+            b, h, length = self.vec_shape()
+            return torch.empty(b, length, h, device=self.device, dtype=torch.float32).transpose(1, 2)
+        return torch.empty(self.vec_shape(), device=self.device, dtype=torch.float32)
+
 
 def _run_forward(prep: _Prepared) -> Tuple[Tensor, Tensor]:
     lib = _lib.load()
-    out = torch.empty_like(prep.q)
-    lse = torch.empty(prep.vec_shape(), device=prep.device, dtype=torch.float32)
+    out = torch.empty_like(prep.q)  # keeps a token-major view's layout
+    lse = prep.empty_vec()
     ws_bytes = lib.fst_forward_workspace_bytes(*prep.dims())
     ws = torch.empty(max(ws_bytes, 1), device=prep.device, dtype=torch.uint8)
     with torch.cuda.device(prep.device):
@@ -328,7 +364,9 @@ def _attention_scattered(q, k, v, feats, weight, bias, valid, scale, use_attn_bi
     out = flash_spacetime_attention_varlen(rows(q), rows(k), rows(v), feats[valid], weight, bias, cu, scale,
                                            use_attn_bias, use_activation_bias)
     full = out.new_zeros(b, length, h, d).index_put((valid,), out)
-    return full.transpose(1, 2).contiguous()
+    # Heads-first view of the token-major result when q was one, else
+    # contiguous [B, H, L, D].
+    return full.transpose(1, 2) if is_token_major(q) else full.transpose(1, 2).contiguous()
 
 
 def flash_spacetime_attention_varlen(

@@ -11,6 +11,9 @@
  *   padded : q, k, v, out, dq, dk, dv  [B, H, L, D]   lse, rowsum [B, H, L]
  *            pos4 [B, L, 4] fp32 (x, y, z, t), lens = seqlens [B] int32
  *            (valid tokens of event b are 0 .. seqlens[b]-1)
+ *   padded, FST_TOKEN_MAJOR :
+ *            q, k, v, out, grad_out, dq, dk, dv  [B, L, H, D]
+ *            lse, rowsum [B, L, H]; pos4 and lens as padded
  *   packed : q, k, v, out, dq, dk, dv  [T, H, D]      lse, rowsum [T, H]
  *            pos4 [T, 4] fp32, lens = cu_seqlens [B+1] int32 (cu[0] = 0,
  *            cu[B] = T)
@@ -40,7 +43,12 @@ enum fst_dtype { FST_BF16 = 0, FST_F32 = 1 };
 enum fst_flags {
   FST_ATTN_BIAS = 1, /* add qt_i . R_ij to the logits (use_attn_bias)        */
   FST_ACT_BIAS = 2,  /* add sum_j P_ij R_ij to the output (use_activation_bias) */
-  FST_PACKED = 4     /* packed [T, H, D] layout with cu_seqlens              */
+  FST_PACKED = 4,    /* packed [T, H, D] layout with cu_seqlens              */
+  FST_TOKEN_MAJOR = 8 /* padded tensors stored [B, L, H, D] (vectors [B, L, H]):
+                         the heads-first views of a [B, L, H*D] projection
+                         (reference.py:187-196 split_heads) read in place.
+                         No reference counterpart: the reference makes them
+                         contiguous [B, H, L, D] first (forward.py:274).    */
 };
 
 /* Phases of one operator call, for callers that time or schedule them

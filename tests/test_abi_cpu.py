@@ -103,6 +103,12 @@ def test_argument_errors_are_reported_before_any_launch():
     rc = lib.fst_forward(0, 3 | 64, 1, 4, 8, 0, 32, 16, None, None, None, None, None, None, None, 1.0,
                          None, None, None, 0, None)
     assert rc == _lib.FST_EINVAL and "flag" in _lib.last_error()
+    # token-major is a padded layout; packed tensors are token-major already
+    rc = lib.fst_forward(0, 3 | _lib.FST_PACKED | _lib.FST_TOKEN_MAJOR, 1, 4, 0, 8, 32, 16, None, None, None,
+                         None, None, None, None, 1.0, None, None, None, 0, None)
+    assert rc == _lib.FST_EINVAL and "TOKEN_MAJOR" in _lib.last_error()
+    assert lib.fst_backward_workspace_bytes(_lib.FST_BF16, 3 | _lib.FST_TOKEN_MAJOR, 256, 12, 768, 0, 32, 16) == \
+        lib.fst_backward_workspace_bytes(_lib.FST_BF16, 3, 256, 12, 768, 0, 32, 16)
     # empty problems are valid no-ops
     assert lib.fst_forward(0, 3, 0, 4, 8, 0, 32, 16, None, None, None, None, None, None, None, 1.0,
                            None, None, None, 0, None) == _lib.FST_OK

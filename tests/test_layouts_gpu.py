@@ -1,4 +1,4 @@
-"""GPU tests of the input formats the build adds to the reference's API.
+"""GPU tests of the input formats and layouts the build adds to the reference's API.
 
 * `torch.nested` jagged q / k / v (and feats) for the packed operator: the
   result and every gradient are bitwise those of the dense packed call on the
@@ -7,6 +7,9 @@
   reference accepts front-packed lengths only): valid rows and all gradients
   against the float64 oracle evaluated with the same mask (`pair_mask`, the
   spec's one-sided key mask), padding rows exactly zero.
+* Heads-first views of token-major `[B, L, H, D]` memory (what `split_heads`
+  makes of a projection) are read in place: results bitwise those of the
+  contiguous call, returned as the same kind of view.
 """
 
 import pytest
@@ -141,3 +144,97 @@ def test_nested_inputs_match_dense_packed(dtype):
     assert torch.equal(out_d, out_n)
     for a, b in zip(grads_d, grads_n):
         assert torch.equal(a, b)
+
+
+def _token_major(x: torch.Tensor) -> torch.Tensor:
+    """The same values as a heads-first view of [B, L, H, D] memory."""
+    return x.transpose(1, 2).contiguous().transpose(1, 2)
+
+
+# (dtype, shape): bf16 tile kernels, the bf16 layout on the fallback backward
+# (H=16, D=C=64), fp32 kernels; fp32 has no backward at H=16, D=C=64.
+_TM_CASES = [(torch.bfloat16, (3, 50, 12, 32, 16)), (torch.bfloat16, (2, 40, 16, 64, 64)),
+             (torch.bfloat16, (2, 33, 5, 48, 32)), (torch.float32, (3, 50, 12, 32, 16)),
+             (torch.float32, (2, 40, 8, 64, 64)), (torch.float32, (2, 33, 5, 48, 32))]
+
+
+@pytest.mark.parametrize("dtype,shape", _TM_CASES,
+                         ids=[f"{str(d)[6:]}-{'x'.join(map(str, s))}" for d, s in _TM_CASES])
+@pytest.mark.parametrize("flags", FLAGS[:3], ids=["attn1act1", "attn1act0", "attn0act1"])
+def test_token_major_views_match_contiguous(dtype, shape, flags):
+    """Heads-first views of [B, L, H, D] memory (split_heads of a projection)
+    are read in place: output, lse and every gradient are bitwise those of
+    the contiguous [B, H, L, D] call, and come back as the same kind of view."""
+    case = make_padded(*shape, seed=seed_of("token-major", dtype, shape, flags))
+    dev = "cuda"
+    seqlens = case["seqlens"].to(dev)
+    feats = case["feats"].to(dev)
+    gw = torch.randn(shape[0], shape[2], shape[1], shape[3], generator=torch.Generator().manual_seed(9))
+
+    def run(token_major: bool):
+        conv = _token_major if token_major else (lambda x: x.contiguous())
+        leaves = {k: conv(case[k].to(dev, dtype)).requires_grad_(True) for k in ("q", "k", "v")}
+        w = case["weight"].to(dev, dtype).requires_grad_(True)
+        b = case["bias"].to(dev, dtype).requires_grad_(True)
+        out = flash_spacetime_attention(leaves["q"], leaves["k"], leaves["v"], feats, w, b, seqlens,
+                                        use_attn_bias=flags[0], use_activation_bias=flags[1])
+        (out.float() * conv(gw.to(dev))).sum().backward()
+        return out.detach(), [leaves[k].grad for k in ("q", "k", "v")] + [w.grad, b.grad]
+
+    out_c, grads_c = run(False)
+    out_t, grads_t = run(True)
+    assert out_t.transpose(1, 2).is_contiguous() and not out_t.is_contiguous()
+    assert torch.equal(out_c, out_t)
+    for a, b in zip(grads_c, grads_t):
+        assert (a is None) == (b is None)
+        if a is not None:
+            assert torch.equal(a, b)
+    for g in grads_t[:3]:
+        assert g.transpose(1, 2).is_contiguous()
+
+
+def test_token_major_launcher_lse_and_rowsum():
+    """flash_spacetime_forward / _backward with token-major operands: lse comes
+    back as a heads-first view with the contiguous call's values; a
+    contiguous rowsum buffer and a contiguous grad_out are accepted."""
+    from flash_spacetime_amd import flash_spacetime_backward, flash_spacetime_forward
+
+    shape = (3, 45, 8, 32, 16)
+    case = make_padded(*shape, seed=seed_of("token-major-launcher"))
+    dev, dt = "cuda", torch.bfloat16
+    q, k, v = (case[n].to(dev, dt) for n in ("q", "k", "v"))
+    feats, w, b = case["feats"].to(dev), case["weight"].to(dev), case["bias"].to(dev)
+    sl = case["seqlens"].to(dev)
+    do = torch.randn(q.shape, generator=torch.Generator().manual_seed(4)).to(dev, dt)
+    o_c, lse_c = flash_spacetime_forward(q, k, v, feats, w, b, sl)
+    tq, tk, tv = (_token_major(x) for x in (q, k, v))
+    o_t, lse_t = flash_spacetime_forward(tq, tk, tv, feats, w, b, sl)
+    assert torch.equal(o_c, o_t) and torch.equal(lse_c, lse_t)
+    assert lse_t.transpose(1, 2).is_contiguous()
+    rs_c = torch.full(lse_c.shape, float("nan"), device=dev)
+    rs_t = torch.full(lse_c.shape, float("nan"), device=dev)
+    g_c = flash_spacetime_backward(q, k, v, feats, w, b, sl, lse_c, do, rowsum=rs_c)
+    # The token-major call gets lse contiguous and grad_out contiguous: both
+    # are brought into the operands' layout.
+    g_t = flash_spacetime_backward(tq, tk, tv, feats, w, b, sl, lse_c, do, rowsum=rs_t)
+    for a, c in zip(g_c, g_t):
+        assert torch.equal(a, c)
+    assert torch.equal(rs_c, rs_t)
+
+
+def test_token_major_with_holey_mask_and_mixed_layouts():
+    """A mask with holes on token-major views matches the contiguous call; q
+    token-major with k, v contiguous takes the contiguous path."""
+    shape = (3, 40, 4, 32, 16)
+    case = make_padded(*shape, seed=seed_of("token-major-mixed"), masked=False)
+    dev, dt = "cuda", torch.bfloat16
+    q, k, v = (case[n].to(dev, dt) for n in ("q", "k", "v"))
+    feats, w, b = case["feats"].to(dev), case["weight"].to(dev), case["bias"].to(dev)
+    holey = _holey_mask(3, 40, seed_of("token-major-holes")).to(dev)
+    base = flash_spacetime_attention(q, k, v, feats, w, b, key_padding_mask=~holey)
+    tm = flash_spacetime_attention(_token_major(q), _token_major(k), _token_major(v), feats, w, b,
+                                   key_padding_mask=~holey)
+    assert torch.equal(base, tm) and tm.transpose(1, 2).is_contiguous()
+    sl = case["seqlens"].to(dev)
+    mixed = flash_spacetime_attention(_token_major(q), k, v, feats, w, b, sl)
+    assert torch.equal(mixed, flash_spacetime_attention(q, k, v, feats, w, b, sl))
