@@ -26,8 +26,10 @@ from .reference import (  # noqa: F401
 )
 
 __all__ = [
+    "SpacetimeAttention",
     "flash_spacetime_attention",
     "flash_spacetime_attention_varlen",
+    "flash_spacetime_attention_qkv",
     "flash_spacetime_forward",
     "flash_spacetime_backward",
     "spacetime_attention_reference",
@@ -46,8 +48,10 @@ __all__ = [
 ]
 
 _OPS = {
+    "SpacetimeAttention": "attention",
     "flash_spacetime_attention": "forward",
     "flash_spacetime_attention_varlen": "forward",
+    "flash_spacetime_attention_qkv": "forward",
     "flash_spacetime_forward": "forward",
     "flash_spacetime_backward": "backward",
 }

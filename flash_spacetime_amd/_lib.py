@@ -21,6 +21,7 @@ FST_ATTN_BIAS = 1
 FST_ACT_BIAS = 2
 FST_PACKED = 4
 FST_TOKEN_MAJOR = 8
+FST_QKV_INTERLEAVED = 16
 
 FST_PHASE_WORKLIST = 1
 FST_PHASE_FWD = 2

@@ -25,19 +25,25 @@ def _same_layout(a: Tensor, b: Tensor) -> bool:
 
 
 def _run_backward(dims, q, k, v, pos4, w32, b32, lens, lse, grad_out, scale, vec_shape,
-                  rowsum: Optional[Tensor] = None):
+                  rowsum: Optional[Tensor] = None, out_like: Optional[Tensor] = None,
+                  grads: Optional[Tuple[Tensor, Tensor, Tensor]] = None):
+    """Launch the backward. grad_out is brought into the layout of `out_like`
+    (default q: contiguous, or token-major when the flags say so; empty_like
+    keeps a dense view's strides); dq, dk, dv are written into `grads` when
+    given (the slots of one interleaved gradient tensor), else into tensors
+    laid out like q, k, v."""
     lib = _lib.load()
     _lib.require_gpu(grad_out)
     if grad_out.shape != q.shape:
         raise ValueError(f"grad_out must have the shape of the output {tuple(q.shape)}")
-    # grad_out, dq, dk and dv share q's layout (contiguous, or token-major
-    # when the flags say so): empty_like keeps a dense view's strides.
+    like = q if out_like is None else out_like
     do = grad_out.to(q.dtype)
-    if not _same_layout(do, q):
-        do = torch.empty_like(q).copy_(do)
-    dq = torch.empty_like(q)
-    dk = torch.empty_like(k)
-    dv = torch.empty_like(v)
+    if not _same_layout(do, like):
+        do = torch.empty_like(like).copy_(do)
+    if grads is not None:
+        dq, dk, dv = grads
+    else:
+        dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
     rs = rowsum
     if rowsum is not None and not _same_layout(rowsum, lse):
         rs = torch.empty_like(lse)

@@ -104,7 +104,8 @@ __global__ __launch_bounds__(256, 1) void bwd_rows_kernel(BwdParams prm) {
   const bool act = prm.flags & FST_ACT_BIAS;
   const bool use_e = attn || act;
   const bool use_b = act && prm.bias;
-  const RowAddr ra = row_addr(prm.ev, eb);
+  const RowAddr ra = row_addr(prm.ev, eb);   // dO, lse, dob, D, rowsum, u, w~
+  const RowAddr rx = row_addr_x(prm.ev, eb);  // q, k, v, dq
   const int row0 = eb.blk * Cfg::ROWS;
   const int i0 = row0 + 16 * tile;
 
@@ -132,7 +133,7 @@ __global__ __launch_bounds__(256, 1) void bwd_rows_kernel(BwdParams prm) {
     const int h = ws * HW + hl;
     const bool ok = h < H && row_ok;
     if (ok) {
-      qf[hl].load_scaled(qg + ra.off(h, my_row, D), g, prm.scale);
+      qf[hl].load_scaled(qg + rx.off(h, my_row, D), g, prm.scale);
       dof[hl].load(dog + ra.off(h, my_row, D), g);
     } else {
       qf[hl].zero();
@@ -168,7 +169,7 @@ __global__ __launch_bounds__(256, 1) void bwd_rows_kernel(BwdParams prm) {
     const bool ok = row < len && n < H;
     f32x4 acc[C / 16];
     if (attn) {
-      project_row<T, D, C>(qg + ra.off(0, ok ? row : 0, D), ra.hs * D, ok, prm.scale, prm.weight, g, n, acc);
+      project_row<T, D, C>(qg + rx.off(0, ok ? row : 0, D), rx.hs * D, ok, prm.scale, prm.weight, g, n, acc);
       uf[ri].from_acc(acc);
       if (ok)
 #pragma unroll
@@ -218,7 +219,7 @@ __global__ __launch_bounds__(256, 1) void bwd_rows_kernel(BwdParams prm) {
           const int key = (idx / PER_ROW) % KC;
           const int h = idx / (PER_ROW * KC);
           const int j = j0 + key;
-          const long off = ra.off(h, j < len ? j : 0, D) + dv * 8;
+          const long off = rx.off(h, j < len ? j : 0, D) + dv * 8;
           const bf16x8 kv = j < len ? *reinterpret_cast<const bf16x8*>(kg + off) : VecOf<bf16>::zero();
           const bf16x8 vv = j < len ? *reinterpret_cast<const bf16x8*>(vg + off) : VecOf<bf16>::zero();
           *reinterpret_cast<bf16x8*>(Ks + (h * KC + key) * Cfg::KV_ROW + dv * 8) = kv;
@@ -275,8 +276,8 @@ __global__ __launch_bounds__(256, 1) void bwd_rows_kernel(BwdParams prm) {
           } else {
             int key = j0 + 16 * s + n;
             key = key < len ? key : len - 1;
-            kf.load(kg + ra.off(h, key, D), g);
-            vf.load(vg + ra.off(h, key, D), g);
+            kf.load(kg + rx.off(h, key, D), g);
+            vf.load(vg + rx.off(h, key, D), g);
           }
           S[s] = mma_k<D>(kf, qf[hl], ue);
           P_[s] = mma_k<D>(vf, dof[hl], we);
@@ -317,7 +318,7 @@ __global__ __launch_bounds__(256, 1) void bwd_rows_kernel(BwdParams prm) {
 #pragma unroll
                 for (int r = 0; r < 4; ++r) {
                   const int j = j0 + 16 * s + 4 * g + r;
-                  kt.v[4 * s + r] = j < len ? kg[ra.off(h, j, D) + 16 * dt + n] : 0.f;
+                  kt.v[4 * s + r] = j < len ? kg[rx.off(h, j, D) + 16 * dt + n] : 0.f;
                 }
             }
             dQ[hl][dt] = mma_j(kt, dsf, dQ[hl][dt]);
@@ -406,7 +407,7 @@ __global__ __launch_bounds__(256, 1) void bwd_rows_kernel(BwdParams prm) {
         }
       }
       o = o * prm.scale;
-      if (row_ok) store4<T>(dqg + ra.off(h, my_row, D) + 16 * dt + 4 * g, o);
+      if (row_ok) store4<T>(dqg + rx.off(h, my_row, D) + 16 * dt + 4 * g, o);
     }
     if (attn) __syncthreads();
   }
@@ -452,7 +453,7 @@ __global__ __launch_bounds__(256, 1) void bwd_rows_kernel(BwdParams prm) {
 #pragma unroll
           for (int dt = 0; dt < D / 16; ++dt) {
             const int d = 16 * dt + n;
-            const float aq = (attn && ok) ? (float)qg[ra.off(h, row, D) + d] * prm.scale : 0.f;
+            const float aq = (attn && ok) ? (float)qg[rx.off(h, row, D) + d] * prm.scale : 0.f;
             const float ao = (act && ok) ? (float)dog[ra.off(h, row, D) + d] : 0.f;
             if (ct == 0) dbl[dt] += ao;
             dw[dt][ct] = mfma_f32(aq, bh, dw[dt][ct]);
@@ -482,7 +483,7 @@ __global__ __launch_bounds__(256, 1) void bwd_rows_kernel(BwdParams prm) {
     }
   }
 
-  zero_pad_rows<T>(prm.ev, eb, ra, row0, Cfg::ROWS, D, tid, 256, dqg, prm.rowsum, 1);
+  zero_pad_rows<T>(prm.ev, eb, rx, ra, row0, Cfg::ROWS, D, tid, 256, dqg, prm.rowsum, 1);
 }
 
 // ---------------------------------------------------------------------------
@@ -529,7 +530,8 @@ __global__ __launch_bounds__(256, 1) void bwd_cols_kernel(BwdParams prm) {
   const bool attn = prm.flags & FST_ATTN_BIAS;
   const bool act = prm.flags & FST_ACT_BIAS;
   const bool use_e = attn || act;
-  const RowAddr ra = row_addr(ev, eb);
+  const RowAddr ra = row_addr(ev, eb);   // dO, lse, dob, D, u, w~
+  const RowAddr rx = row_addr_x(ev, eb);  // q, k, v, dk, dv
   const int key0 = eb.blk * Cfg::KEYS;
   const int j0t = key0 + 16 * tile;
 
@@ -556,8 +558,8 @@ __global__ __launch_bounds__(256, 1) void bwd_cols_kernel(BwdParams prm) {
   for (int hl = 0; hl < HW; ++hl) {
     const int h = ws * HW + hl;
     if (h < H && key_ok) {
-      kf[hl].load(kg + ra.off(h, my_key, D), g);
-      vf[hl].load(vg + ra.off(h, my_key, D), g);
+      kf[hl].load(kg + rx.off(h, my_key, D), g);
+      vf[hl].load(vg + rx.off(h, my_key, D), g);
     } else {
       kf[hl].zero();
       vf[hl].zero();
@@ -582,11 +584,10 @@ __global__ __launch_bounds__(256, 1) void bwd_cols_kernel(BwdParams prm) {
         const int i = c0 + il;
         bf16x8 qv = VecOf<bf16>::zero(), ov = VecOf<bf16>::zero();
         if (i < len) {
-          const long off = ra.off(h, i, D) + dv * 8;
-          const bf16x8 raw = *reinterpret_cast<const bf16x8*>(qg + off);
+          const bf16x8 raw = *reinterpret_cast<const bf16x8*>(qg + rx.off(h, i, D) + dv * 8);
 #pragma unroll
           for (int e = 0; e < 8; ++e) qv[e] = (bf16)((float)raw[e] * prm.scale);
-          ov = *reinterpret_cast<const bf16x8*>(dog + off);
+          ov = *reinterpret_cast<const bf16x8*>(dog + ra.off(h, i, D) + dv * 8);
         }
         *reinterpret_cast<bf16x8*>(Qs + (h * KC + il) * Cfg::QO_ROW + dv * 8) = qv;
         *reinterpret_cast<bf16x8*>(Os + (h * KC + il) * Cfg::QO_ROW + dv * 8) = ov;
@@ -661,7 +662,7 @@ __global__ __launch_bounds__(256, 1) void bwd_cols_kernel(BwdParams prm) {
         } else {
           int i = c0 + 16 * s + n;
           i = i < len ? i : len - 1;
-          qa.load_scaled(qg + ra.off(h, i, D), g, prm.scale);
+          qa.load_scaled(qg + rx.off(h, i, D), g, prm.scale);
           oa.load(dog + ra.off(h, i, D), g);
         }
         S[s] = mma_k<D>(qa, kf[hl], ue);
@@ -701,9 +702,9 @@ __global__ __launch_bounds__(256, 1) void bwd_cols_kernel(BwdParams prm) {
             for (int r = 0; r < 4; ++r) {
               const int i = c0 + 16 * s + 4 * g + r;
               const bool ok = i < len;
-              const long off = ra.off(h, ok ? i : 0, D) + 16 * dt + n;
-              ot.v[4 * s + r] = ok ? (float)dog[off] : 0.f;
-              qt.v[4 * s + r] = ok ? (float)qg[off] * prm.scale : 0.f;
+              const int ic = ok ? i : 0;
+              ot.v[4 * s + r] = ok ? (float)dog[ra.off(h, ic, D) + 16 * dt + n] : 0.f;
+              qt.v[4 * s + r] = ok ? (float)qg[rx.off(h, ic, D) + 16 * dt + n] * prm.scale : 0.f;
             }
         }
         dV[hl][dt] = mma_j(ot, pf, dV[hl][dt]);
@@ -721,12 +722,12 @@ __global__ __launch_bounds__(256, 1) void bwd_cols_kernel(BwdParams prm) {
     if (h >= H || !key_ok) continue;
 #pragma unroll
     for (int dt = 0; dt < D / 16; ++dt) {
-      store4<T>(dkg + ra.off(h, my_key, D) + 16 * dt + 4 * g, dK[hl][dt]);
-      store4<T>(dvg + ra.off(h, my_key, D) + 16 * dt + 4 * g, dV[hl][dt]);
+      store4<T>(dkg + rx.off(h, my_key, D) + 16 * dt + 4 * g, dK[hl][dt]);
+      store4<T>(dvg + rx.off(h, my_key, D) + 16 * dt + 4 * g, dV[hl][dt]);
     }
   }
-  zero_pad_rows<T>(ev, eb, ra, key0, Cfg::KEYS, D, tid, 256, dkg, nullptr, 1);
-  zero_pad_rows<T>(ev, eb, ra, key0, Cfg::KEYS, D, tid, 256, dvg, nullptr, 1);
+  zero_pad_rows<T>(ev, eb, rx, rx, key0, Cfg::KEYS, D, tid, 256, dkg, nullptr, 1);
+  zero_pad_rows<T>(ev, eb, rx, rx, key0, Cfg::KEYS, D, tid, 256, dvg, nullptr, 1);
 }
 
 // ---------------------------------------------------------------------------

@@ -91,7 +91,8 @@ __global__ __launch_bounds__(256, 2) void bwd_rows2_kernel(BwdParams prm) {
   const bool attn = FL >= 0 ? (FL & FST_ATTN_BIAS) != 0 : (prm.flags & FST_ATTN_BIAS) != 0;
   const bool act = FL >= 0 ? (FL & FST_ACT_BIAS) != 0 : (prm.flags & FST_ACT_BIAS) != 0;
   const bool use_e = attn || act;
-  const RowAddr ra = row_addr(prm.ev, eb);
+  const RowAddr ra = row_addr(prm.ev, eb);   // dO, lse, D, rowsum, qt
+  const RowAddr rx = row_addr_x(prm.ev, eb);  // q, k, v, dq
   const int i0 = eb.blk * 16;
   const int last = len - 1;
   bf16* dqg = reinterpret_cast<bf16*>(prm.dq);
@@ -101,7 +102,7 @@ __global__ __launch_bounds__(256, 2) void bwd_rows2_kernel(BwdParams prm) {
   const int nbv = len > 0 ? (len + 15) / 16 : (prm.ev.packed ? 0 : 1);
   float* part = eb.blk < nbv ? prm.dw_part + (long)(prm.ev.blkcum[eb.b] + eb.blk) * DCW : nullptr;
   if (i0 >= len) {
-    zero_tile_rows<bf16, D>(prm.ev, ra, i0, len, H, tid, dqg, prm.rowsum);
+    zero_tile_rows<bf16, D>(prm.ev, rx, ra, i0, len, H, tid, dqg, prm.rowsum);
     if (part)
       for (int e = tid; e < DCW; e += 256) part[e] = 0.f;
     return;
@@ -130,7 +131,7 @@ __global__ __launch_bounds__(256, 2) void bwd_rows2_kernel(BwdParams prm) {
 #pragma unroll
   for (int hl = 0; hl < HW; ++hl) {
     const int hc = min(w * HW + hl, H - 1);
-    qf[hl].load(qg + ra.off(hc, rc, D), g);
+    qf[hl].load(qg + rx.off(hc, rc, D), g);
     dof[hl].load(dog + ra.off(hc, rc, D), g);
     lse2[hl] = prm.lse[ra.vec(hc, rc)];
   }
@@ -143,9 +144,9 @@ __global__ __launch_bounds__(256, 2) void bwd_rows2_kernel(BwdParams prm) {
   for (int r = 0; r < 4; ++r) {
     const int row = i0 + 4 * w + r;
     const bool ok = row < len && n < H;
-    const long xo = ra.off(0, row < len ? row : last, D);
-    if (attn) xq[r].load(qg + xo, ra.hs * D, ok, g, n);
-    if (act) xd[r].load(dog + xo, ra.hs * D, ok, g, n);
+    const int rr = row < len ? row : last;
+    if (attn) xq[r].load(qg + rx.off(0, rr, D), rx.hs * D, ok, g, n);
+    if (act) xd[r].load(dog + ra.off(0, rr, D), ra.hs * D, ok, g, n);
   }
   float4 pos_i = float4{0.f, 0.f, 0.f, 0.f};
   float fa[NCT], fb[NCT];
@@ -160,15 +161,15 @@ __global__ __launch_bounds__(256, 2) void bwd_rows2_kernel(BwdParams prm) {
   }
 
   // ---- operand stream: K, V rows of the wave's heads, key positions ----
-  const long ebase = ra.off(0, 0, D);
-  const int rowb = (int)(ra.ts * D * 2);
-  const unsigned ebytes = (unsigned)((prm.ev.tokmajor ? (long)len * ra.ts : (long)H * ra.hs) * D * 2);
+  const long ebase = rx.off(0, 0, D);
+  const int rowb = (int)(rx.ts * D * 2);
+  const unsigned ebytes = (unsigned)((prm.ev.tokmajor ? (long)len * rx.ts : (long)H * rx.hs) * D * 2);
   const Buf kbuf(kg + ebase, ebytes), vbuf(vg + ebase, ebytes);
   const Buf pbuf(prm.ev.pos4 + ra.pos_base, (unsigned)len * 16u);
   int kvo[HW];
 #pragma unroll
   for (int hl = 0; hl < HW; ++hl)
-    kvo[hl] = (int)(min(w * HW + hl, H - 1) * ra.hs * D * 2) + n * rowb + kfrag_goff<D>(g);
+    kvo[hl] = (int)(min(w * HW + hl, H - 1) * rx.hs * D * 2) + n * rowb + kfrag_goff<D>(g);
   KFrag<bf16, D> kf[HW][NS], vf[HW][NS];
   float4 pj[NS];
   auto issue = [&](int jn) __attribute__((always_inline)) {
@@ -496,7 +497,7 @@ __global__ __launch_bounds__(256, 2) void bwd_rows2_kernel(BwdParams prm) {
     for (int hl = 0; hl < HW; ++hl) {
       const int h = w * HW + hl;
       if (h >= H) continue;
-      bf16* orow = dqg + ra.off(h, my_row, D);
+      bf16* orow = dqg + rx.off(h, my_row, D);
       if constexpr (DT::X32) {
 #pragma unroll
         for (int t = 0; t < NQ / 2; ++t)
@@ -577,7 +578,7 @@ __global__ __launch_bounds__(256, 2) void bwd_rows2_kernel(BwdParams prm) {
     for (int e = tid; e < DCW; e += 256) part[e] = 0.f;
   }
 
-  zero_tile_rows<bf16, D>(prm.ev, ra, i0, len, H, tid, dqg, prm.rowsum);
+  zero_tile_rows<bf16, D>(prm.ev, rx, ra, i0, len, H, tid, dqg, prm.rowsum);
 }
 
 // ---------------------------------------------------------------------------
@@ -630,14 +631,15 @@ __global__ __launch_bounds__(256, (Cols2Cfg<HP, D, C, RC>::OCC)) void bwd_cols2_
   const bool attn = FL >= 0 ? (FL & FST_ATTN_BIAS) != 0 : (prm.flags & FST_ATTN_BIAS) != 0;
   const bool act = FL >= 0 ? (FL & FST_ACT_BIAS) != 0 : (prm.flags & FST_ACT_BIAS) != 0;
   const bool use_e = attn || act;
-  const RowAddr ra = row_addr(ev, eb);
+  const RowAddr ra = row_addr(ev, eb);   // qt, dO, lse, D
+  const RowAddr rx = row_addr_x(ev, eb);  // k, v, dk, dv
   const int k0 = eb.blk * 16;
   const int last = len - 1;
   bf16* dkg = reinterpret_cast<bf16*>(prm.dk);
   bf16* dvg = reinterpret_cast<bf16*>(prm.dv);
   if (k0 >= len) {
-    zero_tile_rows<bf16, D>(ev, ra, k0, len, H, tid, dkg, nullptr);
-    zero_tile_rows<bf16, D>(ev, ra, k0, len, H, tid, dvg, nullptr);
+    zero_tile_rows<bf16, D>(ev, rx, rx, k0, len, H, tid, dkg, nullptr);
+    zero_tile_rows<bf16, D>(ev, rx, rx, k0, len, H, tid, dvg, nullptr);
     return;
   }
   const bf16x4 id = ident_x16(g, n);
@@ -654,8 +656,8 @@ __global__ __launch_bounds__(256, (Cols2Cfg<HP, D, C, RC>::OCC)) void bwd_cols2_
   for (int hl = 0; hl < HW; ++hl) {
     // Padded heads (h >= H) compute on head H-1's data and are never stored.
     const int hq = min(w * HW + hl, H - 1);
-    kf[hl].load(kg + ra.off(hq, kc, D), g);
-    vf[hl].load(vg + ra.off(hq, kc, D), g);
+    kf[hl].load(kg + rx.off(hq, kc, D), g);
+    vf[hl].load(vg + rx.off(hq, kc, D), g);
 #pragma unroll
     for (int q = 0; q < NQ; ++q) dK[hl][q] = dV[hl][q] = zero4();
   }
@@ -911,8 +913,8 @@ __global__ __launch_bounds__(256, (Cols2Cfg<HP, D, C, RC>::OCC)) void bwd_cols2_
     for (int hl = 0; hl < HW; ++hl) {
       const int h = w * HW + hl;
       if (h >= H) continue;
-      bf16* krow = dkg + ra.off(h, my_key, D);
-      bf16* vrow = dvg + ra.off(h, my_key, D);
+      bf16* krow = dkg + rx.off(h, my_key, D);
+      bf16* vrow = dvg + rx.off(h, my_key, D);
       if constexpr (DT::X32) {
 #pragma unroll
         for (int t = 0; t < NQ / 2; ++t) {
@@ -928,8 +930,8 @@ __global__ __launch_bounds__(256, (Cols2Cfg<HP, D, C, RC>::OCC)) void bwd_cols2_
       }
     }
   }
-  zero_tile_rows<bf16, D>(ev, ra, k0, len, H, tid, dkg, nullptr);
-  zero_tile_rows<bf16, D>(ev, ra, k0, len, H, tid, dvg, nullptr);
+  zero_tile_rows<bf16, D>(ev, rx, rx, k0, len, H, tid, dkg, nullptr);
+  zero_tile_rows<bf16, D>(ev, rx, rx, k0, len, H, tid, dvg, nullptr);
 }
 
 // ---------------------------------------------------------------------------

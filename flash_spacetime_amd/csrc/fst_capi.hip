@@ -171,8 +171,10 @@ static fwd_dispatch_fn fwd_table(int dtype, int D) {
 
 static int check_common(int dtype, int flags, int B, int H, int L, int T, int D, int C) {
   if (dtype != FST_BF16 && dtype != FST_F32) return fail(FST_EINVAL, "dtype must be FST_BF16 or FST_F32, got %d", dtype);
-  if (flags & ~(FST_ATTN_BIAS | FST_ACT_BIAS | FST_PACKED | FST_TOKEN_MAJOR))
+  if (flags & ~(FST_ATTN_BIAS | FST_ACT_BIAS | FST_PACKED | FST_TOKEN_MAJOR | FST_QKV_INTERLEAVED))
     return fail(FST_EINVAL, "unknown flag bits 0x%x", flags);
+  if ((flags & FST_QKV_INTERLEAVED) && !(flags & (FST_PACKED | FST_TOKEN_MAJOR)))
+    return fail(FST_EINVAL, "FST_QKV_INTERLEAVED needs a token-major layout (FST_PACKED or FST_TOKEN_MAJOR)");
   if ((flags & FST_PACKED) && (flags & FST_TOKEN_MAJOR))
     return fail(FST_EINVAL, "FST_TOKEN_MAJOR applies to the padded layout (packed is token-major already)");
   if (B < 0 || L < 0 || T < 0) return fail(FST_EINVAL, "negative size (B=%d, L=%d, T=%d)", B, L, T);
@@ -380,6 +382,7 @@ int fst_forward_phases(int phases, int dtype, int flags, int B, int H, int L, in
   prm.ev.T = T;
   prm.ev.packed = packed ? 1 : 0;
   prm.ev.tokmajor = (packed || (flags & FST_TOKEN_MAJOR)) ? 1 : 0;
+  prm.ev.xmul = (flags & FST_QKV_INTERLEAVED) ? 3 : 1;
   prm.H = H;
   prm.flags = flags;
   prm.scale = scale;
@@ -470,6 +473,7 @@ int fst_backward_phases(int phases, int dtype, int flags, int B, int H, int L, i
   prm.ev.T = T;
   prm.ev.packed = packed ? 1 : 0;
   prm.ev.tokmajor = (packed || (flags & FST_TOKEN_MAJOR)) ? 1 : 0;
+  prm.ev.xmul = (flags & FST_QKV_INTERLEAVED) ? 3 : 1;
   prm.blkcum_cols = bc_c;
   prm.H = H;
   prm.flags = flags;

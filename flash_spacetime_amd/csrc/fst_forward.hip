@@ -81,7 +81,8 @@ __global__ __launch_bounds__(256, 1) void fwd_kernel(FwdParams prm) {
   const bool attn = prm.flags & FST_ATTN_BIAS;
   const bool act = prm.flags & FST_ACT_BIAS;
   const bool use_e = attn || act;
-  const RowAddr ra = row_addr(prm.ev, eb);
+  const RowAddr ra = row_addr(prm.ev, eb);   // out, lse
+  const RowAddr rx = row_addr_x(prm.ev, eb);  // q, k, v
 
   const int row0 = eb.blk * Cfg::ROWS;
   const int i0 = row0 + 16 * tile;  // first row of this wave's tile
@@ -107,7 +108,7 @@ __global__ __launch_bounds__(256, 1) void fwd_kernel(FwdParams prm) {
   for (int hl = 0; hl < HW; ++hl) {
     const int h = ws * HW + hl;
     if (h < H && row_ok)
-      qf[hl].load_scaled(qg + ra.off(h, my_row, D), g, prm.scale);
+      qf[hl].load_scaled(qg + rx.off(h, my_row, D), g, prm.scale);
     else
       qf[hl].zero();
 #pragma unroll
@@ -125,7 +126,7 @@ __global__ __launch_bounds__(256, 1) void fwd_kernel(FwdParams prm) {
     if (attn) {
       f32x4 acc[C / 16];
       const bool ok = row < len && n < H;
-      project_row<T, D, C>(qg + ra.off(0, ok ? row : 0, D), ra.hs * D, ok, prm.scale, prm.weight, g, n, acc);
+      project_row<T, D, C>(qg + rx.off(0, ok ? row : 0, D), rx.hs * D, ok, prm.scale, prm.weight, g, n, acc);
       uf[ri].from_acc(acc);
     } else {
       uf[ri].zero();
@@ -155,7 +156,7 @@ __global__ __launch_bounds__(256, 1) void fwd_kernel(FwdParams prm) {
         const int key = (idx / PER_ROW) % KC;
         const int h = idx / (PER_ROW * KC);
         const int j = j0 + key;
-        const bf16x8 val = j < len ? *reinterpret_cast<const bf16x8*>(vg + ra.off(h, j, D) + dv * VEC)
+        const bf16x8 val = j < len ? *reinterpret_cast<const bf16x8*>(vg + rx.off(h, j, D) + dv * VEC)
                                    : VecOf<bf16>::zero();
         *reinterpret_cast<bf16x8*>(Vs + (h * KC + key) * Cfg::V_ROW + dv * VEC) = val;
       }
@@ -201,7 +202,7 @@ __global__ __launch_bounds__(256, 1) void fwd_kernel(FwdParams prm) {
         int key = j0 + 16 * s + n;
         key = key < len ? key : len - 1;
         KFrag<T, D> kf;
-        kf.load(kg + ra.off(h, key, D), g);
+        kf.load(kg + rx.off(h, key, D), g);
         S[s] = mma_k<D>(kf, qf[hl], init);
       }
       float mx = -INFINITY;
@@ -240,7 +241,7 @@ __global__ __launch_bounds__(256, 1) void fwd_kernel(FwdParams prm) {
 #pragma unroll
             for (int r = 0; r < 4; ++r) {
               const int j = j0 + 16 * s + 4 * g + r;
-              vf.v[4 * s + r] = j < len ? vg[ra.off(h, j, D) + 16 * dt + n] : 0.f;
+              vf.v[4 * s + r] = j < len ? vg[rx.off(h, j, D) + 16 * dt + n] : 0.f;
             }
         }
         O[hl][dt] = mma_j(vf, pf, O[hl][dt] * alpha);
@@ -325,7 +326,7 @@ __global__ __launch_bounds__(256, 1) void fwd_kernel(FwdParams prm) {
   }
 
   // Padding rows of this block (and past the event for its last block): 0.
-  zero_pad_rows<T>(prm.ev, eb, ra, row0, Cfg::ROWS, D, tid, 256, outg, prm.lse, 1);
+  zero_pad_rows<T>(prm.ev, eb, ra, ra, row0, Cfg::ROWS, D, tid, 256, outg, prm.lse, 1);
 }
 
 // ---------------------------------------------------------------------------

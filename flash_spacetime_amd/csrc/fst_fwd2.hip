@@ -66,12 +66,13 @@ __global__ __launch_bounds__(256, OCC) void fwd2_kernel(FwdParams prm) {
   const bool attn = FL >= 0 ? (FL & FST_ATTN_BIAS) != 0 : (prm.flags & FST_ATTN_BIAS) != 0;
   const bool act = FL >= 0 ? (FL & FST_ACT_BIAS) != 0 : (prm.flags & FST_ACT_BIAS) != 0;
   const bool use_e = attn || act;
-  const RowAddr ra = row_addr(prm.ev, eb);
+  const RowAddr ra = row_addr(prm.ev, eb);   // out, lse
+  const RowAddr rx = row_addr_x(prm.ev, eb);  // q, k, v
   const int i0 = eb.blk * 16;
   const int last = len - 1;
   bf16* outg = reinterpret_cast<bf16*>(prm.out);
   if (i0 >= len) {  // a tile of padding rows only
-    zero_tile_rows<bf16, D>(prm.ev, ra, i0, len, H, tid, outg, prm.lse);
+    zero_tile_rows<bf16, D>(prm.ev, ra, ra, i0, len, H, tid, outg, prm.lse);
     return;
   }
 
@@ -95,7 +96,7 @@ __global__ __launch_bounds__(256, OCC) void fwd2_kernel(FwdParams prm) {
     // Padded heads (h >= H) compute on head H-1's data and are never stored,
     // so the chunk loop needs no per-head branches.
     const int hq = min(w * HW + hl, H - 1);
-    qf[hl].load(qg + ra.off(hq, row_ok ? my_row : last, D), g);
+    qf[hl].load(qg + rx.off(hq, row_ok ? my_row : last, D), g);
   }
 
   // ---- row-owner state: rows i0 + 4w + r, heads on lane n ----
@@ -106,7 +107,7 @@ __global__ __launch_bounds__(256, OCC) void fwd2_kernel(FwdParams prm) {
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       const int row = i0 + 4 * w + r;
-      xq[r].load(qg + ra.off(0, row < len ? row : last, D), ra.hs * D, row < len && n < H, g, n);
+      xq[r].load(qg + rx.off(0, row < len ? row : last, D), rx.hs * D, row < len && n < H, g, n);
     }
   }
   // Angle lane assignment: lane (g, n) evaluates row i0 + 4w + g against key
@@ -126,15 +127,15 @@ __global__ __launch_bounds__(256, OCC) void fwd2_kernel(FwdParams prm) {
   // Buffer views of this event's K, V and positions. Row r of head h sits at
   // element (r ts + h hs) D from the event's base; a chunk advances the
   // scalar offset by KC ts D elements.
-  const long ebase = ra.off(0, 0, D);
-  const int rowb = (int)(ra.ts * D * 2);  // bytes per key row
-  const unsigned ebytes = (unsigned)((prm.ev.tokmajor ? (long)len * ra.ts : (long)H * ra.hs) * D * 2);
+  const long ebase = rx.off(0, 0, D);
+  const int rowb = (int)(rx.ts * D * 2);  // bytes per key row
+  const unsigned ebytes = (unsigned)((prm.ev.tokmajor ? (long)len * rx.ts : (long)H * rx.hs) * D * 2);
   const Buf kbuf(kg + ebase, ebytes), vbuf(vg + ebase, ebytes);
   const Buf pbuf(prm.ev.pos4 + ra.pos_base, (unsigned)len * 16u);
   int kvo[HW];  // lane offset of head hl, key n (bytes)
 #pragma unroll
   for (int hl = 0; hl < HW; ++hl)
-    kvo[hl] = (int)(min(w * HW + hl, H - 1) * ra.hs * D * 2) + n * rowb + kfrag_goff<D>(g);
+    kvo[hl] = (int)(min(w * HW + hl, H - 1) * rx.hs * D * 2) + n * rowb + kfrag_goff<D>(g);
 
   // Operands of the chunk in flight: K, V rows of the wave's heads and the
   // key positions. Loads for chunk j0 + KC are issued as soon as the
@@ -426,7 +427,7 @@ __global__ __launch_bounds__(256, OCC) void fwd2_kernel(FwdParams prm) {
     }
   }
 
-  zero_tile_rows<bf16, D>(prm.ev, ra, i0, len, H, tid, outg, prm.lse);
+  zero_tile_rows<bf16, D>(prm.ev, ra, ra, i0, len, H, tid, outg, prm.lse);
 }
 
 template <int HP, int D, int C>

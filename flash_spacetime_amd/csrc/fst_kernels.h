@@ -18,6 +18,7 @@ struct EventSpec {
   const float4* pos4;     // [B*L] or [T] (x, y, z, t) fp32
   int B, H, L, T, packed;
   int tokmajor;           // rows of one token's heads are adjacent (packed, or padded token-major)
+  int xmul;               // 3: q, k, v (and dq, dk, dv) interleaved per token as [.., 3, H, X]; else 1
 };
 
 struct EventBlock {
@@ -85,6 +86,20 @@ __device__ __forceinline__ RowAddr row_addr(const EventSpec& ev, const EventBloc
     r.hs = ev.L;
     r.ts = 1;
     r.pos_base = (long)eb.b * ev.L;
+  }
+  return r;
+}
+
+// Row addressing of q, k, v, dq, dk and dv. With the operands interleaved
+// per token (one [.., 3, H, D] projection output), a token's q heads are
+// followed by its k heads and v heads: the token stride is three times that
+// of out, grad_out and the per-row vectors, and k, v start H D elements
+// after q.
+__device__ __forceinline__ RowAddr row_addr_x(const EventSpec& ev, const EventBlock& eb) {
+  RowAddr r = row_addr(ev, eb);
+  if (ev.xmul > 1) {
+    r.base_row *= ev.xmul;
+    r.ts *= ev.xmul;
   }
   return r;
 }
@@ -297,11 +312,12 @@ __device__ __forceinline__ void write_embedding(T* erow, float4 pi, float4 pj, c
 
 // Zero the outputs of padding rows [max(row0, len), end) of a padded event,
 // where end is the block's last row, or L for the event's last block
-// (pad-row contract: forward.py:19-22, 288-304).
+// (pad-row contract: forward.py:19-22, 288-304). Rows of out are addressed
+// by ra, those of vec_out by rv.
 template <typename T>
 __device__ __forceinline__ void zero_pad_rows(const EventSpec& ev, const EventBlock& eb, const RowAddr& ra,
-                                              int row0, int rows, int width, int tid, int nthreads, T* out,
-                                              float* vec_out, int vec_count) {
+                                              const RowAddr& rv, int row0, int rows, int width, int tid,
+                                              int nthreads, T* out, float* vec_out, int vec_count) {
   if (ev.packed) return;
   const int nblk = eb.len > 0 ? (eb.len + rows - 1) / rows : 1;
   const int first = row0 > eb.len ? row0 : eb.len;
@@ -319,7 +335,7 @@ __device__ __forceinline__ void zero_pad_rows(const EventSpec& ev, const EventBl
     for (int idx = tid; idx < ev.H * nrows * vec_count; idx += nthreads) {
       const int r = (idx / vec_count) % nrows;
       const int h = idx / (vec_count * nrows);
-      vec_out[ra.vec(h, first + r) * vec_count + idx % vec_count] = 0.f;
+      vec_out[rv.vec(h, first + r) * vec_count + idx % vec_count] = 0.f;
     }
 }
 

@@ -176,11 +176,12 @@ __device__ __forceinline__ bool tile_block(const EventSpec& ev, int w, EventBloc
 }
 
 // Zero rows [max(i0, len), min(i0 + 16, L)) of a padded event for every head
-// (pad-row contract: forward.py:19-22), 16 bytes per store; `vec` gets zeros
-// at the same (head, row) positions when not null.
+// (pad-row contract: forward.py:19-22), 16 bytes per store, addressed by ra;
+// `vec` gets zeros at the same (head, row) positions, addressed by rv, when
+// not null.
 template <typename T, int D>
-__device__ __forceinline__ void zero_tile_rows(const EventSpec& ev, const RowAddr& ra, int i0, int len, int H,
-                                               int tid, T* out, float* vec) {
+__device__ __forceinline__ void zero_tile_rows(const EventSpec& ev, const RowAddr& ra, const RowAddr& rv, int i0,
+                                               int len, int H, int tid, T* out, float* vec) {
   if (ev.packed) return;
   const int first = i0 > len ? i0 : len;
   const int end = i0 + 16 < ev.L ? i0 + 16 : ev.L;
@@ -192,7 +193,7 @@ __device__ __forceinline__ void zero_tile_rows(const EventSpec& ev, const RowAdd
     *reinterpret_cast<u32x4*>(out + ra.off(h, first + r, D) + c * (16 / (int)sizeof(T))) = u32x4{0u, 0u, 0u, 0u};
   }
   if (vec)
-    for (int idx = tid; idx < H * nr; idx += 256) vec[ra.vec(idx / nr, first + idx % nr)] = 0.f;
+    for (int idx = tid; idx < H * nr; idx += 256) vec[rv.vec(idx / nr, first + idx % nr)] = 0.f;
 }
 
 // The W operand of project_slots: lane (g, n) holds W[Qd g + s][channel(16

@@ -111,7 +111,7 @@ class _Prepared:
     the reference does (forward.py:274)."""
 
     def __init__(self, q, k, v, feats, weight, bias, seqlens, scale, use_attn_bias,
-                 use_activation_bias, cu_seqlens):
+                 use_activation_bias, cu_seqlens, interleaved: bool = False):
         for t in (q, k, v, feats, weight):
             _lib.require_gpu(t)
         if q.dtype not in _DTYPES:
@@ -155,12 +155,16 @@ class _Prepared:
         self.heads, self.dim, self.channels = heads, dim, c
         self.dtype = _DTYPES[q.dtype]
         self.scale = float(dim ** -0.5 if scale is None else scale)
-        self.token_major = not self.packed and all(is_token_major(t) for t in (q, k, v))
+        # interleaved: q, k, v are the slots of one [B, L, 3, H, D] / [T, 3, H, D]
+        # tensor (the caller, `_FlashSpacetimeAttentionQKV`, guarantees it).
+        self.interleaved = interleaved
+        self.token_major = not self.packed and (interleaved or all(is_token_major(t) for t in (q, k, v)))
         self.flags = ((_lib.FST_ATTN_BIAS if use_attn_bias else 0)
                       | (_lib.FST_ACT_BIAS if use_activation_bias else 0)
                       | (_lib.FST_PACKED if self.packed else 0)
-                      | (_lib.FST_TOKEN_MAJOR if self.token_major else 0))
-        if self.token_major:
+                      | (_lib.FST_TOKEN_MAJOR if self.token_major else 0)
+                      | (_lib.FST_QKV_INTERLEAVED if interleaved else 0))
+        if self.token_major or interleaved:
             self.q, self.k, self.v = q, k, v
         else:
             self.q, self.k, self.v = (t.contiguous() for t in (q, k, v))
@@ -179,6 +183,16 @@ class _Prepared:
             return (self.tokens, self.heads)
         return (self.batch, self.heads, self.length)
 
+    def empty_out(self) -> Tensor:
+        """The output (and grad_out) in the layout the kernels write: q's, or
+        for interleaved operands the dense token-major one."""
+        if not self.interleaved:
+            return torch.empty_like(self.q)
+        if self.packed:
+            return torch.empty(self.tokens, self.heads, self.dim, device=self.device, dtype=self.q.dtype)
+        return torch.empty(self.batch, self.length, self.heads, self.dim, device=self.device,
+                           dtype=self.q.dtype).transpose(1, 2)
+
     def empty_vec(self) -> Tensor:
         """A float32 per-row vector (lse, rowsum) in the operands' layout."""
         if self.token_major:
@@ -189,7 +203,7 @@ class _Prepared:
 
 def _run_forward(prep: _Prepared) -> Tuple[Tensor, Tensor]:
     lib = _lib.load()
-    out = torch.empty_like(prep.q)  # keeps a token-major view's layout
+    out = prep.empty_out()
     lse = prep.empty_vec()
     ws_bytes = lib.fst_forward_workspace_bytes(*prep.dims())
     ws = torch.empty(max(ws_bytes, 1), device=prep.device, dtype=torch.uint8)
@@ -411,4 +425,134 @@ def flash_spacetime_attention_varlen(
         raise ValueError("cu_seqlens is required for dense packed inputs")
     return _FlashSpacetimeAttention.apply(
         q, k, v, feats, weight, bias, None, scale, use_attn_bias, use_activation_bias, cu_seqlens
+    )
+
+
+def _qkv_views(qkv: Tensor, packed: bool) -> Tuple[Tensor, Tensor, Tensor]:
+    """q, k, v as the kernels index them: `[T, H, D]` slots of a packed
+    `[T, 3, H, D]`, or heads-first `[B, H, L, D]` views of `[B, L, 3, H, D]`."""
+    if packed:
+        return qkv[:, 0], qkv[:, 1], qkv[:, 2]
+    return qkv[:, :, 0].transpose(1, 2), qkv[:, :, 1].transpose(1, 2), qkv[:, :, 2].transpose(1, 2)
+
+
+class _FlashSpacetimeAttentionQKV(torch.autograd.Function):
+    """The fused op on one interleaved q/k/v tensor; its gradient is one
+    tensor of the same layout, written by the kernels slot by slot."""
+
+    @staticmethod
+    def forward(  # type: ignore[override]
+        ctx: Any,
+        qkv: Tensor,
+        feats: Tensor,
+        weight: Tensor,
+        bias: Optional[Tensor],
+        seqlens: Optional[Tensor],
+        scale: Optional[float],
+        use_attn_bias: bool,
+        use_activation_bias: bool,
+        cu_seqlens: Optional[Tensor],
+    ) -> Tensor:
+        if feats.requires_grad:
+            raise ValueError("feats (detector data) must not require grad")
+        packed = cu_seqlens is not None
+        q, k, v = _qkv_views(qkv, packed)
+        prep = _Prepared(q, k, v, feats, weight, bias, seqlens, scale, use_attn_bias,
+                         use_activation_bias, cu_seqlens, interleaved=True)
+        out, lse = _run_forward(prep)
+        ctx.save_for_backward(qkv, prep.pos4, prep.lens, lse)
+        ctx.prep_meta = (prep.weight, prep.bias, weight.dtype, None if bias is None else bias.dtype)
+        ctx.dims = prep.dims()
+        ctx.scale = prep.scale
+        ctx.packed = packed
+        ctx.flags = (use_attn_bias, use_activation_bias)
+        ctx.vec_shape = prep.vec_shape()
+        return out if packed else out.transpose(1, 2)  # [T, H, D] / [B, L, H, D], dense
+
+    @staticmethod
+    def backward(ctx: Any, grad_out: Tensor) -> Tuple[Optional[Tensor], ...]:  # type: ignore[override]
+        from .backward import _run_backward
+
+        qkv, pos4, lens, lse = ctx.saved_tensors
+        w32, b32, w_dtype, b_dtype = ctx.prep_meta
+        q, k, v = _qkv_views(qkv, ctx.packed)
+        dqkv = torch.empty_like(qkv)
+        g = grad_out if ctx.packed else grad_out.transpose(1, 2)
+        if ctx.packed:
+            like = torch.empty(q.shape, device=qkv.device, dtype=qkv.dtype)
+        else:
+            b, h, length, d = q.shape
+            like = torch.empty(b, length, h, d, device=qkv.device, dtype=qkv.dtype).transpose(1, 2)
+        _, _, _, dw, db = _run_backward(
+            ctx.dims, q, k, v, pos4, w32, b32, lens, lse, g, ctx.scale, ctx.vec_shape,
+            out_like=like, grads=_qkv_views(dqkv, ctx.packed),
+        )
+        use_attn_bias, use_activation_bias = ctx.flags
+        proj_used = use_attn_bias or use_activation_bias
+        return (
+            dqkv if ctx.needs_input_grad[0] else None,
+            None,
+            dw.to(w_dtype) if (ctx.needs_input_grad[2] and proj_used) else None,
+            db.to(b_dtype) if (ctx.needs_input_grad[3] and proj_used and db is not None) else None,
+            None, None, None, None, None,
+        )
+
+
+def flash_spacetime_attention_qkv(
+    qkv: Tensor,
+    feats: Tensor,
+    weight: Tensor,
+    bias: Optional[Tensor],
+    seqlens: Optional[Tensor] = None,
+    scale: Optional[float] = None,
+    use_attn_bias: bool = True,
+    use_activation_bias: bool = True,
+    *,
+    cu_seqlens: Optional[Tensor] = None,
+    key_padding_mask: Optional[Tensor] = None,
+) -> Tensor:
+    """The fused op on the output of one fused q/k/v projection.
+
+    `qkv` is `[B, L, 3, H, D]` (padded; a `[B, L, 3*H*D]` linear's output
+    viewed so) or `[T, 3, H, D]` with `cu_seqlens` (packed). The kernels read
+    the three slots in place and write the gradient as one tensor of the same
+    layout, so neither the projection's output nor its gradient is copied,
+    split or stacked. Returns `[B, L, H, D]` (padding rows zero) or
+    `[T, H, D]`: the layout the output projection consumes. Lengths and
+    masks as in `flash_spacetime_attention` (a mask with holes runs the
+    packed path on the gathered valid tokens). Same values as
+    `flash_spacetime_attention(q, k, v, ...)` on the split heads. No
+    reference counterpart: the reference takes three separate tensors
+    (forward.py:481-501).
+    """
+    if cu_seqlens is not None:
+        if qkv.dim() != 4 or qkv.shape[1] != 3:
+            raise ValueError(f"packed qkv must be [T, 3, H, D], got {tuple(qkv.shape)}")
+        return _FlashSpacetimeAttentionQKV.apply(
+            qkv.contiguous(), feats, weight, bias, None, scale, use_attn_bias, use_activation_bias,
+            cu_seqlens,
+        )
+    if qkv.dim() != 5 or qkv.shape[2] != 3:
+        raise ValueError(f"qkv must be [B, L, 3, H, D], got {tuple(qkv.shape)}")
+    mask = key_padding_mask
+    if mask is None and seqlens is not None and seqlens.dim() == 2:
+        mask, seqlens = seqlens, None
+    if mask is not None:
+        if seqlens is not None:
+            raise ValueError("pass either seqlens or key_padding_mask, not both")
+        b, length = qkv.shape[:2]
+        valid = _valid_from_mask(mask, length)
+        if not _is_front_packed(valid):
+            if feats.dim() != 3 or feats.shape[:2] != (b, length):
+                raise ValueError(f"feats must be [B, L, F>=4], got {tuple(feats.shape)}")
+            cu = torch.zeros(b + 1, dtype=torch.int32, device=qkv.device)
+            cu[1:] = torch.cumsum(valid.sum(1, dtype=torch.int32), 0, dtype=torch.int32)
+            out = _FlashSpacetimeAttentionQKV.apply(
+                qkv[valid], feats[valid], weight, bias, None, scale, use_attn_bias,
+                use_activation_bias, cu,
+            )
+            return out.new_zeros(b, length, *out.shape[1:]).index_put((valid,), out)
+        seqlens = valid.sum(1, dtype=torch.int32)
+    return _FlashSpacetimeAttentionQKV.apply(
+        qkv.contiguous(), feats, weight, bias, seqlens, scale, use_attn_bias, use_activation_bias, None,
     )

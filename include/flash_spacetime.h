@@ -17,6 +17,11 @@
  *   packed : q, k, v, out, dq, dk, dv  [T, H, D]      lse, rowsum [T, H]
  *            pos4 [T, 4] fp32, lens = cu_seqlens [B+1] int32 (cu[0] = 0,
  *            cu[B] = T)
+ *   FST_QKV_INTERLEAVED (with FST_TOKEN_MAJOR or FST_PACKED): q, k, v are
+ *            the three slots of one [B, L, 3, H, D] / [T, 3, H, D] tensor
+ *            (q = its base, k = base + H*D, v = base + 2*H*D elements), and
+ *            dq, dk, dv likewise of one gradient tensor; out, grad_out,
+ *            lse and rowsum keep the [B, L, H, D] / [T, H, D] layout.
  *   weight [D, C] fp32 (nn.Linear layout), bias [D] fp32 or NULL.
  *   dtype FST_BF16: q, k, v, out, grad_out, dq, dk, dv are bfloat16;
  *   dtype FST_F32 : they are float32. lse, pos4, weight, bias, dweight,
@@ -44,11 +49,15 @@ enum fst_flags {
   FST_ATTN_BIAS = 1, /* add qt_i . R_ij to the logits (use_attn_bias)        */
   FST_ACT_BIAS = 2,  /* add sum_j P_ij R_ij to the output (use_activation_bias) */
   FST_PACKED = 4,    /* packed [T, H, D] layout with cu_seqlens              */
-  FST_TOKEN_MAJOR = 8 /* padded tensors stored [B, L, H, D] (vectors [B, L, H]):
+  FST_TOKEN_MAJOR = 8, /* padded tensors stored [B, L, H, D] (vectors [B, L, H]):
                          the heads-first views of a [B, L, H*D] projection
                          (reference.py:187-196 split_heads) read in place.
                          No reference counterpart: the reference makes them
                          contiguous [B, H, L, D] first (forward.py:274).    */
+  FST_QKV_INTERLEAVED = 16 /* q, k, v (and dq, dk, dv) interleaved per token as
+                              one fused projection's [.., 3, H, D] output; see
+                              Layouts. No reference counterpart (the reference
+                              takes three separate tensors, forward.py:481). */
 };
 
 /* Phases of one operator call, for callers that time or schedule them

@@ -10,6 +10,10 @@
 * Heads-first views of token-major `[B, L, H, D]` memory (what `split_heads`
   makes of a projection) are read in place: results bitwise those of the
   contiguous call, returned as the same kind of view.
+* One interleaved q/k/v tensor (`flash_spacetime_attention_qkv`, the output
+  of a fused projection, padded `[B, L, 3, H, D]` or packed `[T, 3, H, D]`):
+  output and the one gradient tensor bitwise those of the op on the split
+  heads.
 """
 
 import pytest
@@ -238,3 +242,83 @@ def test_token_major_with_holey_mask_and_mixed_layouts():
     sl = case["seqlens"].to(dev)
     mixed = flash_spacetime_attention(_token_major(q), k, v, feats, w, b, sl)
     assert torch.equal(mixed, flash_spacetime_attention(q, k, v, feats, w, b, sl))
+
+
+_QKV_CASES = [(torch.bfloat16, (3, 50, 12, 32, 16)), (torch.bfloat16, (2, 40, 16, 64, 64)),
+              (torch.float32, (3, 50, 12, 32, 16)), (torch.float32, (2, 33, 5, 48, 32))]
+
+
+@pytest.mark.parametrize("dtype,shape", _QKV_CASES,
+                         ids=[f"{str(d)[6:]}-{'x'.join(map(str, s))}" for d, s in _QKV_CASES])
+@pytest.mark.parametrize("flags", FLAGS[:3], ids=["attn1act1", "attn1act0", "attn0act1"])
+def test_qkv_interleaved_matches_split_heads(dtype, shape, flags):
+    """flash_spacetime_attention_qkv on one [B, L, 3, H, D] tensor: output and
+    the gradient tensor bitwise those of flash_spacetime_attention on the
+    contiguous split heads (dq, dk, dv stacked into the same layout)."""
+    from flash_spacetime_amd import flash_spacetime_attention_qkv
+
+    bsz, length, heads, dim, _ = shape
+    case = make_padded(*shape, seed=seed_of("qkv", dtype, shape, flags))
+    dev = "cuda"
+    seqlens, feats = case["seqlens"].to(dev), case["feats"].to(dev)
+    qkv0 = torch.stack([case[n].transpose(1, 2) for n in ("q", "k", "v")], 2).to(dev, dtype).contiguous()
+    gw = torch.randn(bsz, length, heads, dim, generator=torch.Generator().manual_seed(11)).to(dev)
+    w0, b0 = case["weight"].to(dev, dtype), case["bias"].to(dev, dtype)
+
+    qkv = qkv0.clone().requires_grad_(True)
+    w, b = w0.clone().requires_grad_(True), b0.clone().requires_grad_(True)
+    out = flash_spacetime_attention_qkv(qkv, feats, w, b, seqlens, use_attn_bias=flags[0],
+                                        use_activation_bias=flags[1])
+    assert out.shape == (bsz, length, heads, dim) and out.is_contiguous()
+    (out.float() * gw).sum().backward()
+
+    leaves = [qkv0[:, :, i].transpose(1, 2).contiguous().requires_grad_(True) for i in range(3)]
+    w2, b2 = w0.clone().requires_grad_(True), b0.clone().requires_grad_(True)
+    ref = flash_spacetime_attention(*leaves, feats, w2, b2, seqlens, use_attn_bias=flags[0],
+                                    use_activation_bias=flags[1])
+    (ref.float() * gw.transpose(1, 2)).sum().backward()
+
+    assert torch.equal(out, ref.transpose(1, 2))
+    assert torch.equal(qkv.grad, torch.stack([t.grad.transpose(1, 2) for t in leaves], 2))
+    for a, c in ((w.grad, w2.grad), (b.grad, b2.grad)):
+        assert (a is None) == (c is None) and (a is None or torch.equal(a, c))
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16], ids=["fp32", "bf16"])
+def test_qkv_interleaved_packed_and_masks(dtype):
+    """Packed [T, 3, H, D] with cu_seqlens against the varlen op on q, k, v;
+    a padded qkv with a mask with holes against the split-heads op with the
+    same mask (both bitwise, gradients included)."""
+    from flash_spacetime_amd import flash_spacetime_attention_qkv
+
+    dev = "cuda"
+    lengths = [17, 64, 1, 120, 33]
+    case = make_packed(lengths, 6, 32, 16, seed_of("qkv-packed", dtype))
+    cu, feats = case["cu"].to(dev), case["feats"].to(dev)
+    w, b = case["weight"].to(dev, dtype), case["bias"].to(dev, dtype)
+    qkv0 = torch.stack([case[n] for n in ("q", "k", "v")], 1).to(dev, dtype).contiguous()
+    gw = torch.randn(qkv0.shape[0], 6, 32, generator=torch.Generator().manual_seed(12)).to(dev)
+    qkv = qkv0.clone().requires_grad_(True)
+    out = flash_spacetime_attention_qkv(qkv, feats, w, b, cu_seqlens=cu)
+    (out.float() * gw).sum().backward()
+    leaves = [qkv0[:, i].contiguous().requires_grad_(True) for i in range(3)]
+    ref = flash_spacetime_attention_varlen(*leaves, feats, w, b, cu)
+    (ref.float() * gw).sum().backward()
+    assert torch.equal(out, ref)
+    assert torch.equal(qkv.grad, torch.stack([t.grad for t in leaves], 1))
+
+    shape = (3, 40, 4, 32, 16)
+    pc = make_padded(*shape, seed=seed_of("qkv-holes", dtype), masked=False)
+    holey = _holey_mask(3, 40, seed_of("qkv-holes-mask", dtype)).to(dev)
+    feats = pc["feats"].to(dev)
+    w, b = pc["weight"].to(dev, dtype), pc["bias"].to(dev, dtype)
+    qkv0 = torch.stack([pc[n].transpose(1, 2) for n in ("q", "k", "v")], 2).to(dev, dtype).contiguous()
+    qkv = qkv0.clone().requires_grad_(True)
+    out = flash_spacetime_attention_qkv(qkv, feats, w, b, key_padding_mask=~holey)
+    gw = torch.randn(out.shape, generator=torch.Generator().manual_seed(13)).to(dev)
+    (out.float() * gw).sum().backward()
+    leaves = [qkv0[:, :, i].transpose(1, 2).contiguous().requires_grad_(True) for i in range(3)]
+    ref = flash_spacetime_attention(*leaves, feats, w, b, key_padding_mask=~holey)
+    (ref.float() * gw.transpose(1, 2)).sum().backward()
+    assert torch.equal(out, ref.transpose(1, 2))
+    assert torch.equal(qkv.grad, torch.stack([t.grad.transpose(1, 2) for t in leaves], 2))
