@@ -14,7 +14,7 @@ times of the individual launches, the MFMA roofline of the dominant kernel,
 and the CPU baseline (the oracle's eager restatement of the spec, fp32,
 fwd+bwd, timed on this host's cores on a bounded sample of events).
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload cfg2|cfg3|cfg4|cfg4-fp32]
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload cfg2|cfg3|cfg4|cfg4-fp32|cfg2-model]
 """
 
 from __future__ import annotations
@@ -200,7 +200,66 @@ WORKLOADS = {
             "q and k x30, bf16",
     "cfg4-fp32": "configs[4]: flash_spacetime_attention fwd+bwd, B=8 L=4096 (no padding) H=8 D=64 C=64, "
                  "q and k x30, fp32",
+    "cfg2-model": "SpacetimeAttention fwd+bwd (fused QKV linear, flash_spacetime_attention_qkv, output "
+                  "linear) at cfg2 sizes: x [256, 768, 384] bf16, H=12 D=32 C=16, lengths U{16..768}",
 }
+
+
+def run_model_workload(steps, warmup):
+    """The model-side caller at cfg2 sizes: one fwd+bwd of `SpacetimeAttention`
+    (x -> fused QKV GEMM -> fused op on the interleaved projection -> output
+    GEMM, gradients of x and every parameter). Beside it, the same module's
+    parameters run the way the reference's caller runs them: three linears,
+    split heads made contiguous, the op, heads merged by a copy, output
+    linear (`split_heads_copies_ms`)."""
+    from flash_spacetime_amd import SpacetimeAttention, flash_spacetime_attention, merge_heads
+
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    inp = make_inputs(dev)
+    from flash_spacetime_amd.forward import lengths_from_mask
+
+    seqlens = lengths_from_mask(inp["pad_mask"], L)
+    dim = H * D
+    torch.manual_seed(5)
+    mod = SpacetimeAttention(dim, H, C, qkv_bias=True, device=dev, dtype=torch.bfloat16)
+    gen = torch.Generator().manual_seed(6)
+    x = torch.randn(B, L, dim, generator=gen).to(dev, torch.bfloat16).requires_grad_(True)
+    gy = torch.randn(B, L, dim, generator=gen).to(dev, torch.bfloat16)
+    feats = inp["feats"]
+    params = [x, *mod.parameters()]
+
+    def fused():
+        for t_ in params:
+            t_.grad = None
+        mod(x, feats, seqlens).backward(gy)
+
+    def reference_caller():
+        for t_ in params:
+            t_.grad = None
+        q = torch.nn.functional.linear(x, mod.proj_q.weight, mod.q_bias)
+        k = torch.nn.functional.linear(x, mod.proj_k.weight)
+        v = torch.nn.functional.linear(x, mod.proj_v.weight, mod.v_bias)
+        heads = [t_.view(B, L, H, D).transpose(1, 2).contiguous() for t_ in (q, k, v)]
+        o = flash_spacetime_attention(*heads, feats, mod.rel_proj.weight, mod.rel_proj.bias, seqlens)
+        mod.proj(merge_heads(o).contiguous()).backward(gy)
+
+    stream = torch.cuda.current_stream(dev)
+    res = {}
+    for name, fn in (("fused", fused), ("reference_caller", reference_caller)):
+        for _ in range(warmup):
+            fn()
+        torch.cuda.synchronize(dev)
+        res[name] = time_events(fn, steps, stream)
+        torch.cuda.synchronize(dev)
+    print(json.dumps({
+        "metric": "SpacetimeAttention fwd+bwd ms/step at cfg2 sizes", "value": round(res["fused"], 4),
+        "unit": "ms", "n_gpus": 1, "steps": steps, "warmup": warmup, "ms_per_step": round(res["fused"], 4),
+        "higher_is_better": False, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+        "data": "synthetic (seeded; cfg2 lengths and features, random-init module)",
+        "config": {"workload": WORKLOADS["cfg2-model"]},
+        "split_heads_copies_ms": round(res["reference_caller"], 4),
+    }), flush=True)
 
 
 def run_other_workload(name, steps, warmup):
@@ -297,6 +356,9 @@ def main():
               f"multi-GPU would shard events with no exchange). --gpus {args.gpus} is not run.", file=sys.stderr)
         sys.exit(2)
 
+    if args.workload == "cfg2-model":
+        run_model_workload(args.steps, args.warmup)
+        return
     if args.workload != "cfg2":
         run_other_workload(args.workload, args.steps, args.warmup)
         return

@@ -67,6 +67,25 @@ def read_stats(directory: str):
     return out
 
 
+def read_trace_loop(directory: str, n: int = 10):
+    """Mean duration (us) of each phase's last n dispatches in the kernel
+    trace: the per-phase timing loop that bench.py runs after its steps (n
+    back-to-back launches of one kernel), i.e. the launches the bench's own
+    HIP-event figure covers. Empty when the trace file is absent."""
+    try:
+        path = _find(directory, "kernel_trace.csv")
+    except FileNotFoundError:
+        return {}
+    durs = defaultdict(list)
+    with open(path) as f:
+        rows = sorted(csv.DictReader(f), key=lambda r: int(r["Start_Timestamp"]))
+    for r in rows:
+        ph = phase_of(r["Kernel_Name"])
+        if ph:
+            durs[ph].append((int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3)
+    return {ph: sum(v[-n:]) / len(v[-n:]) for ph, v in durs.items() if len(v) >= n}
+
+
 def read_counter(directory: str, counter: str):
     vals = defaultdict(list)
     meta = {}
@@ -96,6 +115,7 @@ def main():
     args = ap.parse_args()
 
     stats = read_stats(args.trace)
+    loop = read_trace_loop(args.trace)
     fetch, meta = read_counter(args.fetch, "FETCH_SIZE")
     write, _ = read_counter(args.write, "WRITE_SIZE")
     if "calibration_copy" not in fetch or "calibration_copy" not in write:
@@ -104,9 +124,9 @@ def main():
     w_scale = args.calib_bytes / (write["calibration_copy"] * 1024.0)
 
     traffic = {}
-    lines = ["| kernel | launches | avg duration (us) | FETCH_SIZE (KiB) | WRITE_SIZE (KiB) | HBM bytes / launch "
-             "(scaled) | grid | VGPR | AGPR | LDS (B) |",
-             "|---|---|---|---|---|---|---|---|---|---|"]
+    lines = ["| kernel | launches | avg duration (us) | timing-loop avg (us) | FETCH_SIZE (KiB) | WRITE_SIZE (KiB) "
+             "| HBM bytes / launch (scaled) | grid | VGPR | AGPR | LDS (B) |",
+             "|---|---|---|---|---|---|---|---|---|---|---|"]
     for ph in ("fwd", "bwd_rows", "bwd_cols", "bwd_reduce_seg", "bwd_reduce_final", "worklist", "worklist_sort"):
         if ph not in stats:
             continue
@@ -115,8 +135,11 @@ def main():
         if fk is not None and wk is not None:
             nbytes = fk * 1024.0 * f_scale + wk * 1024.0 * w_scale
             traffic[ph] = {"bytes": nbytes, "fetch_kib": fk, "write_kib": wk, "avg_us": stats[ph]["avg_us"]}
+            if ph in loop:
+                traffic[ph]["loop_avg_us"] = loop[ph]
         m = meta.get(ph, {})
-        lines.append(f"| {ph} | {stats[ph]['calls']} | {stats[ph]['avg_us']:.1f} | "
+        lp = f"{loop[ph]:.1f}" if ph in loop else ""
+        lines.append(f"| {ph} | {stats[ph]['calls']} | {stats[ph]['avg_us']:.1f} | {lp} | "
                      f"{'' if fk is None else f'{fk:.0f}'} | {'' if wk is None else f'{wk:.0f}'} | "
                      f"{'' if nbytes is None else f'{nbytes:.4g}'} | {m.get('Grid_Size', '')} | "
                      f"{m.get('VGPR_Count', '')} | {m.get('Accum_VGPR_Count', '')} | {m.get('LDS_Block_Size', '')} |")
