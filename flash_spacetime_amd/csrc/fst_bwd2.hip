@@ -623,6 +623,7 @@ __global__ __launch_bounds__(256, (Cols2Cfg<HP, D, C, RC>::OCC)) void bwd_cols2_
 
   EventSpec ev = prm.ev;
   ev.blkcum = prm.blkcum_cols;
+  ev.scum = prm.scum_cols;
   EventBlock eb;
   if (!tile_block(ev, blockIdx.x, eb)) return;
   const int len = eb.len;
@@ -951,7 +952,9 @@ int bwd2_launch_t(const BwdParams& prm, int which, hipStream_t stream, int grid)
   if constexpr (!P::OK) {
     return FST_EUNSUPPORTED;
   } else {
-    const int g8 = (grid + 7) & ~7;
+    // The grid is rounded up to a multiple of 64 for the XCD schedules
+    // (tile_block); logical blocks past the work list exit at once.
+    const int g8 = (grid + 63) & ~63;
     if (which == 0) {
       auto kern = (prm.flags & 3) == 3 ? bwd_rows2_kernel<HP, D, C, P::KC, P::HB, 3>
                                        : bwd_rows2_kernel<HP, D, C, P::KC, P::HB, -1>;

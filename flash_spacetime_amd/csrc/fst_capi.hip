@@ -55,10 +55,11 @@ static void freq_table(int C, FreqTable& ft) {
   }
 }
 
-// Number of row blocks of each event and their prefix sum (one workgroup).
+// Number of row blocks of each event and their prefix sum (one workgroup),
+// over the events in index order, or in the order perm gives when not null.
 // Padded events always get one block so that their padding rows are zeroed.
 __global__ __launch_bounds__(1024) void blkcum_kernel(const int32_t* lens, int packed, int B, int L, int T, int rows,
-                                                      int32_t* blkcum) {
+                                                      const int32_t* perm, int32_t* blkcum) {
   __shared__ int buf[1024];
   __shared__ int carry;
   const int t = threadIdx.x;
@@ -78,7 +79,7 @@ __global__ __launch_bounds__(1024) void blkcum_kernel(const int32_t* lens, int p
     int nb = 0;
     if (b < B) {
       int tok0, len;
-      event_range(ev, b, tok0, len);
+      event_range(ev, perm ? perm[b] : b, tok0, len);
       nb = len > 0 ? (len + rows - 1) / rows : (packed ? 0 : 1);
     }
     buf[t] = nb;
@@ -96,25 +97,33 @@ __global__ __launch_bounds__(1024) void blkcum_kernel(const int32_t* lens, int p
   }
 }
 
-// Padded schedule of the tile kernels: the events ordered by decreasing valid
-// length (ties by index), one workgroup, bitonic sort in LDS. Past 8192
-// events, or lengths of 2^18 and more, the identity order is used.
+// Schedule of the tile kernels: the events ordered by decreasing valid
+// length (ties by index; lengths past 2^18 - 1 count as 2^18 - 1), one
+// workgroup, bitonic sort in LDS. Past 8192 events the identity order is used.
 constexpr int kSortMax = 8192;
 
-__global__ __launch_bounds__(1024) void sort_events_kernel(const int32_t* lens, int B, int L, int32_t* perm) {
+__global__ __launch_bounds__(1024) void sort_events_kernel(const int32_t* lens, int packed, int B, int L, int T,
+                                                           int32_t* perm) {
   extern __shared__ int keys[];
   const int t = threadIdx.x;
-  if (B > kSortMax || L >= (1 << 18)) {
+  if (B > kSortMax) {
     for (int i = t; i < B; i += 1024) perm[i] = i;
     return;
   }
+  EventSpec ev;
+  ev.lens = lens;
+  ev.packed = packed;
+  ev.B = B;
+  ev.L = L;
+  ev.T = T;
   int p2 = 1;
   while (p2 < B) p2 <<= 1;
   for (int i = t; i < p2; i += 1024) {
     int key = -1;
     if (i < B) {
-      int l = lens[i];
-      l = l < 0 ? 0 : (l > L ? L : l);
+      int tok0, l;
+      event_range(ev, i, tok0, l);
+      l = l < (1 << 18) - 1 ? l : (1 << 18) - 1;
       key = (l << 13) | (kSortMax - 1 - i);
     }
     keys[i] = key;
@@ -137,14 +146,14 @@ __global__ __launch_bounds__(1024) void sort_events_kernel(const int32_t* lens, 
   for (int i = t; i < B; i += 1024) perm[i] = kSortMax - 1 - (keys[i] & (kSortMax - 1));
 }
 
-static int launch_sort(const int32_t* lens, int B, int L, int32_t* perm, hipStream_t st) {
+static int launch_sort(const int32_t* lens, int packed, int B, int L, int T, int32_t* perm, hipStream_t st) {
   int p2 = 1;
   while (p2 < B && p2 < kSortMax) p2 <<= 1;
   const int lds = B > kSortMax ? 0 : p2 * (int)sizeof(int);
   if (hipFuncSetAttribute((const void*)sort_events_kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
                           kSortMax * (int)sizeof(int)) != hipSuccess)
     return FST_ELAUNCH;
-  hipLaunchKernelGGL(sort_events_kernel, dim3(1), dim3(1024), lds, st, lens, B, L, perm);
+  hipLaunchKernelGGL(sort_events_kernel, dim3(1), dim3(1024), lds, st, lens, packed, B, L, T, perm);
   return hipGetLastError() == hipSuccess ? FST_OK : FST_ELAUNCH;
 }
 
@@ -184,8 +193,10 @@ static int check_common(int dtype, int flags, int B, int H, int L, int T, int D,
   return FST_OK;
 }
 
-// Work list of one kernel family: blkcum [B+1], then perm [B] (padded schedule).
-static size_t blkcum_bytes(int B) { return align_up((size_t)(2 * B + 1) * sizeof(int32_t), 256); }
+// Work list of one kernel family: blkcum [B+1] (row blocks in event order:
+// the slots of per-tile outputs), perm [B] (events by decreasing length),
+// scum [B+1] (packed: row blocks in perm order, the schedule).
+static size_t blkcum_bytes(int B) { return align_up((size_t)(3 * B + 2) * sizeof(int32_t), 256); }
 
 typedef int (*bwd_dispatch_fn)(const BwdParams&, int, int, int, hipStream_t, int, bool, int*);
 
@@ -365,16 +376,24 @@ int fst_forward_phases(int phases, int dtype, int flags, int B, int H, int L, in
   int32_t* blkcum = reinterpret_cast<int32_t*>(workspace);
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
   int32_t* perm = blkcum + (B + 1);
+  int32_t* scum = perm + B;
   if (phases & FST_PHASE_WORKLIST) {
-    hipLaunchKernelGGL(blkcum_kernel, dim3(1), dim3(1024), 0, st, lens, packed ? 1 : 0, B, L, T, rows, blkcum);
+    hipLaunchKernelGGL(blkcum_kernel, dim3(1), dim3(1024), 0, st, lens, packed ? 1 : 0, B, L, T, rows,
+                       (const int32_t*)nullptr, blkcum);
     if (hipGetLastError() != hipSuccess) return fail(FST_ELAUNCH, "work-list kernel launch failed");
-    if (!packed && launch_sort(lens, B, L, perm, st) != FST_OK) return fail(FST_ELAUNCH, "schedule kernel launch failed");
+    if (launch_sort(lens, packed ? 1 : 0, B, L, T, perm, st) != FST_OK)
+      return fail(FST_ELAUNCH, "schedule kernel launch failed");
+    if (packed) {
+      hipLaunchKernelGGL(blkcum_kernel, dim3(1), dim3(1024), 0, st, lens, 1, B, L, T, rows, (const int32_t*)perm, scum);
+      if (hipGetLastError() != hipSuccess) return fail(FST_ELAUNCH, "schedule kernel launch failed");
+    }
   }
   if (!(phases & FST_PHASE_FWD)) return FST_OK;
 
   prm.ev.lens = lens;
   prm.ev.blkcum = blkcum;
   prm.ev.perm = perm;
+  prm.ev.scum = packed ? scum : nullptr;
   prm.ev.pos4 = reinterpret_cast<const float4*>(pos4);
   prm.ev.B = B;
   prm.ev.H = H;
@@ -453,19 +472,32 @@ int fst_backward_phases(int phases, int dtype, int flags, int B, int H, int L, i
   unsigned char* ws = reinterpret_cast<unsigned char*>(workspace);
   int32_t* bc_r = reinterpret_cast<int32_t*>(ws + lay.off_bc_r);
   int32_t* bc_c = reinterpret_cast<int32_t*>(ws + lay.off_bc_c);
+  int32_t* perm_r = bc_r + (B + 1);
+  int32_t* scum_r = perm_r + B;
+  int32_t* scum_c = bc_c + (B + 1) + B;
   if (phases & FST_PHASE_WORKLIST) {
-    hipLaunchKernelGGL(blkcum_kernel, dim3(1), dim3(1024), 0, st, lens, packed ? 1 : 0, B, L, T, lay.rows_r, bc_r);
-    hipLaunchKernelGGL(blkcum_kernel, dim3(1), dim3(1024), 0, st, lens, packed ? 1 : 0, B, L, T, lay.rows_c, bc_c);
+    hipLaunchKernelGGL(blkcum_kernel, dim3(1), dim3(1024), 0, st, lens, packed ? 1 : 0, B, L, T, lay.rows_r,
+                       (const int32_t*)nullptr, bc_r);
+    hipLaunchKernelGGL(blkcum_kernel, dim3(1), dim3(1024), 0, st, lens, packed ? 1 : 0, B, L, T, lay.rows_c,
+                       (const int32_t*)nullptr, bc_c);
     if (hipGetLastError() != hipSuccess) return fail(FST_ELAUNCH, "work-list kernel launch failed");
-    if (!packed && launch_sort(lens, B, L, bc_r + (B + 1), st) != FST_OK)
+    if (launch_sort(lens, packed ? 1 : 0, B, L, T, perm_r, st) != FST_OK)
       return fail(FST_ELAUNCH, "schedule kernel launch failed");
+    if (packed) {
+      hipLaunchKernelGGL(blkcum_kernel, dim3(1), dim3(1024), 0, st, lens, 1, B, L, T, lay.rows_r,
+                         (const int32_t*)perm_r, scum_r);
+      hipLaunchKernelGGL(blkcum_kernel, dim3(1), dim3(1024), 0, st, lens, 1, B, L, T, lay.rows_c,
+                         (const int32_t*)perm_r, scum_c);
+      if (hipGetLastError() != hipSuccess) return fail(FST_ELAUNCH, "schedule kernel launch failed");
+    }
   }
 
   BwdParams prm;
   std::memset(&prm, 0, sizeof(prm));
   prm.ev.lens = lens;
   prm.ev.blkcum = bc_r;
-  prm.ev.perm = bc_r + (B + 1);
+  prm.ev.perm = perm_r;
+  prm.ev.scum = packed ? scum_r : nullptr;
   prm.ev.pos4 = reinterpret_cast<const float4*>(pos4);
   prm.ev.B = B;
   prm.ev.H = H;
@@ -475,6 +507,7 @@ int fst_backward_phases(int phases, int dtype, int flags, int B, int H, int L, i
   prm.ev.tokmajor = (packed || (flags & FST_TOKEN_MAJOR)) ? 1 : 0;
   prm.ev.xmul = (flags & FST_QKV_INTERLEAVED) ? 3 : 1;
   prm.blkcum_cols = bc_c;
+  prm.scum_cols = packed ? scum_c : nullptr;
   prm.H = H;
   prm.flags = flags;
   prm.scale = scale;

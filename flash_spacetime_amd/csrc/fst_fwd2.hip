@@ -455,9 +455,9 @@ int fwd2_launch_t(const FwdParams& prm, hipStream_t stream, int grid) {
     if (hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, P::Cfg::LDS_BYTES) !=
         hipSuccess)
       return FST_ELAUNCH;
-    // The grid is rounded up to a multiple of 8 for the XCD remapping;
-    // logical blocks past the work list exit at once.
-    const int g8 = (grid + 7) & ~7;
+    // The grid is rounded up to a multiple of 64 for the XCD schedules
+    // (tile_block); logical blocks past the work list exit at once.
+    const int g8 = (grid + 63) & ~63;
     if (grid > 0) hipLaunchKernelGGL(kern, dim3(g8), dim3(256), P::Cfg::LDS_BYTES, stream, prm);
     return hipGetLastError() == hipSuccess ? FST_OK : FST_ELAUNCH;
   }

@@ -14,7 +14,8 @@ namespace fst {
 struct EventSpec {
   const int32_t* lens;    // seqlens [B] (padded) or cu_seqlens [B+1] (packed)
   const int32_t* blkcum;  // [B+1] prefix sums of row blocks per event
-  const int32_t* perm;    // [B] events by decreasing length (padded tile kernels' schedule)
+  const int32_t* perm;    // [B] events by decreasing length (the tile kernels' schedules)
+  const int32_t* scum;    // [B+1] packed: prefix sums of row blocks in perm order (or null)
   const float4* pos4;     // [B*L] or [T] (x, y, z, t) fp32
   int B, H, L, T, packed;
   int tokmajor;           // rows of one token's heads are adjacent (packed, or padded token-major)
@@ -119,6 +120,7 @@ struct FwdParams {
 struct BwdParams {
   EventSpec ev;     // rows-kernel work list in ev.blkcum
   const int32_t* blkcum_cols;  // cols-kernel work list
+  const int32_t* scum_cols;    // its packed schedule (row blocks in ev.perm order), or null
   int H, flags;
   float scale;
   const void *q, *k, *v, *dout;

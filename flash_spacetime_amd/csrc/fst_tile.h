@@ -150,8 +150,17 @@ struct DTiles {
 // Work items of the 16-row tile kernels. Padded events map directly: logical
 // block w is tile w % nb of event w / nb (nb = ceil(L / 16)), so a tile wholly
 // past its event's length only zeroes its rows. Packed events have no padding
-// and use the per-event prefix sums of tiles.
+// and use prefix sums of their tile counts.
 // ---------------------------------------------------------------------------
+//
+// Packed schedule. The events' tiles are listed longest event first (ev.perm,
+// prefix sums ev.scum) and dealt to the XCDs in groups of eight consecutive
+// tiles, round robin: XCD x takes groups x, x + 8, x + 16, ... A tile's cost
+// grows with its event's length, so neighbouring groups cost about the same
+// and every XCD gets an equal share of each length class, longest first,
+// while the eight tiles of a group share their event's K and V in one L2.
+// Hardware workgroup w runs on XCD w % 8 as its (w / 8)-th tile; the grid is
+// a multiple of 64.
 //
 // Padded schedule. Every padded event has nb tiles, so the work of an event
 // grows with its length squared while its tile count does not: events are
@@ -162,7 +171,24 @@ struct DTiles {
 // w % 8 as its (w / 8)-th tile: tile (w / 8) % nb of the XCD's (w / 8) / nb-th
 // event. The grid is 8 ceil(B / 8) nb.
 __device__ __forceinline__ bool tile_block(const EventSpec& ev, int w, EventBlock& eb) {
-  if (ev.packed) return locate_block(ev, xcd_remap(w, gridDim.x), eb);
+  if (ev.packed) {
+    if (!ev.scum) return locate_block(ev, xcd_remap(w, gridDim.x), eb);
+    const int x = w & 7, k = w >> 3;
+    const int t = (((k >> 3) << 3) + x) * 8 + (k & 7);
+    if (t >= ev.scum[ev.B]) return false;
+    int lo = 0, hi = ev.B;
+    while (hi - lo > 1) {
+      const int mid = (lo + hi) >> 1;
+      if (ev.scum[mid] <= t)
+        lo = mid;
+      else
+        hi = mid;
+    }
+    eb.b = ev.perm[lo];
+    eb.blk = t - ev.scum[lo];
+    event_range(ev, eb.b, eb.tok0, eb.len);
+    return true;
+  }
   const int nb = (ev.L + 15) >> 4;
   const int x = w & 7, k = w >> 3;
   const int j = k / nb;
