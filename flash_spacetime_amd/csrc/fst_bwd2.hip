@@ -50,30 +50,35 @@ namespace fst {
 // ---------------------------------------------------------------------------
 // Rows kernel.
 // ---------------------------------------------------------------------------
-template <int HP, int D, int C, int KC>
+// NW waves of 64 lanes: 4 (two workgroups per CU), or 8 (one workgroup per
+// CU) where the state of a four-wave lane would not fit the registers
+// (Bwd2Pick). A wave is head-owner of HP / NW heads and row-owner of
+// RPW = 16 / NW rows.
+template <int HP, int D, int C, int KC, int NW = 4>
 struct Rows2Cfg {
-  static constexpr int HW = HP / 4, NS = KC / 16, NCT = C / 16;
+  static constexpr int HW = HP / NW, NS = KC / 16, NCT = C / 16, RPW = 16 / NW;
   static constexpr int E_BYTES = ETile<C, KC>::BYTES;
   static constexpr int REGION = (KC / 4) * 16 * 16 * 16;  // one fp32 term of KC keys per (row, 16 head slots)
   static constexpr int SCAL_BYTES = 16 * 17 * 4;
   static constexpr int MAIN = E_BYTES + 2 * REGION + SCAL_BYTES;
-  // Epilogue: the tile's qt (or dO) rows, then per-wave dW / db partials in
-  // the same bytes; one channel step of H (or G) after them.
+  // Epilogue: the tile's qt (or dO) rows, then four dW / db partials (one per
+  // wave, or per pair of waves w, w + 4) in the same bytes; one channel step
+  // of H (or G) after them.
   static constexpr int DW_BYTES = 4 * (D * C + D) * 4;
   static constexpr int XS_BYTES = 16 * HP * D * 2;
   static constexpr int X_DW = DW_BYTES > XS_BYTES ? DW_BYTES : XS_BYTES;
   static constexpr int HG_BYTES = 16 * HP * 16 * 4;
   static constexpr int EPI = X_DW + HG_BYTES;
   static constexpr int LDS_BYTES = MAIN > EPI ? MAIN : EPI;
-  static constexpr bool FITS = LDS_BYTES <= 80 * 1024 && HP % 4 == 0;
+  static constexpr bool FITS = LDS_BYTES <= (NW == 4 ? 80 : 160) * 1024 && HP % NW == 0 && (NW == 4 || NW == 8);
 };
 
-template <int HP, int D, int C, int KC, int HB, int FL>
-__global__ __launch_bounds__(256, 2) void bwd_rows2_kernel(BwdParams prm) {
-  using Cfg = Rows2Cfg<HP, D, C, KC>;
+template <int HP, int D, int C, int KC, int HB, int FL, int NW>
+__global__ __launch_bounds__(64 * NW, (NW == 4 ? 2 : 1)) void bwd_rows2_kernel(BwdParams prm) {
+  using Cfg = Rows2Cfg<HP, D, C, KC, NW>;
   using ET = ETile<C, KC>;
   using DT = DTiles<D>;
-  constexpr int HW = Cfg::HW, NS = Cfg::NS, NCT = Cfg::NCT, NQ = DT::NQ;
+  constexpr int HW = Cfg::HW, NS = Cfg::NS, NCT = Cfg::NCT, NQ = DT::NQ, RPW = Cfg::RPW, NT = 64 * NW;
   constexpr int DCW = D * C + D;
   extern __shared__ __align__(16) unsigned char smem[];
   bf16* Es = reinterpret_cast<bf16*>(smem);
@@ -102,11 +107,12 @@ __global__ __launch_bounds__(256, 2) void bwd_rows2_kernel(BwdParams prm) {
   const int nbv = len > 0 ? (len + 15) / 16 : (prm.ev.packed ? 0 : 1);
   float* part = eb.blk < nbv ? prm.dw_part + (long)(prm.ev.blkcum[eb.b] + eb.blk) * DCW : nullptr;
   if (i0 >= len) {
-    zero_tile_rows<bf16, D>(prm.ev, rx, ra, i0, len, H, tid, dqg, prm.rowsum);
+    zero_tile_rows<bf16, D, NT>(prm.ev, rx, ra, i0, len, H, tid, dqg, prm.rowsum);
     if (part)
-      for (int e = tid; e < DCW; e += 256) part[e] = 0.f;
+      for (int e = tid; e < DCW; e += NT) part[e] = 0.f;
     return;
   }
+  const int row0 = RPW * w;  // the row-owner's first row in the tile
 
   const bf16* __restrict__ qg = reinterpret_cast<const bf16*>(prm.q);
   const bf16* __restrict__ kg = reinterpret_cast<const bf16*>(prm.k);
@@ -139,10 +145,10 @@ __global__ __launch_bounds__(256, 2) void bwd_rows2_kernel(BwdParams prm) {
   // ---- row-owner state: rows i0 + 4w + r, heads on lane n ----
   WSlots<D, C> wv;
   if (use_e) wv.load(prm.weight, g, n);
-  SlotRow<D> xq[4], xd[4];
+  SlotRow<D> xq[RPW], xd[RPW];
 #pragma unroll
-  for (int r = 0; r < 4; ++r) {
-    const int row = i0 + 4 * w + r;
+  for (int r = 0; r < RPW; ++r) {
+    const int row = i0 + row0 + r;
     const bool ok = row < len && n < H;
     const int rr = row < len ? row : last;
     if (attn) xq[r].load(qg + rx.off(0, rr, D), rx.hs * D, ok, g, n);
@@ -151,7 +157,9 @@ __global__ __launch_bounds__(256, 2) void bwd_rows2_kernel(BwdParams prm) {
   float4 pos_i = float4{0.f, 0.f, 0.f, 0.f};
   float fa[NCT], fb[NCT];
   if (use_e) {
-    const int row = i0 + 4 * w + g;
+    // Angle lanes: lane group g evaluates row row0 + g % RPW (with two rows a
+    // wave, lane groups 2 and 3 repeat 0 and 1).
+    const int row = i0 + row0 + g % RPW;
     pos_i = ra.pos(prm.ev.pos4, row < len ? row : last);
 #pragma unroll
     for (int ct = 0; ct < NCT; ++ct) {
@@ -226,30 +234,31 @@ __global__ __launch_bounds__(256, 2) void bwd_rows2_kernel(BwdParams prm) {
 #pragma unroll
     for (int q = 0; q < NQ; ++q) dQ[hl][q] = A2[hl][q] = zero4();
   }
-  bf16x4 uf[4][NCT], wf[4][NCT];
-  f32x4 Hacc[4][NCT], Gacc[4][NCT];
+  bf16x4 uf[RPW][NCT], wf[RPW][NCT];
+  f32x4 Hacc[RPW][NCT], Gacc[RPW][NCT];
   // u and w~ of the row group go to the cols kernel's scratch; rows past the
   // event are written as zeros, so every row of a group the cols kernel
   // reads is defined.
-  const long uwg = ((long)prm.ev.blkcum[eb.b] + eb.blk) * 4 + w;
+  const long uwg = ((long)prm.ev.blkcum[eb.b] + eb.blk) * 4 + (row0 >> 2);
   bf16* ug = reinterpret_cast<bf16*>(prm.u) + uwg * uw_group_elems(H, NCT);
   bf16* wtg = reinterpret_cast<bf16*>(prm.wt) + uwg * uw_group_elems(H, NCT);
 #pragma unroll
-  for (int r = 0; r < 4; ++r) {
-    const bool ok = i0 + 4 * w + r < len && n < H;
+  for (int r = 0; r < RPW; ++r) {
+    const bool ok = i0 + row0 + r < len && n < H;
+    const int rg = (row0 & 3) + r;  // row within its group of four
     if (attn) {
       project_loaded<D, C>(xq[r], ok, prm.scale, wv, uf[r]);
       if (n < H)
 #pragma unroll
         for (int ct = 0; ct < NCT; ++ct)
-          *reinterpret_cast<bf16x4*>(ug + uw_off(r >> 1, ct, n, g, r & 1, H, NCT)) = uf[r][ct];
+          *reinterpret_cast<bf16x4*>(ug + uw_off(rg >> 1, ct, n, g, rg & 1, H, NCT)) = uf[r][ct];
     }
     if (act) {
       project_loaded<D, C>(xd[r], ok, 1.f, wv, wf[r]);
       if (n < H)
 #pragma unroll
         for (int ct = 0; ct < NCT; ++ct)
-          *reinterpret_cast<bf16x4*>(wtg + uw_off(r >> 1, ct, n, g, r & 1, H, NCT)) = wf[r][ct];
+          *reinterpret_cast<bf16x4*>(wtg + uw_off(rg >> 1, ct, n, g, rg & 1, H, NCT)) = wf[r][ct];
     }
 #pragma unroll
     for (int ct = 0; ct < NCT; ++ct) Hacc[r][ct] = Gacc[r][ct] = zero4();
@@ -257,24 +266,24 @@ __global__ __launch_bounds__(256, 2) void bwd_rows2_kernel(BwdParams prm) {
 
   auto chunk = [&](int j0, auto tail_tag) __attribute__((always_inline)) {
     constexpr bool TAIL = decltype(tail_tag)::value;
-    // ---- row-owner: E, u.E and w~.E of rows 4w..4w+3 ----
+    // ---- row-owner: E, u.E and w~.E of rows row0 .. row0 + RPW - 1 ----
     if (use_e) {
       float xg[NS][4];
 #pragma unroll
       for (int s = 0; s < NS; ++s) group_gather(pair_angle_unit(pos_i, pj[s]), xg[s]);
       issue_pos(j0 + KC);
 #pragma unroll
-      for (int r = 0; r < 4; ++r)
+      for (int r = 0; r < RPW; ++r)
 #pragma unroll
         for (int s = 0; s < NS; ++s) {
           bf16x4 ef[NCT];
 #pragma unroll
           for (int ct = 0; ct < NCT; ++ct) {
             ef[ct] = embed_step<C>(xg[s][r], fa[ct], fb[ct], ct);
-            ET::store(Es, 4 * w + r, ct, 16 * s + n, g, ef[ct]);
+            ET::store(Es, row0 + r, ct, 16 * s + n, g, ef[ct]);
           }
           // Lanes of heads past HP fill padding slots nobody reads.
-          const int so = stage_off(4 * s + g, 4 * w + r, n);
+          const int so = stage_off(4 * s + g, row0 + r, n);
           if (attn) {
             f32x4 ue = zero4();
 #pragma unroll
@@ -400,8 +409,8 @@ __global__ __launch_bounds__(256, 2) void bwd_rows2_kernel(BwdParams prm) {
     // ---- row-owner: H -= dD G; H += E^T dS; G += E^T P ----
     if (use_e) {
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const int il = 4 * w + r;
+      for (int r = 0; r < RPW; ++r) {
+        const int il = row0 + r;
         // Lanes of padded heads (n >= H) read some other slot of the row:
         // finite values whose columns of H and G are never used.
         const int hn = n < HP ? n : HP - 1;
@@ -470,13 +479,13 @@ __global__ __launch_bounds__(256, 2) void bwd_rows2_kernel(BwdParams prm) {
     if (attn) {
       __syncthreads();  // the stage is free (last chunk, or previous round)
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
+      for (int r = 0; r < RPW; ++r) {
         f32x4 acc = zero4();
 #pragma unroll
         for (int ct = 0; ct < NCT; ++ct)
 #pragma unroll
           for (int sp = 0; sp < 4; ++sp) acc = mfma_f32(wdq[q][ct][sp], Hacc[r][ct][sp], acc);
-        *reinterpret_cast<f32x4*>(stU + stage_off(g, 4 * w + r, n)) = acc;
+        *reinterpret_cast<f32x4*>(stU + stage_off(g, row0 + r, n)) = acc;
       }
       __syncthreads();
     }
@@ -540,13 +549,13 @@ __global__ __launch_bounds__(256, 2) void bwd_rows2_kernel(BwdParams prm) {
 #pragma unroll
       for (int ct = 0; ct < NCT; ++ct) {
 #pragma unroll
-        for (int r = 0; r < 4; ++r)
+        for (int r = 0; r < RPW; ++r)
           if (n < HP)
-            *reinterpret_cast<f32x4*>(HGs + ((4 * w + r) * HP + n) * 16 + 4 * g) = op == 0 ? Hacc[r][ct] : Gacc[r][ct];
+            *reinterpret_cast<f32x4*>(HGs + ((row0 + r) * HP + n) * 16 + 4 * g) = op == 0 ? Hacc[r][ct] : Gacc[r][ct];
         __syncthreads();
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const int il = 4 * w + r;
+        for (int r = 0; r < RPW; ++r) {
+          const int il = row0 + r;
 #pragma unroll
           for (int s4 = 0; s4 < HP / 4; ++s4) {
             const int h = 4 * s4 + g;
@@ -562,23 +571,36 @@ __global__ __launch_bounds__(256, 2) void bwd_rows2_kernel(BwdParams prm) {
         __syncthreads();
       }
     }
-    float* wr = Wred + w * DCW;
+    // Four partials: wave w's (w < 4), then with eight waves wave w + 4's
+    // added to slot w in a second round (a fixed order of additions).
+    float* wr = Wred + (w & 3) * DCW;
+    float dbs[NQ];
 #pragma unroll
-    for (int q = 0; q < NQ; ++q) {
+    for (int q = 0; q < NQ; ++q) dbs[q] = group_allsum(dbl[q]);
 #pragma unroll
-      for (int ct = 0; ct < NCT; ++ct)
+    for (int round = 0; round < NW / 4; ++round) {
+      if (round > 0) __syncthreads();
+      if ((w >> 2) == round) {
 #pragma unroll
-        for (int r = 0; r < 4; ++r) wr[(16 * q + 4 * g + r) * C + slot_channel<C>(16 * ct + n)] = dw[q][ct][r];
-      const float dbs = group_allsum(dbl[q]);
-      if (g == 0) wr[D * C + 16 * q + n] = dbs;
+        for (int q = 0; q < NQ; ++q) {
+#pragma unroll
+          for (int ct = 0; ct < NCT; ++ct)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+              float& slot = wr[(16 * q + 4 * g + r) * C + slot_channel<C>(16 * ct + n)];
+              slot = round > 0 ? slot + dw[q][ct][r] : dw[q][ct][r];
+            }
+          if (g == 0) wr[D * C + 16 * q + n] = round > 0 ? wr[D * C + 16 * q + n] + dbs[q] : dbs[q];
+        }
+      }
     }
     __syncthreads();
-    for (int e = tid; e < DCW; e += 256) part[e] = Wred[e] + Wred[DCW + e] + Wred[2 * DCW + e] + Wred[3 * DCW + e];
+    for (int e = tid; e < DCW; e += NT) part[e] = Wred[e] + Wred[DCW + e] + Wred[2 * DCW + e] + Wred[3 * DCW + e];
   } else {
-    for (int e = tid; e < DCW; e += 256) part[e] = 0.f;
+    for (int e = tid; e < DCW; e += NT) part[e] = 0.f;
   }
 
-  zero_tile_rows<bf16, D>(prm.ev, rx, ra, i0, len, H, tid, dqg, prm.rowsum);
+  zero_tile_rows<bf16, D, NT>(prm.ev, rx, ra, i0, len, H, tid, dqg, prm.rowsum);
 }
 
 // ---------------------------------------------------------------------------
@@ -943,7 +965,13 @@ struct Bwd2Pick {
   static constexpr int KC = FST_ROWS_KC;  // keys per rows-kernel chunk
   static constexpr int HB = FST_ROWS_HB;  // heads per phase batch of the rows kernel
   static constexpr int RC = 16;  // rows per cols-kernel chunk
-  static constexpr bool OK = Rows2Cfg<HP, D, C, KC>::FITS && Cols2Cfg<HP, D, C, RC>::FITS;
+  // Waves of the rows kernel: eight where a four-wave lane's state would not
+  // fit its registers. (HP / 4) D + 3 C tracks that state (the head-owner's
+  // fragments and accumulators, the row-owner's H, G, u, w~); compiled for
+  // gfx950, the four-wave instances spill from about 160 on and the
+  // eight-wave ones fit (spills remain only at HP = 16 with D, C >= 48).
+  static constexpr int NW = (HP % 8 == 0 && rows_wave_load(HP, D, C) >= 160) ? 8 : 4;
+  static constexpr bool OK = Rows2Cfg<HP, D, C, KC, NW>::FITS && Cols2Cfg<HP, D, C, RC>::FITS;
 };
 
 template <int HP, int D, int C>
@@ -956,12 +984,12 @@ int bwd2_launch_t(const BwdParams& prm, int which, hipStream_t stream, int grid)
     // (tile_block); logical blocks past the work list exit at once.
     const int g8 = (grid + 63) & ~63;
     if (which == 0) {
-      auto kern = (prm.flags & 3) == 3 ? bwd_rows2_kernel<HP, D, C, P::KC, P::HB, 3>
-                                       : bwd_rows2_kernel<HP, D, C, P::KC, P::HB, -1>;
-      constexpr int lds = Rows2Cfg<HP, D, C, P::KC>::LDS_BYTES;
+      auto kern = (prm.flags & 3) == 3 ? bwd_rows2_kernel<HP, D, C, P::KC, P::HB, 3, P::NW>
+                                       : bwd_rows2_kernel<HP, D, C, P::KC, P::HB, -1, P::NW>;
+      constexpr int lds = Rows2Cfg<HP, D, C, P::KC, P::NW>::LDS_BYTES;
       if (hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, lds) != hipSuccess)
         return FST_ELAUNCH;
-      if (grid > 0) hipLaunchKernelGGL(kern, dim3(g8), dim3(256), lds, stream, prm);
+      if (grid > 0) hipLaunchKernelGGL(kern, dim3(g8), dim3(64 * P::NW), lds, stream, prm);
     } else {
       auto kern = (prm.flags & 3) == 3 ? bwd_cols2_kernel<HP, D, C, P::RC, 3> : bwd_cols2_kernel<HP, D, C, P::RC, -1>;
       constexpr int lds = Cols2Cfg<HP, D, C, P::RC>::LDS_BYTES;

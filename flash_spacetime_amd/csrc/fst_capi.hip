@@ -28,6 +28,16 @@ static bool supported_dim(int x) { return x == 16 || x == 32 || x == 48 || x == 
 
 static int head_padding(int H) { return H <= 4 ? 4 : (H <= 8 ? 8 : (H <= 12 ? 12 : 16)); }
 
+// Head padding of the bf16 rows kernel: where its four-wave instance would
+// spill, heads are padded to the next multiple of 8 so that it runs eight
+// waves (padded heads compute on a real head's data and store nothing). The
+// cols kernel keeps head_padding: the scratch between them is laid out by H.
+static int rows_head_padding(int dtype, int H, int D, int C) {
+  const int hp = head_padding(H);
+  if (dtype == FST_BF16 && hp % 8 != 0 && rows_wave_load(hp, D, C) >= 160) return hp + 4;
+  return hp;
+}
+
 // fp32 frequency ladder exp(-i * ln(1e4) / (C/2)) evaluated with the same
 // fp32 steps as the reference (reference.py:45-56): fp32 log of 1e4, fp32
 // division by C/2, fp32 product with i, exponential rounded to fp32.
@@ -275,8 +285,8 @@ static int bwd_layout(int dtype, int flags, int B, int H, int L, int T, int D, i
   bwd_dispatch_fn fn = bwd_table(dtype, D);
   BwdParams dummy;
   std::memset(&dummy, 0, sizeof(dummy));
-  const int HP = head_padding(H);
-  if (fn(dummy, 0, HP, C, nullptr, 0, true, &lay.rows_r) != FST_OK || lay.rows_r <= 0) return FST_EUNSUPPORTED;
+  const int HP = head_padding(H), HPR = rows_head_padding(dtype, H, D, C);
+  if (fn(dummy, 0, HPR, C, nullptr, 0, true, &lay.rows_r) != FST_OK || lay.rows_r <= 0) return FST_EUNSUPPORTED;
   if (fn(dummy, 1, HP, C, nullptr, 0, true, &lay.rows_c) != FST_OK || lay.rows_c <= 0) return FST_EUNSUPPORTED;
   const bool packed = flags & FST_PACKED;
   const long rows = packed ? (long)T : (long)B * L;
@@ -533,10 +543,10 @@ int fst_backward_phases(int phases, int dtype, int flags, int B, int H, int L, i
   freq_table(C, prm.freq);
 
   bwd_dispatch_fn fn = bwd_table(dtype, D);
-  const int HP = head_padding(H);
+  const int HP = head_padding(H), HPR = rows_head_padding(dtype, H, D, C);
   int dummy_rows = 0;
   if (phases & FST_PHASE_BWD_ROWS) {
-    rc = fn(prm, 0, HP, C, st, (int)lay.grid_r, false, &dummy_rows);
+    rc = fn(prm, 0, HPR, C, st, (int)lay.grid_r, false, &dummy_rows);
     if (rc != FST_OK) return fail(rc, "backward rows kernel launch failed");
   }
   if (phases & FST_PHASE_BWD_COLS) {

@@ -91,6 +91,11 @@ __device__ __forceinline__ RowAddr row_addr(const EventSpec& ev, const EventBloc
   return r;
 }
 
+// Register load of a four-wave bf16 rows-kernel lane, in the units of
+// (HP / 4) D + 3 C: at 160 and more such instances spill, and the rows kernel
+// runs eight waves instead (which needs HP % 8 == 0).
+__host__ __device__ constexpr int rows_wave_load(int HP, int D, int C) { return (HP / 4) * D + 3 * C; }
+
 // Row addressing of q, k, v, dq, dk and dv. With the operands interleaved
 // per token (one [.., 3, H, D] projection output), a token's q heads are
 // followed by its k heads and v heads: the token stride is three times that

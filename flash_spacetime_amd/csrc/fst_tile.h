@@ -205,7 +205,7 @@ __device__ __forceinline__ bool tile_block(const EventSpec& ev, int w, EventBloc
 // (pad-row contract: forward.py:19-22), 16 bytes per store, addressed by ra;
 // `vec` gets zeros at the same (head, row) positions, addressed by rv, when
 // not null.
-template <typename T, int D>
+template <typename T, int D, int NT = 256>
 __device__ __forceinline__ void zero_tile_rows(const EventSpec& ev, const RowAddr& ra, const RowAddr& rv, int i0,
                                                int len, int H, int tid, T* out, float* vec) {
   if (ev.packed) return;
@@ -214,12 +214,12 @@ __device__ __forceinline__ void zero_tile_rows(const EventSpec& ev, const RowAdd
   if (first >= end) return;
   const int nr = end - first;
   constexpr int CH = D * (int)sizeof(T) / 16;
-  for (int idx = tid; idx < H * nr * CH; idx += 256) {
+  for (int idx = tid; idx < H * nr * CH; idx += NT) {
     const int c = idx % CH, r = (idx / CH) % nr, h = idx / (CH * nr);
     *reinterpret_cast<u32x4*>(out + ra.off(h, first + r, D) + c * (16 / (int)sizeof(T))) = u32x4{0u, 0u, 0u, 0u};
   }
   if (vec)
-    for (int idx = tid; idx < H * nr; idx += 256) vec[rv.vec(idx / nr, first + idx % nr)] = 0.f;
+    for (int idx = tid; idx < H * nr; idx += NT) vec[rv.vec(idx / nr, first + idx % nr)] = 0.f;
 }
 
 // The W operand of project_slots: lane (g, n) holds W[Qd g + s][channel(16
