@@ -15,6 +15,15 @@ roofline's `traffic`.
 Usage:
   python -m flash_spacetime_amd.rocprof_summary --trace DIR --fetch DIR --write DIR \
       [--md OUT.md] [--json OUT.json] [--command "..."]
+  python -m flash_spacetime_amd.rocprof_summary --counters DIR [DIR ...] [--trace DIR] \
+      [--md OUT.md] [--command "..."]
+
+The second form summarises any counter passes (`--pmc ...`, csv output) of
+the library kernels: the mean reading per launch, and utilisation figures
+derived with the GPU's own geometry from rocprofv3's agent_info.csv
+(`GRBM_GUI_ACTIVE` counts cycles on every XCD, `SQ_VALU_MFMA_BUSY_CYCLES`
+on every SIMD, `SQ_LDS_BANK_CONFLICT` on every CU; `SQ_ACTIVE_INST_*` and
+`SQ_WAVE_CYCLES` / `SQ_WAIT_*` are in units of four cycles).
 """
 
 from __future__ import annotations
@@ -102,17 +111,105 @@ def read_counter(directory: str, counter: str):
     return {ph: sum(v) / len(v) for ph, v in vals.items()}, meta
 
 
+def read_agent(directory: str):
+    """(XCDs, CUs, SIMDs) of the GPU agent in rocprofv3's agent_info.csv."""
+    with open(_find(directory, "agent_info.csv")) as f:
+        for r in csv.DictReader(f):
+            if r.get("Agent_Type") == "GPU":
+                return int(r["Num_Xcc"]), int(r["Cu_Count"]), int(r["Simd_Count"])
+    raise SystemExit("no GPU agent in agent_info.csv")
+
+
+def read_all_counters(directories):
+    vals = defaultdict(lambda: defaultdict(list))
+    for d in directories:
+        with open(_find(d, "counter_collection.csv")) as f:
+            for r in csv.DictReader(f):
+                ph = phase_of(r["Kernel_Name"])
+                if ph in ("fwd", "bwd_rows", "bwd_cols"):
+                    vals[ph][r["Counter_Name"]].append(float(r["Counter_Value"]))
+    return {ph: {c: sum(v) / len(v) for c, v in cs.items()} for ph, cs in vals.items()}
+
+
+def counters_main(args):
+    xcc, cus, simds = read_agent(args.counters[0])
+    data = read_all_counters(args.counters)
+    loop = read_trace_loop(args.trace) if args.trace else {}
+    phases = [ph for ph in ("fwd", "bwd_rows", "bwd_cols") if ph in data]
+
+    def derived(c):
+        out = {}
+        if "GRBM_GUI_ACTIVE" in c:
+            cyc = c["GRBM_GUI_ACTIVE"] / xcc  # cycles of one XCD over the launch
+            out["cycles"] = cyc
+            if "SQ_VALU_MFMA_BUSY_CYCLES" in c:
+                out["MFMA busy (per SIMD)"] = c["SQ_VALU_MFMA_BUSY_CYCLES"] / (cyc * simds)
+            if "SQ_ACTIVE_INST_VALU" in c:
+                out["VALU issue (per SIMD)"] = 4 * c["SQ_ACTIVE_INST_VALU"] / (cyc * simds)
+            if "SQ_ACTIVE_INST_LDS" in c:
+                out["LDS issue (per SIMD)"] = 4 * c["SQ_ACTIVE_INST_LDS"] / (cyc * simds)
+            if "SQ_LDS_BANK_CONFLICT" in c:
+                out["LDS bank-conflict stall (per CU)"] = c["SQ_LDS_BANK_CONFLICT"] / (cyc * cus)
+        if "SQ_WAVE_CYCLES" in c:
+            for k, name in (("SQ_WAIT_INST_ANY", "waves waiting on a dependency"),
+                            ("SQ_WAIT_ANY", "waves waiting (any)"),
+                            ("SQ_ACTIVE_INST_ANY", "waves issuing")):
+                if k in c:
+                    out[name] = c[k] / c["SQ_WAVE_CYCLES"]
+        if "SQ_VALU_MFMA_BUSY_CYCLES" in c and c.get("SQ_INSTS_MFMA"):
+            out["cycles per MFMA"] = c["SQ_VALU_MFMA_BUSY_CYCLES"] / c["SQ_INSTS_MFMA"]
+        return out
+
+    der = {ph: derived(data[ph]) for ph in phases}
+    names = []
+    for ph in phases:
+        for k in der[ph]:
+            if k not in names:
+                names.append(k)
+    lines = ["| | " + " | ".join(phases) + " |", "|---|" + "---|" * len(phases)]
+    if loop:
+        lines.append("| timing-loop avg (us, kernel trace) | " + " | ".join(
+            f"{loop[ph]:.1f}" if ph in loop else "" for ph in phases) + " |")
+    for k in names:
+        cells = []
+        for ph in phases:
+            v = der[ph].get(k)
+            cells.append("" if v is None else (f"{v:.4g}" if k in ("cycles", "cycles per MFMA") else f"{100 * v:.1f} %"))
+        lines.append(f"| {k} | " + " | ".join(cells) + " |")
+    raw = ["| counter (mean per launch) | " + " | ".join(phases) + " |", "|---|" + "---|" * len(phases)]
+    counters = sorted({c for ph in phases for c in data[ph]})
+    for c in counters:
+        raw.append(f"| {c} | " + " | ".join(f"{data[ph].get(c, float('nan')):.4g}" for ph in phases) + " |")
+    md = "\n".join([
+        *(["Command:", "", "```", args.command, "```", ""] if args.command else []),
+        f"GPU: {xcc} XCDs, {cus} CUs, {simds} SIMDs (rocprofv3 agent_info).", "",
+        *lines, "", *raw, "",
+    ])
+    if args.md:
+        with open(args.md, "w") as f:
+            f.write(md)
+    else:
+        print(md)
+
+
 def main():
     ap = argparse.ArgumentParser()
-    ap.add_argument("--trace", required=True)
-    ap.add_argument("--fetch", required=True)
-    ap.add_argument("--write", required=True)
+    ap.add_argument("--trace")
+    ap.add_argument("--fetch")
+    ap.add_argument("--write")
+    ap.add_argument("--counters", nargs="+",
+                    help="counter-pass directories to summarise (second form); --trace optional")
     ap.add_argument("--calib-bytes", type=float, default=float(2 ** 30),
                     help="bytes the calibration kernel reads (and writes) per dispatch")
     ap.add_argument("--md")
     ap.add_argument("--json")
     ap.add_argument("--command", default="")
     args = ap.parse_args()
+    if args.counters:
+        counters_main(args)
+        return
+    if not (args.trace and args.fetch and args.write):
+        ap.error("--trace, --fetch and --write are required (or --counters)")
 
     stats = read_stats(args.trace)
     loop = read_trace_loop(args.trace)
