@@ -14,7 +14,7 @@ times of the individual launches, the MFMA roofline of the dominant kernel,
 and the CPU baseline (the oracle's eager restatement of the spec, fp32,
 fwd+bwd, timed on this host's cores on a bounded sample of events).
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload cfg2|cfg3|cfg4|cfg4-fp32|cfg2-model]
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload cfg2|cfg3|cfg4|cfg4-fp32|cfg2-model|lscale]
 """
 
 from __future__ import annotations
@@ -200,9 +200,62 @@ WORKLOADS = {
             "q and k x30, bf16",
     "cfg4-fp32": "configs[4]: flash_spacetime_attention fwd+bwd, B=8 L=4096 (no padding) H=8 D=64 C=64, "
                  "q and k x30, fp32",
+    "lscale": "configs[2] at L = 384, 768, 1536: flash_spacetime_attention fwd+bwd, B=256 H=12 D=32 C=16 "
+              "bf16, lengths U{16..L}",
     "cfg2-model": "SpacetimeAttention fwd+bwd (fused QKV linear, flash_spacetime_attention_qkv, output "
                   "linear) at cfg2 sizes: x [256, 768, 384] bf16, H=12 D=32 C=16, lengths U{16..768}",
 }
+
+
+def run_length_scaling(steps, warmup):
+    """cfg2's step at L = 384, 768, 1536 (B = 256, lengths U{16..L}, same
+    distributions): ms/step, peak GiB above the inputs, valid pairs. Time
+    follows the valid pairs (sum of squared lengths); memory grows linearly
+    in L (nothing O(L^2) is materialised)."""
+    from flash_spacetime_amd import flash_spacetime_attention
+
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    out = {}
+    for length in (384, 768, 1536):
+        gen = torch.Generator().manual_seed(length)
+        rn = lambda *s_: torch.randn(*s_, generator=gen)
+        q, k, v, do = (rn(B, H, length, D).to(dev, torch.bfloat16) for _ in range(4))
+        feats = torch.cat([(torch.rand(B, length, 3, generator=gen) - 0.5) * 1000.0,
+                           torch.rand(B, length, 1, generator=gen) * 2e4], -1).to(dev)
+        w = (rn(D, C) / C ** 0.5).to(dev)
+        bias = (rn(D) * 0.02).to(dev)
+        lens = torch.randint(16, length + 1, (B,), generator=gen)
+        seqlens = lens.to(dev, torch.int32)
+        leaves = [x.clone().requires_grad_(True) for x in (q, k, v)]
+        wl, bl = w.clone().requires_grad_(True), bias.clone().requires_grad_(True)
+
+        def step():
+            for t_ in (*leaves, wl, bl):
+                t_.grad = None
+            flash_spacetime_attention(*leaves, feats, wl, bl, seqlens).backward(do)
+
+        for _ in range(warmup):
+            step()
+        torch.cuda.synchronize(dev)
+        ms = time_events(step, steps, torch.cuda.current_stream(dev))
+        torch.cuda.synchronize(dev)
+        torch.cuda.reset_peak_memory_stats(dev)
+        base = torch.cuda.memory_allocated(dev)
+        step()
+        torch.cuda.synchronize(dev)
+        peak = (torch.cuda.max_memory_allocated(dev) - base) / 2 ** 30
+        out[str(length)] = {"ms": round(ms, 4), "peak_gib": round(peak, 4),
+                            "valid_pairs": float((lens.double() ** 2).sum())}
+        del q, k, v, do, feats, leaves
+        torch.cuda.empty_cache()
+    print(json.dumps({
+        "metric": "fwd+bwd ms/step and peak GiB vs L at cfg2's other sizes", "value": out["768"]["ms"],
+        "unit": "ms", "n_gpus": 1, "steps": steps, "warmup": warmup, "ms_per_step": out["768"]["ms"],
+        "higher_is_better": False, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+        "data": "synthetic (seeded; cfg2 distributions at each L)",
+        "config": {"workload": WORKLOADS["lscale"]}, "by_length": out,
+    }), flush=True)
 
 
 def run_model_workload(steps, warmup):
@@ -358,6 +411,9 @@ def main():
 
     if args.workload == "cfg2-model":
         run_model_workload(args.steps, args.warmup)
+        return
+    if args.workload == "lscale":
+        run_length_scaling(args.steps, args.warmup)
         return
     if args.workload != "cfg2":
         run_other_workload(args.workload, args.steps, args.warmup)
