@@ -736,7 +736,7 @@ __global__ __launch_bounds__(256, (Cols2Cfg<HP, D, C, RC>::OCC)) void bwd_cols2_
   // QL: the wave's heads' qt and dO rows of a chunk go straight to LDS, lane
   // l of a block load fetching the quarter QoTile keeps in slot l; rows past
   // the event are clamped to its last row.
-  const int qo_r = lane >> 2, qo_c = (lane & 3) ^ ((qo_r >> 2) & 3);
+  const int qo_r = lane >> 2, qo_c = (lane & 3) ^ QoTile::swz(qo_r);
   auto issue_qo = [&](int in) __attribute__((always_inline)) {
     if constexpr (QL) {
       const bool full = in + RC <= len;
@@ -930,7 +930,10 @@ __global__ __launch_bounds__(256, (Cols2Cfg<HP, D, C, RC>::OCC)) void bwd_cols2_
   for (; i0c + RC <= len; i0c += RC) chunk(i0c, std::false_type{});
   if (i0c < len) chunk(i0c, std::true_type{});
 
-  // ---- store dk, dv (lane n = key, 8 consecutive features per lane group) ----
+  // ---- store dk, dv (lane n = key) ----
+  // With the tiles in LDS (QL) accumulator q holds features 16 q + 4 g + r
+  // (the transposed reads' order); otherwise DTiles::dmap's, 8 consecutive
+  // features per lane group across the accumulator pair 2t, 2t + 1.
   if (key_ok) {
 #pragma unroll
     for (int hl = 0; hl < HW; ++hl) {
@@ -938,7 +941,13 @@ __global__ __launch_bounds__(256, (Cols2Cfg<HP, D, C, RC>::OCC)) void bwd_cols2_
       if (h >= H) continue;
       bf16* krow = dkg + rx.off(h, my_key, D);
       bf16* vrow = dvg + rx.off(h, my_key, D);
-      if constexpr (DT::X32) {
+      if constexpr (QL) {
+#pragma unroll
+        for (int q = 0; q < NQ; ++q) {
+          *reinterpret_cast<bf16x4*>(krow + 16 * q + 4 * g) = pack4(dK[hl][q]);
+          *reinterpret_cast<bf16x4*>(vrow + 16 * q + 4 * g) = pack4(dV[hl][q]);
+        }
+      } else if constexpr (DT::X32) {
 #pragma unroll
         for (int t = 0; t < NQ / 2; ++t) {
           *reinterpret_cast<bf16x8*>(krow + DT::dmap(2 * t, g, 0)) = cat8(pack4(dK[hl][2 * t]), pack4(dK[hl][2 * t + 1]));

@@ -402,26 +402,32 @@ __device__ __forceinline__ int half_off(int c, int i, int h, int half) {
   return stage_off(c, i, h) + ((half ^ (((h ^ i) >> 3) & 1)) << 3);
 }
 
-// Operand rows of one 16-row (or 16-key) chunk in LDS (qt and dO in the cols
-// kernel, K and V in the forward): per (tensor, head, 32-feature part) a 1 KB
-// block of 16 rows x 4 16-byte quarters, quarter c of row r at slot
-// 4 r + (c ^ ((r >> 2) & 3)). A 16-byte read of quarter g by the 16 rows of
-// a lane group, and the transposing 8-byte read of 4 rows x 4 quarters, both
-// hit distinct banks. One direct-to-LDS load (lane l -> slot l) fills a block.
+// Operand rows of one 16-row chunk in LDS (qt and dO in the cols kernel): per
+// (tensor, head, 32-feature part) a 1 KB block of 16 rows x 4 16-byte
+// quarters, quarter c of row r at slot 4 r + (c ^ swz(r)), swz(r) = (r >> 2)
+// with its two bits swapped (0, 2, 1, 3). One direct-to-LDS load (lane l ->
+// slot l) fills a block. Bank model of gfx950 LDS reads (256 bytes a pass:
+// 16 lanes of a 16-byte read, 32 of an 8-byte read): the 16-byte read of
+// quarter g by a lane group's 16 rows covers the pass once because swz is a
+// permutation of r >> 2; the transposing 8-byte read of 16-feature slice q
+// takes quarters 2q, 2q + 1 of rows 0-7 (or 8-15) in one pass, and rows r,
+// r + 4 (which share banks) find them at quarters 2q ^ 2, 2q ^ 3 of each
+// other, since swz(r) ^ swz(r + 4) = 2 for those rows.
 struct QoTile {
-  static __device__ __forceinline__ int slot(int r, int c) { return 4 * r + (c ^ ((r >> 2) & 3)); }
+  static __device__ __forceinline__ int swz(int r) { return ((r >> 1) & 2) | ((r >> 3) & 1); }
+  static __device__ __forceinline__ int slot(int r, int c) { return 4 * r + (c ^ swz(r)); }
   // Row-major fragment part (row n, features 8g .. 8g + 7 of the part).
   static __device__ __forceinline__ bf16x8 row_frag(const unsigned char* blk, int g, int n) {
     return *reinterpret_cast<const bf16x8*>(blk + 16 * slot(n, g));
   }
-  // Transposed 16x16 operand of 16-feature slice q of the part (q & 1 picks
-  // the half of each quarter): lane (g, n) receives rows 4g .. 4g + 3 of the
-  // feature the row-major fragment's slice q holds in slot n (DTiles::dmap).
-  // Source lane s of the group supplies row 4g + s / 4, features 8 (s % 4) +
-  // 4 (q & 1) .. +3 of the part.
+  // Transposed 16x16 operand of 16-feature slice q & 1 of the part (features
+  // 16 (q & 1) .. +15, quarters 2 (q & 1) and 2 (q & 1) + 1): lane (g, n)
+  // receives rows 4g .. 4g + 3 of feature 16 (q & 1) + n of the part. Source
+  // lane s of the group supplies row 4g + s / 4, features 16 (q & 1) +
+  // 4 (s % 4) .. +3.
   static __device__ __forceinline__ bf16x4 tr_frag(const unsigned char* blk, int q, int g, int n) {
-    const int r = 4 * g + (n >> 2);
-    const unsigned char* p = blk + 16 * slot(r, n & 3) + 8 * (q & 1);
+    const int r = 4 * g + (n >> 2), j = n & 3;
+    const unsigned char* p = blk + 16 * slot(r, 2 * (q & 1) + (j >> 1)) + 8 * (j & 1);
     return __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4*)(p));
   }
 };
