@@ -19,8 +19,10 @@
 // rescale factors head-owner -> row-owner; E is private to the wave that
 // computed it. Two barriers per key chunk.
 //
-// K and V come from global memory in row-major operand layout; V^T is made
-// on the matrix core (identity product). Keys past the event are clamped to
+// K comes from global memory in row-major operand layout. Where the LDS plan
+// allows (D a multiple of 32), each chunk's V rows go straight to LDS by
+// direct loads and are read transposed (QoTile); otherwise V^T is made on the
+// matrix core (identity product). Keys past the event are clamped to
 // the last valid key for loads and masked to -inf in the last chunk only.
 // The softmax reference m is raised only when a row's chunk maximum exceeds
 // it by more than 2^8 (log2 domain), so O, l and A are rescaled rarely.
@@ -36,7 +38,13 @@ struct Fwd2Cfg {
   static constexpr int E_BYTES = ETile<C, KC>::BYTES;
   static constexpr int STAGE_BYTES = (KC / 4) * 16 * 16 * 16;  // fp32 u.E of KC keys per (row, head)
   static constexpr int SCAL_BYTES = 16 * 17 * 4 + 16;  // rescale factors, then one flag per wave
-  static constexpr int LDS_BYTES = E_BYTES + STAGE_BYTES + SCAL_BYTES;
+  static constexpr int BASE_BYTES = E_BYTES + STAGE_BYTES + SCAL_BYTES;
+  // VL: each chunk's V rows go straight to LDS (QoTile blocks, one per head
+  // and 32-feature part) and are read transposed there, where D is a multiple
+  // of 32, the chunk 16 keys and the blocks fit the occupancy's LDS share.
+  static constexpr int V_BYTES = HP * (D / 32) * 1024;
+  static constexpr bool VL = D % 32 == 0 && KC == 16 && BASE_BYTES + V_BYTES <= (160 / OCC) * 1024;
+  static constexpr int LDS_BYTES = BASE_BYTES + (VL ? V_BYTES : 0);
   // OCC: workgroups per CU the register and LDS plan is built for.
   static constexpr bool FITS = LDS_BYTES <= (160 / OCC) * 1024 && HP % 4 == 0 && (KC == 16 || KC == 32);
 };
@@ -49,11 +57,14 @@ __global__ __launch_bounds__(256, OCC) void fwd2_kernel(FwdParams prm) {
   using ET = ETile<C, KC>;
   using DT = DTiles<D>;
   constexpr int HW = Cfg::HW, NS = Cfg::NS, NCT = Cfg::NCT, NQ = DT::NQ;
+  constexpr bool VL = Cfg::VL;
+  constexpr int NP = D / 32;  // 32-feature parts of a row (VL)
   extern __shared__ __align__(16) unsigned char smem[];
   bf16* Es = reinterpret_cast<bf16*>(smem);
   unsigned char* stage = smem + Cfg::E_BYTES;
   unsigned char* scal = stage + Cfg::STAGE_BYTES;
   int* rflag = reinterpret_cast<int*>(scal + 16 * 17 * 4);  // wave w rescaled its heads this chunk
+  unsigned char* vtile = smem + Cfg::BASE_BYTES;  // VL: [head][part] QoTile blocks of the chunk's V
 
   const int tid = threadIdx.x;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63, g = lane >> 4, n = lane & 15;
@@ -144,7 +155,7 @@ __global__ __launch_bounds__(256, OCC) void fwd2_kernel(FwdParams prm) {
   // and V; past the last chunk they reread clamped keys), so the wait at the
   // top of a chunk covers the positions only and E is formed while K and V
   // are still in flight.
-  KFrag<bf16, D> kf[HW][NS], vf[HW][NS];
+  KFrag<bf16, D> kf[HW][NS], vf[VL ? 1 : HW][NS];
   float4 pj[NS];
   auto issue = [&](int jn) __attribute__((always_inline)) {
     const bool full = jn + KC <= len;
@@ -155,7 +166,27 @@ __global__ __launch_bounds__(256, OCC) void fwd2_kernel(FwdParams prm) {
         const int voff = full ? kvo[hl] + 16 * s * rowb : kvo[hl] + (min(jn + 16 * s + n, last) - n) * rowb;
         const int soff = full ? jn * rowb : 0;
         load_kfrag<D>(kf[hl][s], kbuf, voff, soff);
-        load_kfrag<D>(vf[hl][s], vbuf, voff, soff);
+        if constexpr (!VL) load_kfrag<D>(vf[hl][s], vbuf, voff, soff);
+      }
+    }
+  };
+  // VL: the wave's heads' V rows of chunk jn straight to LDS, lane l of a
+  // block load fetching the quarter QoTile keeps in slot l; keys past the
+  // event are clamped to its last key (their P is zero).
+  const int vo_r = lane >> 2, vo_c = (lane & 3) ^ QoTile::swz(vo_r);
+  auto issue_v = [&](int jn) __attribute__((always_inline)) {
+    if constexpr (VL) {
+      const bool full = jn + KC <= len;
+      const int rel = full ? vo_r * rowb : min(jn + vo_r, last) * rowb;
+      const int soff = full ? jn * rowb : 0;
+#pragma unroll
+      for (int hl = 0; hl < HW; ++hl) {
+        const int h = w * HW + hl;
+        const int voff = (int)(min(h, H - 1) * rx.hs * D * 2) + rel + 16 * vo_c;
+#pragma unroll
+        for (int t = 0; t < NP; ++t)
+          __builtin_amdgcn_raw_ptr_buffer_load_lds(vbuf.r, (__attribute__((address_space(3))) void*)(vtile + (h * NP + t) * 1024),
+                                                   16, voff + 64 * t, soff, 0, 0);
       }
     }
   };
@@ -198,6 +229,7 @@ __global__ __launch_bounds__(256, OCC) void fwd2_kernel(FwdParams prm) {
 
   auto chunk = [&](int j0, auto tail_tag) __attribute__((always_inline)) {
     constexpr bool TAIL = decltype(tail_tag)::value;
+    issue_v(j0);  // lands during the row-owner part
 
     // ---- row-owner: E of rows 4w..4w+3 x KC keys; u.E staged ----
     if (use_e) {
@@ -289,12 +321,18 @@ __global__ __launch_bounds__(256, OCC) void fwd2_kernel(FwdParams prm) {
       lsum[hl] = ls;
       pf[hl].from_tiles(S[hl]);
     }
+    // This wave's V rows are in LDS (VL): only its own loads need waiting
+    // for, and the previous chunk's reads of the blocks ended at its closing
+    // barrier.
+    if constexpr (VL) wait_vmem();
 #pragma unroll
     for (int hl = 0; hl < HW; ++hl) {
 #pragma unroll
       for (int q = 0; q < NQ; ++q) {
         JFrag<bf16, NS> vt;
-        if constexpr (NS == 2)
+        if constexpr (VL)
+          vt.v = QoTile::tr_frag(vtile + ((w * HW + hl) * NP + (q >> 1)) * 1024, q, g, n);
+        else if constexpr (NS == 2)
           vt.v = cat8(transpose_x16(DT::part(vf[hl][0], q), id), transpose_x16(DT::part(vf[hl][1], q), id));
         else
           vt.v = transpose_x16(DT::part(vf[hl][0], q), id);
@@ -377,15 +415,18 @@ __global__ __launch_bounds__(256, OCC) void fwd2_kernel(FwdParams prm) {
     if (g == 0 && row_ok && h < H) prm.lse[ra.vec(h, my_row)] = mref[hl] * kLn2 + __logf(l);
   }
 
+  // O's accumulator q holds features omap(q, g, r): 16 q + 4 g + r when V was
+  // read transposed from LDS, DTiles::dmap otherwise.
+  auto omap = [&](int q, int gg, int r) { return VL ? 16 * q + 4 * gg + r : DT::dmap(q, gg, r); };
   // One head-dim tile per round: the row-owner forms o2^T_i[d, h] =
   // sum_slot W[d, channel(slot)] A^T_i[slot, h] on fp32 MFMA (lane n of the
-  // A operand is the tile's feature dmap(q, n/4, n%4)) and stages it; the
+  // A operand is the tile's feature omap(q, n/4, n%4)) and stages it; the
   // head-owner forms out = (O + o2) / l + b in place.
 #pragma unroll
   for (int q = 0; q < NQ; ++q) {
     if (act) {
       __syncthreads();  // previous round (or the last chunk) done with the stage
-      const int dn = DT::dmap(q, n >> 2, n & 3);
+      const int dn = omap(q, n >> 2, n & 3);
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         f32x4 acc = zero4();
@@ -405,7 +446,7 @@ __global__ __launch_bounds__(256, OCC) void fwd2_kernel(FwdParams prm) {
       o = o * inv_l[hl];
       if (act && prm.bias) {
 #pragma unroll
-        for (int r = 0; r < 4; ++r) o[r] += prm.bias[DT::dmap(q, g, r)];
+        for (int r = 0; r < 4; ++r) o[r] += prm.bias[omap(q, g, r)];
       }
       O[hl][q] = o;
     }
@@ -416,7 +457,10 @@ __global__ __launch_bounds__(256, OCC) void fwd2_kernel(FwdParams prm) {
       const int h = w * HW + hl;
       if (h >= H) continue;
       bf16* orow = outg + ra.off(h, my_row, D);
-      if constexpr (DT::X32) {
+      if constexpr (VL) {
+#pragma unroll
+        for (int q = 0; q < NQ; ++q) *reinterpret_cast<bf16x4*>(orow + 16 * q + 4 * g) = pack4(O[hl][q]);
+      } else if constexpr (DT::X32) {
 #pragma unroll
         for (int t = 0; t < NQ / 2; ++t)
           *reinterpret_cast<bf16x8*>(orow + DT::dmap(2 * t, g, 0)) = cat8(pack4(O[hl][2 * t]), pack4(O[hl][2 * t + 1]));
