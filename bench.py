@@ -14,7 +14,7 @@ times of the individual launches, the MFMA roofline of the dominant kernel,
 and the CPU baseline (the oracle's eager restatement of the spec, fp32,
 fwd+bwd, timed on this host's cores on a bounded sample of events).
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload cfg2|cfg3|cfg4|cfg4-fp32|cfg2-model|lscale]
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload cfg2|cfg1|cfg3|cfg4|cfg4-fp32|cfg2-model|lscale]
 """
 
 from __future__ import annotations
@@ -200,11 +200,50 @@ WORKLOADS = {
             "q and k x30, bf16",
     "cfg4-fp32": "configs[4]: flash_spacetime_attention fwd+bwd, B=8 L=4096 (no padding) H=8 D=64 C=64, "
                  "q and k x30, fp32",
+    "cfg1": "configs[1]: flash_spacetime_attention forward only, B=256 L=768 H=12 D=32 C=16 bf16, valid "
+            "lengths U{16..768} (bool key_padding_mask -> seqlens once), W/b fp32",
     "lscale": "configs[2] at L = 384, 768, 1536: flash_spacetime_attention fwd+bwd, B=256 H=12 D=32 C=16 "
               "bf16, lengths U{16..L}",
     "cfg2-model": "SpacetimeAttention fwd+bwd (fused QKV linear, flash_spacetime_attention_qkv, output "
                   "linear) at cfg2 sizes: x [256, 768, 384] bf16, H=12 D=32 C=16, lengths U{16..768}",
 }
+
+
+def run_forward_only(steps, warmup):
+    """the forward alone at cfg2's shape (the op under no_grad, the
+    bool key_padding_mask converted to lengths once): ms/step, peak GiB above
+    the inputs, and the MFMA fraction of the forward's algorithmic FLOPs."""
+    from flash_spacetime_amd import flash_spacetime_attention
+    from flash_spacetime_amd.forward import lengths_from_mask
+
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    inp = make_inputs(dev)
+    seqlens = lengths_from_mask(inp["pad_mask"], L)
+
+    def step():
+        with torch.no_grad():
+            flash_spacetime_attention(inp["q"], inp["k"], inp["v"], inp["feats"], inp["w"], inp["b"], seqlens)
+
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize(dev)
+    ms = time_events(step, steps, torch.cuda.current_stream(dev))
+    torch.cuda.synchronize(dev)
+    torch.cuda.reset_peak_memory_stats(dev)
+    base = torch.cuda.memory_allocated(dev)
+    step()
+    torch.cuda.synchronize(dev)
+    peak = (torch.cuda.max_memory_allocated(dev) - base) / 2 ** 30
+    f_fwd = flop_counts(inp["lengths"])["fwd"]
+    print(json.dumps({
+        "metric": "fwd ms/step & peak GiB at B=256,L=768,C=16 bf16; % MFMA peak", "value": round(ms, 4),
+        "unit": "ms", "n_gpus": 1, "steps": steps, "warmup": warmup, "ms_per_step": round(ms, 4),
+        "higher_is_better": False, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
+        "data": "synthetic (seeded; BASELINE.json configs[1] distributions)",
+        "config": {"workload": WORKLOADS["cfg1"]}, "peak_gib": round(peak, 4),
+        "mfma_pct_of_peak": round(100.0 * f_fwd / (ms * 1e-3) / (PEAK_BF16_TFLOPS * 1e12), 3),
+    }), flush=True)
 
 
 def run_length_scaling(steps, warmup):
@@ -411,6 +450,9 @@ def main():
 
     if args.workload == "cfg2-model":
         run_model_workload(args.steps, args.warmup)
+        return
+    if args.workload == "cfg1":
+        run_forward_only(args.steps, args.warmup)
         return
     if args.workload == "lscale":
         run_length_scaling(args.steps, args.warmup)
