@@ -32,10 +32,15 @@ def _run_backward(dims, q, k, v, pos4, w32, b32, lens, lse, grad_out, scale, vec
     keeps a dense view's strides); dq, dk, dv are written into `grads` when
     given (the slots of one interleaved gradient tensor), else into tensors
     laid out like q, k, v."""
-    lib = _lib.load()
-    _lib.require_gpu(grad_out)
     if grad_out.shape != q.shape:
         raise ValueError(f"grad_out must have the shape of the output {tuple(q.shape)}")
+    interleaved = bool(dims[1] & _lib.FST_QKV_INTERLEAVED)
+    if interleaved and (grads is None or out_like is None):
+        # empty_like of a slot view of [.., 3, H, D] is contiguous, not
+        # interleaved: the kernels would write past its end.
+        raise ValueError("interleaved q / k / v need the gradient slots of one tensor and the output layout")
+    lib = _lib.load()
+    _lib.require_gpu(grad_out)
     like = q if out_like is None else out_like
     do = grad_out.to(q.dtype)
     if not _same_layout(do, like):
@@ -44,6 +49,13 @@ def _run_backward(dims, q, k, v, pos4, w32, b32, lens, lse, grad_out, scale, vec
         dq, dk, dv = grads
     else:
         dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
+    # The kernels address dq, dk, dv exactly as q, k, v (and rowsum as lse):
+    # buffers of another layout or shape are refused rather than overrun.
+    for name, gb, src in (("dq", dq, q), ("dk", dk, k), ("dv", dv, v)):
+        if gb.shape != src.shape or gb.dtype != src.dtype or not _same_layout(gb, src):
+            raise ValueError(f"{name} buffer must have the shape, dtype and layout of its operand")
+    if rowsum is not None and rowsum.shape != lse.shape:
+        raise ValueError(f"rowsum must have the shape of lse {tuple(lse.shape)}")
     rs = rowsum
     if rowsum is not None and not _same_layout(rowsum, lse):
         rs = torch.empty_like(lse)

@@ -54,3 +54,22 @@ def test_module_parameters_follow_attention_rel():
             "proj.bias", "rel_proj.weight", "rel_proj.bias"} == names
     assert m.rel_proj.weight.shape == (32, 16) and m.num_heads == 3
     assert _module(False).q_bias is None
+
+
+def test_backward_refuses_gradient_buffers_of_another_layout():
+    """Regression: the kernels address dq, dk, dv exactly as q, k, v. With
+    interleaved operands, `empty_like` of a slot view is contiguous and would
+    be written past its end, so the host layer must refuse it (and any
+    mismatched buffer) before launching anything."""
+    from flash_spacetime_amd import _lib
+    from flash_spacetime_amd.backward import _run_backward
+    from flash_spacetime_amd.forward import _qkv_views
+
+    B, L, H, D, C = 2, 5, 3, 32, 16
+    qkv = torch.zeros(B, L, 3, H, D)
+    q, k, v = _qkv_views(qkv, False)
+    dims = (_lib.FST_F32, 3 | _lib.FST_TOKEN_MAJOR | _lib.FST_QKV_INTERLEAVED, B, H, L, 0, D, C)
+    lse = torch.zeros(B, L, H).transpose(1, 2)
+    do = torch.zeros(B, L, H, D).transpose(1, 2)
+    with pytest.raises(ValueError, match="interleaved"):
+        _run_backward(dims, q, k, v, None, None, None, None, lse, do, 1.0, (B, H, L))
