@@ -39,6 +39,13 @@ def _run_backward(dims, q, k, v, pos4, w32, b32, lens, lse, grad_out, scale, vec
         # empty_like of a slot view of [.., 3, H, D] is contiguous, not
         # interleaved: the kernels would write past its end.
         raise ValueError("interleaved q / k / v need the gradient slots of one tensor and the output layout")
+    token_major = bool(dims[1] & (_lib.FST_TOKEN_MAJOR | _lib.FST_PACKED))
+    if (tuple(lse.shape) != tuple(vec_shape) or lse.dtype != torch.float32 or lse.device != q.device
+            or not (lse.transpose(1, 2).is_contiguous() if token_major and lse.dim() == 3 else lse.is_contiguous())):
+        raise ValueError(f"lse must be float32 {tuple(vec_shape)} on the operands' device, laid out as they are")
+    if rowsum is not None and (rowsum.shape != lse.shape or rowsum.dtype != torch.float32
+                               or rowsum.device != q.device):
+        raise ValueError(f"rowsum must be float32 of the shape of lse {tuple(lse.shape)} on the operands' device")
     lib = _lib.load()
     _lib.require_gpu(grad_out)
     like = q if out_like is None else out_like
@@ -54,8 +61,6 @@ def _run_backward(dims, q, k, v, pos4, w32, b32, lens, lse, grad_out, scale, vec
     for name, gb, src in (("dq", dq, q), ("dk", dk, k), ("dv", dv, v)):
         if gb.shape != src.shape or gb.dtype != src.dtype or not _same_layout(gb, src):
             raise ValueError(f"{name} buffer must have the shape, dtype and layout of its operand")
-    if rowsum is not None and rowsum.shape != lse.shape:
-        raise ValueError(f"rowsum must have the shape of lse {tuple(lse.shape)}")
     rs = rowsum
     if rowsum is not None and not _same_layout(rowsum, lse):
         rs = torch.empty_like(lse)

@@ -73,3 +73,18 @@ def test_backward_refuses_gradient_buffers_of_another_layout():
     do = torch.zeros(B, L, H, D).transpose(1, 2)
     with pytest.raises(ValueError, match="interleaved"):
         _run_backward(dims, q, k, v, None, None, None, None, lse, do, 1.0, (B, H, L))
+
+
+def test_backward_refuses_lse_of_another_shape():
+    """The kernels read lse at every (row, head) of the operands: a smaller
+    lse is refused before any launch (as is one of another dtype)."""
+    from flash_spacetime_amd import _lib
+    from flash_spacetime_amd.backward import _run_backward
+
+    B, L, H, D, C = 2, 5, 3, 32, 16
+    q = torch.zeros(B, H, L, D)
+    dims = (_lib.FST_F32, 3, B, H, L, 0, D, C)
+    do = torch.zeros(B, H, L, D)
+    for lse in (torch.zeros(B, H, L - 1), torch.zeros(B, H, L, dtype=torch.float64)):
+        with pytest.raises(ValueError, match="lse"):
+            _run_backward(dims, q, q, q, None, None, None, None, lse, do, 1.0, (B, H, L))
