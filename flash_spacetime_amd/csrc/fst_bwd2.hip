@@ -28,11 +28,19 @@
 //
 // Cols kernel (one 16-key tile per workgroup, rows streamed): S = Qt K^T and
 // dP = dO V^T with the keys on the lanes, dV^T += dO^T P and dK^T += Qt^T dS
-// (Qt^T, dO^T transposed on the matrix core). The row-owner part forms
+// (Qt^T, dO^T read transposed from the chunk's qt / dO rows, which go
+// straight to LDS, or made on the matrix core where those do not fit). The
+// row-owner part forms
 // u_i E_i^T and w~_i E_i^T for the streamed rows with the heads on the
 // registers; four consecutive rows of a lane are regrouped in registers so
 // that the exchange to the head-owners is one 16-byte write and read per
 // (row group, head, key).
+//
+// The rows kernel runs four waves per workgroup, or eight where a four-wave
+// lane's state would spill (Rows2Cfg, Bwd2Pick). Rows are addressed through
+// two RowAddr: q, k, v, dq, dk, dv through row_addr_x (their token stride is
+// three times the others' when they are the slots of one fused projection),
+// dO, the per-row vectors and the scratch through row_addr.
 //
 // Both kernels write every output exactly once in a fixed order (no atomics),
 // so results are bitwise reproducible.
@@ -142,7 +150,7 @@ __global__ __launch_bounds__(64 * NW, (NW == 4 ? 2 : 1)) void bwd_rows2_kernel(B
     lse2[hl] = prm.lse[ra.vec(hc, rc)];
   }
 
-  // ---- row-owner state: rows i0 + 4w + r, heads on lane n ----
+  // ---- row-owner state: rows i0 + row0 + r (r < RPW), heads on lane n ----
   WSlots<D, C> wv;
   if (use_e) wv.load(prm.weight, g, n);
   SlotRow<D> xq[RPW], xd[RPW];

@@ -22,7 +22,9 @@
 // K comes from global memory in row-major operand layout. Where the LDS plan
 // allows (D a multiple of 32), each chunk's V rows go straight to LDS by
 // direct loads and are read transposed (QoTile); otherwise V^T is made on the
-// matrix core (identity product). Keys past the event are clamped to
+// matrix core (identity product). q, k and v are addressed through
+// row_addr_x (token stride three times out's when they are the slots of one
+// fused projection), out and lse through row_addr. Keys past the event are clamped to
 // the last valid key for loads and masked to -inf in the last chunk only.
 // The softmax reference m is raised only when a row's chunk maximum exceeds
 // it by more than 2^8 (log2 domain), so O, l and A are rescaled rarely.
