@@ -40,7 +40,8 @@ class SpacetimeAttention(nn.Module):
     of the operator (`weight [D, C]`, `bias [D]`, nn.Linear layout).
     `forward(x, feats, seqlens | key_padding_mask)` takes `x [B, L, dim]`,
     detector features `feats [B, L, F >= 4]` and the event lengths, and
-    returns `[B, L, dim]`.
+    returns `[B, L, dim]`; with `cu_seqlens` it takes packed events, `x
+    [T, dim]` and `feats [T, F]`, and returns `[T, dim]`.
     """
 
     def __init__(self, dim: int, num_heads: int = 8, channels: int = 16, qkv_bias: bool = False,
@@ -92,11 +93,22 @@ class SpacetimeAttention(nn.Module):
         return tuple(split_heads(t, self.num_heads) for t in (q, k, v))
 
     def forward(self, x: Tensor, feats: Tensor, seqlens: Optional[Tensor] = None,
-                key_padding_mask: Optional[Tensor] = None, kv: Optional[Tensor] = None) -> Tensor:
+                key_padding_mask: Optional[Tensor] = None, kv: Optional[Tensor] = None,
+                cu_seqlens: Optional[Tensor] = None) -> Tensor:
         from .forward import flash_spacetime_attention, flash_spacetime_attention_qkv
 
-        b, length, _ = x.shape
         flags = (self.use_attn_bias, self.use_activation_bias)
+        if cu_seqlens is not None:
+            if kv is not None or seqlens is not None or key_padding_mask is not None:
+                raise ValueError("packed input takes cu_seqlens only (self-attention, no lengths or mask)")
+            if x.dim() != 2:
+                raise ValueError(f"packed x must be [T, dim], got {tuple(x.shape)}")
+            w, bias = self.qkv_weight()
+            qkv = F.linear(x, w, bias).view(x.shape[0], 3, self.num_heads, self.head_dim)
+            out = flash_spacetime_attention_qkv(qkv, feats, self.rel_proj.weight, self.rel_proj.bias, None, None,
+                                                *flags, cu_seqlens=cu_seqlens)
+            return self.proj(out.reshape(x.shape[0], -1))
+        b, length, _ = x.shape
         if kv is None:
             w, bias = self.qkv_weight()
             qkv = F.linear(x, w, bias).view(b, length, 3, self.num_heads, self.head_dim)
