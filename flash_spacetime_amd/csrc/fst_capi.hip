@@ -200,6 +200,13 @@ static int check_common(int dtype, int flags, int B, int H, int L, int T, int D,
   if (H < 1 || H > 16) return fail(FST_EUNSUPPORTED, "heads must be in [1, 16], got %d", H);
   if (!supported_dim(D)) return fail(FST_EUNSUPPORTED, "head_dim D must be one of 16, 32, 48, 64, got %d", D);
   if (!supported_dim(C)) return fail(FST_EUNSUPPORTED, "channel count C must be one of 16, 32, 48, 64, got %d", C);
+  // The kernels address one event's rows with 32-bit byte offsets (buffer
+  // loads over the event's span): a padded event's rows of every head must
+  // span less than 2 GiB. Packed events are bounded by the caller (the
+  // lengths live on the device).
+  const long long span = (long long)L * H * D * (dtype == FST_BF16 ? 2 : 4) * ((flags & FST_QKV_INTERLEAVED) ? 3 : 1);
+  if (!(flags & FST_PACKED) && span >= (1LL << 31))
+    return fail(FST_EUNSUPPORTED, "one padded event spans %lld bytes; the kernels address at most 2^31 - 1", span);
   return FST_OK;
 }
 

@@ -28,7 +28,10 @@
  *   dbias, rowsum are float32 in both.
  *
  * Supported shapes: 1 <= H <= 16, D in {16, 32, 48, 64}, C in {16, 32, 48,
- * 64} (C even, sin/cos halves); see fst_supported().
+ * 64} (C even, sin/cos halves); see fst_supported(). One event's rows of all
+ * heads (times 3 with FST_QKV_INTERLEAVED) must span less than 2 GiB: the
+ * kernels address them with 32-bit byte offsets. Padded calls beyond that
+ * return FST_EUNSUPPORTED; packed events are the caller's to bound.
  *
  * Return value: 0 on success, a negative FST_E* code otherwise; the message
  * of the last failure on the calling thread is in fst_last_error().

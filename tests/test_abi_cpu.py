@@ -109,6 +109,10 @@ def test_argument_errors_are_reported_before_any_launch():
     assert rc == _lib.FST_EINVAL and "TOKEN_MAJOR" in _lib.last_error()
     assert lib.fst_backward_workspace_bytes(_lib.FST_BF16, 3 | _lib.FST_TOKEN_MAJOR, 256, 12, 768, 0, 32, 16) == \
         lib.fst_backward_workspace_bytes(_lib.FST_BF16, 3, 256, 12, 768, 0, 32, 16)
+    # one padded event past 2 GiB (the kernels' 32-bit offsets) is refused
+    rc = lib.fst_forward(0, 3, 1, 16, 1 << 20, 0, 64, 16, None, None, None, None, None, None, None, 1.0,
+                         None, None, None, 0, None)
+    assert rc == _lib.FST_EUNSUPPORTED and "2^31" in _lib.last_error()
     # empty problems are valid no-ops
     assert lib.fst_forward(0, 3, 0, 4, 8, 0, 32, 16, None, None, None, None, None, None, None, 1.0,
                            None, None, None, 0, None) == _lib.FST_OK
