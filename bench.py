@@ -14,7 +14,8 @@ times of the individual launches, the MFMA roofline of the dominant kernel,
 and the CPU baseline (the oracle's eager restatement of the spec, fp32,
 fwd+bwd, timed on this host's cores on a bounded sample of events).
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload cfg2|cfg1|cfg3|cfg4|cfg4-fp32|cfg2-model|lscale]
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--autotune]
+       [--workload cfg2|cfg1|cfg3|cfg4|cfg4-fp32|cfg2-model|lscale|plans]
 """
 
 from __future__ import annotations
@@ -82,18 +83,37 @@ def time_events(fn, iters, stream):
     return start.elapsed_time(end) / iters
 
 
-def kernel_times(inp, seqlens, iters=10, cu=None):
+def current_plan():
+    """FST_PLAN_* bits the operators ran with: the tuner's choices (one forward
+    and one backward entry per workload), 0 for the library's static plan."""
+    from flash_spacetime_amd import tune
+
+    plan = 0
+    for bits in tune.chosen().values():
+        plan |= bits
+    return plan
+
+
+def plan_label(plan):
+    from flash_spacetime_amd import tune
+
+    return tune.plan_names(plan) if plan else "static"
+
+
+def kernel_times(inp, seqlens, iters=10, cu=None, plan=0, flags=(True, True)):
     """Average duration of each launch, timed with HIP events on the stream the
-    library launches on (torch's current stream), one phase at a time."""
+    library launches on (torch's current stream), one phase at a time, with
+    the FST_PLAN_* bits `plan` (0: the library's static choice)."""
     from flash_spacetime_amd import _lib
     from flash_spacetime_amd.forward import _Prepared
 
     lib = _lib.load()
     dev = inp["q"].device
     prep = _Prepared(inp["q"], inp["k"], inp["v"], inp["feats"], inp["w"], inp["b"], seqlens, None,
-                     True, True, cu)
+                     flags[0], flags[1], cu)
     d_, c_ = inp["w"].shape
     dims = prep.dims()
+    dims = (dims[0], dims[1] | plan) + tuple(dims[2:])
     stream = torch.cuda.current_stream(dev)
     sh = stream.cuda_stream
     out = torch.empty_like(prep.q)
@@ -204,6 +224,8 @@ WORKLOADS = {
             "lengths U{16..768} (bool key_padding_mask -> seqlens once), W/b fp32",
     "lscale": "configs[2] at L = 384, 768, 1536: flash_spacetime_attention fwd+bwd, B=256 H=12 D=32 C=16 "
               "bf16, lengths U{16..L}",
+    "plans": "per-kernel times of every compiled FST_PLAN_* variant against the static choice, bf16, "
+             "cfg2, cfg3 and ten other head layouts",
     "cfg2-model": "SpacetimeAttention fwd+bwd (fused QKV linear, flash_spacetime_attention_qkv, output "
                   "linear) at cfg2 sizes: x [256, 768, 384] bf16, H=12 D=32 C=16, lengths U{16..768}",
 }
@@ -414,7 +436,8 @@ def run_other_workload(name, steps, warmup):
     ms = time_events(step, steps, stream)
     torch.cuda.synchronize(dev)
     inp = dict(q=q, k=k, v=v, feats=feats, w=w, b=bias, do=do)
-    kt = kernel_times(inp, seqlens, cu=cu)
+    plan = current_plan()
+    kt = kernel_times(inp, seqlens, cu=cu, plan=plan)
     sl2 = float((lens.double() ** 2).sum())
     f_total = h * sl2 * (4 * (d + c) + 10 * d + 8 * c)
     peak = PEAK_BF16_TFLOPS if dtype == torch.bfloat16 else 157.3
@@ -424,9 +447,85 @@ def run_other_workload(name, steps, warmup):
         "scaling": "weak", "vs_baseline": None, "dtype": "bf16" if dtype == torch.bfloat16 else "fp32",
         "data": "synthetic (seeded; BASELINE.json distributions)",
         "config": {"workload": WORKLOADS[name], "valid_pairs": sl2},
+        "plan": plan_label(plan),
         "mfma_pct_of_peak": round(100.0 * f_total / (ms * 1e-3) / (peak * 1e12), 3),
         "algorithmic_tflop": round(f_total / 1e12, 4),
         "kernels_ms": {k_: round(v_, 4) for k_, v_ in kt.items()},
+    }), flush=True)
+
+
+PLAN_SHAPES = [
+    # (name, H, D, C, B, L or None for cfg3's packed events, (use_attn_bias, use_activation_bias))
+    ("cfg2", 12, 32, 16, 256, 768, (True, True)),
+    ("cfg2, use_activation_bias=False", 12, 32, 16, 256, 768, (True, False)),
+    ("cfg2, B=16", 12, 32, 16, 16, 768, (True, True)),
+    ("cfg3", 12, 32, 16, 4096, None, (True, True)),
+    ("H=8 D=32 C=16", 8, 32, 16, 128, 1024, (True, True)),
+    ("H=16 D=16 C=16", 16, 16, 16, 128, 1024, (True, True)),
+    ("H=4 D=64 C=16", 4, 64, 16, 256, 512, (True, True)),
+    ("H=8 D=16 C=32", 8, 16, 32, 128, 1024, (True, True)),
+    ("H=12 D=16 C=32", 12, 16, 32, 128, 768, (True, True)),
+    ("H=4 D=32 C=32", 4, 32, 32, 256, 768, (True, True)),
+    ("H=8 D=48 C=16", 8, 48, 16, 128, 768, (True, True)),
+    ("H=8 D=64 C=64", 8, 64, 64, 64, 1024, (True, True)),
+]
+
+
+def run_plan_sweep(steps, warmup):
+    """Per-kernel times (ms) of every compiled variant (FST_PLAN_*) of the
+    forward, rows and cols kernels, and of the library's static choice, over
+    bf16 shapes with lengths U{16..L} (cfg3: its packed lognormal events)."""
+    import math
+
+    from flash_spacetime_amd import _lib, tune
+
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    lib = _lib.load()
+    gen = torch.Generator().manual_seed(11)
+    names = {_lib.FST_PLAN_FWD_OCC2: "occ2", _lib.FST_PLAN_FWD_OCC3: "occ3", _lib.FST_PLAN_ROWS_W4: "w4",
+             _lib.FST_PLAN_ROWS_W8: "w8", _lib.FST_PLAN_COLS_OCC2: "occ2", _lib.FST_PLAN_COLS_OCC3: "occ3"}
+    rows_out = []
+    for name, h, d, c, bsz, length, flags in PLAN_SHAPES:
+        rn = lambda *s_: torch.randn(*s_, generator=gen)  # noqa: E731
+        if length is None:
+            lens = torch.exp(5.0 + torch.randn(bsz, generator=gen, dtype=torch.float64)).round().clamp(1, 3000).long()
+            lens[torch.randperm(bsz, generator=gen)[: math.ceil(0.01 * bsz)]] = 1
+            total = int(lens.sum())
+            shape, fshape = (total, h, d), (total,)
+            cu = torch.zeros(bsz + 1, dtype=torch.int32)
+            cu[1:] = torch.cumsum(lens, 0)
+            cu, seqlens = cu.to(dev), None
+        else:
+            lens = torch.randint(16, length + 1, (bsz,), generator=gen)
+            shape, fshape = (bsz, h, length, d), (bsz, length)
+            cu, seqlens = None, lens.to(dev, torch.int32)
+        inp = {n_: rn(*shape).to(dev, torch.bfloat16) for n_ in ("q", "k", "v", "do")}
+        inp["feats"] = torch.cat([(torch.rand(*fshape, 3, generator=gen) - 0.5) * 1000.0,
+                                  torch.rand(*fshape, 1, generator=gen) * 2e4], -1).to(dev)
+        inp["w"] = (rn(d, c) / c ** 0.5).to(dev)
+        inp["b"] = (rn(d) * 0.02).to(dev)
+        mask = lib.fst_plans(_lib.FST_BF16, h, d, c)
+        groups = {"fwd": [b_ for b_ in (_lib.FST_PLAN_FWD_OCC2, _lib.FST_PLAN_FWD_OCC3) if mask & b_],
+                  "bwd_rows": [b_ for b_ in (_lib.FST_PLAN_ROWS_W4, _lib.FST_PLAN_ROWS_W8) if mask & b_],
+                  "bwd_cols": [b_ for b_ in (_lib.FST_PLAN_COLS_OCC2, _lib.FST_PLAN_COLS_OCC3) if mask & b_]}
+        n_var = max(len(g_) for g_ in groups.values())
+        best = {k_: {} for k_ in groups}
+        for _ in range(2):  # two interleaved rounds; the minimum of each is kept
+            for i in range(-1, n_var):
+                plan = 0 if i < 0 else sum(g_[i % len(g_)] for g_ in groups.values())
+                kt = kernel_times(inp, seqlens, iters=max(steps // 2, 5), cu=cu, plan=plan, flags=flags)
+                for k_, g_ in groups.items():
+                    label = "static" if i < 0 else names[g_[i % len(g_)]]
+                    best[k_][label] = min(best[k_].get(label, float("inf")), kt[k_])
+        rows_out.append({"shape": name, "plans": tune.plan_names(mask),
+                         **{k_: {l_: round(t_, 4) for l_, t_ in v_.items()} for k_, v_ in best.items()}})
+        del inp
+        torch.cuda.empty_cache()
+    print(json.dumps({
+        "metric": "per-kernel ms of each compiled plan variant", "unit": "ms", "n_gpus": 1, "dtype": "bf16",
+        "higher_is_better": False, "data": "synthetic (seeded)",
+        "config": {"workload": WORKLOADS["plans"]}, "by_shape": rows_out,
     }), flush=True)
 
 
@@ -442,7 +541,14 @@ def main():
                          "that rocprof counter runs use to scale FETCH_SIZE / WRITE_SIZE")
     ap.add_argument("--workload", default="cfg2", choices=["cfg2", *WORKLOADS],
                     help="cfg2 (default) is the metric's configuration; the others print a line of their own")
+    ap.add_argument("--autotune", action="store_true",
+                    help="time the compiled kernel variants of each shape on its first call (a warm-up "
+                         "step) and run the fastest; without it the library's static choice runs")
     args = ap.parse_args()
+    if args.autotune:
+        from flash_spacetime_amd import tune
+
+        tune.set_autotune(True)
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this build's hot path is single-device (events are independent; "
               f"multi-GPU would shard events with no exchange). --gpus {args.gpus} is not run.", file=sys.stderr)
@@ -450,6 +556,9 @@ def main():
 
     if args.workload == "cfg2-model":
         run_model_workload(args.steps, args.warmup)
+        return
+    if args.workload == "plans":
+        run_plan_sweep(args.steps, args.warmup)
         return
     if args.workload == "cfg1":
         run_forward_only(args.steps, args.warmup)
@@ -493,7 +602,8 @@ def main():
     peak_gib = (torch.cuda.max_memory_allocated(dev) - base) / 2 ** 30
 
     flops = flop_counts(inp["lengths"])
-    kt = kernel_times(inp, seqlens)
+    plan = current_plan()
+    kt = kernel_times(inp, seqlens, plan=plan)
     f_total = flops["fwd"] + flops["bwd_rows"] + flops["bwd_cols"]
     mfma_pct = 100.0 * f_total / (ms * 1e-3) / (PEAK_BF16_TFLOPS * 1e12)
     dominant = max(("fwd", "bwd_rows", "bwd_cols"), key=lambda k_: kt[k_])
@@ -517,6 +627,7 @@ def main():
             "B": B, "L": L, "H": H, "D": D, "C": C,
             "valid_pairs": flops["sum_l2"],
         },
+        "plan": plan_label(plan),
         "peak_gib": round(peak_gib, 4),
         "mfma_pct_of_peak": round(mfma_pct, 3),
         "algorithmic_tflop": round(f_total / 1e12, 4),

@@ -22,6 +22,13 @@ FST_ACT_BIAS = 2
 FST_PACKED = 4
 FST_TOKEN_MAJOR = 8
 FST_QKV_INTERLEAVED = 16
+FST_PLAN_FWD_OCC2 = 1 << 8
+FST_PLAN_FWD_OCC3 = 1 << 9
+FST_PLAN_ROWS_W4 = 1 << 10
+FST_PLAN_ROWS_W8 = 1 << 11
+FST_PLAN_COLS_OCC2 = 1 << 12
+FST_PLAN_COLS_OCC3 = 1 << 13
+FST_PLAN_MASK = 0x3F00
 
 FST_PHASE_WORKLIST = 1
 FST_PHASE_FWD = 2
@@ -41,6 +48,7 @@ FST_ELAUNCH = -4
 _vp, _i, _f, _sz = ctypes.c_void_p, ctypes.c_int, ctypes.c_float, ctypes.c_size_t
 SIGNATURES = {
     "fst_supported": (_i, [_i, _i, _i, _i]),
+    "fst_plans": (_i, [_i, _i, _i, _i]),
     "fst_forward_workspace_bytes": (_sz, [_i, _i, _i, _i, _i, _i, _i, _i]),
     "fst_forward": (
         _i,

@@ -16,7 +16,7 @@ from typing import Optional, Tuple
 import torch
 from torch import Tensor
 
-from . import _lib
+from . import _lib, tune
 from .forward import _Prepared, _vec_in_layout
 
 
@@ -68,14 +68,19 @@ def _run_backward(dims, q, k, v, pos4, w32, b32, lens, lse, grad_out, scale, vec
     db = torch.empty(q.shape[-1], device=q.device, dtype=torch.float32) if b32 is not None else None
     ws_bytes = lib.fst_backward_workspace_bytes(*dims)
     ws = torch.empty(max(ws_bytes, 1), device=q.device, dtype=torch.uint8)
-    with torch.cuda.device(q.device):
-        rc = lib.fst_backward(
-            *dims,
+
+    def run(phases: int, flags: int) -> int:
+        return lib.fst_backward_phases(
+            phases, dims[0], flags, *dims[2:],
             _lib.ptr(q), _lib.ptr(k), _lib.ptr(v), _lib.ptr(pos4), _lib.ptr(w32), _lib.ptr(b32),
             _lib.ptr(lens), _lib.ptr(lse), _lib.ptr(do), scale,
             _lib.ptr(dq), _lib.ptr(dk), _lib.ptr(dv), _lib.ptr(dw), _lib.ptr(db), _lib.ptr(rs),
             _lib.ptr(ws), ws_bytes, _lib.stream_handle(q.device),
         )
+
+    with torch.cuda.device(q.device):
+        plan = tune.backward_plan(dims, run)
+        rc = run(_lib.FST_BWD_ALL, dims[1] | plan)
     _lib.check(rc, "flash_spacetime_backward")
     if rs is not rowsum:
         rowsum.copy_(rs)

@@ -635,8 +635,8 @@ struct Cols2Cfg {
 };
 
 
-template <int HP, int D, int C, int RC, int FL>
-__global__ __launch_bounds__(256, (Cols2Cfg<HP, D, C, RC>::OCC)) void bwd_cols2_kernel(BwdParams prm) {
+template <int HP, int D, int C, int RC, int FL, int OCC>
+__global__ __launch_bounds__(256, OCC) void bwd_cols2_kernel(BwdParams prm) {
   using Cfg = Cols2Cfg<HP, D, C, RC>;
   using DT = DTiles<D>;
   constexpr int HW = Cfg::HW, NS = Cfg::NS, NCT = Cfg::NCT, NQ = DT::NQ, RGW = Cfg::RGW;
@@ -989,32 +989,86 @@ struct Bwd2Pick {
   // eight-wave ones fit (spills remain only at HP = 16 with D, C >= 48).
   static constexpr int NW = (HP % 8 == 0 && rows_wave_load(HP, D, C) >= 160) ? 8 : 4;
   static constexpr bool OK = Rows2Cfg<HP, D, C, KC, NW>::FITS && Cols2Cfg<HP, D, C, RC>::FITS;
+  // Variants a caller may choose instead (FST_PLAN_ROWS_W4 / _W8,
+  // FST_PLAN_COLS_OCC2 / _OCC3); each computes every row with the same
+  // arithmetic. The rows kernel at HP heads offers four waves below the
+  // spilling load and eight where HP is a multiple of 8 (the library pads
+  // heads to 8 for that plan); the cols kernel offers three workgroups per CU
+  // where its LDS plan fits a third of the CU and the lane state is that of
+  // the small layouts ((HP / 4) D + 3 C < 160).
+  static constexpr bool ROWS_W4 = Rows2Cfg<HP, D, C, KC, 4>::FITS && rows_wave_load(HP, D, C) < 160;
+  static constexpr bool ROWS_W8 = HP % 8 == 0 && Rows2Cfg<HP, D, C, KC, 8>::FITS;
+  using CC = Cols2Cfg<HP, D, C, RC>;
+  static constexpr bool COLS_OCC3 = CC::FITS && CC::LDS_BYTES <= 160 * 1024 / 3 && rows_wave_load(HP, D, C) < 160;
+  static constexpr int COLS_PLANS = CC::FITS ? (FST_PLAN_COLS_OCC2 | (COLS_OCC3 ? FST_PLAN_COLS_OCC3 : 0)) : 0;
 };
 
+template <int HP, int D, int C, int NW>
+int bwd2_launch_rows(const BwdParams& prm, hipStream_t stream, int g8) {
+  using P = Bwd2Pick<HP, D, C>;
+  using Cfg = Rows2Cfg<HP, D, C, P::KC, NW>;
+  if constexpr (!Cfg::FITS) {
+    return FST_EUNSUPPORTED;
+  } else {
+    auto kern = (prm.flags & 3) == 3 ? bwd_rows2_kernel<HP, D, C, P::KC, P::HB, 3, NW>
+                                     : bwd_rows2_kernel<HP, D, C, P::KC, P::HB, -1, NW>;
+    if (hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, Cfg::LDS_BYTES) !=
+        hipSuccess)
+      return FST_ELAUNCH;
+    if (g8 > 0) hipLaunchKernelGGL(kern, dim3(g8), dim3(64 * NW), Cfg::LDS_BYTES, stream, prm);
+    return hipGetLastError() == hipSuccess ? FST_OK : FST_ELAUNCH;
+  }
+}
+
+template <int HP, int D, int C, int OCC>
+int bwd2_launch_cols(const BwdParams& prm, hipStream_t stream, int g8) {
+  using P = Bwd2Pick<HP, D, C>;
+  using Cfg = Cols2Cfg<HP, D, C, P::RC>;
+  auto kern = (prm.flags & 3) == 3 ? bwd_cols2_kernel<HP, D, C, P::RC, 3, OCC>
+                                   : bwd_cols2_kernel<HP, D, C, P::RC, -1, OCC>;
+  if (hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, Cfg::LDS_BYTES) !=
+      hipSuccess)
+    return FST_ELAUNCH;
+  if (g8 > 0) hipLaunchKernelGGL(kern, dim3(g8), dim3(256), Cfg::LDS_BYTES, stream, prm);
+  return hipGetLastError() == hipSuccess ? FST_OK : FST_ELAUNCH;
+}
+
+// Launches the rows (which = 0) or cols (which = 1) kernel. For the rows
+// kernel HP is the rows head padding, which the library rounds to a multiple
+// of 8 when the eight-wave plan (static or chosen) runs.
 template <int HP, int D, int C>
 int bwd2_launch_t(const BwdParams& prm, int which, hipStream_t stream, int grid) {
   using P = Bwd2Pick<HP, D, C>;
-  if constexpr (!P::OK) {
+  // The grid is rounded up to a multiple of 64 for the XCD schedules
+  // (tile_block); logical blocks past the work list exit at once.
+  const int g8 = grid > 0 ? (grid + 63) & ~63 : 0;
+  if (which == 0) {
+    // The plan bits were checked against the shape's plans by the caller.
+    const int nw = (prm.flags & FST_PLAN_ROWS_W8) ? 8 : (prm.flags & FST_PLAN_ROWS_W4) ? 4 : P::NW;
+    if (nw == 8) {
+      if constexpr (P::ROWS_W8) return bwd2_launch_rows<HP, D, C, 8>(prm, stream, g8);
+      return FST_EUNSUPPORTED;
+    }
+    // Four waves run where they fit without spilling; elsewhere the library
+    // pads the heads to a multiple of 8 and runs eight (rows_head_padding).
+    if constexpr (P::ROWS_W4) return bwd2_launch_rows<HP, D, C, 4>(prm, stream, g8);
+    return FST_EUNSUPPORTED;
+  }
+  if constexpr (!P::CC::FITS) {
     return FST_EUNSUPPORTED;
   } else {
-    // The grid is rounded up to a multiple of 64 for the XCD schedules
-    // (tile_block); logical blocks past the work list exit at once.
-    const int g8 = (grid + 63) & ~63;
-    if (which == 0) {
-      auto kern = (prm.flags & 3) == 3 ? bwd_rows2_kernel<HP, D, C, P::KC, P::HB, 3, P::NW>
-                                       : bwd_rows2_kernel<HP, D, C, P::KC, P::HB, -1, P::NW>;
-      constexpr int lds = Rows2Cfg<HP, D, C, P::KC, P::NW>::LDS_BYTES;
-      if (hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, lds) != hipSuccess)
-        return FST_ELAUNCH;
-      if (grid > 0) hipLaunchKernelGGL(kern, dim3(g8), dim3(64 * P::NW), lds, stream, prm);
-    } else {
-      auto kern = (prm.flags & 3) == 3 ? bwd_cols2_kernel<HP, D, C, P::RC, 3> : bwd_cols2_kernel<HP, D, C, P::RC, -1>;
-      constexpr int lds = Cols2Cfg<HP, D, C, P::RC>::LDS_BYTES;
-      if (hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, lds) != hipSuccess)
-        return FST_ELAUNCH;
-      if (grid > 0) hipLaunchKernelGGL(kern, dim3(g8), dim3(256), lds, stream, prm);
+    // Static choice: Cols2Cfg::OCC for the compile-time bias flags; two
+    // workgroups per CU for the run-time-flag instance, which keeps both bias
+    // paths live and spills at three (cfg2's layout: 1.13 -> 0.72 ms).
+    const int occ = (prm.flags & FST_PLAN_COLS_OCC2)   ? 2
+                    : (prm.flags & FST_PLAN_COLS_OCC3) ? 3
+                    : (prm.flags & 3) == 3             ? P::CC::OCC
+                                                       : 2;
+    if (occ == 3) {
+      if constexpr (P::COLS_OCC3 || P::CC::OCC == 3) return bwd2_launch_cols<HP, D, C, 3>(prm, stream, g8);
+      return FST_EUNSUPPORTED;
     }
-    return hipGetLastError() == hipSuccess ? FST_OK : FST_ELAUNCH;
+    return bwd2_launch_cols<HP, D, C, 2>(prm, stream, g8);
   }
 }
 

@@ -40,4 +40,37 @@ int FST_CAT(bwd_dispatch_, FST_NAME)(const BwdParams& prm, int which, int HP, in
   return FST_EUNSUPPORTED;
 }
 
+// FST_PLAN_ROWS_* / FST_PLAN_COLS_* bits compiled for head padding HP and C
+// channels. The eight-wave rows plan runs at HP rounded up to a multiple of 8.
+template <int HP, int C>
+static int bwd_plans_at() {
+  if constexpr (!is_bf16<FST_T>::value) {
+    return 0;
+  } else {
+    using P = Bwd2Pick<HP, FST_D, C>;
+    if constexpr (!P::OK) {
+      return 0;
+    } else {
+      constexpr int HP8 = (HP + 7) / 8 * 8;
+      int plans = P::COLS_PLANS;
+      if constexpr (P::ROWS_W4) plans |= FST_PLAN_ROWS_W4;
+      if constexpr (Bwd2Pick<HP8, FST_D, C>::OK && Bwd2Pick<HP8, FST_D, C>::ROWS_W8) plans |= FST_PLAN_ROWS_W8;
+      return plans;
+    }
+  }
+}
+
+int FST_CAT(bwd_plans_, FST_NAME)(int HP, int C) {
+#define FST_CASE(HPV, CV) \
+  if (HP == HPV && C == CV) return bwd_plans_at<HPV, CV>();
+#define FST_CASES(HPV) FST_CASE(HPV, 16) FST_CASE(HPV, 32) FST_CASE(HPV, 48) FST_CASE(HPV, 64)
+  FST_CASES(4)
+  FST_CASES(8)
+  FST_CASES(12)
+  FST_CASES(16)
+#undef FST_CASES
+#undef FST_CASE
+  return 0;
+}
+
 }  // namespace fst

@@ -32,9 +32,14 @@ static int head_padding(int H) { return H <= 4 ? 4 : (H <= 8 ? 8 : (H <= 12 ? 12
 // spill, heads are padded to the next multiple of 8 so that it runs eight
 // waves (padded heads compute on a real head's data and store nothing). The
 // cols kernel keeps head_padding: the scratch between them is laid out by H.
-static int rows_head_padding(int dtype, int H, int D, int C) {
+// The eight-wave plan (FST_PLAN_ROWS_W8) pads to a multiple of 8 likewise;
+// the four-wave plan keeps head_padding.
+static int rows_head_padding(int dtype, int flags, int H, int D, int C) {
   const int hp = head_padding(H);
-  if (dtype == FST_BF16 && hp % 8 != 0 && rows_wave_load(hp, D, C) >= 160) return hp + 4;
+  if (dtype != FST_BF16) return hp;
+  if (flags & FST_PLAN_ROWS_W8) return (hp + 7) & ~7;
+  if (flags & FST_PLAN_ROWS_W4) return hp;
+  if (hp % 8 != 0 && rows_wave_load(hp, D, C) >= 160) return hp + 4;
   return hp;
 }
 
@@ -188,10 +193,28 @@ static fwd_dispatch_fn fwd_table(int dtype, int D) {
   return nullptr;
 }
 
+typedef int (*plans_fn)(int, int);
+
+static int shape_plans(int dtype, int H, int D, int C) {
+  plans_fn f = nullptr, b = nullptr;
+  if (dtype == FST_BF16) {
+    switch (D) {
+      case 16: f = fwd_plans_bf16_16; b = bwd_plans_bf16_16; break;
+      case 32: f = fwd_plans_bf16_32; b = bwd_plans_bf16_32; break;
+      case 48: f = fwd_plans_bf16_48; b = bwd_plans_bf16_48; break;
+      case 64: f = fwd_plans_bf16_64; b = bwd_plans_bf16_64; break;
+    }
+  }
+  if (!f || H < 1 || H > 16) return 0;
+  return f(head_padding(H), C) | b(head_padding(H), C);
+}
+
 static int check_common(int dtype, int flags, int B, int H, int L, int T, int D, int C) {
   if (dtype != FST_BF16 && dtype != FST_F32) return fail(FST_EINVAL, "dtype must be FST_BF16 or FST_F32, got %d", dtype);
-  if (flags & ~(FST_ATTN_BIAS | FST_ACT_BIAS | FST_PACKED | FST_TOKEN_MAJOR | FST_QKV_INTERLEAVED))
+  if (flags & ~(FST_ATTN_BIAS | FST_ACT_BIAS | FST_PACKED | FST_TOKEN_MAJOR | FST_QKV_INTERLEAVED | FST_PLAN_MASK))
     return fail(FST_EINVAL, "unknown flag bits 0x%x", flags);
+  for (int pair = FST_PLAN_FWD_OCC2 | FST_PLAN_FWD_OCC3; pair & FST_PLAN_MASK; pair <<= 2)
+    if ((flags & pair) == pair) return fail(FST_EINVAL, "plan bits 0x%x name two variants of one kernel", flags & pair);
   if ((flags & FST_QKV_INTERLEAVED) && !(flags & (FST_PACKED | FST_TOKEN_MAJOR)))
     return fail(FST_EINVAL, "FST_QKV_INTERLEAVED needs a token-major layout (FST_PACKED or FST_TOKEN_MAJOR)");
   if ((flags & FST_PACKED) && (flags & FST_TOKEN_MAJOR))
@@ -207,6 +230,10 @@ static int check_common(int dtype, int flags, int B, int H, int L, int T, int D,
   const long long span = (long long)L * H * D * (dtype == FST_BF16 ? 2 : 4) * ((flags & FST_QKV_INTERLEAVED) ? 3 : 1);
   if (!(flags & FST_PACKED) && span >= (1LL << 31))
     return fail(FST_EUNSUPPORTED, "one padded event spans %lld bytes; the kernels address at most 2^31 - 1", span);
+  const int plan = flags & FST_PLAN_MASK;
+  if (plan & ~shape_plans(dtype, H, D, C))
+    return fail(FST_EUNSUPPORTED, "plan bits 0x%x are not compiled for dtype %d, H=%d, D=%d, C=%d", plan, dtype, H, D,
+                C);
   return FST_OK;
 }
 
@@ -292,7 +319,7 @@ static int bwd_layout(int dtype, int flags, int B, int H, int L, int T, int D, i
   bwd_dispatch_fn fn = bwd_table(dtype, D);
   BwdParams dummy;
   std::memset(&dummy, 0, sizeof(dummy));
-  const int HP = head_padding(H), HPR = rows_head_padding(dtype, H, D, C);
+  const int HP = head_padding(H), HPR = rows_head_padding(dtype, flags, H, D, C);
   if (fn(dummy, 0, HPR, C, nullptr, 0, true, &lay.rows_r) != FST_OK || lay.rows_r <= 0) return FST_EUNSUPPORTED;
   if (fn(dummy, 1, HP, C, nullptr, 0, true, &lay.rows_c) != FST_OK || lay.rows_c <= 0) return FST_EUNSUPPORTED;
   const bool packed = flags & FST_PACKED;
@@ -340,6 +367,11 @@ const char* fst_version(void) { return "flash-spacetime-gfx950 0.1.0"; }
 
 void fst_frequencies(int C, float* out) {
   if (C > 0 && C <= 64 && C % 2 == 0 && out) frequencies(C, out);
+}
+
+int fst_plans(int dtype, int H, int D, int C) {
+  if (check_common(dtype, 0, 0, H, 0, 0, D, C) != FST_OK) return 0;
+  return shape_plans(dtype, H, D, C);
 }
 
 int fst_supported(int dtype, int H, int D, int C) {
@@ -550,7 +582,7 @@ int fst_backward_phases(int phases, int dtype, int flags, int B, int H, int L, i
   freq_table(C, prm.freq);
 
   bwd_dispatch_fn fn = bwd_table(dtype, D);
-  const int HP = head_padding(H), HPR = rows_head_padding(dtype, H, D, C);
+  const int HP = head_padding(H), HPR = rows_head_padding(dtype, flags, H, D, C);
   int dummy_rows = 0;
   if (phases & FST_PHASE_BWD_ROWS) {
     rc = fn(prm, 0, HPR, C, st, (int)lay.grid_r, false, &dummy_rows);

@@ -478,16 +478,45 @@ __global__ __launch_bounds__(256, OCC) void fwd2_kernel(FwdParams prm) {
 
 template <int HP, int D, int C>
 struct Fwd2Pick {
-  // Small head layouts (HP <= 12, D <= 32, C = 16) run 16-key chunks at three
-  // workgroups per CU: measured faster than 32-key chunks at two, the extra
-  // waves hiding more latency than the shorter chunks cost. Larger layouts
-  // run two workgroups per CU with 16-key chunks.
-  static constexpr bool SMALL = HP <= 12 && D <= 32 && C <= 16;
   static constexpr int KC = 16;
-  static constexpr int OCC = SMALL ? 3 : 2;
+  // Three workgroups per CU where the LDS plan fits a third of the CU and the
+  // lane state stays near the 168 registers of that budget ((HP / 4) D + 3 C
+  // < 160: beyond it the instances spill); two otherwise. Measured on the
+  // small layouts, the extra waves hide more latency than the smaller LDS
+  // share costs (16-key chunks at three beat 32-key chunks at two), and at
+  // the other layouts three is as fast or faster (HP = 16, D = C = 16: -23 %;
+  // HP = 12, D = 16, C = 32: -19 %).
+  static constexpr bool OCC3 = Fwd2Cfg<HP, D, C, KC, 3>::FITS && rows_wave_load(HP, D, C) < 160;
+  static constexpr bool OCC2 = Fwd2Cfg<HP, D, C, KC, 2>::FITS;
+  static constexpr int OCC = OCC3 ? 3 : 2;
   using Cfg = Fwd2Cfg<HP, D, C, KC, OCC>;
   static constexpr bool OK = Cfg::FITS;
+  // Either occupancy may be chosen instead (FST_PLAN_FWD_OCC2 / _OCC3) where
+  // it exists: both compute every row with the same arithmetic, only the
+  // register and LDS budget differs.
+  static constexpr int PLANS = OK ? ((OCC2 ? FST_PLAN_FWD_OCC2 : 0) | (OCC3 ? FST_PLAN_FWD_OCC3 : 0)) : 0;
 };
+
+template <int HP, int D, int C, int OCC>
+int fwd2_launch_occ(const FwdParams& prm, hipStream_t stream, int grid) {
+  using P = Fwd2Pick<HP, D, C>;
+  using Cfg = Fwd2Cfg<HP, D, C, P::KC, OCC>;
+  if constexpr (!Cfg::FITS) {
+    return FST_EUNSUPPORTED;
+  } else {
+    // Both bias flags (the operators' default) run an instance with the flags
+    // fixed at compile time; other combinations read them at run time.
+    auto kern = (prm.flags & 3) == 3 ? fwd2_kernel<HP, D, C, P::KC, OCC, 3> : fwd2_kernel<HP, D, C, P::KC, OCC, -1>;
+    if (hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, Cfg::LDS_BYTES) !=
+        hipSuccess)
+      return FST_ELAUNCH;
+    // The grid is rounded up to a multiple of 64 for the XCD schedules
+    // (tile_block); logical blocks past the work list exit at once.
+    const int g8 = (grid + 63) & ~63;
+    if (grid > 0) hipLaunchKernelGGL(kern, dim3(g8), dim3(256), Cfg::LDS_BYTES, stream, prm);
+    return hipGetLastError() == hipSuccess ? FST_OK : FST_ELAUNCH;
+  }
+}
 
 template <int HP, int D, int C>
 int fwd2_launch_t(const FwdParams& prm, hipStream_t stream, int grid) {
@@ -495,17 +524,14 @@ int fwd2_launch_t(const FwdParams& prm, hipStream_t stream, int grid) {
   if constexpr (!P::OK) {
     return FST_EUNSUPPORTED;
   } else {
-    // Both bias flags (the operators' default) run an instance with the flags
-    // fixed at compile time; other combinations read them at run time.
-    auto kern = (prm.flags & 3) == 3 ? fwd2_kernel<HP, D, C, P::KC, P::OCC, 3> : fwd2_kernel<HP, D, C, P::KC, P::OCC, -1>;
-    if (hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, P::Cfg::LDS_BYTES) !=
-        hipSuccess)
-      return FST_ELAUNCH;
-    // The grid is rounded up to a multiple of 64 for the XCD schedules
-    // (tile_block); logical blocks past the work list exit at once.
-    const int g8 = (grid + 63) & ~63;
-    if (grid > 0) hipLaunchKernelGGL(kern, dim3(g8), dim3(256), P::Cfg::LDS_BYTES, stream, prm);
-    return hipGetLastError() == hipSuccess ? FST_OK : FST_ELAUNCH;
+    // The plan bits were checked against P::PLANS by the caller.
+    const int occ = (prm.flags & FST_PLAN_FWD_OCC2) ? 2 : (prm.flags & FST_PLAN_FWD_OCC3) ? 3 : P::OCC;
+    if (occ == 3) {
+      if constexpr (P::OCC3) return fwd2_launch_occ<HP, D, C, 3>(prm, stream, grid);
+      return FST_EUNSUPPORTED;
+    }
+    if constexpr (P::OCC2) return fwd2_launch_occ<HP, D, C, 2>(prm, stream, grid);
+    return FST_EUNSUPPORTED;
   }
 }
 

@@ -45,4 +45,21 @@ int FST_CAT(fwd_dispatch_, FST_NAME)(const FwdParams& prm, int HP, int C, hipStr
   return FST_EUNSUPPORTED;
 }
 
+// FST_PLAN_FWD_* bits compiled for head padding HP and C channels.
+int FST_CAT(fwd_plans_, FST_NAME)(int HP, int C) {
+#define FST_CASE(HPV, CV)                                                   \
+  if (HP == HPV && C == CV) {                                               \
+    if constexpr (is_bf16<FST_T>::value) return Fwd2Pick<HPV, FST_D, CV>::PLANS; \
+    return 0;                                                               \
+  }
+#define FST_CASES(HPV) FST_CASE(HPV, 16) FST_CASE(HPV, 32) FST_CASE(HPV, 48) FST_CASE(HPV, 64)
+  FST_CASES(4)
+  FST_CASES(8)
+  FST_CASES(12)
+  FST_CASES(16)
+#undef FST_CASES
+#undef FST_CASE
+  return 0;
+}
+
 }  // namespace fst

@@ -349,8 +349,10 @@ __device__ __forceinline__ void zero_pad_rows(const EventSpec& ev, const EventBl
 // Forward dispatch per (dtype, D), one translation unit each
 // (fst_fwd_inst.hip). With query set, only reports the rows per workgroup
 // of the kernel that (HP, C) selects (0 = unsupported) in *rows.
-#define FST_DECL_FWD(NAME) \
-  int fwd_dispatch_##NAME(const FwdParams& prm, int HP, int C, hipStream_t stream, int grid, bool query, int* rows);
+// fwd_plans_* reports the FST_PLAN_FWD_* bits compiled for (HP, C).
+#define FST_DECL_FWD(NAME)                                                                                       \
+  int fwd_dispatch_##NAME(const FwdParams& prm, int HP, int C, hipStream_t stream, int grid, bool query, int* rows); \
+  int fwd_plans_##NAME(int HP, int C);
 FST_DECL_FWD(bf16_16)
 FST_DECL_FWD(bf16_32)
 FST_DECL_FWD(bf16_48)
@@ -363,10 +365,12 @@ FST_DECL_FWD(f32_64)
 
 // Backward dispatch per (dtype, D) (fst_bwd_inst.hip). which = 0: rows
 // kernel, 1: cols kernel. With query set, reports rows (or keys) per
-// workgroup in *rows (0 = unsupported).
+// workgroup in *rows (0 = unsupported). bwd_plans_* reports the
+// FST_PLAN_ROWS_* / FST_PLAN_COLS_* bits compiled for (HP, C).
 #define FST_DECL_BWD(NAME)                                                                                   \
   int bwd_dispatch_##NAME(const BwdParams& prm, int which, int HP, int C, hipStream_t stream, int grid, bool query, \
-                          int* rows);
+                          int* rows);                                                                        \
+  int bwd_plans_##NAME(int HP, int C);
 FST_DECL_BWD(bf16_16)
 FST_DECL_BWD(bf16_32)
 FST_DECL_BWD(bf16_48)

@@ -19,7 +19,7 @@ from typing import Any, Optional, Tuple
 import torch
 from torch import Tensor
 
-from . import _lib
+from . import _lib, tune
 
 _DTYPES = {torch.bfloat16: _lib.FST_BF16, torch.float32: _lib.FST_F32}
 
@@ -215,15 +215,21 @@ def _run_forward(prep: _Prepared) -> Tuple[Tensor, Tensor]:
     lib = _lib.load()
     out = prep.empty_out()
     lse = prep.empty_vec()
-    ws_bytes = lib.fst_forward_workspace_bytes(*prep.dims())
+    dims = prep.dims()
+    ws_bytes = lib.fst_forward_workspace_bytes(*dims)
     ws = torch.empty(max(ws_bytes, 1), device=prep.device, dtype=torch.uint8)
-    with torch.cuda.device(prep.device):
-        rc = lib.fst_forward(
-            *prep.dims(),
+
+    def run(flags: int) -> int:
+        return lib.fst_forward(
+            dims[0], flags, *dims[2:],
             _lib.ptr(prep.q), _lib.ptr(prep.k), _lib.ptr(prep.v), _lib.ptr(prep.pos4),
             _lib.ptr(prep.weight), _lib.ptr(prep.bias), _lib.ptr(prep.lens), prep.scale,
             _lib.ptr(out), _lib.ptr(lse), _lib.ptr(ws), ws_bytes, _lib.stream_handle(prep.device),
         )
+
+    with torch.cuda.device(prep.device):
+        plan = tune.forward_plan(dims, run)
+        rc = run(dims[1] | plan)
     _lib.check(rc, "flash_spacetime_forward")
     return out, lse
 

@@ -57,10 +57,26 @@ enum fst_flags {
                          (reference.py:187-196 split_heads) read in place.
                          No reference counterpart: the reference makes them
                          contiguous [B, H, L, D] first (forward.py:274).    */
-  FST_QKV_INTERLEAVED = 16 /* q, k, v (and dq, dk, dv) interleaved per token as
+  FST_QKV_INTERLEAVED = 16, /* q, k, v (and dq, dk, dv) interleaved per token as
                               one fused projection's [.., 3, H, D] output; see
                               Layouts. No reference counterpart (the reference
                               takes three separate tensors, forward.py:481). */
+  /* Plan bits (bf16 kernels): a choice among compiled variants of a kernel
+   * that compute every output row with the same arithmetic and differ only
+   * in their register / LDS budget, for callers that time them (at most one
+   * bit of each pair; none = the library's static choice). out, lse, dq, dk,
+   * dv and rowsum do not depend on the plan; dweight / dbias depend on the
+   * rows plan only through the order of their fp32 partial sums. Only the
+   * bits fst_plans() reports for the shape are accepted. No reference
+   * counterpart: the reference's Triton kernels take fixed tile constants
+   * (_tiles.py) and are not autotuned (README.md:86-95). */
+  FST_PLAN_FWD_OCC2 = 1 << 8,   /* forward: two workgroups per CU            */
+  FST_PLAN_FWD_OCC3 = 1 << 9,   /* forward: three workgroups per CU          */
+  FST_PLAN_ROWS_W4 = 1 << 10,   /* backward rows: four waves per workgroup   */
+  FST_PLAN_ROWS_W8 = 1 << 11,   /* backward rows: eight waves (heads padded to a multiple of 8) */
+  FST_PLAN_COLS_OCC2 = 1 << 12, /* backward cols: two workgroups per CU      */
+  FST_PLAN_COLS_OCC3 = 1 << 13, /* backward cols: three workgroups per CU    */
+  FST_PLAN_MASK = 0x3f00
 };
 
 /* Phases of one operator call, for callers that time or schedule them
@@ -89,6 +105,11 @@ enum fst_status {
  * No reference counterpart: the Triton reference JIT-compiles per shape and
  * raises ValueError for C outside {16, 32, 48} (forward.py:261-265). */
 int fst_supported(int dtype, int H, int D, int C);
+
+/* The FST_PLAN_* bits compiled for (dtype, H, D, C): a bit is set when its
+ * variant exists for the shape (0 for float32 and unsupported shapes).
+ * No reference counterpart (see FST_PLAN_FWD_OCC2). */
+int fst_plans(int dtype, int H, int D, int C);
 
 /* Scratch bytes fst_forward needs for these sizes (rows = B*L padded, T packed). */
 size_t fst_forward_workspace_bytes(int dtype, int flags, int B, int H, int L, int T,
