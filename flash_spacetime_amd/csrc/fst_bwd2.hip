@@ -1024,8 +1024,13 @@ template <int HP, int D, int C, int OCC>
 int bwd2_launch_cols(const BwdParams& prm, hipStream_t stream, int g8) {
   using P = Bwd2Pick<HP, D, C>;
   using Cfg = Cols2Cfg<HP, D, C, P::RC>;
-  auto kern = (prm.flags & 3) == 3 ? bwd_cols2_kernel<HP, D, C, P::RC, 3, OCC>
-                                   : bwd_cols2_kernel<HP, D, C, P::RC, -1, OCC>;
+  // One instance per bias-flag combination: a kernel reading the flags at
+  // run time keeps both bias paths live and spills at the larger layouts.
+  const int fl = prm.flags & 3;
+  auto kern = fl == 3   ? bwd_cols2_kernel<HP, D, C, P::RC, 3, OCC>
+              : fl == 1 ? bwd_cols2_kernel<HP, D, C, P::RC, 1, OCC>
+              : fl == 2 ? bwd_cols2_kernel<HP, D, C, P::RC, 2, OCC>
+                        : bwd_cols2_kernel<HP, D, C, P::RC, 0, OCC>;
   if (hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, Cfg::LDS_BYTES) !=
       hipSuccess)
     return FST_ELAUNCH;
@@ -1057,13 +1062,7 @@ int bwd2_launch_t(const BwdParams& prm, int which, hipStream_t stream, int grid)
   if constexpr (!P::CC::FITS) {
     return FST_EUNSUPPORTED;
   } else {
-    // Static choice: Cols2Cfg::OCC for the compile-time bias flags; two
-    // workgroups per CU for the run-time-flag instance, which keeps both bias
-    // paths live and spills at three (cfg2's layout: 1.13 -> 0.72 ms).
-    const int occ = (prm.flags & FST_PLAN_COLS_OCC2)   ? 2
-                    : (prm.flags & FST_PLAN_COLS_OCC3) ? 3
-                    : (prm.flags & 3) == 3             ? P::CC::OCC
-                                                       : 2;
+    const int occ = (prm.flags & FST_PLAN_COLS_OCC2) ? 2 : (prm.flags & FST_PLAN_COLS_OCC3) ? 3 : P::CC::OCC;
     if (occ == 3) {
       if constexpr (P::COLS_OCC3 || P::CC::OCC == 3) return bwd2_launch_cols<HP, D, C, 3>(prm, stream, g8);
       return FST_EUNSUPPORTED;

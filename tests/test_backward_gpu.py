@@ -127,6 +127,23 @@ def test_backward_bf16_relative(shape, flags, pos):
         assert err <= 2e-2, f"grad {key}: bf16 relative error {err:.3e}"
 
 
+@pytest.mark.parametrize("shape", [(2, 96, 12, 32, 16), (1, 70, 8, 48, 16), (1, 50, 16, 64, 48)],
+                         ids=lambda s: "x".join(map(str, s)))
+def test_backward_bf16_no_bias(shape):
+    """Both bias flags off in bf16: plain attention gradients within 2e-2 of
+    float64, and W / b get no gradient (reference forward.py:417-431)."""
+    flags = (False, False)
+    case = make_padded(*shape, seed=seed_of("bwd16-nobias", shape))
+    gw = torch.randn(case["q"].permute(0, 2, 1, 3).shape, dtype=torch.float64,
+                     generator=torch.Generator().manual_seed(9))
+    kern = _grads_kernel(case, flags, torch.bfloat16, gw)
+    ref = _grads_fp64(case, flags, gw)
+    assert kern["W"] is None and kern["b"] is None
+    for key in ("q", "k", "v"):
+        err = rel_err(kern[key], ref[key])
+        assert err <= 2e-2, f"grad {key}: bf16 relative error {err:.3e}"
+
+
 def _rowsum_case(shape, dtype, qk_scale, seed):
     case = make_padded(*shape, seed=seed, qk_scale=qk_scale)
     dev = "cuda"
