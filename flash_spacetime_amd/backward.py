@@ -17,7 +17,7 @@ import torch
 from torch import Tensor
 
 from . import _lib, tune
-from .forward import _Prepared, _vec_in_layout
+from .forward import _Prepared, _vec_in_layout, head_groups
 
 
 def _same_layout(a: Tensor, b: Tensor) -> bool:
@@ -48,6 +48,10 @@ def _run_backward(dims, q, k, v, pos4, w32, b32, lens, lse, grad_out, scale, vec
         raise ValueError(f"rowsum must be float32 of the shape of lse {tuple(lse.shape)} on the operands' device")
     lib = _lib.load()
     _lib.require_gpu(grad_out)
+    groups = head_groups(dims[0], dims[3], dims[6], dims[7])
+    if len(groups) > 1:
+        return _run_backward_grouped(groups, dims, q, k, v, pos4, w32, b32, lens, lse, grad_out, scale,
+                                     rowsum, grads)
     like = q if out_like is None else out_like
     do = grad_out.to(q.dtype)
     if not _same_layout(do, like):
@@ -84,6 +88,36 @@ def _run_backward(dims, q, k, v, pos4, w32, b32, lens, lse, grad_out, scale, vec
     _lib.check(rc, "flash_spacetime_backward")
     if rs is not rowsum:
         rowsum.copy_(rs)
+    return dq, dk, dv, dw, db
+
+
+def _run_backward_grouped(groups, dims, q, k, v, pos4, w32, b32, lens, lse, grad_out, scale, rowsum, grads):
+    """The backward one head group at a time (head_groups): each group's
+    operands as contiguous tensors, its gradients copied into the full ones,
+    dW and db summed over the groups in order."""
+    if grads is not None:
+        dq, dk, dv = grads
+    else:
+        dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
+    do = grad_out.to(q.dtype)
+    dw = torch.zeros(w32.shape, device=q.device, dtype=torch.float32)
+    db = torch.zeros(q.shape[-1], device=q.device, dtype=torch.float32) if b32 is not None else None
+    flags = dims[1] & ~(_lib.FST_TOKEN_MAJOR | _lib.FST_QKV_INTERLEAVED)
+    for h0, h1 in groups:
+        part = lambda t: t[:, h0:h1].contiguous()  # noqa: E731
+        lse_g = part(lse)
+        rs_g = torch.empty_like(lse_g) if rowsum is not None else None
+        sub = (dims[0], flags, dims[2], h1 - h0) + tuple(dims[4:])
+        g_dq, g_dk, g_dv, g_dw, g_db = _run_backward(sub, part(q), part(k), part(v), pos4, w32, b32, lens,
+                                                     lse_g, part(do), scale, tuple(lse_g.shape), rowsum=rs_g)
+        dq[:, h0:h1].copy_(g_dq)
+        dk[:, h0:h1].copy_(g_dk)
+        dv[:, h0:h1].copy_(g_dv)
+        dw += g_dw
+        if db is not None:
+            db += g_db
+        if rowsum is not None:
+            rowsum[:, h0:h1].copy_(rs_g)
     return dq, dk, dv, dw, db
 
 

@@ -379,8 +379,9 @@ int fst_supported(int dtype, int H, int D, int C) {
   int rows = 0;
   FwdParams dummy;
   std::memset(&dummy, 0, sizeof(dummy));
-  if (fwd_table(dtype, D)(dummy, head_padding(H), C, nullptr, 0, true, &rows) != FST_OK) return 0;
-  return rows > 0;
+  if (fwd_table(dtype, D)(dummy, head_padding(H), C, nullptr, 0, true, &rows) != FST_OK || rows <= 0) return 0;
+  BwdLayout lay;
+  return bwd_layout(dtype, 0, 1, H, 16, 0, D, C, lay) == FST_OK;
 }
 
 size_t fst_forward_workspace_bytes(int dtype, int flags, int B, int H, int L, int T, int D, int C) {

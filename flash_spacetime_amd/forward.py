@@ -13,8 +13,9 @@ tensor raises.
 
 from __future__ import annotations
 
+import copy
 import os
-from typing import Any, Optional, Tuple
+from typing import Any, List, Optional, Tuple
 
 import torch
 from torch import Tensor
@@ -101,6 +102,21 @@ def _resolve_lengths(seqlens: Optional[Tensor], key_padding_mask: Optional[Tenso
     return seqlens
 
 
+def head_groups(dtype: int, heads: int, dim: int, channels: int) -> List[Tuple[int, int]]:
+    """Head ranges [h0, h1) the kernels run one call each: all heads at once
+    where the library has a kernel for that many, else the fewest equal
+    groups (sizes differing by at most one) it has one for -- more than 16
+    heads, or float32 at D = C = 64 with more than 8. The reference pads heads
+    to the next power of two inside one kernel and takes any count
+    (forward.py:22, backward.py:574)."""
+    lib = _lib.load()
+    for n in range(1, heads + 1):
+        if lib.fst_supported(dtype, -(-heads // n), dim, channels):
+            bounds = [i * heads // n for i in range(n + 1)]
+            return [(bounds[i], bounds[i + 1]) for i in range(n)]
+    raise ValueError(f"no kernel for head_dim {dim} and C={channels} in this dtype")
+
+
 class _Prepared:
     """Validated kernel operands shared by forward and backward.
 
@@ -148,12 +164,13 @@ class _Prepared:
             raise ValueError(f"kernel supports C in (16, 32, 48, 64), got {c}")
         if dim not in (16, 32, 48, 64):
             raise ValueError(f"kernel supports head_dim in (16, 32, 48, 64), got {dim}")
-        if not 1 <= heads <= 16:
-            raise ValueError(f"kernel supports 1 to 16 heads, got {heads}")
+        if heads < 1:
+            raise ValueError(f"need at least one head, got {heads}")
         if bias is not None and bias.shape != (dim,):
             raise ValueError(f"bias must be [D={dim}], got {tuple(bias.shape)}")
         self.heads, self.dim, self.channels = heads, dim, c
         self.dtype = _DTYPES[q.dtype]
+        self.groups = head_groups(self.dtype, heads, dim, c)
         self.scale = float(dim ** -0.5 if scale is None else scale)
         # interleaved: q, k, v are the slots of one [B, L, 3, H, D] / [T, 3, H, D]
         # tensor (the caller, `_FlashSpacetimeAttentionQKV`, guarantees it).
@@ -203,6 +220,17 @@ class _Prepared:
         return torch.empty(self.batch, self.length, self.heads, self.dim, device=self.device,
                            dtype=self.q.dtype).transpose(1, 2)
 
+    def head_slice(self, h0: int, h1: int) -> "_Prepared":
+        """The operands of heads [h0, h1) as contiguous tensors of their own
+        (heads-first padded or packed, no longer token-major or interleaved)."""
+        sub = copy.copy(self)
+        sub.q, sub.k, sub.v = (t[:, h0:h1].contiguous() for t in (self.q, self.k, self.v))
+        sub.heads = h1 - h0
+        sub.token_major = sub.interleaved = False
+        sub.flags = self.flags & ~(_lib.FST_TOKEN_MAJOR | _lib.FST_QKV_INTERLEAVED)
+        sub.groups = [(0, h1 - h0)]
+        return sub
+
     def empty_vec(self) -> Tensor:
         """A float32 per-row vector (lse, rowsum) in the operands' layout."""
         if self.token_major:
@@ -215,6 +243,12 @@ def _run_forward(prep: _Prepared) -> Tuple[Tensor, Tensor]:
     lib = _lib.load()
     out = prep.empty_out()
     lse = prep.empty_vec()
+    if len(prep.groups) > 1:
+        for h0, h1 in prep.groups:
+            o, l_ = _run_forward(prep.head_slice(h0, h1))
+            out[:, h0:h1].copy_(o)
+            lse[:, h0:h1].copy_(l_)
+        return out, lse
     dims = prep.dims()
     ws_bytes = lib.fst_forward_workspace_bytes(*dims)
     ws = torch.empty(max(ws_bytes, 1), device=prep.device, dtype=torch.uint8)

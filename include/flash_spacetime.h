@@ -28,7 +28,8 @@
  *   dbias, rowsum are float32 in both.
  *
  * Supported shapes: 1 <= H <= 16, D in {16, 32, 48, 64}, C in {16, 32, 48,
- * 64} (C even, sin/cos halves); see fst_supported(). One event's rows of all
+ * 64} (C even, sin/cos halves); see fst_supported(). Callers run more heads
+ * as head groups of their own (the Python operators take any H). One event's rows of all
  * heads (times 3 with FST_QKV_INTERLEAVED) must span less than 2 GiB: the
  * kernels address them with 32-bit byte offsets. Padded calls beyond that
  * return FST_EUNSUPPORTED; packed events are the caller's to bound.
@@ -101,7 +102,9 @@ enum fst_status {
   FST_ELAUNCH = -4       /* HIP launch error                                 */
 };
 
-/* 1 if (dtype, H, D, C) has a compiled kernel, else 0.
+/* 1 if (dtype, H, D, C) has compiled forward and backward kernels, else 0
+ * (float32 at D = C = 64 has them up to H = 8; callers split more heads
+ * into groups, as the Python operators do).
  * No reference counterpart: the Triton reference JIT-compiles per shape and
  * raises ValueError for C outside {16, 32, 48} (forward.py:261-265). */
 int fst_supported(int dtype, int H, int D, int C);

@@ -107,3 +107,26 @@ def test_save_and_load(tmp_path):
     tune.load(str(path))
     assert tune.chosen() == saved
     tune.clear()
+
+
+@needs_lib
+def test_head_groups():
+    from flash_spacetime_amd.forward import head_groups
+
+    bf, f32 = _lib.FST_BF16, _lib.FST_F32
+    assert head_groups(bf, 12, 32, 16) == [(0, 12)]
+    assert head_groups(bf, 16, 64, 64) == [(0, 16)]
+    assert head_groups(bf, 24, 32, 16) == [(0, 12), (12, 24)]
+    assert head_groups(bf, 17, 32, 16) == [(0, 8), (8, 17)]
+    assert head_groups(bf, 64, 16, 16) == [(0, 16), (16, 32), (32, 48), (48, 64)]
+    # float32 at D = C = 64 has kernels up to 8 heads (LDS)
+    assert head_groups(f32, 8, 64, 64) == [(0, 8)]
+    assert head_groups(f32, 12, 64, 64) == [(0, 6), (6, 12)]
+    for heads in range(1, 70):
+        groups = head_groups(bf, heads, 48, 32)
+        assert groups[0][0] == 0 and groups[-1][1] == heads
+        sizes = [h1 - h0 for h0, h1 in groups]
+        assert max(sizes) <= 16 and max(sizes) - min(sizes) <= 1
+        assert all(a[1] == b[0] for a, b in zip(groups, groups[1:]))
+    with pytest.raises(ValueError):
+        head_groups(bf, 12, 24, 16)
