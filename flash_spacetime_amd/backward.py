@@ -17,7 +17,7 @@ import torch
 from torch import Tensor
 
 from . import _lib, tune
-from .forward import _Prepared, _vec_in_layout, head_groups
+from .forward import _Prepared, _bf16, _vec_in_layout, head_groups
 
 
 def _same_layout(a: Tensor, b: Tensor) -> bool:
@@ -150,6 +150,11 @@ def flash_spacetime_backward(
     tuning arguments are accepted and ignored.
     """
     del block_m, block_n, num_warps, num_stages
+    if q.dtype == torch.float16:  # the bf16 path, as the forward launcher runs it
+        dq, dk, dv, dw, db = flash_spacetime_backward(
+            *_bf16(q, k, v), feats, weight, bias, seqlens, lse, grad_out.to(torch.bfloat16), scale,
+            use_attn_bias, use_activation_bias, cu_seqlens=cu_seqlens, rowsum=rowsum)
+        return dq.to(q.dtype), dk.to(q.dtype), dv.to(q.dtype), dw, db
     prep = _Prepared(q, k, v, feats, weight, bias, seqlens, scale, use_attn_bias,
                      use_activation_bias, cu_seqlens)
     dq, dk, dv, dw, db = _run_backward(

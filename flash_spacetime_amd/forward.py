@@ -102,6 +102,18 @@ def _resolve_lengths(seqlens: Optional[Tensor], key_padding_mask: Optional[Tenso
     return seqlens
 
 
+_HALF = torch.float16
+
+
+def _bf16(*ts: Tensor) -> Tuple[Tensor, ...]:
+    """float16 operands for the bf16 kernels. The reference computes every
+    operand that is not float32 in bf16 (forward.py:271, backward.py:523:
+    `compute_bf16 = q.dtype != torch.float32`), so float16 inputs run the
+    bf16 path and results go back to float16. `to` keeps a dense view's
+    strides, so token-major views stay token-major."""
+    return tuple(t.to(torch.bfloat16) for t in ts)
+
+
 def head_groups(dtype: int, heads: int, dim: int, channels: int) -> List[Tuple[int, int]]:
     """Head ranges [h0, h1) the kernels run one call each: all heads at once
     where the library has a kernel for that many, else the fewest equal
@@ -299,6 +311,10 @@ def flash_spacetime_forward(
     gfx950's 160 KiB LDS.
     """
     del block_m, block_n, num_warps, num_stages
+    if q.dtype == _HALF:
+        out, lse = flash_spacetime_forward(*_bf16(q, k, v), feats, weight, bias, seqlens, scale, use_attn_bias,
+                                           use_activation_bias, cu_seqlens=cu_seqlens)
+        return out.to(_HALF), lse
     prep = _Prepared(q, k, v, feats, weight, bias, seqlens, scale, use_attn_bias,
                      use_activation_bias, cu_seqlens)
     return _run_forward(prep)
@@ -390,6 +406,9 @@ def flash_spacetime_attention(
     `key_padding_mask=`. A front-packed mask becomes lengths (one readback);
     a mask with holes runs the packed kernels on the gathered valid tokens.
     """
+    if q.dtype == _HALF:
+        return flash_spacetime_attention(*_bf16(q, k, v), feats, weight, bias, seqlens, scale, use_attn_bias,
+                                         use_activation_bias, key_padding_mask=key_padding_mask).to(_HALF)
     mask = key_padding_mask
     if mask is None and seqlens is not None and seqlens.dim() == 2:
         mask = seqlens
@@ -457,6 +476,9 @@ def flash_spacetime_attention_varlen(
     the nested tensor's, `cu_seqlens` may be omitted (or must equal its
     offsets), and the output is a jagged tensor with the same offsets.
     """
+    if q.dtype == _HALF:
+        return flash_spacetime_attention_varlen(*_bf16(q, k, v), feats, weight, bias, cu_seqlens, scale,
+                                                use_attn_bias, use_activation_bias).to(_HALF)
     if q.is_nested:
         if not (k.is_nested and v.is_nested):
             raise ValueError("q, k and v must all be nested tensors, or none of them")
@@ -575,6 +597,10 @@ def flash_spacetime_attention_qkv(
     reference counterpart: the reference takes three separate tensors
     (forward.py:481-501).
     """
+    if qkv.dtype == _HALF:
+        return flash_spacetime_attention_qkv(qkv.to(torch.bfloat16), feats, weight, bias, seqlens, scale,
+                                             use_attn_bias, use_activation_bias, cu_seqlens=cu_seqlens,
+                                             key_padding_mask=key_padding_mask).to(_HALF)
     if cu_seqlens is not None:
         if qkv.dim() != 4 or qkv.shape[1] != 3:
             raise ValueError(f"packed qkv must be [T, 3, H, D], got {tuple(qkv.shape)}")
