@@ -114,8 +114,12 @@ __global__ __launch_bounds__(1024) void blkcum_kernel(const int32_t* lens, int p
 
 // Schedule of the tile kernels: the events ordered by decreasing valid
 // length (ties by index; lengths past 2^18 - 1 count as 2^18 - 1), one
-// workgroup, bitonic sort in LDS. Past 8192 events the identity order is used.
+// workgroup. Up to 1024 events each thread ranks one key by counting the
+// larger ones (the keys are distinct, so the ranks are a permutation; one
+// barrier, broadcast LDS reads); up to 8192 a bitonic sort in LDS. Past 8192
+// events the identity order is used.
 constexpr int kSortMax = 8192;
+constexpr int kRankMax = 1024;
 
 __global__ __launch_bounds__(1024) void sort_events_kernel(const int32_t* lens, int packed, int B, int L, int T,
                                                            int32_t* perm) {
@@ -142,6 +146,16 @@ __global__ __launch_bounds__(1024) void sort_events_kernel(const int32_t* lens, 
       key = (l << 13) | (kSortMax - 1 - i);
     }
     keys[i] = key;
+  }
+  if (B <= kRankMax) {
+    __syncthreads();
+    if (t < B) {
+      const int mine = keys[t];
+      int rank = 0;
+      for (int j = 0; j < B; ++j) rank += keys[j] > mine;
+      perm[rank] = kSortMax - 1 - (mine & (kSortMax - 1));
+    }
+    return;
   }
   for (int k = 2; k <= p2; k <<= 1)
     for (int j = k >> 1; j > 0; j >>= 1) {

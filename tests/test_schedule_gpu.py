@@ -120,3 +120,35 @@ def test_packed_sorted_schedule_is_deterministic():
     a = _run_packed(q, k, v, do, feats, w, b, lens)
     c = _run_packed(q, k, v, do, feats, w, b, lens)
     assert torch.equal(a[0], c[0]) and all(torch.equal(x, y) for x, y in zip(a[1], c[1]))
+
+
+@pytest.mark.parametrize("batch", [1, 5, 256, 1024, 1025, 3000, 8192, 9000])
+def test_event_sort_order(batch):
+    """The forward work list's event order (workspace ints B+1 .. 2B): events
+    by decreasing length, ties by index, up to 8192 events (rank sort up to
+    1024, bitonic above); the identity past that."""
+    from flash_spacetime_amd import _lib
+
+    lib = _lib.load()
+    gen = torch.Generator().manual_seed(batch)
+    length, heads, dim, chans = 8, 1, 16, 16
+    lens = torch.randint(0, length + 1, (batch,), generator=gen, dtype=torch.int32)
+    q = torch.zeros(batch, heads, length, dim, device=DEV, dtype=torch.bfloat16)
+    pos4 = torch.zeros(batch, length, 4, device=DEV)
+    w = torch.zeros(dim, chans, device=DEV)
+    out, lse = torch.empty_like(q), torch.empty(batch, heads, length, device=DEV)
+    dims = (_lib.FST_BF16, 3, batch, heads, length, 0, dim, chans)
+    ws_bytes = lib.fst_forward_workspace_bytes(*dims)
+    ws = torch.zeros(ws_bytes // 4, device=DEV, dtype=torch.int32)
+    rc = lib.fst_forward_phases(_lib.FST_PHASE_WORKLIST, *dims, q.data_ptr(), q.data_ptr(), q.data_ptr(),
+                                pos4.data_ptr(), w.data_ptr(), None, lens.to(DEV).data_ptr(), 1.0,
+                                out.data_ptr(), lse.data_ptr(), ws.data_ptr(), ws_bytes,
+                                torch.cuda.current_stream().cuda_stream)
+    _lib.check(rc, "work list")
+    torch.cuda.synchronize()
+    perm = ws[batch + 1: 2 * batch + 1].cpu().tolist()
+    if batch <= 8192:
+        want = sorted(range(batch), key=lambda i: (-int(lens[i]), i))
+    else:
+        want = list(range(batch))
+    assert perm == want
