@@ -70,32 +70,24 @@ static void freq_table(int C, FreqTable& ft) {
   }
 }
 
-// Number of row blocks of each event and their prefix sum (one workgroup),
-// over the events in index order, or in the order perm gives when not null.
+// Number of row blocks of each event and their prefix sum, over the events
+// in index order, or in the order perm gives when not null; one workgroup.
 // Padded events always get one block so that their padding rows are zeroed.
-__global__ __launch_bounds__(1024) void blkcum_kernel(const int32_t* lens, int packed, int B, int L, int T, int rows,
-                                                      const int32_t* perm, int32_t* blkcum) {
-  __shared__ int buf[1024];
-  __shared__ int carry;
+__device__ void blkcum_steps(const EventSpec& ev, int rows, const int32_t* perm, int32_t* blkcum, int* buf,
+                             int& carry) {
   const int t = threadIdx.x;
   if (t == 0) {
     carry = 0;
     blkcum[0] = 0;
   }
   __syncthreads();
-  EventSpec ev;
-  ev.lens = lens;
-  ev.packed = packed;
-  ev.B = B;
-  ev.L = L;
-  ev.T = T;
-  for (int base = 0; base < B; base += 1024) {
+  for (int base = 0; base < ev.B; base += 1024) {
     const int b = base + t;
     int nb = 0;
-    if (b < B) {
+    if (b < ev.B) {
       int tok0, len;
       event_range(ev, perm ? perm[b] : b, tok0, len);
-      nb = len > 0 ? (len + rows - 1) / rows : (packed ? 0 : 1);
+      nb = len > 0 ? (len + rows - 1) / rows : (ev.packed ? 0 : 1);
     }
     buf[t] = nb;
     __syncthreads();
@@ -105,7 +97,7 @@ __global__ __launch_bounds__(1024) void blkcum_kernel(const int32_t* lens, int p
       buf[t] += add;
       __syncthreads();
     }
-    if (b < B) blkcum[b + 1] = carry + buf[t];
+    if (b < ev.B) blkcum[b + 1] = carry + buf[t];
     __syncthreads();
     if (t == 1023) carry += buf[1023];
     __syncthreads();
@@ -121,20 +113,12 @@ __global__ __launch_bounds__(1024) void blkcum_kernel(const int32_t* lens, int p
 constexpr int kSortMax = 8192;
 constexpr int kRankMax = 1024;
 
-__global__ __launch_bounds__(1024) void sort_events_kernel(const int32_t* lens, int packed, int B, int L, int T,
-                                                           int32_t* perm) {
-  extern __shared__ int keys[];
-  const int t = threadIdx.x;
+__device__ void sort_steps(const EventSpec& ev, int32_t* perm, int* keys) {
+  const int t = threadIdx.x, B = ev.B;
   if (B > kSortMax) {
     for (int i = t; i < B; i += 1024) perm[i] = i;
     return;
   }
-  EventSpec ev;
-  ev.lens = lens;
-  ev.packed = packed;
-  ev.B = B;
-  ev.L = L;
-  ev.T = T;
   int p2 = 1;
   while (p2 < B) p2 <<= 1;
   for (int i = t; i < p2; i += 1024) {
@@ -147,8 +131,8 @@ __global__ __launch_bounds__(1024) void sort_events_kernel(const int32_t* lens, 
     }
     keys[i] = key;
   }
+  __syncthreads();
   if (B <= kRankMax) {
-    __syncthreads();
     if (t < B) {
       const int mine = keys[t];
       int rank = 0;
@@ -159,7 +143,6 @@ __global__ __launch_bounds__(1024) void sort_events_kernel(const int32_t* lens, 
   }
   for (int k = 2; k <= p2; k <<= 1)
     for (int j = k >> 1; j > 0; j >>= 1) {
-      __syncthreads();
       for (int i = t; i < p2; i += 1024) {
         const int l = i ^ j;
         if (l > i) {
@@ -170,19 +153,48 @@ __global__ __launch_bounds__(1024) void sort_events_kernel(const int32_t* lens, 
           }
         }
       }
+      __syncthreads();
     }
-  __syncthreads();
   for (int i = t; i < B; i += 1024) perm[i] = kSortMax - 1 - (keys[i] & (kSortMax - 1));
 }
 
-static int launch_sort(const int32_t* lens, int packed, int B, int L, int T, int32_t* perm, hipStream_t st) {
+// The work list of one operator call in one launch (one workgroup, steps
+// separated by barriers, which also order the global writes of perm before
+// their reads): row-block prefix sums in event order for the row-block sizes
+// rows_a and, when blk_b is not null, rows_b; the length-sorted order perm;
+// for packed events the prefix sums in perm order (scum_a, scum_b), which
+// are the tile kernels' schedule.
+__global__ __launch_bounds__(1024) void worklist_kernel(const int32_t* lens, int packed, int B, int L, int T,
+                                                        int rows_a, int32_t* blk_a, int rows_b, int32_t* blk_b,
+                                                        int32_t* perm, int32_t* scum_a, int32_t* scum_b) {
+  extern __shared__ int keys[];
+  __shared__ int buf[1024];
+  __shared__ int carry;
+  EventSpec ev;
+  ev.lens = lens;
+  ev.packed = packed;
+  ev.B = B;
+  ev.L = L;
+  ev.T = T;
+  blkcum_steps(ev, rows_a, nullptr, blk_a, buf, carry);
+  if (blk_b) blkcum_steps(ev, rows_b, nullptr, blk_b, buf, carry);
+  sort_steps(ev, perm, keys);
+  __syncthreads();
+  if (scum_a) blkcum_steps(ev, rows_a, perm, scum_a, buf, carry);
+  if (scum_b) blkcum_steps(ev, rows_b, perm, scum_b, buf, carry);
+}
+
+static int launch_worklist(const int32_t* lens, bool packed, int B, int L, int T, int rows_a, int32_t* blk_a,
+                           int rows_b, int32_t* blk_b, int32_t* perm, int32_t* scum_a, int32_t* scum_b,
+                           hipStream_t st) {
   int p2 = 1;
   while (p2 < B && p2 < kSortMax) p2 <<= 1;
   const int lds = B > kSortMax ? 0 : p2 * (int)sizeof(int);
-  if (hipFuncSetAttribute((const void*)sort_events_kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
+  if (hipFuncSetAttribute((const void*)worklist_kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
                           kSortMax * (int)sizeof(int)) != hipSuccess)
     return FST_ELAUNCH;
-  hipLaunchKernelGGL(sort_events_kernel, dim3(1), dim3(1024), lds, st, lens, packed, B, L, T, perm);
+  hipLaunchKernelGGL(worklist_kernel, dim3(1), dim3(1024), lds, st, lens, packed ? 1 : 0, B, L, T, rows_a, blk_a,
+                     rows_b, blk_b, perm, packed ? scum_a : nullptr, packed ? scum_b : nullptr);
   return hipGetLastError() == hipSuccess ? FST_OK : FST_ELAUNCH;
 }
 
@@ -442,16 +454,10 @@ int fst_forward_phases(int phases, int dtype, int flags, int B, int H, int L, in
   int32_t* perm = blkcum + (B + 1);
   int32_t* scum = perm + B;
   if (phases & FST_PHASE_WORKLIST) {
-    hipLaunchKernelGGL(blkcum_kernel, dim3(1), dim3(1024), 0, st, lens, packed ? 1 : 0, B, L, T, rows,
-                       (const int32_t*)nullptr, blkcum);
-    if (hipGetLastError() != hipSuccess) return fail(FST_ELAUNCH, "work-list kernel launch failed");
-    if (launch_sort(lens, packed ? 1 : 0, B, L, T, perm, st) != FST_OK)
-      return fail(FST_ELAUNCH, "schedule kernel launch failed");
-    if (packed) {
-      hipLaunchKernelGGL(blkcum_kernel, dim3(1), dim3(1024), 0, st, lens, 1, B, L, T, rows, (const int32_t*)perm, scum);
-      if (hipGetLastError() != hipSuccess) return fail(FST_ELAUNCH, "schedule kernel launch failed");
-    }
+    if (launch_worklist(lens, packed, B, L, T, rows, blkcum, 0, nullptr, perm, scum, nullptr, st) != FST_OK)
+      return fail(FST_ELAUNCH, "work-list kernel launch failed");
   }
+
   if (!(phases & FST_PHASE_FWD)) return FST_OK;
 
   prm.ev.lens = lens;
@@ -540,21 +546,11 @@ int fst_backward_phases(int phases, int dtype, int flags, int B, int H, int L, i
   int32_t* scum_r = perm_r + B;
   int32_t* scum_c = bc_c + (B + 1) + B;
   if (phases & FST_PHASE_WORKLIST) {
-    hipLaunchKernelGGL(blkcum_kernel, dim3(1), dim3(1024), 0, st, lens, packed ? 1 : 0, B, L, T, lay.rows_r,
-                       (const int32_t*)nullptr, bc_r);
-    hipLaunchKernelGGL(blkcum_kernel, dim3(1), dim3(1024), 0, st, lens, packed ? 1 : 0, B, L, T, lay.rows_c,
-                       (const int32_t*)nullptr, bc_c);
-    if (hipGetLastError() != hipSuccess) return fail(FST_ELAUNCH, "work-list kernel launch failed");
-    if (launch_sort(lens, packed ? 1 : 0, B, L, T, perm_r, st) != FST_OK)
-      return fail(FST_ELAUNCH, "schedule kernel launch failed");
-    if (packed) {
-      hipLaunchKernelGGL(blkcum_kernel, dim3(1), dim3(1024), 0, st, lens, 1, B, L, T, lay.rows_r,
-                         (const int32_t*)perm_r, scum_r);
-      hipLaunchKernelGGL(blkcum_kernel, dim3(1), dim3(1024), 0, st, lens, 1, B, L, T, lay.rows_c,
-                         (const int32_t*)perm_r, scum_c);
-      if (hipGetLastError() != hipSuccess) return fail(FST_ELAUNCH, "schedule kernel launch failed");
-    }
+    if (launch_worklist(lens, packed, B, L, T, lay.rows_r, bc_r, lay.rows_c, bc_c, perm_r, scum_r, scum_c, st) !=
+        FST_OK)
+      return fail(FST_ELAUNCH, "work-list kernel launch failed");
   }
+
 
   BwdParams prm;
   std::memset(&prm, 0, sizeof(prm));

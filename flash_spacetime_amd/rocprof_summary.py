@@ -42,7 +42,7 @@ PHASES = {"fwd2_kernel": "fwd", "fwd_kernel": "fwd",
           "bwd_rows2_kernel": "bwd_rows", "bwd_rows_kernel": "bwd_rows",
           "bwd_cols2_kernel": "bwd_cols", "bwd_cols_kernel": "bwd_cols",
           "dw_reduce_seg_kernel": "bwd_reduce_seg", "dw_reduce_final_kernel": "bwd_reduce_final",
-          "blkcum_kernel": "worklist", "sort_events_kernel": "worklist_sort"}
+          "worklist_kernel": "worklist"}
 
 
 def _find(directory: str, suffix: str) -> str:

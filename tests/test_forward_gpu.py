@@ -165,6 +165,7 @@ def test_unsupported_shapes_raise():
     with pytest.raises(ValueError, match="C in"):
         flash_spacetime_forward(g["q"], g["k"], g["v"], g["feats"], g["weight"][:, :12], g["bias"],
                                 g["seqlens"])
+    # float64 is refused (float16 runs the bf16 path, tests/test_half_gpu.py)
     with pytest.raises(ValueError):
-        flash_spacetime_forward(g["q"].half(), g["k"].half(), g["v"].half(), g["feats"], g["weight"],
+        flash_spacetime_forward(g["q"].double(), g["k"].double(), g["v"].double(), g["feats"], g["weight"],
                                 g["bias"], g["seqlens"])
