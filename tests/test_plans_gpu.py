@@ -5,7 +5,8 @@ arithmetic, so for every plan a shape offers, out, lse, dq, dk, dv and the
 dS row sums must equal the static plan's bitwise; dW and db, whose fp32
 per-tile partials the eight-wave rows kernel combines in another order,
 agree to fp32 rounding. The tuner, switched on, must pick plans the shape
-offers and leave every result as the static plan computes it.
+offers (or keep the static one) and leave every result as the static plan
+computes it.
 """
 
 import itertools
@@ -137,7 +138,7 @@ def test_autotune_picks_offered_plans_and_keeps_results():
     assert kinds == ["bwd", "fwd"], picked
     mask = tune.plans(_lib.FST_BF16, heads, dim, chans)
     for key, plan in picked.items():
-        assert plan & ~mask == 0 and plan != 0, (key, hex(plan))
+        assert plan & ~mask == 0, (key, hex(plan))  # 0: the static choice kept
         print(key, tune.plan_names(plan), flush=True)
     for run in (first, second):
         assert torch.equal(run[0], ref[0])
