@@ -130,8 +130,8 @@ int fst_forward(int dtype, int flags, int B, int H, int L, int T, int D, int C,
                 size_t workspace_bytes, void* stream);
 
 /* fst_forward restricted to the given phases (FST_PHASE_WORKLIST,
- * FST_PHASE_FWD). Survey's split launcher fst_fwd; no reference counterpart
- * beyond forward.py:306-331 (the launch itself). */
+ * FST_PHASE_FWD), for callers that time or schedule the phases; no
+ * reference counterpart beyond forward.py:306-331 (the launch itself). */
 int fst_forward_phases(int phases, int dtype, int flags, int B, int H, int L, int T, int D,
                        int C, const void* q, const void* k, const void* v,
                        const float* pos4, const float* weight, const float* bias,
