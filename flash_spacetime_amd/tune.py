@@ -43,6 +43,11 @@ _enabled = os.environ.get("FST_AUTOTUNE", "0") == "1"
 _reps = 3
 _cache: Dict[Tuple, int] = {}
 _fixed: Optional[int] = None
+# FST_AUTOTUNE_CACHE=<path>: choices are loaded from that JSON file (when it
+# exists) on first use and written back after every new choice, so the
+# processes of a training job time each shape once.
+_cache_path: Optional[str] = os.environ.get("FST_AUTOTUNE_CACHE") or None
+_cache_loaded = False
 
 
 def set_autotune(enabled: bool, reps: int = 3) -> None:
@@ -88,9 +93,12 @@ def clear() -> None:
 
 
 def save(path: str) -> None:
-    """Write the chosen plans to a JSON file (keys as lists)."""
-    with open(path, "w") as fh:
+    """Write the chosen plans to a JSON file (keys as lists), replacing it in
+    one rename so a reader never sees a partial file."""
+    tmp = f"{path}.{os.getpid()}.tmp"
+    with open(tmp, "w") as fh:
         json.dump([[list(k), v] for k, v in _cache.items()], fh)
+    os.replace(tmp, path)
 
 
 def load(path: str) -> None:
@@ -143,6 +151,21 @@ def _fastest(run: Callable[[int], int], cands: List[int], base: int, what: str) 
     return best if times[best] < _MARGIN * times[0] else 0
 
 
+def _record(key: Tuple, plan: int) -> None:
+    _cache[key] = plan
+    if _cache_path:
+        save(_cache_path)
+
+
+def _lookup(key: Tuple) -> Optional[int]:
+    global _cache_loaded
+    if _cache_path and not _cache_loaded:
+        _cache_loaded = True
+        if os.path.exists(_cache_path):
+            load(_cache_path)
+    return _cache.get(key)
+
+
 def _usable() -> bool:
     # No timing (which synchronises) while the caller captures a graph.
     return _enabled and not torch.cuda.is_current_stream_capturing()
@@ -154,11 +177,12 @@ def forward_plan(dims: Tuple[int, ...], run: Callable[[int], int]) -> int:
     if _fixed is not None:
         return _fixed & sum(_FWD_BITS)
     key = shape_key("fwd", dims)
-    if key in _cache or not _usable():
-        return _cache.get(key, 0)
+    known = _lookup(key)
+    if known is not None or not _usable():
+        return known or 0
     cands = _candidates(plans(dims[0], dims[3], dims[6], dims[7]), _FWD_BITS)
     choice = _fastest(run, cands, dims[1], "flash_spacetime_forward (tuning)")
-    _cache[key] = choice
+    _record(key, choice)
     return choice
 
 
@@ -171,8 +195,9 @@ def backward_plan(dims: Tuple[int, ...], run: Callable[[int, int], int]) -> int:
     if _fixed is not None:
         return _fixed & sum(_ROWS_BITS + _COLS_BITS)
     key = shape_key("bwd", dims)
-    if key in _cache or not _usable():
-        return _cache.get(key, 0)
+    known = _lookup(key)
+    if known is not None or not _usable():
+        return known or 0
     mask = plans(dims[0], dims[3], dims[6], dims[7])
     rows, cols = _candidates(mask, _ROWS_BITS), _candidates(mask, _COLS_BITS)
     what = "flash_spacetime_backward (tuning)"
@@ -182,7 +207,7 @@ def backward_plan(dims: Tuple[int, ...], run: Callable[[int, int], int]) -> int:
     if len(cols) > 1 and len(rows) < 2:  # the cols kernel reads the rows kernel's scratch
         _lib.check(run(_lib.FST_PHASE_BWD_ROWS, dims[1] | r), what)
     c = _fastest(lambda f: run(_lib.FST_PHASE_BWD_COLS, f), cols, dims[1] | r, what)
-    _cache[key] = r | c
+    _record(key, r | c)
     return r | c
 
 

@@ -130,3 +130,22 @@ def test_head_groups():
         assert all(a[1] == b[0] for a, b in zip(groups, groups[1:]))
     with pytest.raises(ValueError):
         head_groups(bf, 12, 24, 16)
+
+
+def test_cache_file_round_trip(tmp_path, monkeypatch):
+    """FST_AUTOTUNE_CACHE: a new choice is written to the file, and a fresh
+    cache reads it back instead of timing."""
+    path = str(tmp_path / "plans.json")
+    dims = (0, 3, 4, 12, 64, 0, 32, 16)
+    monkeypatch.setattr(tune, "_cache_path", path)
+    monkeypatch.setattr(tune, "_cache_loaded", False)
+    monkeypatch.setattr(tune, "_usable", lambda: True)
+    monkeypatch.setattr(tune, "_fastest", lambda run, cands, base, what: _lib.FST_PLAN_FWD_OCC2)
+    monkeypatch.setattr(tune, "plans", lambda *a: 0x3F00)
+    tune.clear()
+    assert tune.forward_plan(dims, None) == _lib.FST_PLAN_FWD_OCC2
+    tune.clear()
+    monkeypatch.setattr(tune, "_cache_loaded", False)
+    monkeypatch.setattr(tune, "_fastest", lambda *a: pytest.fail("a cached choice must not be timed"))
+    assert tune.forward_plan(dims, None) == _lib.FST_PLAN_FWD_OCC2
+    tune.clear()
