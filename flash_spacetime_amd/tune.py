@@ -179,7 +179,8 @@ def forward_plan(dims: Tuple[int, ...], run: Callable[[int], int]) -> int:
     key = shape_key("fwd", dims)
     known = _lookup(key)
     if known is not None or not _usable():
-        return known or 0
+        # a file written by another build may name variants this one lacks
+        return known & plans(dims[0], dims[3], dims[6], dims[7]) if known else 0
     cands = _candidates(plans(dims[0], dims[3], dims[6], dims[7]), _FWD_BITS)
     choice = _fastest(run, cands, dims[1], "flash_spacetime_forward (tuning)")
     _record(key, choice)
@@ -197,7 +198,7 @@ def backward_plan(dims: Tuple[int, ...], run: Callable[[int, int], int]) -> int:
     key = shape_key("bwd", dims)
     known = _lookup(key)
     if known is not None or not _usable():
-        return known or 0
+        return known & plans(dims[0], dims[3], dims[6], dims[7]) if known else 0
     mask = plans(dims[0], dims[3], dims[6], dims[7])
     rows, cols = _candidates(mask, _ROWS_BITS), _candidates(mask, _COLS_BITS)
     what = "flash_spacetime_backward (tuning)"
