@@ -69,6 +69,7 @@ SIGNATURES = {
         [_i, _i, _i, _i, _i, _i, _i, _i, _i, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _f,
          _vp, _vp, _vp, _vp, _vp, _vp, _vp, _sz, _vp],
     ),
+    "fst_max_event_len": (_i, [_i, _i, _i, _i, _i]),
     "fst_frequencies": (None, [_i, ctypes.POINTER(ctypes.c_float)]),
     "fst_last_error": (ctypes.c_char_p, []),
     "fst_version": (ctypes.c_char_p, []),

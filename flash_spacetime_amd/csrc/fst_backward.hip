@@ -108,6 +108,13 @@ __global__ __launch_bounds__(256, 1) void bwd_rows_kernel(BwdParams prm) {
   const RowAddr rx = row_addr_x(prm.ev, eb);  // q, k, v, dq
   const int row0 = eb.blk * Cfg::ROWS;
   const int i0 = row0 + 16 * tile;
+  if (event_refused(prm.ev, eb)) {
+    fill_rows_nan<T, D>(rx, ra, row0, min(row0 + Cfg::ROWS, len), H, tid, 256, reinterpret_cast<T*>(prm.dq),
+                        prm.rowsum);
+    float* part = prm.dw_part + (long)blockIdx.x * (D * C + D);
+    for (int e = tid; e < D * C + D; e += 256) part[e] = __builtin_nanf("");
+    return;
+  }
 
   T* Ks = reinterpret_cast<T*>(smem);
   T* Vs = Ks + HP * KC * Cfg::KV_ROW;
@@ -534,6 +541,11 @@ __global__ __launch_bounds__(256, 1) void bwd_cols_kernel(BwdParams prm) {
   const RowAddr rx = row_addr_x(ev, eb);  // q, k, v, dk, dv
   const int key0 = eb.blk * Cfg::KEYS;
   const int j0t = key0 + 16 * tile;
+  if (event_refused(ev, eb)) {
+    fill_rows_nan<T, D>(rx, rx, key0, min(key0 + Cfg::KEYS, len), H, tid, 256, reinterpret_cast<T*>(prm.dk), nullptr);
+    fill_rows_nan<T, D>(rx, rx, key0, min(key0 + Cfg::KEYS, len), H, tid, 256, reinterpret_cast<T*>(prm.dv), nullptr);
+    return;
+  }
 
   T* Qs = reinterpret_cast<T*>(smem);                 // [HP][KC][QO_ROW] bf16(q*scale)
   T* Os = Qs + HP * KC * Cfg::QO_ROW;                 // [HP][KC][QO_ROW] dO

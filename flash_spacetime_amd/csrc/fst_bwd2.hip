@@ -114,6 +114,12 @@ __global__ __launch_bounds__(64 * NW, (NW == 4 ? 2 : 1)) void bwd_rows2_kernel(B
   // rows past an event's last tile own none.
   const int nbv = len > 0 ? (len + 15) / 16 : (prm.ev.packed ? 0 : 1);
   float* part = eb.blk < nbv ? prm.dw_part + (long)(prm.ev.blkcum[eb.b] + eb.blk) * DCW : nullptr;
+  if (event_refused(prm.ev, eb)) {
+    fill_rows_nan<bf16, D>(rx, ra, i0, min(i0 + 16, len), H, tid, NT, dqg, prm.rowsum);
+    if (part)
+      for (int e = tid; e < DCW; e += NT) part[e] = __builtin_nanf("");
+    return;
+  }
   if (i0 >= len) {
     zero_tile_rows<bf16, D, NT>(prm.ev, rx, ra, i0, len, H, tid, dqg, prm.rowsum);
     if (part)
@@ -668,6 +674,11 @@ __global__ __launch_bounds__(256, OCC) void bwd_cols2_kernel(BwdParams prm) {
   const int last = len - 1;
   bf16* dkg = reinterpret_cast<bf16*>(prm.dk);
   bf16* dvg = reinterpret_cast<bf16*>(prm.dv);
+  if (event_refused(ev, eb)) {
+    fill_rows_nan<bf16, D>(rx, rx, k0, min(k0 + 16, len), H, tid, 256, dkg, nullptr);
+    fill_rows_nan<bf16, D>(rx, rx, k0, min(k0 + 16, len), H, tid, 256, dvg, nullptr);
+    return;
+  }
   if (k0 >= len) {
     zero_tile_rows<bf16, D>(ev, rx, rx, k0, len, H, tid, dkg, nullptr);
     zero_tile_rows<bf16, D>(ev, rx, rx, k0, len, H, tid, dvg, nullptr);

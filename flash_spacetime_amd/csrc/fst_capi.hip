@@ -158,20 +158,67 @@ __device__ void sort_steps(const EventSpec& ev, int32_t* perm, int* keys) {
   for (int i = t; i < B; i += 1024) perm[i] = kSortMax - 1 - (keys[i] & (kSortMax - 1));
 }
 
+// Packed offsets as the kernels read them: cus[b] = the running maximum of
+// cu[0 .. b], clamped to [0, T], so events never overlap, never leave the
+// tensor and their row blocks never outnumber the per-tile slots the
+// workspace sizes from T (ceil(T / rows) + B). *status = 1 when the caller's
+// offsets were malformed (cu[0] != 0, a decrease, or cu[B] > T); the tile
+// kernels then write NaN into every event's rows instead of computing.
+// cu[B] < T is allowed: tokens past cu[B] belong to no event and are left
+// unwritten.
+__device__ void sanitize_steps(const int32_t* cu, int B, int T, int32_t* cus, int32_t* status, int* buf,
+                               int& carry) {
+  const int t = threadIdx.x;
+  int bad = 0;
+  if (t == 0) carry = 0;
+  __syncthreads();
+  for (int base = 0; base <= B; base += 1024) {
+    const int b = base + t;
+    int x = 0;
+    if (b <= B) {
+      x = cu[b];
+      if (b == 0 ? x != 0 : x < cu[b - 1]) bad = 1;
+      if (b == B && x > T) bad = 1;
+    }
+    buf[t] = x;
+    __syncthreads();
+    for (int off = 1; off < 1024; off <<= 1) {
+      const int o = t >= off ? buf[t - off] : 0;
+      __syncthreads();
+      buf[t] = max(buf[t], o);
+      __syncthreads();
+    }
+    if (b <= B) cus[b] = min(max(carry, buf[t]), T);
+    __syncthreads();
+    if (t == 1023) carry = max(carry, buf[1023]);
+    __syncthreads();
+  }
+  bad = __syncthreads_or(bad);
+  if (t == 0) *status = bad;
+}
+
 // The work list of one operator call in one launch (one workgroup, steps
 // separated by barriers, which also order the global writes of perm before
-// their reads): row-block prefix sums in event order for the row-block sizes
-// rows_a and, when blk_b is not null, rows_b; the length-sorted order perm;
-// for packed events the prefix sums in perm order (scum_a, scum_b), which
-// are the tile kernels' schedule.
+// their reads): for packed events the sanitised offsets and the call status
+// (sanitize_steps; padded calls get status 0); row-block prefix sums in
+// event order for the row-block sizes rows_a and, when blk_b is not null,
+// rows_b; the length-sorted order perm; for packed events the prefix sums in
+// perm order (scum_a, scum_b), which are the tile kernels' schedule.
 __global__ __launch_bounds__(1024) void worklist_kernel(const int32_t* lens, int packed, int B, int L, int T,
                                                         int rows_a, int32_t* blk_a, int rows_b, int32_t* blk_b,
-                                                        int32_t* perm, int32_t* scum_a, int32_t* scum_b) {
+                                                        int32_t* perm, int32_t* scum_a, int32_t* scum_b,
+                                                        int32_t* cus, int32_t* status) {
   extern __shared__ int keys[];
   __shared__ int buf[1024];
   __shared__ int carry;
+  if (packed) {
+    sanitize_steps(lens, B, T, cus, status, buf, carry);
+  } else if (threadIdx.x == 0) {
+    *status = 0;
+  }
+  __syncthreads();
   EventSpec ev;
-  ev.lens = lens;
+  ev.lens = packed ? cus : lens;
   ev.packed = packed;
   ev.B = B;
   ev.L = L;
@@ -186,7 +233,7 @@ __global__ __launch_bounds__(1024) void worklist_kernel(const int32_t* lens, int
 
 static int launch_worklist(const int32_t* lens, bool packed, int B, int L, int T, int rows_a, int32_t* blk_a,
                            int rows_b, int32_t* blk_b, int32_t* perm, int32_t* scum_a, int32_t* scum_b,
-                           hipStream_t st) {
+                           int32_t* cus, int32_t* status, hipStream_t st) {
   int p2 = 1;
   while (p2 < B && p2 < kSortMax) p2 <<= 1;
   const int lds = B > kSortMax ? 0 : p2 * (int)sizeof(int);
@@ -194,7 +241,7 @@ static int launch_worklist(const int32_t* lens, bool packed, int B, int L, int T
                           kSortMax * (int)sizeof(int)) != hipSuccess)
     return FST_ELAUNCH;
   hipLaunchKernelGGL(worklist_kernel, dim3(1), dim3(1024), lds, st, lens, packed ? 1 : 0, B, L, T, rows_a, blk_a,
-                     rows_b, blk_b, perm, packed ? scum_a : nullptr, packed ? scum_b : nullptr);
+                     rows_b, blk_b, perm, packed ? scum_a : nullptr, packed ? scum_b : nullptr, cus, status);
   return hipGetLastError() == hipSuccess ? FST_OK : FST_ELAUNCH;
 }
 
@@ -235,6 +282,18 @@ static int shape_plans(int dtype, int H, int D, int C) {
   return f(head_padding(H), C) | b(head_padding(H), C);
 }
 
+// Longest event whose rows of all heads the bf16 kernels can address with
+// 32-bit byte offsets: q, k, v rows (times 3 interleaved) and the u / w~
+// scratch of the cols kernel (C values per row and head) must span less than
+// 2^31 bytes. The same bound is kept for float32.
+static int max_event_len(int dtype, int flags, int H, int D, int C) {
+  const long long es = dtype == FST_BF16 ? 2 : 4;
+  const long long xd = (long long)D * ((flags & FST_QKV_INTERLEAVED) ? 3 : 1);
+  const long long span = (long long)H * es * (xd > C ? xd : C);
+  const long long m = ((1LL << 31) - 1) / span;
+  return m > 0x7fffffffLL ? 0x7fffffff : (int)m;
+}
+
 static int check_common(int dtype, int flags, int B, int H, int L, int T, int D, int C) {
   if (dtype != FST_BF16 && dtype != FST_F32) return fail(FST_EINVAL, "dtype must be FST_BF16 or FST_F32, got %d", dtype);
   if (flags & ~(FST_ATTN_BIAS | FST_ACT_BIAS | FST_PACKED | FST_TOKEN_MAJOR | FST_QKV_INTERLEAVED | FST_PLAN_MASK))
@@ -253,9 +312,9 @@ static int check_common(int dtype, int flags, int B, int H, int L, int T, int D,
   // loads over the event's span): a padded event's rows of every head must
   // span less than 2 GiB. Packed events are bounded by the caller (the
   // lengths live on the device).
-  const long long span = (long long)L * H * D * (dtype == FST_BF16 ? 2 : 4) * ((flags & FST_QKV_INTERLEAVED) ? 3 : 1);
-  if (!(flags & FST_PACKED) && span >= (1LL << 31))
-    return fail(FST_EUNSUPPORTED, "one padded event spans %lld bytes; the kernels address at most 2^31 - 1", span);
+  if (!(flags & FST_PACKED) && L > max_event_len(dtype, flags, H, D, C))
+    return fail(FST_EUNSUPPORTED, "padded events of %d tokens span 2^31 bytes or more (the kernels address at most %d "
+                "tokens of this layout)", L, max_event_len(dtype, flags, H, D, C));
   const int plan = flags & FST_PLAN_MASK;
   if (plan & ~shape_plans(dtype, H, D, C))
     return fail(FST_EUNSUPPORTED, "plan bits 0x%x are not compiled for dtype %d, H=%d, D=%d, C=%d", plan, dtype, H, D,
@@ -265,8 +324,22 @@ static int check_common(int dtype, int flags, int B, int H, int L, int T, int D,
 
 // Work list of one kernel family: blkcum [B+1] (row blocks in event order:
 // the slots of per-tile outputs), perm [B] (events by decreasing length),
-// scum [B+1] (packed: row blocks in perm order, the schedule).
-static size_t blkcum_bytes(int B) { return align_up((size_t)(3 * B + 2) * sizeof(int32_t), 256); }
+// scum [B+1] (packed: row blocks in perm order, the schedule), cus [B+1]
+// (packed: the sanitised offsets the kernels read), status [1].
+struct WorkList {
+  int32_t *blkcum, *perm, *scum, *cus, *status;
+};
+static size_t blkcum_bytes(int B) { return align_up((size_t)(4 * B + 4) * sizeof(int32_t), 256); }
+static WorkList worklist_at(void* base, int B) {
+  WorkList w;
+  w.blkcum = reinterpret_cast<int32_t*>(base);
+  w.perm = w.blkcum + (B + 1);
+  w.scum = w.perm + B;
+  w.cus = w.scum + (B + 1);
+  w.status = w.cus + (B + 1);
+  return w;
+}
+
 
 typedef int (*bwd_dispatch_fn)(const BwdParams&, int, int, int, hipStream_t, int, bool, int*);
 
@@ -395,6 +468,11 @@ void fst_frequencies(int C, float* out) {
   if (C > 0 && C <= 64 && C % 2 == 0 && out) frequencies(C, out);
 }
 
+int fst_max_event_len(int dtype, int flags, int H, int D, int C) {
+  if (check_common(dtype, flags & ~FST_PLAN_MASK, 0, H, 0, 0, D, C) != FST_OK) return 0;
+  return max_event_len(dtype, flags, H, D, C);
+}
+
 int fst_plans(int dtype, int H, int D, int C) {
   if (check_common(dtype, 0, 0, H, 0, 0, D, C) != FST_OK) return 0;
   return shape_plans(dtype, H, D, C);
@@ -449,21 +527,22 @@ int fst_forward_phases(int phases, int dtype, int flags, int B, int H, int L, in
   if (rc != FST_OK || rows <= 0)
     return fail(FST_EUNSUPPORTED, "no compiled kernel for dtype=%d H=%d D=%d C=%d", dtype, H, D, C);
 
-  int32_t* blkcum = reinterpret_cast<int32_t*>(workspace);
+  const WorkList wl = worklist_at(workspace, B);
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);
-  int32_t* perm = blkcum + (B + 1);
-  int32_t* scum = perm + B;
   if (phases & FST_PHASE_WORKLIST) {
-    if (launch_worklist(lens, packed, B, L, T, rows, blkcum, 0, nullptr, perm, scum, nullptr, st) != FST_OK)
+    if (launch_worklist(lens, packed, B, L, T, rows, wl.blkcum, 0, nullptr, wl.perm, wl.scum, nullptr, wl.cus,
+                        wl.status, st) != FST_OK)
       return fail(FST_ELAUNCH, "work-list kernel launch failed");
   }
 
   if (!(phases & FST_PHASE_FWD)) return FST_OK;
 
-  prm.ev.lens = lens;
-  prm.ev.blkcum = blkcum;
-  prm.ev.perm = perm;
-  prm.ev.scum = packed ? scum : nullptr;
+  prm.ev.lens = packed ? wl.cus : lens;
+  prm.ev.blkcum = wl.blkcum;
+  prm.ev.perm = wl.perm;
+  prm.ev.scum = packed ? wl.scum : nullptr;
+  prm.ev.status = wl.status;
+  prm.ev.max_len = max_event_len(dtype, flags, H, D, C);
   prm.ev.pos4 = reinterpret_cast<const float4*>(pos4);
   prm.ev.B = B;
   prm.ev.H = H;
@@ -540,24 +619,21 @@ int fst_backward_phases(int phases, int dtype, int flags, int B, int H, int L, i
   if (lay.grid_r > 0x7fffffffL || lay.grid_c > 0x7fffffffL) return fail(FST_EUNSUPPORTED, "problem too large");
 
   unsigned char* ws = reinterpret_cast<unsigned char*>(workspace);
-  int32_t* bc_r = reinterpret_cast<int32_t*>(ws + lay.off_bc_r);
-  int32_t* bc_c = reinterpret_cast<int32_t*>(ws + lay.off_bc_c);
-  int32_t* perm_r = bc_r + (B + 1);
-  int32_t* scum_r = perm_r + B;
-  int32_t* scum_c = bc_c + (B + 1) + B;
+  const WorkList wr = worklist_at(ws + lay.off_bc_r, B), wc = worklist_at(ws + lay.off_bc_c, B);
   if (phases & FST_PHASE_WORKLIST) {
-    if (launch_worklist(lens, packed, B, L, T, lay.rows_r, bc_r, lay.rows_c, bc_c, perm_r, scum_r, scum_c, st) !=
-        FST_OK)
+    if (launch_worklist(lens, packed, B, L, T, lay.rows_r, wr.blkcum, lay.rows_c, wc.blkcum, wr.perm, wr.scum,
+                        wc.scum, wr.cus, wr.status, st) != FST_OK)
       return fail(FST_ELAUNCH, "work-list kernel launch failed");
   }
 
-
   BwdParams prm;
   std::memset(&prm, 0, sizeof(prm));
-  prm.ev.lens = lens;
-  prm.ev.blkcum = bc_r;
-  prm.ev.perm = perm_r;
-  prm.ev.scum = packed ? scum_r : nullptr;
+  prm.ev.lens = packed ? wr.cus : lens;
+  prm.ev.blkcum = wr.blkcum;
+  prm.ev.perm = wr.perm;
+  prm.ev.scum = packed ? wr.scum : nullptr;
+  prm.ev.status = wr.status;
+  prm.ev.max_len = max_event_len(dtype, flags, H, D, C);
   prm.ev.pos4 = reinterpret_cast<const float4*>(pos4);
   prm.ev.B = B;
   prm.ev.H = H;
@@ -566,8 +642,8 @@ int fst_backward_phases(int phases, int dtype, int flags, int B, int H, int L, i
   prm.ev.packed = packed ? 1 : 0;
   prm.ev.tokmajor = (packed || (flags & FST_TOKEN_MAJOR)) ? 1 : 0;
   prm.ev.xmul = (flags & FST_QKV_INTERLEAVED) ? 3 : 1;
-  prm.blkcum_cols = bc_c;
-  prm.scum_cols = packed ? scum_c : nullptr;
+  prm.blkcum_cols = wc.blkcum;
+  prm.scum_cols = packed ? wc.scum : nullptr;
   prm.H = H;
   prm.flags = flags;
   prm.scale = scale;
@@ -610,7 +686,7 @@ int fst_backward_phases(int phases, int dtype, int flags, int B, int H, int L, i
     if (lay.nseg > 65535) return fail(FST_EUNSUPPORTED, "problem too large for the dW reduction");
     if (use_w && lay.nseg > 0)
       hipLaunchKernelGGL(dw_reduce_seg_kernel, dim3((ncol + 255) / 256, (unsigned)lay.nseg), dim3(256), 0, st,
-                         prm.dw_part, bc_r, B, ncol, seg);
+                         prm.dw_part, wr.blkcum, B, ncol, seg);
     hipLaunchKernelGGL(dw_reduce_final_kernel, dim3((ncol + 63) / 64), dim3(256), 0, st, seg, (int)lay.nseg, DC,
                        D, use_w ? 1 : 0, dweight, dbias);
     if (hipGetLastError() != hipSuccess) return fail(FST_ELAUNCH, "dW reduction launch failed");

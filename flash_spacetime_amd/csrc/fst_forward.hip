@@ -86,6 +86,11 @@ __global__ __launch_bounds__(256, 1) void fwd_kernel(FwdParams prm) {
 
   const int row0 = eb.blk * Cfg::ROWS;
   const int i0 = row0 + 16 * tile;  // first row of this wave's tile
+  if (event_refused(prm.ev, eb)) {
+    fill_rows_nan<T, D>(ra, ra, row0, min(row0 + Cfg::ROWS, len), H, tid, 256, reinterpret_cast<T*>(prm.out),
+                        prm.lse);
+    return;
+  }
 
   T* Vs = reinterpret_cast<T*>(smem);
   unsigned char* tbase = smem + Cfg::V_BYTES + tile * Cfg::TILE_BYTES;

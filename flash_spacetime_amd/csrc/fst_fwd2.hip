@@ -84,6 +84,10 @@ __global__ __launch_bounds__(256, OCC) void fwd2_kernel(FwdParams prm) {
   const int i0 = eb.blk * 16;
   const int last = len - 1;
   bf16* outg = reinterpret_cast<bf16*>(prm.out);
+  if (event_refused(prm.ev, eb)) {
+    fill_rows_nan<bf16, D>(ra, ra, i0, min(i0 + 16, len), H, tid, 256, outg, prm.lse);
+    return;
+  }
   if (i0 >= len) {  // a tile of padding rows only
     zero_tile_rows<bf16, D>(prm.ev, ra, ra, i0, len, H, tid, outg, prm.lse);
     return;

@@ -12,14 +12,16 @@ namespace fst {
 // [B, L, H]): the layout a [B, L, H*D] projection has before its heads are
 // split, so the heads-first views a model passes are read in place.
 struct EventSpec {
-  const int32_t* lens;    // seqlens [B] (padded) or cu_seqlens [B+1] (packed)
+  const int32_t* lens;    // seqlens [B] (padded) or the work list's sanitised cu_seqlens [B+1] (packed)
   const int32_t* blkcum;  // [B+1] prefix sums of row blocks per event
   const int32_t* perm;    // [B] events by decreasing length (the tile kernels' schedules)
   const int32_t* scum;    // [B+1] packed: prefix sums of row blocks in perm order (or null)
   const float4* pos4;     // [B*L] or [T] (x, y, z, t) fp32
+  const int32_t* status;  // the work list's verdict on the call's lengths: 0 = well formed (or null)
   int B, H, L, T, packed;
   int tokmajor;           // rows of one token's heads are adjacent (packed, or padded token-major)
   int xmul;               // 3: q, k, v (and dq, dk, dv) interleaved per token as [.., 3, H, X]; else 1
+  int max_len;            // longest event whose rows of all heads span less than 2^31 bytes
 };
 
 struct EventBlock {
@@ -36,9 +38,11 @@ struct RowAddr {
   __device__ __forceinline__ float4 pos(const float4* p4, int i) const { return p4[pos_base + i]; }
 };
 
-// Token range of event b, clamped into the tensor so that malformed
-// lengths can never address memory outside it: padded lengths to [0, L],
-// packed offsets to [0, T] and non-decreasing.
+// Token range of event b, clamped into the tensor: padded lengths to [0, L],
+// packed offsets to [0, T] and non-decreasing. The packed offsets the
+// kernels read are the work list's sanitised copy (running maximum of the
+// caller's offsets, clamped to [0, T]), so events never overlap and their
+// row blocks never outnumber the per-tile slots sized from T.
 __device__ __forceinline__ void event_range(const EventSpec& ev, int b, int& tok0, int& len) {
   if (ev.packed) {
     int a = ev.lens[b], e = ev.lens[b + 1];
@@ -51,6 +55,32 @@ __device__ __forceinline__ void event_range(const EventSpec& ev, int b, int& tok
     tok0 = 0;
     len = l < 0 ? 0 : (l > ev.L ? ev.L : l);
   }
+}
+
+// Whether the kernels refuse event eb and write NaN into its rows instead of
+// computing: the call's packed offsets were malformed (the work list found
+// cu_seqlens[0] != 0, a decreasing offset, or cu_seqlens[B] > T, and ran on
+// sanitised offsets so that no access leaves the tensors), or the event's
+// rows of all heads span 2^31 bytes or more, past the 32-bit byte offsets of
+// the buffer loads (which would read zeros there).
+__device__ __forceinline__ bool event_refused(const EventSpec& ev, const EventBlock& eb) {
+  return (ev.status && *ev.status != 0) || eb.len > ev.max_len;
+}
+
+// NaN into rows [r0, r1) of every head of a refused event: out (rows of
+// width X, addressed by ra) and vec (per-row scalars addressed by rv, when
+// not null).
+template <typename T, int X>
+__device__ void fill_rows_nan(const RowAddr& ra, const RowAddr& rv, int r0, int r1, int H, int tid, int nthreads,
+                              T* out, float* vec) {
+  if (r1 <= r0) return;
+  const int nr = r1 - r0;
+  for (int idx = tid; idx < H * nr * X; idx += nthreads) {
+    const int c = idx % X, r = (idx / X) % nr, h = idx / (X * nr);
+    out[ra.off(h, r0 + r, X) + c] = (T)__builtin_nanf("");
+  }
+  if (vec)
+    for (int idx = tid; idx < H * nr; idx += nthreads) vec[rv.vec(idx / nr, r0 + idx % nr)] = __builtin_nanf("");
 }
 
 // Work item of workgroup w: binary search of blkcum (blkcum[0] == 0).

@@ -202,11 +202,13 @@ class _Prepared:
         self.bias = bias.detach().to(torch.float32).contiguous() if bias is not None else None
         self.lens = lens.to(device=q.device, dtype=torch.int32).contiguous()
         self.device = q.device
-        # The kernels address one event's rows (all heads) with 32-bit byte
-        # offsets. The C library refuses padded events past that; packed
-        # lengths live on the device, so the longest event is read back
-        # only when the whole batch could reach the limit.
-        row_bytes = heads * dim * q.element_size() * (3 if interleaved else 1)
+        # The kernels address one event's rows (all heads; q, k, v and the
+        # C-wide scratch) with 32-bit byte offsets. The C library refuses
+        # padded events past that, and for packed events writes NaN into the
+        # rows of an event past it; packed lengths live on the device, so the
+        # longest event is read back (to raise instead) only when the whole
+        # batch could reach the limit.
+        row_bytes = heads * q.element_size() * max(dim * (3 if interleaved else 1), c)
         if self.packed and self.tokens * row_bytes >= 2 ** 31:
             longest = int((self.lens[1:] - self.lens[:-1]).max()) if self.batch > 0 else 0
             if longest * row_bytes >= 2 ** 31:

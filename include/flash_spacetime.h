@@ -29,10 +29,18 @@
  *
  * Supported shapes: 1 <= H <= 16, D in {16, 32, 48, 64}, C in {16, 32, 48,
  * 64} (C even, sin/cos halves); see fst_supported(). Callers run more heads
- * as head groups of their own (the Python operators take any H). One event's rows of all
- * heads (times 3 with FST_QKV_INTERLEAVED) must span less than 2 GiB: the
- * kernels address them with 32-bit byte offsets. Padded calls beyond that
- * return FST_EUNSUPPORTED; packed events are the caller's to bound.
+ * as head groups of their own (the Python operators take any H). One event
+ * may hold at most fst_max_event_len() tokens: the kernels address an
+ * event's rows of all heads with 32-bit byte offsets. Padded calls beyond
+ * that return FST_EUNSUPPORTED; a packed event beyond it (its length lives on
+ * the device) gets NaN in its rows of out and lse (forward) or dq, dk, dv,
+ * rowsum and in dweight / dbias (backward) instead of results.
+ *
+ * Malformed packed offsets (cu_seqlens[0] != 0, a decreasing offset, or
+ * cu_seqlens[B] > T) never make the kernels access memory outside the
+ * tensors or the workspace: the work list runs on their running maximum
+ * clamped to [0, T] and every row the kernels write gets NaN (as above).
+ * Tokens past cu_seqlens[B] < T belong to no event and are not written.
  *
  * Return value: 0 on success, a negative FST_E* code otherwise; the message
  * of the last failure on the calling thread is in fst_last_error().
@@ -168,6 +176,13 @@ int fst_backward_phases(int phases, int dtype, int flags, int B, int H, int L, i
                         float scale, void* dq, void* dk, void* dv, float* dweight,
                         float* dbias, float* rowsum, void* workspace,
                         size_t workspace_bytes, void* stream);
+
+/* Longest event (in tokens) the kernels take for this dtype, flags and shape:
+ * an event's rows of all heads -- q, k, v (three times D wide with
+ * FST_QKV_INTERLEAVED) and the C-wide scratch of the backward -- must span
+ * less than 2^31 bytes. Host-only, no GPU call. No reference counterpart
+ * (the reference's Triton kernels state no bound). */
+int fst_max_event_len(int dtype, int flags, int H, int D, int C);
 
 /* The fp32 frequency ladder exp(-i ln(1e4) / (C/2)), i < C/2, that the kernels
  * embed with, written to out[0 .. C/2). Counterpart of sinusoidal_frequencies

@@ -22,7 +22,11 @@ How each function is pinned (tests/test_oracle.py):
     the L = 1 closed form, bias-shift invariance;
   * chunked fp64 forward/backward: equality with autograd through the eager
     restatement, `torch.autograd.gradcheck`, and the closed forms
-    (L = 1 gradients, db, rowsum(dS) = 0).
+    (L = 1 gradients, db, rowsum(dS) = 0);
+  * the row-block evaluator `event_rows_fp64`: its blocks summed over an
+    event equal the chunked whole-event evaluators, and a block's gradients
+    equal those of the whole event with the upstream gradient zeroed
+    outside the block.
 """
 
 from .spec import (  # noqa: F401
@@ -33,6 +37,7 @@ from .spec import (  # noqa: F401
     attention,
     attention_fp64_chunked,
     backward_fp64_chunked,
+    event_rows_fp64,
     float_padding_mask,
     frequencies,
     pair_angle,

@@ -368,3 +368,81 @@ def backward_fp64_chunked(
     if return_rowsum:
         return out + (rowsum,)
     return out
+
+
+def event_rows_fp64(
+    q: Tensor,
+    k: Tensor,
+    v: Tensor,
+    feats: Tensor,
+    weight: Tensor,
+    bias: Optional[Tensor],
+    grad_out: Optional[Tensor],
+    rows: Tuple[int, int],
+    scale: Optional[float] = None,
+    use_attn_bias: bool = True,
+    use_activation_bias: bool = True,
+) -> dict:
+    """float64 terms of one event restricted to the query rows [r0, r1).
+
+    q, k, v, grad_out: `[H, n, D]` (one event, valid tokens only); feats
+    `[n, F]`. Returns the rows' `out`, `lse` (over the logits that include
+    the `qt.b` term, like `attention_fp64_chunked`), `dq` and `rowsum`, and the
+    contributions of those rows to `dk`, `dv` (`[H, n, D]`), `dW` and `db`:
+    exactly the gradients of a call whose upstream gradient is zero outside
+    the block, since a row with dO_i = 0 has dP_i = 0, D_i = 0 and dS_i = 0
+    and adds nothing to any gradient (backward.py:3-32). The same
+    closed-form terms as `backward_fp64_chunked` (reference.py:106-167,
+    backward.py:155-168, 371-407, 600-622), evaluated for a row block only so
+    that events of thousands of tokens stay cheap; `tests/test_oracle.py`
+    checks the block sums against the whole-event evaluators.
+    """
+    r0, r1 = rows
+    head_dim = q.shape[-1]
+    s = head_dim ** -0.5 if scale is None else scale
+    qe = q.double().cpu() * s
+    ke = k.double().cpu()
+    ve = v.double().cpu()
+    fe = feats.cpu()
+    w64 = weight.double().cpu()
+    b64 = bias.double().cpu() if bias is not None else None
+    use_rel = use_attn_bias or use_activation_bias
+    qi = qe[:, r0:r1]
+    logits = qi @ ke.transpose(-1, -2)
+    emb = rel = None
+    if use_rel:
+        emb, rel = _row_block_pair_terms(fe[r0:r1], fe, w64, b64)
+        if use_attn_bias:
+            logits = logits + torch.einsum("hid,ijd->hij", qi, rel)
+    lse = torch.logsumexp(logits, -1)
+    probs = torch.exp(logits - lse[..., None])
+    out = probs @ ve
+    if use_activation_bias:
+        out = out + torch.einsum("hij,ijd->hid", probs, rel)
+    res = {"out": out, "lse": lse}
+    if grad_out is None:
+        return res
+    gi = grad_out.double().cpu()[:, r0:r1]
+    dprob = gi @ ve.transpose(-1, -2)
+    if use_activation_bias:
+        dprob = dprob + torch.einsum("hid,ijd->hij", gi, rel)
+    dsum = (probs * dprob).sum(-1, keepdim=True)
+    dlog = probs * (dprob - dsum)
+    dqi = dlog @ ke
+    if use_attn_bias:
+        dqi = dqi + torch.einsum("hij,ijd->hid", dlog, rel)
+    res["dq"] = dqi * s
+    res["rowsum"] = dlog.sum(-1)
+    res["dk"] = dlog.transpose(-1, -2) @ qi
+    res["dv"] = probs.transpose(-1, -2) @ gi
+    if use_rel:
+        drel = torch.zeros_like(rel)
+        if use_attn_bias:
+            drel = drel + torch.einsum("hij,hid->ijd", dlog, qi)
+        if use_activation_bias:
+            drel = drel + torch.einsum("hij,hid->ijd", probs, gi)
+        res["dW"] = torch.einsum("ijd,ijc->dc", drel, emb)
+        res["db"] = drel.sum((0, 1))
+    else:
+        res["dW"] = res["db"] = None
+    return res

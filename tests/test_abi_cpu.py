@@ -187,3 +187,55 @@ def test_mask_to_lengths_validation():
 def test_ctypes_pointer_widths():
     assert ctypes.sizeof(ctypes.c_void_p) == 8
     assert ctypes.sizeof(ctypes.c_size_t) == 8
+
+
+@needs_lib
+@pytest.mark.parametrize("dtype,es", [(_lib.FST_BF16, 2), (_lib.FST_F32, 4)])
+@pytest.mark.parametrize("h,d,c,flags", [(12, 32, 16, 3), (16, 64, 16, 3 | _lib.FST_PACKED),
+                                          (16, 16, 64, 3 | _lib.FST_PACKED),
+                                          (8, 64, 64, 3 | _lib.FST_PACKED | _lib.FST_QKV_INTERLEAVED),
+                                          (1, 16, 16, 3)])
+def test_max_event_len_is_the_32bit_offset_bound(dtype, es, h, d, c, flags):
+    """The longest event the kernels take: its rows of all heads -- q, k, v
+    (3 D wide interleaved) and the C-wide scratch -- span less than 2^31
+    bytes, and one more token would not."""
+    lib = _lib.load()
+    n = lib.fst_max_event_len(dtype, flags, h, d, c)
+    width = max(d * (3 if flags & _lib.FST_QKV_INTERLEAVED else 1), c)
+    row = h * es * width
+    assert n * row < 2 ** 31 <= (n + 1) * row
+    if not flags & _lib.FST_PACKED:
+        # a padded call one token past it is refused before any launch
+        rc = lib.fst_forward(dtype, flags, 1, h, n + 1, 0, d, c, *([None] * 7), 1.0, None, None, None, 0, None)
+        assert rc == _lib.FST_EUNSUPPORTED and "2^31" in _lib.last_error()
+    assert lib.fst_max_event_len(dtype, 0, 17, d, c) == 0  # unsupported shapes report 0
+
+
+def _sanitised(cu, total):
+    """The work list's offsets: running maximum of cu, clamped to [0, T]."""
+    out, run = [], 0
+    for x in cu:
+        run = max(run, x)
+        out.append(min(run, total))
+    return out
+
+
+@pytest.mark.parametrize("seed", range(40))
+def test_sanitised_offsets_fit_the_tile_slots(seed):
+    """Malformed cu_seqlens (decreasing, out of range, overlapping events such
+    as [0, 800, 0, 1600]) must not make the per-tile slots outnumber the
+    ceil(T / 16) + B the backward workspace holds: on the sanitised offsets
+    events never overlap, so their 16-row tiles are at most T / 16 + B."""
+    gen = torch.Generator().manual_seed(seed)
+    b = int(torch.randint(1, 40, (1,), generator=gen))
+    total = int(torch.randint(0, 3000, (1,), generator=gen))
+    cu = torch.randint(-200, total + 400, (b + 1,), generator=gen).tolist()
+    if seed == 0:
+        cu, total = [0, 800, 0, 1600], 1600
+    s = _sanitised(cu, total)
+    assert all(0 <= a <= e <= total for a, e in zip(s, s[1:]))
+    tiles = sum(-(-(e - a) // 16) for a, e in zip(s, s[1:]))
+    assert tiles <= -(-total // 16) + b
+    naive = sum(-(-max(0, min(e, total) - max(0, min(a, total))) // 16) for a, e in zip(cu, cu[1:]))
+    if seed == 0:
+        assert naive > -(-total // 16) + b  # the advisor's overlap case overran before sanitising

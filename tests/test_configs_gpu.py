@@ -1,0 +1,132 @@
+"""configs[0] on the HIP path, and the north star's fp32 tolerance with the biases on.
+
+* B=4, L=64, H=2, D=32, C=16, q, k, v ~ N(0, 1),
+  x, y, z ~ U(-500, 500) and t ~ U(0, 2e4) (detector units: every
+  off-diagonal pair saturates the clip), W ~ N(0, 1/C) [D, C], b = 0, no
+  padding, seed 0, inputs drawn in the order q, k, v, pos, W, b, dO. The
+  reference runs this case in fp64 on the CPU; here the fp32 kernels (the
+  widest the library computes in; float64 operands are refused) and the
+  bf16 kernels run it through the autograd op against the float64 oracle.
+* fp32 with both bias terms (and each alone) at moderate shapes with
+  randn positions (about 15 % of pairs unsaturated, so E varies): every
+  output and gradient within 1e-4 relative of the float64 oracle, the
+  north star's fp32 bound, in padded and packed layouts.
+"""
+
+import pytest
+import torch
+
+import oracle
+from tests._cases import FLAGS, make_packed, make_padded, rel_err
+
+pytestmark = pytest.mark.gpu
+
+if torch.cuda.is_available():
+    from flash_spacetime_amd import flash_spacetime_attention, flash_spacetime_attention_varlen
+
+DEV = "cuda"
+FP32_REL = 1e-4  # north star: fp32 <= 1e-4 relative to the float64 reference
+BF16_REL = 2e-2  # north star: bf16 <= 2e-2 relative
+
+
+def _config0(seed=0):
+    gen = torch.Generator().manual_seed(seed)
+    B, L, H, D, C = 4, 64, 2, 32, 16
+    q = torch.randn(B, H, L, D, generator=gen, dtype=torch.float64)
+    k = torch.randn(B, H, L, D, generator=gen, dtype=torch.float64)
+    v = torch.randn(B, H, L, D, generator=gen, dtype=torch.float64)
+    xyz = (torch.rand(B, L, 3, generator=gen, dtype=torch.float64) - 0.5) * 1000.0
+    t = torch.rand(B, L, 1, generator=gen, dtype=torch.float64) * 2e4
+    feats = torch.cat([xyz, t], -1)
+    w = torch.randn(D, C, generator=gen, dtype=torch.float64) / C ** 0.5
+    b = torch.zeros(D, dtype=torch.float64)
+    seqlens = torch.full((B,), L, dtype=torch.long)
+    do = torch.randn(B, H, L, D, generator=gen, dtype=torch.float64)
+    return q, k, v, feats, w, b, seqlens, do
+
+
+def _run_padded(q, k, v, feats, w, b, seqlens, do, dtype, flags=(True, True)):
+    leaves = [x.to(DEV, dtype).requires_grad_(True) for x in (q, k, v)]
+    wl = w.to(DEV, torch.float32).requires_grad_(True)
+    bl = b.to(DEV, torch.float32).requires_grad_(True)
+    out = flash_spacetime_attention(*leaves, feats.to(DEV, torch.float32), wl, bl, seqlens.to(DEV),
+                                    use_attn_bias=flags[0], use_activation_bias=flags[1])
+    out.backward(do.to(DEV, dtype))
+    torch.cuda.synchronize()
+    return out.detach(), [x.grad for x in leaves] + [wl.grad, bl.grad]
+
+
+def _oracle(q, k, v, feats, w, b, seqlens, do, dtype, flags=(True, True), cu=None):
+    """float64 oracle on the inputs the kernels received (rounded to dtype)."""
+    r = lambda x: x.to(dtype).double()
+    kw = dict(use_attn_bias=flags[0], use_activation_bias=flags[1], cu_seqlens=cu)
+    qr, kr, vr, dor = r(q), r(k), r(v), r(do)
+    fr, wr, br = feats.float().double(), w.float().double(), b.float().double()
+    out, _ = oracle.attention_fp64_chunked(qr, kr, vr, fr, wr, br, seqlens, **kw)
+    if cu is None:
+        valid = oracle.valid_row_mask(q.shape[0], q.shape[2], seqlens)[:, None, :, None]
+        dor = dor * valid
+    grads = oracle.backward_fp64_chunked(qr, kr, vr, fr, wr, br, dor, seqlens, **kw)
+    return out, list(grads)
+
+
+def _assert_rel(names, got, want, tol):
+    for name, a, e in zip(names, got, want):
+        if e is None:
+            continue
+        err = rel_err(a, e)
+        assert err <= tol, f"{name}: relative error {err:.3e} > {tol:.0e}"
+
+
+@pytest.mark.parametrize("dtype,tol", [(torch.float32, FP32_REL), (torch.bfloat16, BF16_REL)], ids=["fp32", "bf16"])
+def test_config0_fwd_bwd(dtype, tol):
+    q, k, v, feats, w, b, seqlens, do = _config0()
+    out, grads = _run_padded(q, k, v, feats, w, b, seqlens, do, dtype)
+    ref_out, ref_grads = _oracle(q, k, v, feats, w, b, seqlens, do, dtype)
+    _assert_rel(["out", "dq", "dk", "dv", "dW", "db"], [out] + grads, [ref_out] + ref_grads, tol)
+    # b = 0 with the value term on: db = sum of dO over every row and head.
+    torch.testing.assert_close(grads[4].double().cpu(), do.to(dtype).double().sum((0, 1, 2)),
+                               rtol=1e-4 if dtype == torch.float32 else 2e-2, atol=1e-3)
+
+
+FP32_SHAPES = [
+    # (B, L, H, D, C, seed)
+    (3, 130, 12, 32, 16, 101),
+    (2, 96, 8, 64, 64, 102),
+    (4, 57, 4, 16, 48, 103),
+]
+
+
+@pytest.mark.parametrize("flags", FLAGS[:3], ids=["both", "attn", "act"])
+@pytest.mark.parametrize("shape", FP32_SHAPES, ids=lambda s: f"B{s[0]}L{s[1]}H{s[2]}D{s[3]}C{s[4]}")
+def test_fp32_tolerance_with_biases_padded(shape, flags):
+    B, L, H, D, C, seed = shape
+    case = make_padded(B, L, H, D, C, seed, masked=True, pos="normal")
+    do = torch.randn(B, H, L, D, generator=torch.Generator().manual_seed(seed + 7), dtype=torch.float64)
+    feats = case["feats"][..., :4]
+    out, grads = _run_padded(case["q"], case["k"], case["v"], feats, case["weight"], case["bias"] * 0.1,
+                             case["seqlens"], do, torch.float32, flags)
+    ref_out, ref_grads = _oracle(case["q"], case["k"], case["v"], feats, case["weight"], case["bias"] * 0.1,
+                                 case["seqlens"], do, torch.float32, flags)
+    valid = oracle.valid_row_mask(B, L, case["seqlens"])[:, None, :, None].to(DEV)
+    _assert_rel(["out", "dq", "dk", "dv", "dW", "db"], [out * valid] + grads, [ref_out] + ref_grads, FP32_REL)
+
+
+@pytest.mark.parametrize("flags", FLAGS[:1], ids=["both"])
+def test_fp32_tolerance_with_biases_packed(flags):
+    lens = [1, 40, 200, 77]
+    H, D, C = 12, 32, 16
+    case = make_packed(lens, H, D, C, 104, pos="normal")
+    do = torch.randn(case["q"].shape, generator=torch.Generator().manual_seed(9), dtype=torch.float64)
+    cu = case["cu"]
+    leaves = [case[n].to(DEV, torch.float32).requires_grad_(True) for n in ("q", "k", "v")]
+    wl = case["weight"].to(DEV, torch.float32).requires_grad_(True)
+    bl = (case["bias"] * 0.1).to(DEV, torch.float32).requires_grad_(True)
+    out = flash_spacetime_attention_varlen(*leaves, case["feats"].to(DEV, torch.float32), wl, bl, cu.to(DEV),
+                                           use_attn_bias=flags[0], use_activation_bias=flags[1])
+    out.backward(do.to(DEV, torch.float32))
+    torch.cuda.synchronize()
+    ref_out, ref_grads = _oracle(case["q"], case["k"], case["v"], case["feats"], case["weight"],
+                                 case["bias"] * 0.1, None, do, torch.float32, flags, cu=cu)
+    _assert_rel(["out", "dq", "dk", "dv", "dW", "db"], [out.detach()] + [x.grad for x in leaves] + [wl.grad, bl.grad],
+                [ref_out] + ref_grads, FP32_REL)

@@ -1,17 +1,28 @@
 """GPU checks at the BASELINE configurations' full sizes.
 
-The float64 oracle cannot evaluate these shapes in test time, so the full
-runs are checked through properties that do not depend on size, and events
-that are small enough are compared with the oracle one by one (events are
-independent, so an event's rows must equal the oracle on that event alone):
+The float64 oracle cannot evaluate whole batches of these shapes in test
+time, but events are independent and a row's results depend only on its
+own event, so events -- and blocks of an event's query rows -- are compared
+with the oracle one at a time (`oracle.event_rows_fp64`):
 
-* cfg2 (B=256, L=768, H=12, D=32, C=16, bf16, lengths U{16..768}) and cfg3
-  (4096 packed events, lognormal lengths in [1, 3000], >= 1 % of length 1):
-  finite results, padding rows exactly zero, sum_j dS_ij = 0 per row within
-  fp32 rounding, bitwise determinism, and sampled events against the oracle;
-* cfg4 (B=8, L=4096, H=8, D=C=64, q and k x30, fp32 and bf16): finite
-  results and gradients, the row sum of dS, and the padded result equal to
-  the packed one on the same events.
+* cfg2 (B=256, L=768, H=12, D=32, C=16, bf16, lengths U{16..768}): the
+  768-token event whole (out, dq, dk, dv), two short events, and dW / db of
+  the 768-token event from a second backward whose upstream gradient is
+  zero outside that event (a row with dO = 0 adds nothing to any gradient);
+* cfg3 (4096 packed events, lognormal lengths in [1, 3000], >= 1 % of
+  length 1): the longest event's first and middle 128-row blocks (out, dq),
+  its dk / dv / dW / db from a backward with dO zero outside the first
+  block, and two events of moderate length whole;
+* cfg4 (B=8, L=4096, H=8, D=C=64, q and k x30, fp32 and bf16): two 128-row
+  blocks of one event (out, dq) and the gradients of a 128-row block's
+  upstream gradient, fp32 within 1e-4 relative (the north star's fp32
+  bound), bf16 within 2e-2;
+
+plus size-independent properties over the whole batch: finite results,
+padding rows exactly zero, bitwise determinism, the padded result equal to
+the packed one. (The kernel's `rowsum` output is formed from the same fp32
+sums as D, so it is checked only loosely here; tests/test_selfconsistency_gpu.py
+measures sum_j dS as the products saw it.)
 """
 
 import math
@@ -60,28 +71,72 @@ def _rowsum_bound(n, do, v):
     return 64 * 2.0 ** -23 * n * do.float().abs().max().item() * (v.float().abs().max().item() + 10.0)
 
 
-def _check_event_against_oracle(q, k, v, feats, w, b, out, grads, do, sl, packed_tok0=None):
-    """One event, sliced from the batch, against the float64 oracle."""
+def _event(x, sl, packed_tok0=None):
+    """[H, n, X] rows of one event, float64 on the CPU."""
     if packed_tok0 is None:
         bi, n = sl
-        ev = lambda x: x[bi:bi + 1, :, :n].double().cpu()
-        fe = feats[bi:bi + 1, :n].double().cpu()
-        o, dq, dk, dv = ev(out), ev(grads[0]), ev(grads[1]), ev(grads[2])
-        g = ev(do)
-        qe, ke, ve = ev(q), ev(k), ev(v)
-    else:
-        t0, n = packed_tok0, sl
-        ev = lambda x: x[t0:t0 + n].double().cpu().permute(1, 0, 2).unsqueeze(0)
-        fe = feats[t0:t0 + n].double().cpu().unsqueeze(0)
-        o, dq, dk, dv = ev(out), ev(grads[0]), ev(grads[1]), ev(grads[2])
-        g = ev(do)
-        qe, ke, ve = ev(q), ev(k), ev(v)
-    leaves = [x.clone().requires_grad_(True) for x in (qe, ke, ve)]
-    ref = oracle.attention(*leaves, fe, w.double().cpu(), b.double().cpu())
-    ref.backward(g)
-    assert rel_err(o, ref.detach()) <= 2e-2
-    for got, leaf in zip((dq, dk, dv), leaves):
-        assert rel_err(got, leaf.grad) <= 2e-2
+        return x[bi, :, :n].double().cpu()
+    return x[packed_tok0:packed_tok0 + sl].double().cpu().transpose(0, 1)
+
+
+def _event_feats(feats, sl, packed_tok0=None):
+    if packed_tok0 is None:
+        bi, n = sl
+        return feats[bi, :n].double().cpu()
+    return feats[packed_tok0:packed_tok0 + sl].double().cpu()
+
+
+def _oracle_rows(q, k, v, feats, w, b, do, sl, rows, packed_tok0=None):
+    ev = lambda x: _event(x, sl, packed_tok0)
+    return oracle.event_rows_fp64(ev(q), ev(k), ev(v), _event_feats(feats, sl, packed_tok0), w.double().cpu(),
+                                  b.double().cpu(), None if do is None else ev(do), rows)
+
+
+def _check_event_against_oracle(q, k, v, feats, w, b, out, grads, do, sl, packed_tok0=None, tol=2e-2,
+                                block=128):
+    """One whole event against the float64 oracle (its row blocks in turn)."""
+    n = sl[1] if packed_tok0 is None else sl
+    ev = lambda x: _event(x, sl, packed_tok0)
+    dk = dv = 0
+    for r0 in range(0, n, block):
+        r1 = min(n, r0 + block)
+        ref = _oracle_rows(q, k, v, feats, w, b, do, sl, (r0, r1), packed_tok0)
+        assert rel_err(ev(out)[:, r0:r1], ref["out"]) <= tol
+        assert rel_err(ev(grads[0])[:, r0:r1], ref["dq"]) <= tol
+        dk = dk + ref["dk"]
+        dv = dv + ref["dv"]
+    assert rel_err(ev(grads[1]), dk) <= tol
+    assert rel_err(ev(grads[2]), dv) <= tol
+
+
+def _check_block(q, k, v, feats, w, b, out, dq, do, sl, rows, packed_tok0=None, tol=2e-2):
+    """out and dq of one block of an event's rows (a row's dq depends on its
+    own upstream gradient only, so the block's oracle terms give it under the
+    full dO)."""
+    ev = lambda x: _event(x, sl, packed_tok0)
+    r0, r1 = rows
+    ref = _oracle_rows(q, k, v, feats, w, b, do, sl, rows, packed_tok0)
+    e_out = rel_err(ev(out)[:, r0:r1], ref["out"])
+    e_dq = rel_err(ev(dq)[:, r0:r1], ref["dq"])
+    assert e_out <= tol and e_dq <= tol, f"rows {rows}: out {e_out:.3e}, dq {e_dq:.3e}"
+
+
+def _check_masked_grads(q, k, v, feats, w, b, grads_m, do, sl, rows, packed_tok0=None, tol=2e-2):
+    """dq of the block and dk, dv, dW, db of a backward whose upstream gradient
+    was zero outside the block, against the block's oracle terms."""
+    ev = lambda x: _event(x, sl, packed_tok0)
+    r0, r1 = rows
+    ref = _oracle_rows(q, k, v, feats, w, b, do, sl, rows, packed_tok0)
+    errs = {
+        "dq": rel_err(ev(grads_m[0])[:, r0:r1], ref["dq"]),
+        "dk": rel_err(ev(grads_m[1]), ref["dk"]),
+        "dv": rel_err(ev(grads_m[2]), ref["dv"]),
+        "dW": rel_err(grads_m[3], ref["dW"]),
+        "db": rel_err(grads_m[4], ref["db"]),
+    }
+    bad = {n_: e for n_, e in errs.items() if not e <= tol}
+    assert not bad, f"rows {rows}: {bad}"
+    return ref
 
 
 def test_cfg2_full_size():
@@ -99,8 +154,16 @@ def test_cfg2_full_size():
     assert rs.abs().max().item() <= _rowsum_bound(768, do, v)
     again = _fwd_bwd(q, k, v, feats, w, b, sl, do=do)
     assert torch.equal(out, again[0]) and all(torch.equal(a, c) for a, c in zip(grads[:4], again[2][:4]))
+    # The longest event whole, and two short ones.
+    _check_event_against_oracle(q, k, v, feats, w, b, out, grads, do, (1, lens[1]))
     _check_event_against_oracle(q, k, v, feats, w, b, out, grads, do, (0, lens[0]))
     _check_event_against_oracle(q, k, v, feats, w, b, out, grads, do, (2, lens[2]))
+    # dW / db of the 768-token event at full size: dO zero on every other event.
+    do_m = do.clone()
+    do_m[torch.arange(256, device=DEV) != 1] = 0
+    grads_m = flash_spacetime_backward(q, k, v, feats, w, b, sl, lse, do_m)
+    torch.cuda.synchronize()
+    _check_masked_grads(q, k, v, feats, w, b, grads_m, do_m, (1, lens[1]), (0, lens[1]))
 
 
 def _lognormal_lengths(n_events, seed, cap=3000):
@@ -135,10 +198,24 @@ def test_cfg3_full_size():
     one = lens.index(1)
     want = v[cu_list[one]].float() + (w[:, 8:].sum(1) + b)[None, :]
     torch.testing.assert_close(out[cu_list[one]].float(), want, atol=3e-2, rtol=2e-2)
-    # Two events of moderate length against the oracle.
+    # Two events of moderate length whole.
     picks = [i for i, n in enumerate(lens) if 50 <= n <= 200][:2]
     for i in picks:
         _check_event_against_oracle(q, k, v, feats, w, b, out, grads, do, lens[i], packed_tok0=cu_list[i])
+    # The longest event: two row blocks (out; dq under the full dO), and the
+    # gradients of its first block's upstream gradient alone.
+    li = max(range(len(lens)), key=lambda i: lens[i])
+    n, t0 = lens[li], cu_list[li]
+    assert n >= 1000
+    for rows in ((0, 128), (n // 2, n // 2 + 128)):
+        _check_block(q, k, v, feats, w, b, out, grads[0], do, n, rows, packed_tok0=t0)
+    do_m = torch.zeros_like(do)
+    do_m[t0:t0 + 128] = do[t0:t0 + 128]
+    grads_m = flash_spacetime_backward(q, k, v, feats, w, b, None, lse, do_m, cu_seqlens=cu)
+    torch.cuda.synchronize()
+    _check_masked_grads(q, k, v, feats, w, b, grads_m, do_m, n, (0, 128), packed_tok0=t0)
+    # dq of the block does not depend on other rows' dO.
+    assert torch.equal(grads_m[0][t0:t0 + 128], grads[0][t0:t0 + 128])
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16], ids=["fp32", "bf16"])
@@ -150,6 +227,17 @@ def test_cfg4_full_size(dtype):
     for gr in grads[:4]:
         assert torch.isfinite(gr).all()
     assert rowsum.abs().max().item() <= _rowsum_bound(4096, do, v)
+    tol = 1e-4 if dtype == torch.float32 else 2e-2
+    # One event's row blocks against the oracle, and a block's gradients.
+    ev = (3, 4096)
+    for rows in ((0, 128), (2048, 2176)):
+        _check_block(q, k, v, feats, w, b, out, grads[0], do, ev, rows, tol=tol)
+    do_m = torch.zeros_like(do)
+    do_m[3, :, 2048:2176] = do[3, :, 2048:2176]
+    grads_m = flash_spacetime_backward(q, k, v, feats, w, b, sl, lse, do_m)
+    torch.cuda.synchronize()
+    _check_masked_grads(q, k, v, feats, w, b, grads_m, do_m, ev, (2048, 2176), tol=tol)
+    assert torch.equal(grads_m[0][3, :, 2048:2176], grads[0][3, :, 2048:2176])
     # The same events packed: rows agree with the padded run.
     pk = lambda x: x.transpose(1, 2).reshape(-1, x.shape[1], x.shape[3]).contiguous()
     cu = torch.arange(0, 8 * 4096 + 1, 4096, dtype=torch.int32, device=DEV)

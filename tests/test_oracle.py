@@ -335,6 +335,55 @@ def test_backward_closed_forms_single_token(flags):
         assert db.abs().max() < 1e-12  # logit-only db vanishes (softmax shift)
 
 
+@pytest.mark.parametrize("flags", FLAGS)
+def test_event_rows_blocks_sum_to_whole_event(flags):
+    """The row-block evaluator, summed over blocks, equals the whole-event
+    chunked forward and backward (out, lse, dq, rowsum row by row; dk, dv, dW,
+    db as the sum of the blocks' contributions)."""
+    n = 19
+    q, k, v, feats, w, b, seqlens = _padded_case(1, n, 3, 16, 8, 61)
+    g = torch.randn(q.shape, dtype=torch.float64, generator=torch.Generator().manual_seed(5))
+    kw = dict(use_attn_bias=flags[0], use_activation_bias=flags[1])
+    out, lse = oracle.attention_fp64_chunked(q, k, v, feats, w, b, seqlens, **kw)
+    dq, dk, dv, dW, db, rs = oracle.backward_fp64_chunked(q, k, v, feats, w, b, g, seqlens, return_rowsum=True,
+                                                          **kw)
+    acc = {"dk": 0, "dv": 0, "dW": 0, "db": 0}
+    for r0, r1 in ((0, 7), (7, 8), (8, 19)):
+        blk = oracle.event_rows_fp64(q[0], k[0], v[0], feats[0], w, b, g[0], (r0, r1), **kw)
+        torch.testing.assert_close(blk["out"], out[0, :, r0:r1], rtol=1e-12, atol=1e-12)
+        torch.testing.assert_close(blk["lse"], lse[0, :, r0:r1], rtol=1e-12, atol=1e-12)
+        torch.testing.assert_close(blk["dq"], dq[0, :, r0:r1], rtol=1e-11, atol=1e-11)
+        torch.testing.assert_close(blk["rowsum"], rs[0, :, r0:r1], rtol=0, atol=1e-12)
+        for name in acc:
+            if blk[name] is not None:
+                acc[name] = acc[name] + blk[name]
+    torch.testing.assert_close(acc["dk"], dk[0], rtol=1e-11, atol=1e-11)
+    torch.testing.assert_close(acc["dv"], dv[0], rtol=1e-11, atol=1e-11)
+    if flags[0] or flags[1]:
+        torch.testing.assert_close(acc["dW"], dW, rtol=1e-11, atol=1e-11)
+        torch.testing.assert_close(acc["db"], db, rtol=1e-11, atol=1e-11)
+
+
+def test_event_rows_block_is_the_masked_upstream_gradient():
+    """A block's gradient contributions are the gradients of the whole event
+    under an upstream gradient that is zero outside the block (autograd
+    through the eager restatement)."""
+    n, r0, r1 = 11, 3, 8
+    q, k, v, feats, w, b, _ = _padded_case(1, n, 2, 8, 6, 71)
+    g = torch.randn(q.shape, dtype=torch.float64, generator=torch.Generator().manual_seed(6))
+    g[:, :, :r0] = 0
+    g[:, :, r1:] = 0
+    leaves = [t.clone().requires_grad_(True) for t in (q, k, v, w, b)]
+    out = oracle.attention(leaves[0], leaves[1], leaves[2], feats, leaves[3], leaves[4])
+    (out * g).sum().backward()
+    blk = oracle.event_rows_fp64(q[0], k[0], v[0], feats[0], w, b, g[0], (r0, r1))
+    torch.testing.assert_close(blk["dq"], leaves[0].grad[0, :, r0:r1], rtol=1e-10, atol=1e-10)
+    torch.testing.assert_close(blk["dk"], leaves[1].grad[0], rtol=1e-10, atol=1e-10)
+    torch.testing.assert_close(blk["dv"], leaves[2].grad[0], rtol=1e-10, atol=1e-10)
+    torch.testing.assert_close(blk["dW"], leaves[3].grad, rtol=1e-10, atol=1e-10)
+    torch.testing.assert_close(blk["db"], leaves[4].grad, rtol=1e-10, atol=1e-10)
+
+
 # ------------------------------------------- planted mistakes must be caught
 
 
