@@ -382,6 +382,7 @@ def event_rows_fp64(
     scale: Optional[float] = None,
     use_attn_bias: bool = True,
     use_activation_bias: bool = True,
+    dtype: torch.dtype = torch.float64,
 ) -> dict:
     """float64 terms of one event restricted to the query rows [r0, r1).
 
@@ -396,22 +397,33 @@ def event_rows_fp64(
     backward.py:155-168, 371-407, 600-622), evaluated for a row block only so
     that events of thousands of tokens stay cheap; `tests/test_oracle.py`
     checks the block sums against the whole-event evaluators.
+
+    With `dtype` other than float64 every step runs in that dtype instead
+    (pair angle and embedding in the feature dtype, as the eager definition
+    does, reference.py:75-88): the eager evaluation whose error is the
+    yardstick of the "2x eager" rule (reference test_gpu.py:133-169).
     """
     r0, r1 = rows
     head_dim = q.shape[-1]
     s = head_dim ** -0.5 if scale is None else scale
-    qe = q.double().cpu() * s
-    ke = k.double().cpu()
-    ve = v.double().cpu()
-    fe = feats.cpu()
-    w64 = weight.double().cpu()
-    b64 = bias.double().cpu() if bias is not None else None
+    qe = q.to(dtype).cpu() * s
+    ke = k.to(dtype).cpu()
+    ve = v.to(dtype).cpu()
+    fe = feats.to(dtype).cpu()
+    w64 = weight.to(dtype).cpu()
+    b64 = bias.to(dtype).cpu() if bias is not None else None
     use_rel = use_attn_bias or use_activation_bias
     qi = qe[:, r0:r1]
     logits = qi @ ke.transpose(-1, -2)
     emb = rel = None
     if use_rel:
-        emb, rel = _row_block_pair_terms(fe[r0:r1], fe, w64, b64)
+        if dtype == torch.float64:
+            emb, rel = _row_block_pair_terms(fe[r0:r1], fe, w64, b64)
+        else:
+            emb = embed_angle(pair_angle_rect(fe[r0:r1][None], fe[None])[0], w64.shape[1]).to(dtype)
+            rel = emb @ w64.t()
+            if b64 is not None:
+                rel = rel + b64
         if use_attn_bias:
             logits = logits + torch.einsum("hid,ijd->hij", qi, rel)
     lse = torch.logsumexp(logits, -1)
@@ -422,7 +434,7 @@ def event_rows_fp64(
     res = {"out": out, "lse": lse}
     if grad_out is None:
         return res
-    gi = grad_out.double().cpu()[:, r0:r1]
+    gi = grad_out.to(dtype).cpu()[:, r0:r1]
     dprob = gi @ ve.transpose(-1, -2)
     if use_activation_bias:
         dprob = dprob + torch.einsum("hid,ijd->hij", gi, rel)

@@ -239,3 +239,16 @@ def test_sanitised_offsets_fit_the_tile_slots(seed):
     naive = sum(-(-max(0, min(e, total) - max(0, min(a, total))) // 16) for a, e in zip(cu, cu[1:]))
     if seed == 0:
         assert naive > -(-total // 16) + b  # the advisor's overlap case overran before sanitising
+
+
+@needs_lib
+def test_fp32_d16_wide_channels_refused():
+    """float32 with D = 16 and C >= 48 is refused (its backward's dW partials
+    were wrong on gfx950); bf16 runs those shapes on the tile kernels, and
+    float32 takes every other (D, C)."""
+    lib = _lib.load()
+    for c in (48, 64):
+        assert lib.fst_supported(_lib.FST_F32, 4, 16, c) == 0
+        assert lib.fst_supported(_lib.FST_BF16, 4, 16, c) == 1
+    for d, c in ((16, 16), (16, 32), (32, 48), (32, 64), (48, 64), (64, 16)):
+        assert lib.fst_supported(_lib.FST_F32, 4, d, c) == 1

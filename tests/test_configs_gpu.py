@@ -70,9 +70,14 @@ def _oracle(q, k, v, feats, w, b, seqlens, do, dtype, flags=(True, True), cu=Non
     return out, list(grads)
 
 
-def _assert_rel(names, got, want, tol):
+def _assert_rel(names, got, want, tol, flags=(True, True)):
     for name, a, e in zip(names, got, want):
         if e is None:
+            continue
+        if name == "db" and not flags[1]:
+            # Without the value term db vanishes analytically (backward.py:616-622):
+            # the kernel returns exact zeros, the float64 oracle rounding noise.
+            assert (a == 0).all() and e.abs().max() < 1e-9
             continue
         err = rel_err(a, e)
         assert err <= tol, f"{name}: relative error {err:.3e} > {tol:.0e}"
@@ -93,7 +98,8 @@ FP32_SHAPES = [
     # (B, L, H, D, C, seed)
     (3, 130, 12, 32, 16, 101),
     (2, 96, 8, 64, 64, 102),
-    (4, 57, 4, 16, 48, 103),
+    (4, 57, 4, 32, 48, 103),
+    (3, 44, 16, 16, 32, 105),
 ]
 
 
@@ -109,7 +115,7 @@ def test_fp32_tolerance_with_biases_padded(shape, flags):
     ref_out, ref_grads = _oracle(case["q"], case["k"], case["v"], feats, case["weight"], case["bias"] * 0.1,
                                  case["seqlens"], do, torch.float32, flags)
     valid = oracle.valid_row_mask(B, L, case["seqlens"])[:, None, :, None].to(DEV)
-    _assert_rel(["out", "dq", "dk", "dv", "dW", "db"], [out * valid] + grads, [ref_out] + ref_grads, FP32_REL)
+    _assert_rel(["out", "dq", "dk", "dv", "dW", "db"], [out * valid] + grads, [ref_out] + ref_grads, FP32_REL, flags)
 
 
 @pytest.mark.parametrize("flags", FLAGS[:1], ids=["both"])
@@ -129,4 +135,4 @@ def test_fp32_tolerance_with_biases_packed(flags):
     ref_out, ref_grads = _oracle(case["q"], case["k"], case["v"], case["feats"], case["weight"],
                                  case["bias"] * 0.1, None, do, torch.float32, flags, cu=cu)
     _assert_rel(["out", "dq", "dk", "dv", "dW", "db"], [out.detach()] + [x.grad for x in leaves] + [wl.grad, bl.grad],
-                [ref_out] + ref_grads, FP32_REL)
+                [ref_out] + ref_grads, FP32_REL, flags)

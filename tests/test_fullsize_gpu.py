@@ -15,8 +15,10 @@ with the oracle one at a time (`oracle.event_rows_fp64`):
   block, and two events of moderate length whole;
 * cfg4 (B=8, L=4096, H=8, D=C=64, q and k x30, fp32 and bf16): two 128-row
   blocks of one event (out, dq) and the gradients of a 128-row block's
-  upstream gradient, fp32 within 1e-4 relative (the north star's fp32
-  bound), bf16 within 2e-2;
+  upstream gradient, bf16 within 2e-2, fp32 within the north star's 1e-4
+  or twice the error of the exact float32 evaluation of the same block,
+  whichever is larger (at logits of O(1e4) that evaluation's dq is off by
+  ~2e-4);
 
 plus size-independent properties over the whole batch: finite results,
 padding rows exactly zero, bitwise determinism, the padded result equal to
@@ -86,10 +88,21 @@ def _event_feats(feats, sl, packed_tok0=None):
     return feats[packed_tok0:packed_tok0 + sl].double().cpu()
 
 
-def _oracle_rows(q, k, v, feats, w, b, do, sl, rows, packed_tok0=None):
+def _oracle_rows(q, k, v, feats, w, b, do, sl, rows, packed_tok0=None, dtype=torch.float64):
     ev = lambda x: _event(x, sl, packed_tok0)
     return oracle.event_rows_fp64(ev(q), ev(k), ev(v), _event_feats(feats, sl, packed_tok0), w.double().cpu(),
-                                  b.double().cpu(), None if do is None else ev(do), rows)
+                                  b.double().cpu(), None if do is None else ev(do), rows, dtype=dtype)
+
+
+def _tolerances(ref, tol, names, eager=None):
+    """tol per quantity, or, when the same inputs evaluated eagerly in the
+    kernel's dtype are given, max(tol, 2 x that evaluation's error): the
+    north star's fp32 bound where fp32 arithmetic can reach it (at logits of
+    O(1e4), cfg4's q, k x30, the exact fp32 definition itself misses 1e-4 on
+    dq), the reference's 2x-eager rule beyond (test_gpu.py:133-169)."""
+    if eager is None:
+        return {n: tol for n in names}
+    return {n: max(tol, 2.0 * rel_err(eager[n], ref[n])) for n in names}
 
 
 def _check_event_against_oracle(q, k, v, feats, w, b, out, grads, do, sl, packed_tok0=None, tol=2e-2,
@@ -109,24 +122,32 @@ def _check_event_against_oracle(q, k, v, feats, w, b, out, grads, do, sl, packed
     assert rel_err(ev(grads[2]), dv) <= tol
 
 
-def _check_block(q, k, v, feats, w, b, out, dq, do, sl, rows, packed_tok0=None, tol=2e-2):
+def _check_block(q, k, v, feats, w, b, out, dq, do, sl, rows, packed_tok0=None, tol=2e-2, eager_dtype=None):
     """out and dq of one block of an event's rows (a row's dq depends on its
     own upstream gradient only, so the block's oracle terms give it under the
     full dO)."""
     ev = lambda x: _event(x, sl, packed_tok0)
     r0, r1 = rows
     ref = _oracle_rows(q, k, v, feats, w, b, do, sl, rows, packed_tok0)
+    eager = None if eager_dtype is None else _oracle_rows(q, k, v, feats, w, b, do, sl, rows, packed_tok0,
+                                                          eager_dtype)
+    tols = _tolerances(ref, tol, ("out", "dq"), eager)
     e_out = rel_err(ev(out)[:, r0:r1], ref["out"])
     e_dq = rel_err(ev(dq)[:, r0:r1], ref["dq"])
-    assert e_out <= tol and e_dq <= tol, f"rows {rows}: out {e_out:.3e}, dq {e_dq:.3e}"
+    print(f"rows {rows}: out {e_out:.2e} (tol {tols['out']:.1e}), dq {e_dq:.2e} (tol {tols['dq']:.1e})")
+    assert e_out <= tols["out"] and e_dq <= tols["dq"], f"rows {rows}: out {e_out:.3e}, dq {e_dq:.3e}"
 
 
-def _check_masked_grads(q, k, v, feats, w, b, grads_m, do, sl, rows, packed_tok0=None, tol=2e-2):
+def _check_masked_grads(q, k, v, feats, w, b, grads_m, do, sl, rows, packed_tok0=None, tol=2e-2,
+                        eager_dtype=None):
     """dq of the block and dk, dv, dW, db of a backward whose upstream gradient
     was zero outside the block, against the block's oracle terms."""
     ev = lambda x: _event(x, sl, packed_tok0)
     r0, r1 = rows
     ref = _oracle_rows(q, k, v, feats, w, b, do, sl, rows, packed_tok0)
+    eager = None if eager_dtype is None else _oracle_rows(q, k, v, feats, w, b, do, sl, rows, packed_tok0,
+                                                          eager_dtype)
+    tols = _tolerances(ref, tol, ("dq", "dk", "dv", "dW", "db"), eager)
     errs = {
         "dq": rel_err(ev(grads_m[0])[:, r0:r1], ref["dq"]),
         "dk": rel_err(ev(grads_m[1]), ref["dk"]),
@@ -134,7 +155,9 @@ def _check_masked_grads(q, k, v, feats, w, b, grads_m, do, sl, rows, packed_tok0
         "dW": rel_err(grads_m[3], ref["dW"]),
         "db": rel_err(grads_m[4], ref["db"]),
     }
-    bad = {n_: e for n_, e in errs.items() if not e <= tol}
+    print(f"rows {rows} (dO zero elsewhere): " + ", ".join(f"{n_} {e:.2e} (tol {tols[n_]:.1e})"
+                                                            for n_, e in errs.items()))
+    bad = {n_: e for n_, e in errs.items() if not e <= tols[n_]}
     assert not bad, f"rows {rows}: {bad}"
     return ref
 
@@ -228,15 +251,16 @@ def test_cfg4_full_size(dtype):
         assert torch.isfinite(gr).all()
     assert rowsum.abs().max().item() <= _rowsum_bound(4096, do, v)
     tol = 1e-4 if dtype == torch.float32 else 2e-2
+    eager_dtype = torch.float32 if dtype == torch.float32 else None
     # One event's row blocks against the oracle, and a block's gradients.
     ev = (3, 4096)
     for rows in ((0, 128), (2048, 2176)):
-        _check_block(q, k, v, feats, w, b, out, grads[0], do, ev, rows, tol=tol)
+        _check_block(q, k, v, feats, w, b, out, grads[0], do, ev, rows, tol=tol, eager_dtype=eager_dtype)
     do_m = torch.zeros_like(do)
     do_m[3, :, 2048:2176] = do[3, :, 2048:2176]
     grads_m = flash_spacetime_backward(q, k, v, feats, w, b, sl, lse, do_m)
     torch.cuda.synchronize()
-    _check_masked_grads(q, k, v, feats, w, b, grads_m, do_m, ev, (2048, 2176), tol=tol)
+    _check_masked_grads(q, k, v, feats, w, b, grads_m, do_m, ev, (2048, 2176), tol=tol, eager_dtype=eager_dtype)
     assert torch.equal(grads_m[0][3, :, 2048:2176], grads[0][3, :, 2048:2176])
     # The same events packed: rows agree with the padded run.
     pk = lambda x: x.transpose(1, 2).reshape(-1, x.shape[1], x.shape[3]).contiguous()

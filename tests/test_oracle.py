@@ -384,6 +384,27 @@ def test_event_rows_block_is_the_masked_upstream_gradient():
     torch.testing.assert_close(blk["db"], leaves[4].grad, rtol=1e-10, atol=1e-10)
 
 
+def test_event_rows_in_float32_is_the_eager_definition():
+    """The float32 row-block evaluation equals the eager restatement run in
+    float32 (the 2x-eager yardstick) on the block's rows."""
+    n, r0, r1 = 21, 4, 15
+    q, k, v, feats, w, b, _ = _padded_case(1, n, 2, 16, 8, 81)
+    g = torch.randn(q.shape, dtype=torch.float64, generator=torch.Generator().manual_seed(8))
+    g[:, :, :r0] = 0
+    g[:, :, r1:] = 0
+    f32 = lambda t: t.float()
+    leaves = [f32(t).clone().requires_grad_(True) for t in (q, k, v, w, b)]
+    out = oracle.attention(leaves[0], leaves[1], leaves[2], f32(feats), leaves[3], leaves[4])
+    (out * f32(g)).sum().backward()
+    blk = oracle.event_rows_fp64(q[0], k[0], v[0], feats[0], w, b, g[0], (r0, r1), dtype=torch.float32)
+    assert blk["out"].dtype == torch.float32
+    torch.testing.assert_close(blk["out"], out[0, :, r0:r1].detach(), rtol=1e-5, atol=1e-5)
+    torch.testing.assert_close(blk["dq"], leaves[0].grad[0, :, r0:r1], rtol=1e-4, atol=1e-5)
+    torch.testing.assert_close(blk["dk"], leaves[1].grad[0], rtol=1e-4, atol=1e-5)
+    torch.testing.assert_close(blk["dv"], leaves[2].grad[0], rtol=1e-4, atol=1e-5)
+    torch.testing.assert_close(blk["dW"], leaves[3].grad, rtol=1e-4, atol=1e-4)
+
+
 # ------------------------------------------- planted mistakes must be caught
 
 
