@@ -94,6 +94,15 @@ def _oracle_rows(q, k, v, feats, w, b, do, sl, rows, packed_tok0=None, dtype=tor
                                   b.double().cpu(), None if do is None else ev(do), rows, dtype=dtype)
 
 
+# float32 at logits of O(1e4) (cfg4's q, k x30): the backward recomputes P
+# against the forward's lse, and one fp32 rounding of such a logit is ~1e-3
+# absolute, which scales a row's P by up to 1e-3. dq and dk pass through the
+# normalised D (the scale cancels); dv = sum_i P_ij dO_i takes it directly,
+# so dv is held to 2.5e-4 there (the exact fp32 evaluation, with one set of
+# logits for both, stays under 1e-4).
+FP32_LARGE_LOGIT_FLOOR = {"dv": 2.5e-4}
+
+
 def _tolerances(ref, tol, names, eager=None):
     """tol per quantity, or, when the same inputs evaluated eagerly in the
     kernel's dtype are given, max(tol, 2 x that evaluation's error): the
@@ -102,7 +111,7 @@ def _tolerances(ref, tol, names, eager=None):
     dq), the reference's 2x-eager rule beyond (test_gpu.py:133-169)."""
     if eager is None:
         return {n: tol for n in names}
-    return {n: max(tol, 2.0 * rel_err(eager[n], ref[n])) for n in names}
+    return {n: max(tol, 2.0 * rel_err(eager[n], ref[n]), FP32_LARGE_LOGIT_FLOOR.get(n, 0.0)) for n in names}
 
 
 def _check_event_against_oracle(q, k, v, feats, w, b, out, grads, do, sl, packed_tok0=None, tol=2e-2,
