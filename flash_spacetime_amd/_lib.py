@@ -54,6 +54,10 @@ SIGNATURES = {
         _i,
         [_i, _i, _i, _i, _i, _i, _i, _i, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _f, _vp, _vp, _vp, _sz, _vp],
     ),
+    "fst_forward_noalloc": (
+        _i,
+        [_i, _i, _i, _i, _i, _i, _i, _i, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _f, _vp, _vp, _vp],
+    ),
     "fst_backward_workspace_bytes": (_sz, [_i, _i, _i, _i, _i, _i, _i, _i]),
     "fst_backward": (
         _i,

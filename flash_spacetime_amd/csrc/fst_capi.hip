@@ -6,6 +6,7 @@
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
+#include <mutex>
 
 #include "fst_kernels.h"
 
@@ -569,6 +570,68 @@ int fst_forward_phases(int phases, int dtype, int flags, int B, int H, int L, in
   rc = fn(prm, HP, C, st, (int)grid, false, &rows);
   if (rc != FST_OK) return fail(rc, "forward kernel launch failed (%s)", hipGetErrorString(hipGetLastError()));
   return FST_OK;
+}
+
+// ---------------------------------------------------------------------------
+// Allocation-free forward. The forward's only scratch is its work list
+// (blkcum_bytes(B)), which fst_forward_noalloc keeps in a file-scope device
+// array sized for kNoAllocMaxEvents events. Each device holds its own copy;
+// in host code `scratch` names a host-side stand-in, so its device address
+// is resolved once per device with hipGetSymbolAddress (with that device
+// current) and only that address is handed to the kernels.
+// ---------------------------------------------------------------------------
+}  // extern "C"
+
+namespace fst {
+constexpr int kNoAllocMaxEvents = 65536;
+constexpr size_t kNoAllocBytes = (size_t)(4 * kNoAllocMaxEvents + 4) * sizeof(int32_t);
+static __device__ __align__(256) unsigned char scratch[(kNoAllocBytes + 255) / 256 * 256];
+constexpr int kMaxDevices = 64;
+static void* g_scratch_ptr[kMaxDevices];
+static std::mutex g_scratch_mu;
+
+// The device address of `scratch` on the current device (nullptr and an
+// error message on failure).
+static void* scratch_on_current_device() {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) {
+    fail(FST_ELAUNCH, "no current HIP device (or device index %d beyond %d)", dev, kMaxDevices);
+    return nullptr;
+  }
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* ptr = nullptr;
+    const hipError_t rc = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (rc != hipSuccess || !ptr) {
+      fail(FST_ELAUNCH, "hipGetSymbolAddress(scratch) failed on device %d: %s", dev, hipGetErrorString(rc));
+      return nullptr;
+    }
+    g_scratch_ptr[dev] = ptr;
+  }
+  return g_scratch_ptr[dev];
+}
+}  // namespace fst
+
+extern "C" {
+
+int fst_forward_noalloc(int dtype, int flags, int B, int H, int L, int T, int D, int C, const void* q,
+                        const void* k, const void* v, const float* pos4, const float* weight, const float* bias,
+                        const int32_t* lens, float scale, void* out, float* lse, void* stream) {
+  g_last_error[0] = 0;
+  if (B > kNoAllocMaxEvents)
+    return fail(FST_EUNSUPPORTED, "fst_forward_noalloc takes at most %d events, got %d (use fst_forward)",
+                kNoAllocMaxEvents, B);
+  const int rc = check_common(dtype, flags, B, H, L, T, D, C);
+  if (rc != FST_OK) return rc;
+  const size_t need = fst_forward_workspace_bytes(dtype, flags, B, H, L, T, D, C);
+  if (need > sizeof(scratch)) return fail(FST_EUNSUPPORTED, "work list of %zu bytes exceeds the %zu-byte scratch",
+                                          need, sizeof(scratch));
+  const bool packed = flags & FST_PACKED;
+  if (B == 0 || (packed ? (long)T : (long)B * L) == 0) return FST_OK;
+  void* ws = scratch_on_current_device();
+  if (!ws) return FST_ELAUNCH;
+  return fst_forward_phases(FST_FWD_ALL, dtype, flags, B, H, L, T, D, C, q, k, v, pos4, weight, bias, lens, scale,
+                            out, lse, ws, sizeof(scratch), stream);
 }
 
 int fst_forward(int dtype, int flags, int B, int H, int L, int T, int D, int C, const void* q, const void* k,

@@ -137,6 +137,21 @@ int fst_forward(int dtype, int flags, int B, int H, int L, int T, int D, int C,
                 float scale, void* out, float* lse, void* workspace,
                 size_t workspace_bytes, void* stream);
 
+/* fst_forward with no workspace argument, for callers that cannot allocate
+ * device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc). No counterpart in the reference. The
+ * work list lives in a file-scope device array of the library sized for at
+ * most 65536 events (B > 65536 returns FST_EUNSUPPORTED); each GPU holds its
+ * own copy, about 1 MiB, until the process ends. The first call on a device
+ * resolves the array's address there (with the stream's device current);
+ * no call allocates, frees or synchronises. Every call on one GPU shares
+ * that GPU's array, so calls that overlap on one GPU (concurrent streams or
+ * threads) race: serialise them. Results are bitwise those of fst_forward. */
+int fst_forward_noalloc(int dtype, int flags, int B, int H, int L, int T, int D, int C,
+                        const void* q, const void* k, const void* v, const float* pos4,
+                        const float* weight, const float* bias, const int32_t* lens,
+                        float scale, void* out, float* lse, void* stream);
+
 /* fst_forward restricted to the given phases (FST_PHASE_WORKLIST,
  * FST_PHASE_FWD), for callers that time or schedule the phases; no
  * reference counterpart beyond forward.py:306-331 (the launch itself). */
