@@ -173,22 +173,31 @@ def calibration_copy(dev, nbytes=2 ** 30):
     del src, dst
 
 
-def cpu_baseline(inp, budget_s=15.0, max_events=B):
-    """The oracle's eager restatement of the spec (materialised R, autograd
-    backward), fp32, padded events of length L with the float mask exactly as
-    the eager module runs, timed one event at a time until the time budget is
-    spent; ms/step is extrapolated to the 256 events (eager padded cost is the
-    same for every event)."""
+def cpu_model():
+    """The host CPU's model name (/proc/cpuinfo), or the platform string."""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    import platform
+
+    return platform.processor() or platform.machine()
+
+
+def _cpu_eager_ms(inp, dtype, budget_s, max_events):
+    """Per-event ms of the oracle's eager fwd+bwd in `dtype` on the CPU,
+    one padded event at a time until the budget is spent; (ms, events)."""
     import oracle
 
-    torch.set_num_threads(os.cpu_count() or 1)
-    threads = torch.get_num_threads()
-    q = inp["q"].float().cpu()
-    k = inp["k"].float().cpu()
-    v = inp["v"].float().cpu()
+    q = inp["q"].to(dtype).cpu()
+    k = inp["k"].to(dtype).cpu()
+    v = inp["v"].to(dtype).cpu()
     feats = inp["feats"].float().cpu()
-    w, b = inp["w"].cpu(), inp["b"].cpu()
-    do = inp["do"].float().cpu()
+    w, b = inp["w"].to(dtype).cpu(), inp["b"].to(dtype).cpu()
+    do = inp["do"].to(dtype).cpu()
     valid = ~inp["pad_mask"].cpu()
     fmask = oracle.float_padding_mask(valid, torch.float32)
     done, t_total = 0, 0.0
@@ -198,18 +207,35 @@ def cpu_baseline(inp, budget_s=15.0, max_events=B):
         wl, bl = w.clone().requires_grad_(True), b.clone().requires_grad_(True)
         t0 = time.perf_counter()
         out = oracle.attention(*leaves, feats[sl], wl, bl, key_padding_mask=fmask[sl])
-        out.backward(do[sl] * valid[sl][:, None, :, None])
+        out.backward(do[sl] * valid[sl][:, None, :, None].to(dtype))
         t_total += time.perf_counter() - t0
         done += 1
-    per_event_ms = 1e3 * t_total / done
+    return 1e3 * t_total / done, done, t_total
+
+
+def cpu_baseline(inp, budget_s=15.0, max_events=B, bf16_budget_s=5.0):
+    """The oracle's eager restatement of the spec (materialised R, autograd
+    backward) on this host's CPU cores: fp32 (`value`) and bf16, padded
+    events of length L with the float mask exactly as the eager module runs,
+    timed one event at a time until each time budget is spent; ms/step is
+    extrapolated to the 256 events (eager padded cost is the same for every
+    event)."""
+    torch.set_num_threads(os.cpu_count() or 1)
+    threads = torch.get_num_threads()
+    ms32, n32, t32 = _cpu_eager_ms(inp, torch.float32, budget_s, max_events)
+    ms16, n16, t16 = _cpu_eager_ms(inp, torch.bfloat16, bf16_budget_s, max_events)
     return {
-        "value": per_event_ms * B,
+        "value": ms32 * B,
         "unit": "ms",
         "cores": threads,
+        "cpu_model": cpu_model(),
         "kind": "port",
-        "sample": f"{done} of {B} padded events (L={L}) fwd+bwd in fp32 eager PyTorch on the CPU "
-                  f"(oracle.attention + autograd, materialised [1,L,L,D] pair tensor), {1e3 * t_total:.0f} ms "
-                  f"total, extrapolated x{B}/{done}",
+        "sample": f"{n32} of {B} padded events (L={L}) fwd+bwd in fp32 eager PyTorch on the CPU "
+                  f"(oracle.attention + autograd, materialised [1,L,L,D] pair tensor), {1e3 * t32:.0f} ms "
+                  f"total, extrapolated x{B}/{n32}",
+        "bf16_value": ms16 * B,
+        "bf16_sample": f"{n16} of {B} events in bf16 (same restatement, bf16 operands), {1e3 * t16:.0f} ms total, "
+                       f"extrapolated x{B}/{n16}",
     }
 
 
@@ -300,6 +326,9 @@ def run_length_scaling(steps, warmup):
             step()
         torch.cuda.synchronize(dev)
         ms = time_events(step, steps, torch.cuda.current_stream(dev))
+        torch.cuda.synchronize(dev)
+        for t_ in (*leaves, wl, bl):
+            t_.grad = None
         torch.cuda.synchronize(dev)
         torch.cuda.reset_peak_memory_stats(dev)
         base = torch.cuda.memory_allocated(dev)
@@ -595,6 +624,12 @@ def main():
     ms = time_events(step, args.steps, stream)
     torch.cuda.synchronize(dev)
 
+    # The step's footprint above the resident inputs: the previous step's
+    # gradients are released before the baseline is read, so the gradients
+    # this step allocates count in the peak.
+    for t in (*leaves, wl, bl):
+        t.grad = None
+    torch.cuda.synchronize(dev)
     torch.cuda.reset_peak_memory_stats(dev)
     base = torch.cuda.memory_allocated(dev)
     step()
@@ -608,6 +643,7 @@ def main():
     mfma_pct = 100.0 * f_total / (ms * 1e-3) / (PEAK_BF16_TFLOPS * 1e12)
     dominant = max(("fwd", "bwd_rows", "bwd_cols"), key=lambda k_: kt[k_])
     achieved = flops[dominant] / (kt[dominant] * 1e-3) / 1e12
+    traffic = measured_traffic(dominant)
     result = {
         "metric": METRIC,
         "value": round(ms, 4),
@@ -640,7 +676,11 @@ def main():
             "peak": PEAK_BF16_TFLOPS,
             "unit": "TFLOP/s",
             "frac": round(achieved / PEAK_BF16_TFLOPS, 5),
-            "traffic": measured_traffic(dominant),
+            "traffic": traffic,
+            # HBM bytes per launch (rocprofv3 FETCH_SIZE + WRITE_SIZE, calibrated)
+            # over this run's launch duration, against the 8 TB/s peak.
+            "hbm_gbs": None if traffic is None else round(traffic / (kt[dominant] * 1e-3) / 1e9, 1),
+            "hbm_frac": None if traffic is None else round(traffic / (kt[dominant] * 1e-3) / 1e9 / PEAK_HBM_GBS, 4),
         },
     }
     if not args.no_cpu_baseline:
