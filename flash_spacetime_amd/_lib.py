@@ -22,13 +22,28 @@ FST_ACT_BIAS = 2
 FST_PACKED = 4
 FST_TOKEN_MAJOR = 8
 FST_QKV_INTERLEAVED = 16
+# Plan bits (include/flash_spacetime.h): one group per kernel knob, at most
+# one bit of a group set.
 FST_PLAN_FWD_OCC2 = 1 << 8
 FST_PLAN_FWD_OCC3 = 1 << 9
 FST_PLAN_ROWS_W4 = 1 << 10
 FST_PLAN_ROWS_W8 = 1 << 11
 FST_PLAN_COLS_OCC2 = 1 << 12
 FST_PLAN_COLS_OCC3 = 1 << 13
-FST_PLAN_MASK = 0x3F00
+FST_PLAN_ROWS_W8X2 = 1 << 14
+FST_PLAN_ROWS_KV_REG = 1 << 15
+FST_PLAN_ROWS_KV_LDS = 1 << 16
+FST_PLAN_FWD_KC16 = 1 << 17
+FST_PLAN_FWD_KC32 = 1 << 18
+FST_PLAN_FWD_T16 = 1 << 19
+FST_PLAN_FWD_T32 = 1 << 20
+FST_PLAN_FWD_T64 = 1 << 21
+FST_PLAN_BWD_T16 = 1 << 22
+FST_PLAN_BWD_T32 = 1 << 23
+FST_PLAN_BWD_T64 = 1 << 24
+FST_PLAN_BWD_KC16 = 1 << 25
+FST_PLAN_BWD_KC32 = 1 << 26
+FST_PLAN_MASK = 0x07FFFF00
 
 FST_PHASE_WORKLIST = 1
 FST_PHASE_FWD = 2
@@ -49,6 +64,7 @@ _vp, _i, _f, _sz = ctypes.c_void_p, ctypes.c_int, ctypes.c_float, ctypes.c_size_
 SIGNATURES = {
     "fst_supported": (_i, [_i, _i, _i, _i]),
     "fst_plans": (_i, [_i, _i, _i, _i]),
+    "fst_plan_supported": (_i, [_i, _i, _i, _i, _i]),
     "fst_forward_workspace_bytes": (_sz, [_i, _i, _i, _i, _i, _i, _i, _i]),
     "fst_forward": (
         _i,

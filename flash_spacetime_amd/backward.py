@@ -134,10 +134,10 @@ def flash_spacetime_backward(
     scale: Optional[float] = None,
     use_attn_bias: bool = True,
     use_activation_bias: bool = True,
-    block_m: int = 16,
-    block_n: int = 16,
-    num_warps: int = 8,
-    num_stages: int = 1,
+    block_m: Optional[int] = None,
+    block_n: Optional[int] = None,
+    num_warps: Optional[int] = None,
+    num_stages: Optional[int] = None,
     cu_seqlens: Optional[Tensor] = None,
     rowsum: Optional[Tensor] = None,
 ) -> Tuple[Tensor, Tensor, Tensor, Tensor, Optional[Tensor]]:
@@ -146,21 +146,28 @@ def flash_spacetime_backward(
     Gradients come back in the input dtypes (dW in the weight dtype, db in
     the bias dtype, or None without a bias). Upstream gradients on padding
     rows are ignored (backward.py:526-532). `rowsum`, if given (float32,
-    shaped like lse), receives sum_j dS_ij per row and head. The Triton
-    tuning arguments are accepted and ignored.
+    shaped like lse), receives sum_j dS_ij per row and head. The reference's
+    tile arguments select compiled kernel variants (tune.plan_from_tiles):
+    block_m the float32 kernels' rows (keys) per workgroup, block_n their
+    chunk, num_warps the bf16 rows kernel's waves per workgroup (4 or 8),
+    each the nearest offered value; None (the default here; the reference
+    defaults to 16, 16, 8) keeps the library's tuned or static choice, and
+    num_stages is accepted with no counterpart (loads run one chunk ahead).
     """
-    del block_m, block_n, num_warps, num_stages
+    del num_stages
     if q.dtype == torch.float16:  # the bf16 path, as the forward launcher runs it
         dq, dk, dv, dw, db = flash_spacetime_backward(
             *_bf16(q, k, v), feats, weight, bias, seqlens, lse, grad_out.to(torch.bfloat16), scale,
-            use_attn_bias, use_activation_bias, cu_seqlens=cu_seqlens, rowsum=rowsum)
+            use_attn_bias, use_activation_bias, block_m=block_m, block_n=block_n, num_warps=num_warps,
+            cu_seqlens=cu_seqlens, rowsum=rowsum)
         return dq.to(q.dtype), dk.to(q.dtype), dv.to(q.dtype), dw, db
     prep = _Prepared(q, k, v, feats, weight, bias, seqlens, scale, use_attn_bias,
                      use_activation_bias, cu_seqlens)
-    dq, dk, dv, dw, db = _run_backward(
-        prep.dims(), prep.q, prep.k, prep.v, prep.pos4, prep.weight, prep.bias, prep.lens,
-        _vec_in_layout(lse, prep.token_major), grad_out, prep.scale, prep.vec_shape(), rowsum,
-    )
+    with tune.tile_request(block_m, block_n, num_warps):
+        dq, dk, dv, dw, db = _run_backward(
+            prep.dims(), prep.q, prep.k, prep.v, prep.pos4, prep.weight, prep.bias, prep.lens,
+            _vec_in_layout(lse, prep.token_major), grad_out, prep.scale, prep.vec_shape(), rowsum,
+        )
     return (
         dq,
         dk,

@@ -745,16 +745,67 @@ __global__ __launch_bounds__(256, 1) void bwd_cols_kernel(BwdParams prm) {
 // ---------------------------------------------------------------------------
 // Dispatch.
 // ---------------------------------------------------------------------------
+// The static choice of each kernel is the (NW, NS) split with the best
+// operand reuse that fits LDS (as for the forward); the plan bits
+// FST_PLAN_BWD_T16 / T32 / T64 fix the rows (rows kernel) and keys (cols
+// kernel) per workgroup, FST_PLAN_BWD_KC16 / KC32 the keys (rows kernel) and
+// rows (cols kernel) per chunk, each kernel taking the first fitting value
+// of a group left empty.
 template <template <typename, int, int, int, int, int> class Cfg, typename T, int HP, int D, int C>
 struct BwdPick {
   template <int NW, int NS>
   using F = Cfg<T, HP, D, C, NW, NS>;
-  static constexpr int NS = (F<1, 2>::FITS || F<2, 2>::FITS || F<4, 2>::FITS) ? 2 : 1;
-  static constexpr int NW = F<1, NS>::FITS ? 1 : (F<2, NS>::FITS ? 2 : 4);
+  static constexpr int STATIC = pick_split<F>(0, 0);
+  static constexpr int NW = STATIC ? STATIC / 10 : 4, NS = STATIC ? STATIC % 10 : 1;
   using Sel = F<NW, NS>;
-  static constexpr bool OK = Sel::FITS;
+  static constexpr bool OK = STATIC != 0;
 };
 
+template <typename T, int HP, int D, int C, int NW, int NS>
+int bwd_launch_v(const BwdParams& prm, int which, hipStream_t stream, int grid, bool query, int* rows) {
+  using R = BwdRowsCfg<T, HP, D, C, NW, NS>;
+  using K = BwdColsCfg<T, HP, D, C, NW, NS>;
+  if (which == 0) {
+    if constexpr (!R::FITS) {
+      return FST_EUNSUPPORTED;
+    } else {
+      *rows = R::ROWS;
+      if (query) return FST_OK;
+      auto kern = bwd_rows_kernel<T, HP, D, C, NW, NS>;
+      if (hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, R::LDS_BYTES) !=
+          hipSuccess)
+        return FST_ELAUNCH;
+      if (grid > 0) hipLaunchKernelGGL(kern, dim3(grid), dim3(256), R::LDS_BYTES, stream, prm);
+      return hipGetLastError() == hipSuccess ? FST_OK : FST_ELAUNCH;
+    }
+  }
+  if constexpr (!K::FITS) {
+    return FST_EUNSUPPORTED;
+  } else {
+    *rows = K::KEYS;
+    if (query) return FST_OK;
+    auto kern = bwd_cols_kernel<T, HP, D, C, NW, NS>;
+    if (hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, K::LDS_BYTES) !=
+        hipSuccess)
+      return FST_ELAUNCH;
+    if (grid > 0) hipLaunchKernelGGL(kern, dim3(grid), dim3(256), K::LDS_BYTES, stream, prm);
+    return hipGetLastError() == hipSuccess ? FST_OK : FST_ELAUNCH;
+  }
+}
+
+// The FST_PLAN_BWD_* bits offered: a value of a group is offered when both
+// kernels have a fitting split with it.
+template <typename T, int HP, int D, int C>
+constexpr int bwd_split_plans() {
+  using PR = BwdPick<BwdRowsCfg, T, HP, D, C>;
+  using PC = BwdPick<BwdColsCfg, T, HP, D, C>;
+  return split_plans<PR::template F>(FST_PLAN_BWD_T16, FST_PLAN_BWD_KC16) &
+         split_plans<PC::template F>(FST_PLAN_BWD_T16, FST_PLAN_BWD_KC16);
+}
+
+// Launches (or, with query, only checks) the rows (which = 0) or cols
+// kernel's split that the plan bits of prm.flags name; *rows receives its
+// rows (keys) per workgroup.
 template <typename T, int HP, int D, int C>
 int bwd_launch_t(const BwdParams& prm, int which, hipStream_t stream, int grid, bool query, int* rows) {
   using PR = BwdPick<BwdRowsCfg, T, HP, D, C>;
@@ -766,31 +817,22 @@ int bwd_launch_t(const BwdParams& prm, int which, hipStream_t stream, int grid, 
   // is reported unsupported rather than computed. The reference itself takes
   // only C == D (forward.py:258-265).
   constexpr bool REFUSED = !is_bf16<T>::value && D == 16 && C >= 48;
+  *rows = 0;
   if constexpr (!PR::OK || !PC::OK || REFUSED) {
-    if (query) *rows = 0;
     return FST_EUNSUPPORTED;
   } else {
-    if (query) {
-      *rows = which == 0 ? PR::Sel::ROWS : PC::Sel::KEYS;
-      return FST_OK;
+    const int nw = plan_nw(prm.flags, bit_index(FST_PLAN_BWD_T16));
+    const int ns = plan_ns(prm.flags, bit_index(FST_PLAN_BWD_KC16));
+    const int split = which == 0 ? pick_split<PR::template F>(nw, ns) : pick_split<PC::template F>(nw, ns);
+    switch (split) {
+      case 11: return bwd_launch_v<T, HP, D, C, 1, 1>(prm, which, stream, grid, query, rows);
+      case 12: return bwd_launch_v<T, HP, D, C, 1, 2>(prm, which, stream, grid, query, rows);
+      case 21: return bwd_launch_v<T, HP, D, C, 2, 1>(prm, which, stream, grid, query, rows);
+      case 22: return bwd_launch_v<T, HP, D, C, 2, 2>(prm, which, stream, grid, query, rows);
+      case 41: return bwd_launch_v<T, HP, D, C, 4, 1>(prm, which, stream, grid, query, rows);
+      case 42: return bwd_launch_v<T, HP, D, C, 4, 2>(prm, which, stream, grid, query, rows);
+      default: return FST_EUNSUPPORTED;
     }
-    const void* kern;
-    int lds;
-    if (which == 0) {
-      kern = (const void*)bwd_rows_kernel<T, HP, D, C, PR::NW, PR::NS>;
-      lds = PR::Sel::LDS_BYTES;
-    } else {
-      kern = (const void*)bwd_cols_kernel<T, HP, D, C, PC::NW, PC::NS>;
-      lds = PC::Sel::LDS_BYTES;
-    }
-    if (hipFuncSetAttribute(kern, hipFuncAttributeMaxDynamicSharedMemorySize, lds) != hipSuccess) return FST_ELAUNCH;
-    if (grid > 0) {
-      if (which == 0)
-        hipLaunchKernelGGL((bwd_rows_kernel<T, HP, D, C, PR::NW, PR::NS>), dim3(grid), dim3(256), lds, stream, prm);
-      else
-        hipLaunchKernelGGL((bwd_cols_kernel<T, HP, D, C, PC::NW, PC::NS>), dim3(grid), dim3(256), lds, stream, prm);
-    }
-    return hipGetLastError() == hipSuccess ? FST_OK : FST_ELAUNCH;
   }
 }
 

@@ -60,11 +60,16 @@ namespace fst {
 // ---------------------------------------------------------------------------
 // NW waves of 64 lanes: 4 (two workgroups per CU), or 8 (one workgroup per
 // CU) where the state of a four-wave lane would not fit the registers
-// (Bwd2Pick). A wave is head-owner of HP / NW heads and row-owner of
-// RPW = 16 / NW rows.
-template <int HP, int D, int C, int KC, int NW = 4>
+// (Bwd2Pick). WPE: waves per SIMD the register plan is built for (2, or 4
+// for eight waves in two workgroups per CU). A wave is row-owner of RPW =
+// 16 / NW rows and head-owner of HW = ceil(HP / NW) heads, or HW - 1 for
+// the waves from NBIG on where NW does not divide HP; waves w and w + 4
+// share a SIMD, so with NBIG = 4 every SIMD owns the same number of heads.
+template <int HP, int D, int C, int KC, int NW = 4, int WPE = 2, bool KLV = false>
 struct Rows2Cfg {
-  static constexpr int HW = HP / NW, NS = KC / 16, NCT = C / 16, RPW = 16 / NW;
+  static constexpr int HW = (HP + NW - 1) / NW, NS = KC / 16, NCT = C / 16, RPW = 16 / NW;
+  static constexpr int NBIG = HP - NW * (HW - 1);
+  static constexpr int WG_PER_CU = 4 * WPE / NW;
   static constexpr int E_BYTES = ETile<C, KC>::BYTES;
   static constexpr int REGION = (KC / 4) * 16 * 16 * 16;  // one fp32 term of KC keys per (row, 16 head slots)
   static constexpr int SCAL_BYTES = 16 * 17 * 4;
@@ -77,22 +82,39 @@ struct Rows2Cfg {
   static constexpr int X_DW = DW_BYTES > XS_BYTES ? DW_BYTES : XS_BYTES;
   static constexpr int HG_BYTES = 16 * HP * 16 * 4;
   static constexpr int EPI = X_DW + HG_BYTES;
-  static constexpr int LDS_BYTES = MAIN > EPI ? MAIN : EPI;
-  static constexpr bool FITS = LDS_BYTES <= (NW == 4 ? 80 : 160) * 1024 && HP % NW == 0 && (NW == 4 || NW == 8);
+  static constexpr int LDS_BYTES = MAIN > EPI ? MAIN : EPI;  // dynamic
+  // KL (FST_PLAN_ROWS_KV_LDS): each chunk's K and V rows go straight to LDS
+  // (QoTile blocks, one per tensor, head and 32-feature part), where D is a
+  // multiple of 32, the chunk 16 keys and the blocks fit the LDS share. S and
+  // dP read them as row fragments and dQ reads K transposed, so no register
+  // holds the next chunk's operands and no transpose runs on the matrix core.
+  // The blocks are a static array of their own: the compiler then tells the
+  // loads into them apart from every other LDS access and does not wait for
+  // those loads before unrelated LDS reads and writes.
+  static constexpr bool KL = KLV;
+  static constexpr int KV_BYTES = 2 * HP * (D / 32) * 1024;
+  static constexpr int LDS_CAP = WG_PER_CU > 0 ? 160 * 1024 / WG_PER_CU : 0;
+  static constexpr bool FITS = (NW == 4 || NW == 8) && WG_PER_CU >= 1 && LDS_BYTES <= LDS_CAP &&
+                               (NBIG == NW || NBIG == 4) &&
+                               (!KL || (D % 32 == 0 && KC == 16 && LDS_BYTES + KV_BYTES <= LDS_CAP));
 };
 
-template <int HP, int D, int C, int KC, int HB, int FL, int NW>
-__global__ __launch_bounds__(64 * NW, (NW == 4 ? 2 : 1)) void bwd_rows2_kernel(BwdParams prm) {
-  using Cfg = Rows2Cfg<HP, D, C, KC, NW>;
+template <int HP, int D, int C, int KC, int HB, int FL, int NW, int WPE, bool KLV>
+__global__ __launch_bounds__(64 * NW, WPE) void bwd_rows2_kernel(BwdParams prm) {
+  using Cfg = Rows2Cfg<HP, D, C, KC, NW, WPE, KLV>;
   using ET = ETile<C, KC>;
   using DT = DTiles<D>;
   constexpr int HW = Cfg::HW, NS = Cfg::NS, NCT = Cfg::NCT, NQ = DT::NQ, RPW = Cfg::RPW, NT = 64 * NW;
   constexpr int DCW = D * C + D;
+  constexpr bool KL = Cfg::KL;
+  constexpr int NP = D / 32;  // 32-feature parts of a row (KL)
   extern __shared__ __align__(16) unsigned char smem[];
   bf16* Es = reinterpret_cast<bf16*>(smem);
   unsigned char* stU = smem + Cfg::E_BYTES;  // u.E, then P
   unsigned char* stW = stU + Cfg::REGION;    // w~.E + dob, then dS
   unsigned char* scal = stW + Cfg::REGION;   // increments of D
+  __shared__ __align__(16) unsigned char kv_lds[KL ? Cfg::KV_BYTES : 16];
+  unsigned char* kvt = kv_lds;  // KL: [K, V][head][part] QoTile blocks of the chunk
 
   const int tid = threadIdx.x;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63, g = lane >> 4, n = lane & 15;
@@ -127,6 +149,11 @@ __global__ __launch_bounds__(64 * NW, (NW == 4 ? 2 : 1)) void bwd_rows2_kernel(B
     return;
   }
   const int row0 = RPW * w;  // the row-owner's first row in the tile
+  // The wave's heads as head-owner: hw0 .. hw0 + nh - 1. A slot hl >= nh
+  // stands for no head (the padding slot 15, past H: only where HP < 16).
+  const int hw0 = w < Cfg::NBIG ? w * HW : Cfg::NBIG * HW + (w - Cfg::NBIG) * (HW - 1);
+  const int nh = w < Cfg::NBIG ? HW : HW - 1;
+  auto head = [&](int hl) __attribute__((always_inline)) { return hl < nh ? hw0 + hl : 15; };
 
   const bf16* __restrict__ qg = reinterpret_cast<const bf16*>(prm.q);
   const bf16* __restrict__ kg = reinterpret_cast<const bf16*>(prm.k);
@@ -150,7 +177,7 @@ __global__ __launch_bounds__(64 * NW, (NW == 4 ? 2 : 1)) void bwd_rows2_kernel(B
   const int rc = row_ok ? my_row : last;
 #pragma unroll
   for (int hl = 0; hl < HW; ++hl) {
-    const int hc = min(w * HW + hl, H - 1);
+    const int hc = min(head(hl), H - 1);
     qf[hl].load(qg + rx.off(hc, rc, D), g);
     dof[hl].load(dog + ra.off(hc, rc, D), g);
     lse2[hl] = prm.lse[ra.vec(hc, rc)];
@@ -191,19 +218,40 @@ __global__ __launch_bounds__(64 * NW, (NW == 4 ? 2 : 1)) void bwd_rows2_kernel(B
   int kvo[HW];
 #pragma unroll
   for (int hl = 0; hl < HW; ++hl)
-    kvo[hl] = (int)(min(w * HW + hl, H - 1) * rx.hs * D * 2) + n * rowb + kfrag_goff<D>(g);
-  KFrag<bf16, D> kf[HW][NS], vf[HW][NS];
+    kvo[hl] = (int)(min(head(hl), H - 1) * rx.hs * D * 2) + n * rowb + kfrag_goff<D>(g);
+  KFrag<bf16, D> kf[KL ? 1 : HW][NS], vf[KL ? 1 : HW][NS];
   float4 pj[NS];
+  // KL: lane l of a block load fetches the quarter QoTile keeps in slot l;
+  // keys past the event are clamped to its last key (their P is zero).
+  const int kl_r = lane >> 2, kl_c = (lane & 3) ^ QoTile::swz(kl_r);
   auto issue = [&](int jn) __attribute__((always_inline)) {
     const bool full = jn + KC <= len;
+    if constexpr (KL) {
+      const int rel = full ? kl_r * rowb : min(jn + kl_r, last) * rowb;
+      const int soff = full ? jn * rowb : 0;
 #pragma unroll
-    for (int hl = 0; hl < HW; ++hl) {
+      for (int hl = 0; hl < HW; ++hl) {
+        if (hl >= nh) break;
+        const int h = hw0 + hl;
+        const int voff = (int)(min(h, H - 1) * rx.hs * D * 2) + rel + 16 * kl_c;
 #pragma unroll
-      for (int s = 0; s < NS; ++s) {
-        const int voff = full ? kvo[hl] + 16 * s * rowb : kvo[hl] + (min(jn + 16 * s + n, last) - n) * rowb;
-        const int soff = full ? jn * rowb : 0;
-        load_kfrag<D>(kf[hl][s], kbuf, voff, soff);
-        load_kfrag<D>(vf[hl][s], vbuf, voff, soff);
+        for (int t = 0; t < NP; ++t) {
+          __builtin_amdgcn_raw_ptr_buffer_load_lds(kbuf.r, (__attribute__((address_space(3))) void*)(kvt + (h * NP + t) * 1024),
+                                                   16, voff + 64 * t, soff, 0, 0);
+          __builtin_amdgcn_raw_ptr_buffer_load_lds(vbuf.r, (__attribute__((address_space(3))) void*)(kvt + ((HP + h) * NP + t) * 1024),
+                                                   16, voff + 64 * t, soff, 0, 0);
+        }
+      }
+    } else {
+#pragma unroll
+      for (int hl = 0; hl < HW; ++hl) {
+#pragma unroll
+        for (int s = 0; s < NS; ++s) {
+          const int voff = full ? kvo[hl] + 16 * s * rowb : kvo[hl] + (min(jn + 16 * s + n, last) - n) * rowb;
+          const int soff = full ? jn * rowb : 0;
+          load_kfrag<D>(kf[hl][s], kbuf, voff, soff);
+          load_kfrag<D>(vf[hl][s], vbuf, voff, soff);
+        }
       }
     }
   };
@@ -226,7 +274,7 @@ __global__ __launch_bounds__(64 * NW, (NW == 4 ? 2 : 1)) void bwd_rows2_kernel(B
   bf16* qtg = reinterpret_cast<bf16*>(prm.qt);
 #pragma unroll
   for (int hl = 0; hl < HW; ++hl) {
-    const int h = w * HW + hl;
+    const int h = head(hl);
     const bool ok = h < H && row_ok;
     if (ok) {
       qf[hl].scale_by(prm.scale);
@@ -285,7 +333,7 @@ __global__ __launch_bounds__(64 * NW, (NW == 4 ? 2 : 1)) void bwd_rows2_kernel(B
       float xg[NS][4];
 #pragma unroll
       for (int s = 0; s < NS; ++s) group_gather(pair_angle_unit(pos_i, pj[s]), xg[s]);
-      issue_pos(j0 + KC);
+      if constexpr (!KL) issue_pos(j0 + KC);
 #pragma unroll
       for (int r = 0; r < RPW; ++r)
 #pragma unroll
@@ -316,24 +364,39 @@ __global__ __launch_bounds__(64 * NW, (NW == 4 ? 2 : 1)) void bwd_rows2_kernel(B
 
     // ---- head-owner: P, dP, online D, dS, dQ (phase by phase over batches
     // of HB heads, so the heads' dependency chains overlap) ----
+    // KL: this wave's K and V blocks (its own loads, issued after the
+    // previous chunk's second barrier) have landed.
+    if constexpr (KL) wait_vmem();
 #pragma unroll
     for (int hb = 0; hb < HW; hb += HB) {
+      if (hb >= nh) break;
       constexpr int NB = HB;
       f32x4 S[NB][NS], dP[NB][NS];
 #pragma unroll
       for (int b = 0; b < NB; ++b) {
         const int hl = hb + b;
-        const int h = w * HW + hl;
+        const int h = head(hl);
 #pragma unroll
         for (int s = 0; s < NS; ++s) {
-          if (hl >= HW) {
+          if (hl >= nh) {
             S[b][s] = dP[b][s] = zero4();
             continue;
           }
           const f32x4 ui = attn ? *reinterpret_cast<const f32x4*>(stU + stage_off(4 * s + g, n, h)) : zero4();
           const f32x4 wi = act ? *reinterpret_cast<const f32x4*>(stW + stage_off(4 * s + g, n, h)) : zero4();
-          S[b][s] = mma_k<D>(kf[hl][s], qf[hl], ui);
-          dP[b][s] = mma_k<D>(vf[hl][s], dof[hl], wi);
+          if constexpr (KL) {
+            KFrag<bf16, D> kc, vc;
+#pragma unroll
+            for (int t = 0; t < NP; ++t) {
+              kc.x32[t] = QoTile::row_frag(kvt + (h * NP + t) * 1024, g, n);
+              vc.x32[t] = QoTile::row_frag(kvt + ((HP + h) * NP + t) * 1024, g, n);
+            }
+            S[b][s] = mma_k<D>(kc, qf[hl], ui);
+            dP[b][s] = mma_k<D>(vc, dof[hl], wi);
+          } else {
+            S[b][s] = mma_k<D>(kf[hl][s], qf[hl], ui);
+            dP[b][s] = mma_k<D>(vf[hl][s], dof[hl], wi);
+          }
         }
       }
       float nt[NB], zt[NB];
@@ -358,7 +421,7 @@ __global__ __launch_bounds__(64 * NW, (NW == 4 ? 2 : 1)) void bwd_rows2_kernel(B
 #pragma unroll
       for (int b = 0; b < NB; ++b) {
         const int hl = hb + b;
-        if (hl >= HW) continue;
+        if (hl >= nh) continue;
         Nn[hl] += group_allsum(nt[b]);
         Zz[hl] += group_allsum(zt[b]);
         const float dn = Zz[hl] > 0.f ? Nn[hl] * __builtin_amdgcn_rcpf(Zz[hl]) : 0.f;
@@ -369,7 +432,7 @@ __global__ __launch_bounds__(64 * NW, (NW == 4 ? 2 : 1)) void bwd_rows2_kernel(B
 #pragma unroll
       for (int b = 0; b < NB; ++b) {
         const int hl = hb + b;
-        if (hl >= HW) continue;
+        if (hl >= nh) continue;
 #pragma unroll
         for (int s = 0; s < NS; ++s)
 #pragma unroll
@@ -380,11 +443,13 @@ __global__ __launch_bounds__(64 * NW, (NW == 4 ? 2 : 1)) void bwd_rows2_kernel(B
 #pragma unroll
       for (int b = 0; b < NB; ++b) {
         const int hl = hb + b;
-        if (hl >= HW) continue;
+        if (hl >= nh) continue;
 #pragma unroll
         for (int q = 0; q < NQ; ++q) {
           JFrag<bf16, NS> kt;
-          if constexpr (NS == 2)
+          if constexpr (KL)
+            kt.v = QoTile::tr_frag_dmap(kvt + (head(hl) * NP + (q >> 1)) * 1024, q, g, n);
+          else if constexpr (NS == 2)
             kt.v = cat8(transpose_x16(DT::part(kf[hl][0], q), id), transpose_x16(DT::part(kf[hl][1], q), id));
           else
             kt.v = transpose_x16(DT::part(kf[hl][0], q), id);
@@ -399,8 +464,8 @@ __global__ __launch_bounds__(64 * NW, (NW == 4 ? 2 : 1)) void bwd_rows2_kernel(B
 #pragma unroll
         for (int b = 0; b < NB; ++b) {
           const int hl = hb + b;
-          const int h = w * HW + hl;
-          if (hl >= HW) continue;
+          const int h = head(hl);
+          if (hl >= nh) continue;
 #pragma unroll
           for (int s = 0; s < NS; ++s) {
             bf16x4 pv, dv;
@@ -417,8 +482,13 @@ __global__ __launch_bounds__(64 * NW, (NW == 4 ? 2 : 1)) void bwd_rows2_kernel(B
         }
       }
     }
-    issue(j0 + KC);
+    if constexpr (!KL) issue(j0 + KC);
     __syncthreads();  // P, dS and D increments staged
+    // KL: the next chunk's positions go out here, its K and V loads at the
+    // end of the chunk: a barrier's release fence waits for loads into LDS,
+    // and so does every transposing LDS read the compiler cannot tell apart
+    // from their destination (the E reads below).
+    if constexpr (KL) issue_pos(j0 + KC);
 
     // ---- row-owner: H -= dD G; H += E^T dS; G += E^T P ----
     if (use_e) {
@@ -456,11 +526,15 @@ __global__ __launch_bounds__(64 * NW, (NW == 4 ? 2 : 1)) void bwd_rows2_kernel(B
         }
       }
     }
+    if constexpr (KL) issue(j0 + KC);
   };
 
   int j0 = 0;
   for (; j0 + KC <= len; j0 += KC) chunk(j0, std::false_type{});
   if (j0 < len) chunk(j0, std::true_type{});
+  // KL: the loads of the chunk past the last finish before the workgroup
+  // ends.
+  if constexpr (KL) wait_vmem();
 
   // ---- epilogue: sigma, D, dq = scale (dQ + W H + sigma b) ----
   // W (d on the lanes, the slots of H on the k index) and b, loaded before
@@ -482,7 +556,7 @@ __global__ __launch_bounds__(64 * NW, (NW == 4 ? 2 : 1)) void bwd_rows2_kernel(B
 #pragma unroll
   for (int hl = 0; hl < HW; ++hl) {
     sig[hl] = Nn[hl] - Dc[hl] * Zz[hl];
-    const int h = w * HW + hl;
+    const int h = head(hl);
     if (g == 0 && row_ok && h < H) {
       prm.dsum[ra.vec(h, my_row)] = Dc[hl];  // D - dob: the cols kernel's dS = P (dP~ - (D - dob))
       if (prm.rowsum) prm.rowsum[ra.vec(h, my_row)] = sig[hl];
@@ -505,7 +579,7 @@ __global__ __launch_bounds__(64 * NW, (NW == 4 ? 2 : 1)) void bwd_rows2_kernel(B
     }
 #pragma unroll
     for (int hl = 0; hl < HW; ++hl) {
-      const int h = w * HW + hl;
+      const int h = head(hl);
       f32x4 o = dQ[hl][q];
       if (attn && h < H) {
         o = o + *reinterpret_cast<const f32x4*>(stU + stage_off(g, n, h));
@@ -518,7 +592,7 @@ __global__ __launch_bounds__(64 * NW, (NW == 4 ? 2 : 1)) void bwd_rows2_kernel(B
   if (row_ok) {
 #pragma unroll
     for (int hl = 0; hl < HW; ++hl) {
-      const int h = w * HW + hl;
+      const int h = head(hl);
       if (h >= H) continue;
       bf16* orow = dqg + rx.off(h, my_row, D);
       if constexpr (DT::X32) {
@@ -557,7 +631,7 @@ __global__ __launch_bounds__(64 * NW, (NW == 4 ? 2 : 1)) void bwd_rows2_kernel(B
       if (!(op == 0 ? attn : act)) continue;
 #pragma unroll
       for (int hl = 0; hl < HW; ++hl) {
-        const int h = w * HW + hl;
+        const int h = head(hl);
         if (h < HP) (op == 0 ? qf[hl] : dof[hl]).store(Xs + (n * HP + h) * D, g);
       }
 #pragma unroll
@@ -1000,29 +1074,37 @@ struct Bwd2Pick {
   // eight-wave ones fit (spills remain only at HP = 16 with D, C >= 48).
   static constexpr int NW = (HP % 8 == 0 && rows_wave_load(HP, D, C) >= 160) ? 8 : 4;
   static constexpr bool OK = Rows2Cfg<HP, D, C, KC, NW>::FITS && Cols2Cfg<HP, D, C, RC>::FITS;
-  // Variants a caller may choose instead (FST_PLAN_ROWS_W4 / _W8,
-  // FST_PLAN_COLS_OCC2 / _OCC3); each computes every row with the same
-  // arithmetic. The rows kernel at HP heads offers four waves below the
-  // spilling load and eight where HP is a multiple of 8 (the library pads
-  // heads to 8 for that plan); the cols kernel offers three workgroups per CU
+  // Variants a caller may choose instead (the FST_PLAN_ROWS_* and
+  // FST_PLAN_COLS_* bits); each computes every row with the same arithmetic.
+  // The rows kernel at HP heads offers four waves below the spilling load,
+  // eight in one workgroup per CU where HP is a multiple of 8 (the library
+  // pads heads to 8 for that plan), eight in two workgroups per CU (four
+  // waves per SIMD, a 128-register lane budget) below the spilling load, and
+  // with either layout below the load its K and V rows staged in LDS where D
+  // is a multiple of 32; the cols kernel offers three workgroups per CU
   // where its LDS plan fits a third of the CU and the lane state is that of
   // the small layouts ((HP / 4) D + 3 C < 160).
-  static constexpr bool ROWS_W4 = Rows2Cfg<HP, D, C, KC, 4>::FITS && rows_wave_load(HP, D, C) < 160;
+  static constexpr bool LIGHT = rows_wave_load(HP, D, C) < 160;
+  static constexpr bool ROWS_W4 = Rows2Cfg<HP, D, C, KC, 4>::FITS && LIGHT;
   static constexpr bool ROWS_W8 = HP % 8 == 0 && Rows2Cfg<HP, D, C, KC, 8>::FITS;
+  static constexpr bool ROWS_W8X2 = Rows2Cfg<HP, D, C, KC, 8, 4>::FITS && LIGHT;
+  static constexpr bool KL_W4 = ROWS_W4 && Rows2Cfg<HP, D, C, KC, 4, 2, true>::FITS;
+  static constexpr bool KL_W8X2 = ROWS_W8X2 && Rows2Cfg<HP, D, C, KC, 8, 4, true>::FITS;
   using CC = Cols2Cfg<HP, D, C, RC>;
-  static constexpr bool COLS_OCC3 = CC::FITS && CC::LDS_BYTES <= 160 * 1024 / 3 && rows_wave_load(HP, D, C) < 160;
+  static constexpr bool COLS_OCC3 = CC::FITS && CC::LDS_BYTES <= 160 * 1024 / 3 && LIGHT;
   static constexpr int COLS_PLANS = CC::FITS ? (FST_PLAN_COLS_OCC2 | (COLS_OCC3 ? FST_PLAN_COLS_OCC3 : 0)) : 0;
 };
 
-template <int HP, int D, int C, int NW>
-int bwd2_launch_rows(const BwdParams& prm, hipStream_t stream, int g8) {
+template <int HP, int D, int C, int NW, int WPE, bool KL>
+int bwd2_launch_rows(const BwdParams& prm, hipStream_t stream, int g8, bool query) {
   using P = Bwd2Pick<HP, D, C>;
-  using Cfg = Rows2Cfg<HP, D, C, P::KC, NW>;
+  using Cfg = Rows2Cfg<HP, D, C, P::KC, NW, WPE, KL>;
   if constexpr (!Cfg::FITS) {
     return FST_EUNSUPPORTED;
   } else {
-    auto kern = (prm.flags & 3) == 3 ? bwd_rows2_kernel<HP, D, C, P::KC, P::HB, 3, NW>
-                                     : bwd_rows2_kernel<HP, D, C, P::KC, P::HB, -1, NW>;
+    if (query) return FST_OK;
+    auto kern = (prm.flags & 3) == 3 ? bwd_rows2_kernel<HP, D, C, P::KC, P::HB, 3, NW, WPE, KL>
+                                     : bwd_rows2_kernel<HP, D, C, P::KC, P::HB, -1, NW, WPE, KL>;
     if (hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, Cfg::LDS_BYTES) !=
         hipSuccess)
       return FST_ELAUNCH;
@@ -1032,9 +1114,10 @@ int bwd2_launch_rows(const BwdParams& prm, hipStream_t stream, int g8) {
 }
 
 template <int HP, int D, int C, int OCC>
-int bwd2_launch_cols(const BwdParams& prm, hipStream_t stream, int g8) {
+int bwd2_launch_cols(const BwdParams& prm, hipStream_t stream, int g8, bool query) {
   using P = Bwd2Pick<HP, D, C>;
   using Cfg = Cols2Cfg<HP, D, C, P::RC>;
+  if (query) return FST_OK;
   // One instance per bias-flag combination: a kernel reading the flags at
   // run time keeps both bias paths live and spills at the larger layouts.
   const int fl = prm.flags & 3;
@@ -1049,36 +1132,51 @@ int bwd2_launch_cols(const BwdParams& prm, hipStream_t stream, int g8) {
   return hipGetLastError() == hipSuccess ? FST_OK : FST_ELAUNCH;
 }
 
-// Launches the rows (which = 0) or cols (which = 1) kernel. For the rows
-// kernel HP is the rows head padding, which the library rounds to a multiple
-// of 8 when the eight-wave plan (static or chosen) runs.
+// Launches (or, with query, only checks) the rows (which = 0) or cols
+// (which = 1) kernel variant the plan bits of prm.flags name. For the rows
+// kernel HP is the rows head padding, which the library rounds to a
+// multiple of 8 when the eight-wave, one-workgroup plan (static or chosen)
+// runs.
 template <int HP, int D, int C>
-int bwd2_launch_t(const BwdParams& prm, int which, hipStream_t stream, int grid) {
+int bwd2_launch_t(const BwdParams& prm, int which, hipStream_t stream, int grid, bool query) {
   using P = Bwd2Pick<HP, D, C>;
   // The grid is rounded up to a multiple of 64 for the XCD schedules
   // (tile_block); logical blocks past the work list exit at once.
   const int g8 = grid > 0 ? (grid + 63) & ~63 : 0;
+  const int f = prm.flags;
   if (which == 0) {
-    // The plan bits were checked against the shape's plans by the caller.
-    const int nw = (prm.flags & FST_PLAN_ROWS_W8) ? 8 : (prm.flags & FST_PLAN_ROWS_W4) ? 4 : P::NW;
-    if (nw == 8) {
-      if constexpr (P::ROWS_W8) return bwd2_launch_rows<HP, D, C, 8>(prm, stream, g8);
+    const bool kl = f & FST_PLAN_ROWS_KV_LDS;
+    const int waves = (f & FST_PLAN_ROWS_W4)     ? 1
+                      : (f & FST_PLAN_ROWS_W8)   ? 2
+                      : (f & FST_PLAN_ROWS_W8X2) ? 3
+                                                 : (P::NW == 8 ? 2 : 1);
+    if (waves == 1) {
+      if constexpr (P::ROWS_W4) {
+        if (!kl) return bwd2_launch_rows<HP, D, C, 4, 2, false>(prm, stream, g8, query);
+        if constexpr (P::KL_W4) return bwd2_launch_rows<HP, D, C, 4, 2, true>(prm, stream, g8, query);
+      }
       return FST_EUNSUPPORTED;
     }
-    // Four waves run where they fit without spilling; elsewhere the library
-    // pads the heads to a multiple of 8 and runs eight (rows_head_padding).
-    if constexpr (P::ROWS_W4) return bwd2_launch_rows<HP, D, C, 4>(prm, stream, g8);
+    if (waves == 2) {
+      if constexpr (P::ROWS_W8)
+        if (!kl) return bwd2_launch_rows<HP, D, C, 8, 2, false>(prm, stream, g8, query);
+      return FST_EUNSUPPORTED;
+    }
+    if constexpr (P::ROWS_W8X2) {
+      if (!kl) return bwd2_launch_rows<HP, D, C, 8, 4, false>(prm, stream, g8, query);
+      if constexpr (P::KL_W8X2) return bwd2_launch_rows<HP, D, C, 8, 4, true>(prm, stream, g8, query);
+    }
     return FST_EUNSUPPORTED;
   }
   if constexpr (!P::CC::FITS) {
     return FST_EUNSUPPORTED;
   } else {
-    const int occ = (prm.flags & FST_PLAN_COLS_OCC2) ? 2 : (prm.flags & FST_PLAN_COLS_OCC3) ? 3 : P::CC::OCC;
+    const int occ = (f & FST_PLAN_COLS_OCC2) ? 2 : (f & FST_PLAN_COLS_OCC3) ? 3 : P::CC::OCC;
     if (occ == 3) {
-      if constexpr (P::COLS_OCC3 || P::CC::OCC == 3) return bwd2_launch_cols<HP, D, C, 3>(prm, stream, g8);
+      if constexpr (P::COLS_OCC3 || P::CC::OCC == 3) return bwd2_launch_cols<HP, D, C, 3>(prm, stream, g8, query);
       return FST_EUNSUPPORTED;
     }
-    return bwd2_launch_cols<HP, D, C, 2>(prm, stream, g8);
+    return bwd2_launch_cols<HP, D, C, 2>(prm, stream, g8, query);
   }
 }
 

@@ -16,15 +16,14 @@ namespace fst {
 int FST_CAT(bwd_dispatch_, FST_NAME)(const BwdParams& prm, int which, int HP, int C, hipStream_t stream, int grid,
                                      bool query, int* rows) {
   // bf16 runs the 16-row / 16-key tile kernels (fst_bwd2.hip) wherever their
-  // LDS plan fits; fp32 and the remaining shapes run fst_backward.hip.
+  // LDS plan fits; fp32 and the remaining shapes run fst_backward.hip. With
+  // query set nothing is launched: the plan bits of prm.flags are checked and
+  // *rows receives the rows (keys) per workgroup of the variant they name.
 #define FST_CASE(HPV, CV)                                                      \
   if (HP == HPV && C == CV) {                                                  \
     if constexpr (is_bf16<FST_T>::value && Bwd2Pick<HPV, FST_D, CV>::OK) {     \
-      if (query) {                                                             \
-        *rows = 16;                                                            \
-        return FST_OK;                                                         \
-      }                                                                        \
-      return bwd2_launch_t<HPV, FST_D, CV>(prm, which, stream, grid);          \
+      *rows = 16;                                                              \
+      return bwd2_launch_t<HPV, FST_D, CV>(prm, which, stream, grid, query);   \
     } else {                                                                   \
       return bwd_launch_t<FST_T, HPV, FST_D, CV>(prm, which, stream, grid, query, rows); \
     }                                                                          \
@@ -40,23 +39,27 @@ int FST_CAT(bwd_dispatch_, FST_NAME)(const BwdParams& prm, int which, int HP, in
   return FST_EUNSUPPORTED;
 }
 
-// FST_PLAN_ROWS_* / FST_PLAN_COLS_* bits compiled for head padding HP and C
-// channels. The eight-wave rows plan runs at HP rounded up to a multiple of 8.
+// FST_PLAN_ROWS_* / FST_PLAN_COLS_* / FST_PLAN_BWD_* bits compiled for head
+// padding HP and C channels. The eight-wave, one-workgroup rows plan runs
+// at HP rounded up to a multiple of 8.
 template <int HP, int C>
 static int bwd_plans_at() {
-  if constexpr (!is_bf16<FST_T>::value) {
-    return 0;
-  } else {
+  if constexpr (is_bf16<FST_T>::value && Bwd2Pick<HP, FST_D, C>::OK) {
     using P = Bwd2Pick<HP, FST_D, C>;
-    if constexpr (!P::OK) {
+    constexpr int HP8 = (HP + 7) / 8 * 8;
+    int plans = P::COLS_PLANS | FST_PLAN_ROWS_KV_REG;
+    if constexpr (P::ROWS_W4) plans |= FST_PLAN_ROWS_W4;
+    if constexpr (Bwd2Pick<HP8, FST_D, C>::OK && Bwd2Pick<HP8, FST_D, C>::ROWS_W8) plans |= FST_PLAN_ROWS_W8;
+    if constexpr (P::ROWS_W8X2) plans |= FST_PLAN_ROWS_W8X2;
+    if constexpr (P::KL_W4 || P::KL_W8X2) plans |= FST_PLAN_ROWS_KV_LDS;
+    return plans;
+  } else {
+    constexpr bool REFUSED = !is_bf16<FST_T>::value && FST_D == 16 && C >= 48;
+    if constexpr (REFUSED || !BwdPick<BwdRowsCfg, FST_T, HP, FST_D, C>::OK ||
+                  !BwdPick<BwdColsCfg, FST_T, HP, FST_D, C>::OK)
       return 0;
-    } else {
-      constexpr int HP8 = (HP + 7) / 8 * 8;
-      int plans = P::COLS_PLANS;
-      if constexpr (P::ROWS_W4) plans |= FST_PLAN_ROWS_W4;
-      if constexpr (Bwd2Pick<HP8, FST_D, C>::OK && Bwd2Pick<HP8, FST_D, C>::ROWS_W8) plans |= FST_PLAN_ROWS_W8;
-      return plans;
-    }
+    else
+      return bwd_split_plans<FST_T, HP, FST_D, C>();
   }
 }
 

@@ -33,13 +33,15 @@ static int head_padding(int H) { return H <= 4 ? 4 : (H <= 8 ? 8 : (H <= 12 ? 12
 // spill, heads are padded to the next multiple of 8 so that it runs eight
 // waves (padded heads compute on a real head's data and store nothing). The
 // cols kernel keeps head_padding: the scratch between them is laid out by H.
-// The eight-wave plan (FST_PLAN_ROWS_W8) pads to a multiple of 8 likewise;
-// the four-wave plan keeps head_padding.
+// The eight-wave, one-workgroup plan (FST_PLAN_ROWS_W8) pads to a multiple
+// of 8 likewise; the four-wave plan and the eight-wave, two-workgroup plan
+// (which gives waves 4 to 7 one head fewer where 8 does not divide the
+// padding) keep head_padding.
 static int rows_head_padding(int dtype, int flags, int H, int D, int C) {
   const int hp = head_padding(H);
   if (dtype != FST_BF16) return hp;
   if (flags & FST_PLAN_ROWS_W8) return (hp + 7) & ~7;
-  if (flags & FST_PLAN_ROWS_W4) return hp;
+  if (flags & (FST_PLAN_ROWS_W4 | FST_PLAN_ROWS_W8X2)) return hp;
   if (hp % 8 != 0 && rows_wave_load(hp, D, C) >= 160) return hp + 4;
   return hp;
 }
@@ -278,6 +280,13 @@ static int shape_plans(int dtype, int H, int D, int C) {
       case 48: f = fwd_plans_bf16_48; b = bwd_plans_bf16_48; break;
       case 64: f = fwd_plans_bf16_64; b = bwd_plans_bf16_64; break;
     }
+  } else if (dtype == FST_F32) {
+    switch (D) {
+      case 16: f = fwd_plans_f32_16; b = bwd_plans_f32_16; break;
+      case 32: f = fwd_plans_f32_32; b = bwd_plans_f32_32; break;
+      case 48: f = fwd_plans_f32_48; b = bwd_plans_f32_48; break;
+      case 64: f = fwd_plans_f32_64; b = bwd_plans_f32_64; break;
+    }
   }
   if (!f || H < 1 || H > 16) return 0;
   return f(head_padding(H), C) | b(head_padding(H), C);
@@ -295,12 +304,25 @@ static int max_event_len(int dtype, int flags, int H, int D, int C) {
   return m > 0x7fffffffLL ? 0x7fffffff : (int)m;
 }
 
+// The plan-bit groups of include/flash_spacetime.h: at most one bit each.
+static const int kPlanGroups[] = {
+    FST_PLAN_FWD_OCC2 | FST_PLAN_FWD_OCC3,
+    FST_PLAN_ROWS_W4 | FST_PLAN_ROWS_W8 | FST_PLAN_ROWS_W8X2,
+    FST_PLAN_COLS_OCC2 | FST_PLAN_COLS_OCC3,
+    FST_PLAN_ROWS_KV_REG | FST_PLAN_ROWS_KV_LDS,
+    FST_PLAN_FWD_KC16 | FST_PLAN_FWD_KC32,
+    FST_PLAN_FWD_T16 | FST_PLAN_FWD_T32 | FST_PLAN_FWD_T64,
+    FST_PLAN_BWD_T16 | FST_PLAN_BWD_T32 | FST_PLAN_BWD_T64,
+    FST_PLAN_BWD_KC16 | FST_PLAN_BWD_KC32,
+};
+
 static int check_common(int dtype, int flags, int B, int H, int L, int T, int D, int C) {
   if (dtype != FST_BF16 && dtype != FST_F32) return fail(FST_EINVAL, "dtype must be FST_BF16 or FST_F32, got %d", dtype);
   if (flags & ~(FST_ATTN_BIAS | FST_ACT_BIAS | FST_PACKED | FST_TOKEN_MAJOR | FST_QKV_INTERLEAVED | FST_PLAN_MASK))
     return fail(FST_EINVAL, "unknown flag bits 0x%x", flags);
-  for (int pair = FST_PLAN_FWD_OCC2 | FST_PLAN_FWD_OCC3; pair & FST_PLAN_MASK; pair <<= 2)
-    if ((flags & pair) == pair) return fail(FST_EINVAL, "plan bits 0x%x name two variants of one kernel", flags & pair);
+  for (int group : kPlanGroups)
+    if ((flags & group) & ((flags & group) - 1))
+      return fail(FST_EINVAL, "plan bits 0x%x name two variants of one kernel knob", flags & group);
   if ((flags & FST_QKV_INTERLEAVED) && !(flags & (FST_PACKED | FST_TOKEN_MAJOR)))
     return fail(FST_EINVAL, "FST_QKV_INTERLEAVED needs a token-major layout (FST_PACKED or FST_TOKEN_MAJOR)");
   if ((flags & FST_PACKED) && (flags & FST_TOKEN_MAJOR))
@@ -419,6 +441,7 @@ static int bwd_layout(int dtype, int flags, int B, int H, int L, int T, int D, i
   bwd_dispatch_fn fn = bwd_table(dtype, D);
   BwdParams dummy;
   std::memset(&dummy, 0, sizeof(dummy));
+  dummy.flags = flags;  // the queries resolve the plan bits
   const int HP = head_padding(H), HPR = rows_head_padding(dtype, flags, H, D, C);
   if (fn(dummy, 0, HPR, C, nullptr, 0, true, &lay.rows_r) != FST_OK || lay.rows_r <= 0) return FST_EUNSUPPORTED;
   if (fn(dummy, 1, HP, C, nullptr, 0, true, &lay.rows_c) != FST_OK || lay.rows_c <= 0) return FST_EUNSUPPORTED;
@@ -446,11 +469,16 @@ static int bwd_layout(int dtype, int flags, int B, int H, int L, int T, int D, i
   off += align_up((size_t)rows * H * 4, 256);
   lay.off_dsum = off;
   off += align_up((size_t)rows * H * 4, 256);
+  // The dW / db partials (one per rows-kernel workgroup) are sized for
+  // 16-row workgroups, the smallest of any plan, so that the workspace a
+  // caller sizes without plan bits serves every plan.
+  const long grid16 = packed ? ((long)T + 15) / 16 + B : B8 * ((L + 15) / 16);
+  const long nseg16 = (grid16 + kRedSeg - 1) / kRedSeg;
   lay.off_part = off;
-  off += align_up((size_t)(lay.grid_r > 0 ? lay.grid_r : 0) * (D * C + D) * 4, 256);
+  off += align_up((size_t)(grid16 > 0 ? grid16 : 0) * (D * C + D) * 4, 256);
   lay.nseg = lay.grid_r > 0 ? (lay.grid_r + kRedSeg - 1) / kRedSeg : 0;
   lay.off_seg = off;
-  off += align_up((size_t)lay.nseg * (D * C + D) * 4, 256);
+  off += align_up((size_t)(nseg16 > 0 ? nseg16 : 0) * (D * C + D) * 4, 256);
   lay.total = off;
   return FST_OK;
 }
@@ -477,6 +505,18 @@ int fst_max_event_len(int dtype, int flags, int H, int D, int C) {
 int fst_plans(int dtype, int H, int D, int C) {
   if (check_common(dtype, 0, 0, H, 0, 0, D, C) != FST_OK) return 0;
   return shape_plans(dtype, H, D, C);
+}
+
+int fst_plan_supported(int dtype, int H, int D, int C, int plan) {
+  if (plan & ~FST_PLAN_MASK) return 0;
+  if (check_common(dtype, plan, 0, H, 0, 0, D, C) != FST_OK) return 0;
+  int rows = 0;
+  FwdParams dummy;
+  std::memset(&dummy, 0, sizeof(dummy));
+  dummy.flags = plan;
+  if (fwd_table(dtype, D)(dummy, head_padding(H), C, nullptr, 0, true, &rows) != FST_OK || rows <= 0) return 0;
+  BwdLayout lay;
+  return bwd_layout(dtype, plan, 1, H, 16, 0, D, C, lay) == FST_OK;
 }
 
 int fst_supported(int dtype, int H, int D, int C) {
@@ -523,10 +563,12 @@ int fst_forward_phases(int phases, int dtype, int flags, int B, int H, int L, in
   const int HP = head_padding(H);
   FwdParams prm;
   std::memset(&prm, 0, sizeof(prm));
+  prm.flags = flags;  // the query resolves the plan bits
   int rows = 0;
   rc = fn(prm, HP, C, nullptr, 0, true, &rows);
   if (rc != FST_OK || rows <= 0)
-    return fail(FST_EUNSUPPORTED, "no compiled kernel for dtype=%d H=%d D=%d C=%d", dtype, H, D, C);
+    return fail(FST_EUNSUPPORTED, "no compiled forward kernel for dtype=%d H=%d D=%d C=%d with plan bits 0x%x", dtype,
+                H, D, C, flags & FST_PLAN_MASK);
 
   const WorkList wl = worklist_at(workspace, B);
   hipStream_t st = reinterpret_cast<hipStream_t>(stream);

@@ -335,39 +335,64 @@ __global__ __launch_bounds__(256, 1) void fwd_kernel(FwdParams prm) {
 }
 
 // ---------------------------------------------------------------------------
-// Dispatch: pick the (NW, NS) split with the best operand reuse that fits
-// LDS -- 32-key chunks first (full-width bf16 MFMA), then the fewest waves
-// per 16-row tile (V and K shared by more rows).
+// Dispatch. The static choice is the (NW, NS) split with the best operand
+// reuse that fits LDS: 32-key chunks first (full-width bf16 MFMA), then the
+// fewest waves per 16-row tile (V and K shared by more rows). The plan bits
+// FST_PLAN_FWD_T16 / T32 / T64 fix the rows per workgroup (NW = 4, 2, 1) and
+// FST_PLAN_FWD_KC16 / KC32 the keys per chunk (NS = 1, 2); a group left
+// empty takes the first value in that order that fits with the other.
+// Every split computes each (row, head) with the same sequence of
+// operations; the key chunk moves the online softmax's rescaling points.
 // ---------------------------------------------------------------------------
 template <typename T, int HP, int D, int C>
 struct FwdPick {
   template <int NW, int NS>
   using F = FwdCfg<T, HP, D, C, NW, NS>;
-  static constexpr int NS = (F<1, 2>::FITS || F<2, 2>::FITS || F<4, 2>::FITS) ? 2 : 1;
-  static constexpr int NW = F<1, NS>::FITS ? 1 : (F<2, NS>::FITS ? 2 : 4);
+  static constexpr int STATIC = pick_split<F>(0, 0);
+  static constexpr int NW = STATIC ? STATIC / 10 : 4, NS = STATIC ? STATIC % 10 : 1;
   using Cfg = F<NW, NS>;
-  static constexpr bool OK = Cfg::FITS;
+  static constexpr bool OK = STATIC != 0;
+  static constexpr int PLANS = OK ? split_plans<F>(FST_PLAN_FWD_T16, FST_PLAN_FWD_KC16) : 0;
 };
 
-template <typename T, int HP, int D, int C>
-int fwd_launch_t(const FwdParams& prm, hipStream_t stream, int grid) {
-  using P = FwdPick<T, HP, D, C>;
-  if constexpr (!P::OK) {
+template <typename T, int HP, int D, int C, int NW, int NS>
+int fwd_launch_v(const FwdParams& prm, hipStream_t stream, int grid, bool query, int* rows) {
+  using Cfg = FwdCfg<T, HP, D, C, NW, NS>;
+  if constexpr (!Cfg::FITS) {
     return FST_EUNSUPPORTED;
   } else {
-    auto kern = fwd_kernel<T, HP, D, C, P::NW, P::NS>;
-    if (hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, P::Cfg::LDS_BYTES) !=
+    *rows = Cfg::ROWS;
+    if (query) return FST_OK;
+    auto kern = fwd_kernel<T, HP, D, C, NW, NS>;
+    if (hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, Cfg::LDS_BYTES) !=
         hipSuccess)
       return FST_ELAUNCH;
-    if (grid > 0) hipLaunchKernelGGL(kern, dim3(grid), dim3(256), P::Cfg::LDS_BYTES, stream, prm);
+    if (grid > 0) hipLaunchKernelGGL(kern, dim3(grid), dim3(256), Cfg::LDS_BYTES, stream, prm);
     return hipGetLastError() == hipSuccess ? FST_OK : FST_ELAUNCH;
   }
 }
 
+// Launches (or, with query, only checks) the split the plan bits of
+// prm.flags name; *rows receives its rows per workgroup.
 template <typename T, int HP, int D, int C>
-int fwd_rows_t() {
+int fwd_launch_t(const FwdParams& prm, hipStream_t stream, int grid, bool query, int* rows) {
   using P = FwdPick<T, HP, D, C>;
-  return P::OK ? P::Cfg::ROWS : 0;
+  *rows = 0;
+  if constexpr (!P::OK) {
+    return FST_EUNSUPPORTED;
+  } else {
+    const int split = pick_split<P::template F>(plan_nw(prm.flags, bit_index(FST_PLAN_FWD_T16)),
+                                                plan_ns(prm.flags, bit_index(FST_PLAN_FWD_KC16)));
+    switch (split) {
+      case 11: return fwd_launch_v<T, HP, D, C, 1, 1>(prm, stream, grid, query, rows);
+      case 12: return fwd_launch_v<T, HP, D, C, 1, 2>(prm, stream, grid, query, rows);
+      case 21: return fwd_launch_v<T, HP, D, C, 2, 1>(prm, stream, grid, query, rows);
+      case 22: return fwd_launch_v<T, HP, D, C, 2, 2>(prm, stream, grid, query, rows);
+      case 41: return fwd_launch_v<T, HP, D, C, 4, 1>(prm, stream, grid, query, rows);
+      case 42: return fwd_launch_v<T, HP, D, C, 4, 2>(prm, stream, grid, query, rows);
+      default: return FST_EUNSUPPORTED;
+    }
+  }
 }
 
 }  // namespace fst

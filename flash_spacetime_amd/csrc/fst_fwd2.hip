@@ -482,7 +482,7 @@ __global__ __launch_bounds__(256, OCC) void fwd2_kernel(FwdParams prm) {
 
 template <int HP, int D, int C>
 struct Fwd2Pick {
-  static constexpr int KC = 16;
+  static constexpr int KC = 16;  // the static choice's keys per chunk
   // Three workgroups per CU where the LDS plan fits a third of the CU and the
   // lane state stays near the 168 registers of that budget ((HP / 4) D + 3 C
   // < 160: beyond it the instances spill); two otherwise. Measured on the
@@ -495,22 +495,29 @@ struct Fwd2Pick {
   static constexpr int OCC = OCC3 ? 3 : 2;
   using Cfg = Fwd2Cfg<HP, D, C, KC, OCC>;
   static constexpr bool OK = Cfg::FITS;
-  // Either occupancy may be chosen instead (FST_PLAN_FWD_OCC2 / _OCC3) where
-  // it exists: both compute every row with the same arithmetic, only the
-  // register and LDS budget differs.
-  static constexpr int PLANS = OK ? ((OCC2 ? FST_PLAN_FWD_OCC2 : 0) | (OCC3 ? FST_PLAN_FWD_OCC3 : 0)) : 0;
+  // 32-key chunks (FST_PLAN_FWD_KC32) at two workgroups per CU, where their
+  // LDS plan fits and the lane state is that of the small layouts.
+  static constexpr bool KC32 = OK && Fwd2Cfg<HP, D, C, 32, 2>::FITS && rows_wave_load(HP, D, C) < 160;
+  // Occupancy and key-chunk variants a caller may choose instead (the plan
+  // bits of include/flash_spacetime.h); the occupancy variants compute every
+  // row with the same arithmetic.
+  static constexpr int PLANS = OK ? ((OCC2 ? FST_PLAN_FWD_OCC2 : 0) | (OCC3 ? FST_PLAN_FWD_OCC3 : 0) |
+                                     FST_PLAN_FWD_KC16 | (KC32 ? FST_PLAN_FWD_KC32 : 0))
+                                  : 0;
 };
 
-template <int HP, int D, int C, int OCC>
-int fwd2_launch_occ(const FwdParams& prm, hipStream_t stream, int grid) {
+template <int HP, int D, int C, int KC, int OCC>
+int fwd2_launch_occ(const FwdParams& prm, hipStream_t stream, int grid, bool query) {
+  using Cfg = Fwd2Cfg<HP, D, C, KC, OCC>;
   using P = Fwd2Pick<HP, D, C>;
-  using Cfg = Fwd2Cfg<HP, D, C, P::KC, OCC>;
-  if constexpr (!Cfg::FITS) {
+  constexpr bool OFFERED = KC == 16 ? (OCC == 2 ? P::OCC2 : P::OCC3) : (P::KC32 && OCC == 2);
+  if constexpr (!Cfg::FITS || !OFFERED) {
     return FST_EUNSUPPORTED;
   } else {
+    if (query) return FST_OK;
     // Both bias flags (the operators' default) run an instance with the flags
     // fixed at compile time; other combinations read them at run time.
-    auto kern = (prm.flags & 3) == 3 ? fwd2_kernel<HP, D, C, P::KC, OCC, 3> : fwd2_kernel<HP, D, C, P::KC, OCC, -1>;
+    auto kern = (prm.flags & 3) == 3 ? fwd2_kernel<HP, D, C, KC, OCC, 3> : fwd2_kernel<HP, D, C, KC, OCC, -1>;
     if (hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, Cfg::LDS_BYTES) !=
         hipSuccess)
       return FST_ELAUNCH;
@@ -522,20 +529,20 @@ int fwd2_launch_occ(const FwdParams& prm, hipStream_t stream, int grid) {
   }
 }
 
+// Launches (or, with query, only checks) the variant the plan bits of
+// prm.flags name: an empty occupancy group takes the static occupancy (two
+// with 32-key chunks), an empty key-chunk group 16 keys.
 template <int HP, int D, int C>
-int fwd2_launch_t(const FwdParams& prm, hipStream_t stream, int grid) {
+int fwd2_launch_t(const FwdParams& prm, hipStream_t stream, int grid, bool query) {
   using P = Fwd2Pick<HP, D, C>;
   if constexpr (!P::OK) {
     return FST_EUNSUPPORTED;
   } else {
-    // The plan bits were checked against P::PLANS by the caller.
-    const int occ = (prm.flags & FST_PLAN_FWD_OCC2) ? 2 : (prm.flags & FST_PLAN_FWD_OCC3) ? 3 : P::OCC;
-    if (occ == 3) {
-      if constexpr (P::OCC3) return fwd2_launch_occ<HP, D, C, 3>(prm, stream, grid);
-      return FST_EUNSUPPORTED;
-    }
-    if constexpr (P::OCC2) return fwd2_launch_occ<HP, D, C, 2>(prm, stream, grid);
-    return FST_EUNSUPPORTED;
+    const bool kc32 = prm.flags & FST_PLAN_FWD_KC32;
+    const int occ = (prm.flags & FST_PLAN_FWD_OCC2) ? 2 : (prm.flags & FST_PLAN_FWD_OCC3) ? 3 : (kc32 ? 2 : P::OCC);
+    if (kc32) return occ == 2 ? fwd2_launch_occ<HP, D, C, 32, 2>(prm, stream, grid, query) : FST_EUNSUPPORTED;
+    if (occ == 3) return fwd2_launch_occ<HP, D, C, 16, 3>(prm, stream, grid, query);
+    return fwd2_launch_occ<HP, D, C, 16, 2>(prm, stream, grid, query);
   }
 }
 

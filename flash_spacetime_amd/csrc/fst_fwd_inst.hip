@@ -17,21 +17,16 @@ namespace fst {
 int FST_CAT(fwd_dispatch_, FST_NAME)(const FwdParams& prm, int HP, int C, hipStream_t stream, int grid, bool query,
                                      int* rows) {
   // bf16 runs the 16-row-tile kernel (fst_fwd2.hip) wherever its LDS plan
-  // fits; fp32 and the remaining shapes run fst_forward.hip.
+  // fits; fp32 and the remaining shapes run fst_forward.hip. With query set
+  // nothing is launched: the plan bits of prm.flags are checked and *rows
+  // receives the rows per workgroup of the variant they name.
 #define FST_CASE(HPV, CV)                                                       \
   if (HP == HPV && C == CV) {                                                   \
     if constexpr (is_bf16<FST_T>::value && Fwd2Pick<HPV, FST_D, CV>::OK) {      \
-      if (query) {                                                              \
-        *rows = 16;                                                             \
-        return FST_OK;                                                          \
-      }                                                                         \
-      return fwd2_launch_t<HPV, FST_D, CV>(prm, stream, grid);                  \
+      *rows = 16;                                                               \
+      return fwd2_launch_t<HPV, FST_D, CV>(prm, stream, grid, query);           \
     } else {                                                                    \
-      if (query) {                                                              \
-        *rows = fwd_rows_t<FST_T, HPV, FST_D, CV>();                            \
-        return *rows ? FST_OK : FST_EUNSUPPORTED;                               \
-      }                                                                         \
-      return fwd_launch_t<FST_T, HPV, FST_D, CV>(prm, stream, grid);            \
+      return fwd_launch_t<FST_T, HPV, FST_D, CV>(prm, stream, grid, query, rows); \
     }                                                                           \
   }
 #define FST_CASES(HPV) FST_CASE(HPV, 16) FST_CASE(HPV, 32) FST_CASE(HPV, 48) FST_CASE(HPV, 64)
@@ -49,8 +44,10 @@ int FST_CAT(fwd_dispatch_, FST_NAME)(const FwdParams& prm, int HP, int C, hipStr
 int FST_CAT(fwd_plans_, FST_NAME)(int HP, int C) {
 #define FST_CASE(HPV, CV)                                                   \
   if (HP == HPV && C == CV) {                                               \
-    if constexpr (is_bf16<FST_T>::value) return Fwd2Pick<HPV, FST_D, CV>::PLANS; \
-    return 0;                                                               \
+    if constexpr (is_bf16<FST_T>::value && Fwd2Pick<HPV, FST_D, CV>::OK)    \
+      return Fwd2Pick<HPV, FST_D, CV>::PLANS;                               \
+    else                                                                    \
+      return FwdPick<FST_T, HPV, FST_D, CV>::PLANS;                         \
   }
 #define FST_CASES(HPV) FST_CASE(HPV, 16) FST_CASE(HPV, 32) FST_CASE(HPV, 48) FST_CASE(HPV, 64)
   FST_CASES(4)

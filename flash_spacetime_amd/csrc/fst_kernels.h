@@ -411,4 +411,48 @@ FST_DECL_BWD(f32_48)
 FST_DECL_BWD(f32_64)
 #undef FST_DECL_BWD
 
+// ---------------------------------------------------------------------------
+// Plan requests of the first-generation kernels (fst_forward.hip,
+// fst_backward.hip), which come in (NW, NS) splits: NW waves per 16-row tile
+// (16 * 4 / NW rows or keys per workgroup) and 16 * NS keys (or rows) per
+// chunk.
+// ---------------------------------------------------------------------------
+// (NW, NS) of a plan request for a family of configurations F<NW, NS>
+// (nw, ns = 0: not requested), as 10 NW + NS, or 0 when nothing fits.
+template <template <int, int> class F>
+constexpr int pick_split(int nw, int ns) {
+  const bool fits[3][2] = {{F<1, 1>::FITS, F<1, 2>::FITS}, {F<2, 1>::FITS, F<2, 2>::FITS},
+                           {F<4, 1>::FITS, F<4, 2>::FITS}};
+  const int nws[3] = {1, 2, 4};
+  for (int s = 2; s >= 1; --s) {
+    if (ns && s != ns) continue;
+    for (int w = 0; w < 3; ++w) {
+      if (nw && nws[w] != nw) continue;
+      if (fits[w][s - 1]) return 10 * nws[w] + s;
+    }
+  }
+  return 0;
+}
+
+// The requested (nw, ns) of the plan bits in flags, for the groups starting
+// at bit t (three tile-height bits) and bit k (two key-chunk bits).
+__host__ __device__ inline int plan_nw(int flags, int t) {
+  return (flags >> t) & 1 ? 4 : ((flags >> (t + 1)) & 1 ? 2 : ((flags >> (t + 2)) & 1 ? 1 : 0));
+}
+__host__ __device__ inline int plan_ns(int flags, int k) { return (flags >> k) & 1 ? 1 : ((flags >> (k + 1)) & 1 ? 2 : 0); }
+constexpr int bit_index(int b) { return b <= 1 ? 0 : 1 + bit_index(b >> 1); }
+
+// The plan bits of a (NW, NS) family: a tile-height bit for each NW and a
+// key-chunk bit for each NS that fits with some value of the other.
+template <template <int, int> class F>
+constexpr int split_plans(int t16, int k16) {
+  int bits = 0;
+  const int nws[3] = {4, 2, 1};
+  for (int w = 0; w < 3; ++w)
+    if (pick_split<F>(nws[w], 0)) bits |= t16 << w;
+  for (int s = 1; s <= 2; ++s)
+    if (pick_split<F>(0, s)) bits |= k16 << (s - 1);
+  return bits;
+}
+
 }  // namespace fst

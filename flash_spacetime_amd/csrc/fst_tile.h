@@ -430,6 +430,14 @@ struct QoTile {
     const unsigned char* p = blk + 16 * slot(r, 2 * (q & 1) + (j >> 1)) + 8 * (j & 1);
     return __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4*)(p));
   }
+  // The same operand with the features in the order of DTiles::dmap: lane
+  // (g, n) receives rows 4g .. 4g + 3 of feature 8 (n >> 2) + 4 (q & 1) +
+  // (n & 3) of the part. Source lane s of the group supplies row 4g + s / 4,
+  // features 8 (s % 4) + 4 (q & 1) .. +3 (half q & 1 of quarter s % 4).
+  static __device__ __forceinline__ bf16x4 tr_frag_dmap(const unsigned char* blk, int q, int g, int n) {
+    const unsigned char* p = blk + 16 * slot(4 * g + (n >> 2), n & 3) + 8 * (q & 1);
+    return __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4*)(p));
+  }
 };
 
 // Per-(row, head) scalars (rescale factors): [head][17].

@@ -293,10 +293,10 @@ def flash_spacetime_forward(
     scale: Optional[float] = None,
     use_attn_bias: bool = True,
     use_activation_bias: bool = True,
-    block_m: int = 16,
+    block_m: Optional[int] = None,
     block_n: Optional[int] = None,
-    num_warps: int = 8,
-    num_stages: int = 1,
+    num_warps: Optional[int] = None,
+    num_stages: Optional[int] = None,
     cu_seqlens: Optional[Tensor] = None,
 ) -> Tuple[Tensor, Tensor]:
     """Fused forward: (out `[B, H, L, D]` with padding rows 0, lse `[B, H, L]`).
@@ -307,19 +307,25 @@ def flash_spacetime_forward(
     offsets) the tensors are packed `[T, H, D]` / `[T, F]` and `seqlens` is
     ignored. `weight` is `[D, C]` (nn.Linear layout; the reference's
     `[C, C]` with C == D is the special case). lse excludes the row-constant
-    `qt . b` term, as the reference kernel's does. The Triton tuning
-    arguments (block_m, block_n, num_warps, num_stages) are accepted for
-    signature compatibility and ignored: tiles are fixed per shape for
-    gfx950's 160 KiB LDS.
+    `qt . b` term, as the reference kernel's does. The reference's tile
+    arguments select compiled kernel variants (tune.plan_from_tiles): block_m
+    the float32 kernel's query rows per workgroup, block_n its keys per chunk
+    (16 or 32; the bf16 kernel's too), each the nearest offered value. None
+    (the default here; the reference defaults to 16 / 32 bf16, 16 fp32)
+    keeps the library's tuned or static choice. num_warps has no forward
+    counterpart (the kernels run four waves per workgroup) and num_stages
+    none at all (loads run one chunk ahead); both are accepted.
     """
-    del block_m, block_n, num_warps, num_stages
+    del num_stages
     if q.dtype == _HALF:
         out, lse = flash_spacetime_forward(*_bf16(q, k, v), feats, weight, bias, seqlens, scale, use_attn_bias,
-                                           use_activation_bias, cu_seqlens=cu_seqlens)
+                                           use_activation_bias, block_m=block_m, block_n=block_n,
+                                           num_warps=num_warps, cu_seqlens=cu_seqlens)
         return out.to(_HALF), lse
     prep = _Prepared(q, k, v, feats, weight, bias, seqlens, scale, use_attn_bias,
                      use_activation_bias, cu_seqlens)
-    return _run_forward(prep)
+    with tune.tile_request(block_m, block_n, None):
+        return _run_forward(prep)
 
 
 class _FlashSpacetimeAttention(torch.autograd.Function):

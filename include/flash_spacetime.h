@@ -70,22 +70,50 @@ enum fst_flags {
                               one fused projection's [.., 3, H, D] output; see
                               Layouts. No reference counterpart (the reference
                               takes three separate tensors, forward.py:481). */
-  /* Plan bits (bf16 kernels): a choice among compiled variants of a kernel
-   * that compute every output row with the same arithmetic and differ only
-   * in their register / LDS budget, for callers that time them (at most one
-   * bit of each pair; none = the library's static choice). out, lse, dq, dk,
-   * dv and rowsum do not depend on the plan; dweight / dbias depend on the
-   * rows plan only through the order of their fp32 partial sums. Only the
-   * bits fst_plans() reports for the shape are accepted. No reference
-   * counterpart: the reference's Triton kernels take fixed tile constants
-   * (_tiles.py) and are not autotuned (README.md:86-95). */
-  FST_PLAN_FWD_OCC2 = 1 << 8,   /* forward: two workgroups per CU            */
-  FST_PLAN_FWD_OCC3 = 1 << 9,   /* forward: three workgroups per CU          */
-  FST_PLAN_ROWS_W4 = 1 << 10,   /* backward rows: four waves per workgroup   */
-  FST_PLAN_ROWS_W8 = 1 << 11,   /* backward rows: eight waves (heads padded to a multiple of 8) */
-  FST_PLAN_COLS_OCC2 = 1 << 12, /* backward cols: two workgroups per CU      */
-  FST_PLAN_COLS_OCC3 = 1 << 13, /* backward cols: three workgroups per CU    */
-  FST_PLAN_MASK = 0x3f00
+  /* Plan bits: a choice among compiled variants of the kernels, for callers
+   * that time them. Each group below is one knob of one kernel; at most one
+   * bit of a group may be set, and a group left empty takes the library's
+   * static choice. fst_plans() lists the bits compiled for a shape and
+   * fst_plan_supported() whether one combination of them is.
+   * Variants of the occupancy, wave, K/V-staging and tile-height groups
+   * compute every output row with the same arithmetic: out, lse, dq, dk, dv
+   * and rowsum are the same bit for bit, and dweight / dbias differ only in
+   * the order in which their fp32 partial sums are added. The key-chunk
+   * groups move the points where the online softmax rescales and the order
+   * of the sums over keys, so their results agree to rounding.
+   * No reference counterpart: the reference's Triton kernels take fixed tile
+   * constants (_tiles.py), are not autotuned (README.md:86-95), and its
+   * launchers' block_m / block_n / num_warps arguments (forward.py:233-236,
+   * backward.py:501-504) select those constants; the Python operators map
+   * them onto the tile-height, key-chunk and wave groups. */
+  /* bf16 forward: workgroups per CU */
+  FST_PLAN_FWD_OCC2 = 1 << 8,
+  FST_PLAN_FWD_OCC3 = 1 << 9,
+  /* bf16 backward rows kernel: waves per workgroup and workgroups per CU */
+  FST_PLAN_ROWS_W4 = 1 << 10,   /* four waves, two workgroups per CU               */
+  FST_PLAN_ROWS_W8 = 1 << 11,   /* eight waves, one per CU (heads padded to 8k)    */
+  FST_PLAN_ROWS_W8X2 = 1 << 14, /* eight waves, two per CU (four waves per SIMD)   */
+  /* bf16 backward cols kernel: workgroups per CU */
+  FST_PLAN_COLS_OCC2 = 1 << 12,
+  FST_PLAN_COLS_OCC3 = 1 << 13,
+  /* bf16 backward rows kernel: where a key chunk's K and V rows are held */
+  FST_PLAN_ROWS_KV_REG = 1 << 15, /* registers, loaded a chunk ahead            */
+  FST_PLAN_ROWS_KV_LDS = 1 << 16, /* LDS, by direct loads (D a multiple of 32)  */
+  /* forward: keys per chunk (bf16 and float32) */
+  FST_PLAN_FWD_KC16 = 1 << 17,
+  FST_PLAN_FWD_KC32 = 1 << 18,
+  /* float32 forward: query rows per workgroup (tile height) */
+  FST_PLAN_FWD_T16 = 1 << 19,
+  FST_PLAN_FWD_T32 = 1 << 20,
+  FST_PLAN_FWD_T64 = 1 << 21,
+  /* float32 backward: rows (rows kernel) and keys (cols kernel) per workgroup */
+  FST_PLAN_BWD_T16 = 1 << 22,
+  FST_PLAN_BWD_T32 = 1 << 23,
+  FST_PLAN_BWD_T64 = 1 << 24,
+  /* float32 backward: keys (rows kernel) and rows (cols kernel) per chunk */
+  FST_PLAN_BWD_KC16 = 1 << 25,
+  FST_PLAN_BWD_KC32 = 1 << 26,
+  FST_PLAN_MASK = 0x07ffff00
 };
 
 /* Phases of one operator call, for callers that time or schedule them
@@ -118,9 +146,16 @@ enum fst_status {
 int fst_supported(int dtype, int H, int D, int C);
 
 /* The FST_PLAN_* bits compiled for (dtype, H, D, C): a bit is set when its
- * variant exists for the shape (0 for float32 and unsupported shapes).
- * No reference counterpart (see FST_PLAN_FWD_OCC2). */
+ * variant exists for the shape in some combination with the other groups
+ * (0 for unsupported shapes).
+ * No reference counterpart (see the plan bits above). */
 int fst_plans(int dtype, int H, int D, int C);
+
+/* 1 if the combination `plan` of FST_PLAN_* bits (at most one per group;
+ * the empty groups take the static choice) is compiled for (dtype, H, D, C)
+ * in both the forward and the backward, else 0.
+ * No reference counterpart (see the plan bits above). */
+int fst_plan_supported(int dtype, int H, int D, int C, int plan);
 
 /* Scratch bytes fst_forward needs for these sizes (rows = B*L padded, T packed). */
 size_t fst_forward_workspace_bytes(int dtype, int flags, int B, int H, int L, int T,
