@@ -250,8 +250,8 @@ WORKLOADS = {
             "lengths U{16..768} (bool key_padding_mask -> seqlens once), W/b fp32",
     "lscale": "configs[2] at L = 384, 768, 1536: flash_spacetime_attention fwd+bwd, B=256 H=12 D=32 C=16 "
               "bf16, lengths U{16..L}",
-    "plans": "per-kernel times of every compiled FST_PLAN_* variant against the static choice, bf16, "
-             "cfg2, cfg3 and ten other head layouts",
+    "plans": "per-kernel times of every supported FST_PLAN_* combination of each kernel family against the "
+             "static choice: bf16 cfg2, cfg3, cfg4 and seven other head layouts, fp32 cfg4, cfg2 and one small",
     "cfg2-model": "SpacetimeAttention fwd+bwd (fused QKV linear, flash_spacetime_attention_qkv, output "
                   "linear) at cfg2 sizes: x [256, 768, 384] bf16, H=12 D=32 C=16, lengths U{16..768}",
 }
@@ -484,39 +484,40 @@ def run_other_workload(name, steps, warmup):
 
 
 PLAN_SHAPES = [
-    # (name, H, D, C, B, L or None for cfg3's packed events, (use_attn_bias, use_activation_bias))
-    ("cfg2", 12, 32, 16, 256, 768, (True, True)),
-    ("cfg2, use_activation_bias=False", 12, 32, 16, 256, 768, (True, False)),
-    ("cfg2, B=16", 12, 32, 16, 16, 768, (True, True)),
-    ("cfg3", 12, 32, 16, 4096, None, (True, True)),
-    ("H=8 D=32 C=16", 8, 32, 16, 128, 1024, (True, True)),
-    ("H=16 D=16 C=16", 16, 16, 16, 128, 1024, (True, True)),
-    ("H=4 D=64 C=16", 4, 64, 16, 256, 512, (True, True)),
-    ("H=8 D=16 C=32", 8, 16, 32, 128, 1024, (True, True)),
-    ("H=12 D=16 C=32", 12, 16, 32, 128, 768, (True, True)),
-    ("H=4 D=32 C=32", 4, 32, 32, 256, 768, (True, True)),
-    ("H=8 D=48 C=16", 8, 48, 16, 128, 768, (True, True)),
-    ("H=8 D=64 C=64", 8, 64, 64, 64, 1024, (True, True)),
+    # (name, dtype, H, D, C, B, L (None: cfg3's packed events), full-length events, (attn, act bias))
+    ("cfg2", "bf16", 12, 32, 16, 256, 768, False, (True, True)),
+    ("cfg2, use_activation_bias=False", "bf16", 12, 32, 16, 256, 768, False, (True, False)),
+    ("cfg3", "bf16", 12, 32, 16, 4096, None, False, (True, True)),
+    ("cfg4", "bf16", 8, 64, 64, 8, 4096, True, (True, True)),
+    ("H=8 D=32 C=16", "bf16", 8, 32, 16, 128, 1024, False, (True, True)),
+    ("H=16 D=16 C=16", "bf16", 16, 16, 16, 128, 1024, False, (True, True)),
+    ("H=4 D=64 C=16", "bf16", 4, 64, 16, 256, 512, False, (True, True)),
+    ("H=12 D=16 C=32", "bf16", 12, 16, 32, 128, 768, False, (True, True)),
+    ("H=8 D=48 C=16", "bf16", 8, 48, 16, 128, 768, False, (True, True)),
+    ("H=12 D=64 C=32", "bf16", 12, 64, 32, 64, 1024, False, (True, True)),
+    ("cfg4-fp32", "fp32", 8, 64, 64, 8, 4096, True, (True, True)),
+    ("cfg2-fp32", "fp32", 12, 32, 16, 256, 768, False, (True, True)),
+    ("H=4 D=16 C=16 fp32", "fp32", 4, 16, 16, 128, 1024, False, (True, True)),
 ]
 
 
 def run_plan_sweep(steps, warmup):
     """Per-kernel times (ms) of every compiled variant (FST_PLAN_*) of the
-    forward, rows and cols kernels, and of the library's static choice, over
-    bf16 shapes with lengths U{16..L} (cfg3: its packed lognormal events)."""
+    forward, rows and cols kernels, and of the library's static choice: for
+    each kernel family, every supported combination of its plan groups (one
+    offered bit per group), over bf16 and fp32 shapes with lengths U{16..L}
+    (cfg3: its packed lognormal events; cfg4: full-length events)."""
     import math
 
     from flash_spacetime_amd import _lib, tune
 
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
-    lib = _lib.load()
     gen = torch.Generator().manual_seed(11)
-    names = {_lib.FST_PLAN_FWD_OCC2: "occ2", _lib.FST_PLAN_FWD_OCC3: "occ3", _lib.FST_PLAN_ROWS_W4: "w4",
-             _lib.FST_PLAN_ROWS_W8: "w8", _lib.FST_PLAN_COLS_OCC2: "occ2", _lib.FST_PLAN_COLS_OCC3: "occ3"}
     rows_out = []
-    for name, h, d, c, bsz, length, flags in PLAN_SHAPES:
+    for name, dt, h, d, c, bsz, length, full, flags in PLAN_SHAPES:
         rn = lambda *s_: torch.randn(*s_, generator=gen)  # noqa: E731
+        tdt = torch.bfloat16 if dt == "bf16" else torch.float32
         if length is None:
             lens = torch.exp(5.0 + torch.randn(bsz, generator=gen, dtype=torch.float64)).round().clamp(1, 3000).long()
             lens[torch.randperm(bsz, generator=gen)[: math.ceil(0.01 * bsz)]] = 1
@@ -526,33 +527,38 @@ def run_plan_sweep(steps, warmup):
             cu[1:] = torch.cumsum(lens, 0)
             cu, seqlens = cu.to(dev), None
         else:
-            lens = torch.randint(16, length + 1, (bsz,), generator=gen)
+            lens = torch.full((bsz,), length) if full else torch.randint(16, length + 1, (bsz,), generator=gen)
             shape, fshape = (bsz, h, length, d), (bsz, length)
             cu, seqlens = None, lens.to(dev, torch.int32)
-        inp = {n_: rn(*shape).to(dev, torch.bfloat16) for n_ in ("q", "k", "v", "do")}
+        inp = {n_: rn(*shape).to(dev, tdt) for n_ in ("q", "k", "v", "do")}
         inp["feats"] = torch.cat([(torch.rand(*fshape, 3, generator=gen) - 0.5) * 1000.0,
                                   torch.rand(*fshape, 1, generator=gen) * 2e4], -1).to(dev)
         inp["w"] = (rn(d, c) / c ** 0.5).to(dev)
         inp["b"] = (rn(d) * 0.02).to(dev)
-        mask = lib.fst_plans(_lib.FST_BF16, h, d, c)
-        groups = {"fwd": [b_ for b_ in (_lib.FST_PLAN_FWD_OCC2, _lib.FST_PLAN_FWD_OCC3) if mask & b_],
-                  "bwd_rows": [b_ for b_ in (_lib.FST_PLAN_ROWS_W4, _lib.FST_PLAN_ROWS_W8) if mask & b_],
-                  "bwd_cols": [b_ for b_ in (_lib.FST_PLAN_COLS_OCC2, _lib.FST_PLAN_COLS_OCC3) if mask & b_]}
-        n_var = max(len(g_) for g_ in groups.values())
-        best = {k_: {} for k_ in groups}
+        dtype = _lib.FST_BF16 if dt == "bf16" else _lib.FST_F32
+        dims = (dtype, 3, bsz, h, length or 0, int(lens.sum()), d, c)
+        families = {"fwd": (tune._combos(dims, tune._FWD_GROUPS), ("fwd",)),
+                    "bwd_rows": (tune._combos(dims, tune._ROWS_GROUPS), ("bwd_rows",)),
+                    "bwd_cols": (tune._combos(dims, tune._COLS_GROUPS), ("bwd_cols",)),
+                    "bwd_fp32": (tune._combos(dims, tune._BWD_GROUPS), ("bwd_rows", "bwd_cols"))}
+        res = {}
+        iters = max(steps // 4, 3) if full else max(steps // 2, 5)
         for _ in range(2):  # two interleaved rounds; the minimum of each is kept
-            for i in range(-1, n_var):
-                plan = 0 if i < 0 else sum(g_[i % len(g_)] for g_ in groups.values())
-                kt = kernel_times(inp, seqlens, iters=max(steps // 2, 5), cu=cu, plan=plan, flags=flags)
-                for k_, g_ in groups.items():
-                    label = "static" if i < 0 else names[g_[i % len(g_)]]
-                    best[k_][label] = min(best[k_].get(label, float("inf")), kt[k_])
-        rows_out.append({"shape": name, "plans": tune.plan_names(mask),
-                         **{k_: {l_: round(t_, 4) for l_, t_ in v_.items()} for k_, v_ in best.items()}})
+            for fam, (combos, kernels) in families.items():
+                if not combos:
+                    continue
+                for plan in [0, *combos]:
+                    kt = kernel_times(inp, seqlens, iters=iters, cu=cu, plan=plan, flags=flags)
+                    label = tune.plan_names(plan) or "static"
+                    t_ = sum(kt[k_] for k_ in kernels)
+                    res.setdefault(fam, {})[label] = min(res.get(fam, {}).get(label, float("inf")), t_)
+        rows_out.append({"shape": name, "dtype": dt, "plans": tune.plan_names(tune.plans(dtype, h, d, c)),
+                         **{k_: {l_: round(t_, 4) for l_, t_ in v_.items()} for k_, v_ in res.items()}})
+        print(json.dumps(rows_out[-1]), flush=True)
         del inp
         torch.cuda.empty_cache()
     print(json.dumps({
-        "metric": "per-kernel ms of each compiled plan variant", "unit": "ms", "n_gpus": 1, "dtype": "bf16",
+        "metric": "per-kernel ms of each compiled plan variant", "unit": "ms", "n_gpus": 1, "dtype": "bf16+fp32",
         "higher_is_better": False, "data": "synthetic (seeded)",
         "config": {"workload": WORKLOADS["plans"]}, "by_shape": rows_out,
     }), flush=True)

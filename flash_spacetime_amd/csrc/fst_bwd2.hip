@@ -709,9 +709,6 @@ struct Cols2Cfg {
   static constexpr bool QL = D % 32 == 0 && RC == 16 && BASE_BYTES + QO_BYTES <= 80 * 1024;
   static constexpr int LDS_BYTES = BASE_BYTES + (QL ? QO_BYTES : 0);
   static constexpr bool FITS = LDS_BYTES <= 80 * 1024 && HP % 4 == 0;
-  // Workgroups per CU the register plan is built for: three for the small
-  // head layouts whose staged tiles fit a third of the LDS.
-  static constexpr int OCC = (QL && HP <= 12 && D <= 32 && C <= 16 && LDS_BYTES <= 160 * 1024 / 3) ? 3 : 2;
 };
 
 
@@ -1093,6 +1090,15 @@ struct Bwd2Pick {
   using CC = Cols2Cfg<HP, D, C, RC>;
   static constexpr bool COLS_OCC3 = CC::FITS && CC::LDS_BYTES <= 160 * 1024 / 3 && LIGHT;
   static constexpr int COLS_PLANS = CC::FITS ? (FST_PLAN_COLS_OCC2 | (COLS_OCC3 ? FST_PLAN_COLS_OCC3 : 0)) : 0;
+  // Static choices among them, as measured on gfx950 with lengths U{16..L}:
+  // where HP is a multiple of 8 and the lane state is light, eight rows-kernel
+  // waves in two workgroups per CU (H=8, D=32, C=16: 0.567 against 0.636 ms
+  // with four; H=16, D=C=16: 0.710 against 0.847), elsewhere four (H=12
+  // gains nothing: its eight-wave split is uneven); the cols kernel at three
+  // workgroups per CU wherever that is offered (H=8, D=48, C=16: 0.367
+  // against 0.437 ms; within 1 % elsewhere).
+  static constexpr int ROWS_STATIC = NW == 8 ? 2 : ((HP % 8 == 0 && ROWS_W8X2) ? 3 : 1);
+  static constexpr int COLS_STATIC = COLS_OCC3 ? 3 : 2;
 };
 
 template <int HP, int D, int C, int NW, int WPE, bool KL>
@@ -1149,7 +1155,7 @@ int bwd2_launch_t(const BwdParams& prm, int which, hipStream_t stream, int grid,
     const int waves = (f & FST_PLAN_ROWS_W4)     ? 1
                       : (f & FST_PLAN_ROWS_W8)   ? 2
                       : (f & FST_PLAN_ROWS_W8X2) ? 3
-                                                 : (P::NW == 8 ? 2 : 1);
+                                                 : P::ROWS_STATIC;
     if (waves == 1) {
       if constexpr (P::ROWS_W4) {
         if (!kl) return bwd2_launch_rows<HP, D, C, 4, 2, false>(prm, stream, g8, query);
@@ -1171,9 +1177,9 @@ int bwd2_launch_t(const BwdParams& prm, int which, hipStream_t stream, int grid,
   if constexpr (!P::CC::FITS) {
     return FST_EUNSUPPORTED;
   } else {
-    const int occ = (f & FST_PLAN_COLS_OCC2) ? 2 : (f & FST_PLAN_COLS_OCC3) ? 3 : P::CC::OCC;
+    const int occ = (f & FST_PLAN_COLS_OCC2) ? 2 : (f & FST_PLAN_COLS_OCC3) ? 3 : P::COLS_STATIC;
     if (occ == 3) {
-      if constexpr (P::COLS_OCC3 || P::CC::OCC == 3) return bwd2_launch_cols<HP, D, C, 3>(prm, stream, g8, query);
+      if constexpr (P::COLS_OCC3) return bwd2_launch_cols<HP, D, C, 3>(prm, stream, g8, query);
       return FST_EUNSUPPORTED;
     }
     return bwd2_launch_cols<HP, D, C, 2>(prm, stream, g8, query);

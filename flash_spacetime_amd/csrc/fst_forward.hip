@@ -335,9 +335,8 @@ __global__ __launch_bounds__(256, 1) void fwd_kernel(FwdParams prm) {
 }
 
 // ---------------------------------------------------------------------------
-// Dispatch. The static choice is the (NW, NS) split with the best operand
-// reuse that fits LDS: 32-key chunks first (full-width bf16 MFMA), then the
-// fewest waves per 16-row tile (V and K shared by more rows). The plan bits
+// Dispatch. The static choice is the split with the most waves per 16-row
+// tile that fits LDS, then 32-key chunks (see pick_split). The plan bits
 // FST_PLAN_FWD_T16 / T32 / T64 fix the rows per workgroup (NW = 4, 2, 1) and
 // FST_PLAN_FWD_KC16 / KC32 the keys per chunk (NS = 1, 2); a group left
 // empty takes the first value in that order that fits with the other.
