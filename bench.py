@@ -174,17 +174,27 @@ def calibration_copy(dev, nbytes=2 ** 30):
 
 
 def cpu_model():
-    """The host CPU's model name (/proc/cpuinfo), or the platform string."""
+    """The host CPU as /proc/cpuinfo names it: model name, family / model /
+    stepping numbers (virtual machines often report a generic name) and the
+    logical CPUs this process may use; else the platform string."""
+    fields = {}
     try:
         with open("/proc/cpuinfo") as f:
             for line in f:
-                if line.startswith("model name"):
-                    return line.split(":", 1)[1].strip()
+                key, _, val = line.partition(":")
+                key = key.strip()
+                if key in ("model name", "cpu family", "model", "stepping") and key not in fields:
+                    fields[key] = val.strip()
+                if not line.strip() and fields:
+                    break
     except OSError:
         pass
-    import platform
+    if "model name" not in fields:
+        import platform
 
-    return platform.processor() or platform.machine()
+        return platform.processor() or platform.machine()
+    ids = ", ".join(f"{k} {fields[k]}" for k in ("cpu family", "model", "stepping") if k in fields)
+    return f"{fields['model name']} ({ids}; {len(os.sched_getaffinity(0))} logical CPUs available)"
 
 
 def _cpu_eager_ms(inp, dtype, budget_s, max_events):
