@@ -63,9 +63,7 @@ struct BwdRowsCfg {
   static constexpr int ESZ = sizeof(T);
   static constexpr int PAD = 16 / ESZ;
   static constexpr int KV_ROW = D + PAD;
-  static constexpr int KV_BYTES = BF ? 2 * HP * KC * KV_ROW * ESZ : 0;  // K and V (bf16 only)
   static constexpr int DW_BYTES = 4 * (D * C + D) * 4;                  // per-wave dW/db partials
-  static constexpr int R0_BYTES = KV_BYTES > DW_BYTES ? KV_BYTES : DW_BYTES;
   static constexpr int E_ROW = C + PAD;
   static constexpr int E_TILE = 16 * KC * E_ROW * ESZ;
   static constexpr int U_ROW = KC + 4;   // fp32 per staged u.E / w~.E
@@ -79,6 +77,17 @@ struct BwdRowsCfg {
   static constexpr int SLOT = SLOT_1 > SLOT_2 ? SLOT_1 : SLOT_2;
   static constexpr int STAGE_TILE = 16 * HP * SLOT;
   static constexpr int TILE_BYTES = E_TILE + STAGE_TILE;
+  // KVS: each chunk's K and V rows are staged in LDS by the whole workgroup
+  // (coalesced 16-byte loads, then row fragments and transposed K read back
+  // from LDS); bf16 only. For float32 every head-owner wave loads its K and
+  // V fragments from global memory instead: staged, the float32 kernel was
+  // slower on gfx950 (cfg4: 45.7 against 41.2 ms; B=256 L=768 H=12 D=32
+  // C=16: 10.6 against 9.7 ms), its synchronous staging serialising what
+  // the waves' own loads overlap.
+  static constexpr int KV_STAGED = 2 * HP * KC * KV_ROW * ESZ;
+  static constexpr bool KVS = BF;
+  static constexpr int KV_BYTES = KVS ? KV_STAGED : 0;                 // K and V
+  static constexpr int R0_BYTES = KV_BYTES > DW_BYTES ? KV_BYTES : DW_BYTES;
   static constexpr int LDS_BYTES = R0_BYTES + TILES * TILE_BYTES;
   static constexpr bool FITS = LDS_BYTES <= 160 * 1024 && HP % NW == 0;
   static_assert(SLOT % 16 == 0, "slot alignment");
@@ -217,20 +226,22 @@ __global__ __launch_bounds__(256, 1) void bwd_rows_kernel(BwdParams prm) {
 
   for (int pass = 0; pass < 2; ++pass) {
     for (int j0 = 0; j0 < len; j0 += KC) {
-      // ---- bf16: stage K and V rows of the chunk (zero past the event) ----
-      if constexpr (BF) {
-        constexpr int PER_ROW = D / 8;
+      // ---- KVS: stage K and V rows of the chunk (zero past the event) ----
+      if constexpr (Cfg::KVS) {
+        using V16 = typename VecOf<T>::type;
+        constexpr int VEC = 16 / Cfg::ESZ;
+        constexpr int PER_ROW = D / VEC;
         const int total = H * KC * PER_ROW;
         for (int idx = tid; idx < total; idx += 256) {
           const int dv = idx % PER_ROW;
           const int key = (idx / PER_ROW) % KC;
           const int h = idx / (PER_ROW * KC);
           const int j = j0 + key;
-          const long off = rx.off(h, j < len ? j : 0, D) + dv * 8;
-          const bf16x8 kv = j < len ? *reinterpret_cast<const bf16x8*>(kg + off) : VecOf<bf16>::zero();
-          const bf16x8 vv = j < len ? *reinterpret_cast<const bf16x8*>(vg + off) : VecOf<bf16>::zero();
-          *reinterpret_cast<bf16x8*>(Ks + (h * KC + key) * Cfg::KV_ROW + dv * 8) = kv;
-          *reinterpret_cast<bf16x8*>(Vs + (h * KC + key) * Cfg::KV_ROW + dv * 8) = vv;
+          const long off = rx.off(h, j < len ? j : 0, D) + dv * VEC;
+          const V16 kv = j < len ? *reinterpret_cast<const V16*>(kg + off) : VecOf<T>::zero();
+          const V16 vv = j < len ? *reinterpret_cast<const V16*>(vg + off) : VecOf<T>::zero();
+          *reinterpret_cast<V16*>(Ks + (h * KC + key) * Cfg::KV_ROW + dv * VEC) = kv;
+          *reinterpret_cast<V16*>(Vs + (h * KC + key) * Cfg::KV_ROW + dv * VEC) = vv;
         }
       }
       // ---- row-owner: embedding, u.E and w~.E staged per (row, head) ----
@@ -277,7 +288,7 @@ __global__ __launch_bounds__(256, 1) void bwd_rows_kernel(BwdParams prm) {
           const f32x4 ue = attn ? *reinterpret_cast<const f32x4*>(slot + 16 * s + 4 * g) : zero4();
           const f32x4 we = act ? *reinterpret_cast<const f32x4*>(slot + Cfg::U_ROW + 16 * s + 4 * g) : zero4();
           KFrag<T, D> kf, vf;
-          if constexpr (BF) {
+          if constexpr (Cfg::KVS) {
             kf.load(Ks + (h * KC + 16 * s + n) * Cfg::KV_ROW, g);
             vf.load(Vs + (h * KC + 16 * s + n) * Cfg::KV_ROW, g);
           } else {
@@ -317,7 +328,7 @@ __global__ __launch_bounds__(256, 1) void bwd_rows_kernel(BwdParams prm) {
 #pragma unroll
           for (int dt = 0; dt < D / 16; ++dt) {
             JFrag<T, NS> kt;
-            if constexpr (BF) {
+            if constexpr (Cfg::KVS) {
               kt.load_tr(Ks + h * KC * Cfg::KV_ROW, Cfg::KV_ROW, 16 * dt, g, n);
             } else {
 #pragma unroll
@@ -505,13 +516,20 @@ struct BwdColsCfg {
   static constexpr int ESZ = sizeof(T);
   static constexpr int PAD = 16 / ESZ;
   static constexpr int QO_ROW = D + PAD;
-  static constexpr int QO_BYTES = BF ? 2 * HP * KC * QO_ROW * ESZ : 0;  // qt and dO (bf16 only)
   static constexpr int VEC_BYTES = 3 * HP * KC * 4;                     // lse2, D, dob
   static constexpr int E_ROW = C + PAD;
   static constexpr int E_TILE = KC * 16 * E_ROW * ESZ;                   // [row][key][c]
   static constexpr int UW_ROW = KC + 4;                                 // fp32 rows per (head, key)
   static constexpr int UW_TILE = 2 * HP * 16 * UW_ROW * 4;              // u.E and w~.E
   static constexpr int TILE_BYTES = E_TILE + UW_TILE;
+  // QOS: each chunk's qt (= q * scale) and dO rows are staged in LDS by the
+  // whole workgroup: always for bf16, for float32 wherever the staged plan
+  // fits (the transposed operands are otherwise gathered element by element
+  // from global memory; staged, cfg4's float32 cols kernel took 30.7 against
+  // 33.1 ms and B=256 L=768 H=12 D=32 C=16's 8.39 against 9.02 ms).
+  static constexpr int QO_STAGED = 2 * HP * KC * QO_ROW * ESZ;
+  static constexpr bool QOS = BF || QO_STAGED + VEC_BYTES + TILES * TILE_BYTES <= 160 * 1024;
+  static constexpr int QO_BYTES = QOS ? QO_STAGED : 0;  // qt and dO
   static constexpr int LDS_BYTES = QO_BYTES + VEC_BYTES + TILES * TILE_BYTES;
   static constexpr bool FITS = LDS_BYTES <= 160 * 1024 && HP % NW == 0 && RWS >= 4 && RWS % 4 == 0;
 };
@@ -547,7 +565,7 @@ __global__ __launch_bounds__(256, 1) void bwd_cols_kernel(BwdParams prm) {
     return;
   }
 
-  T* Qs = reinterpret_cast<T*>(smem);                 // [HP][KC][QO_ROW] bf16(q*scale)
+  T* Qs = reinterpret_cast<T*>(smem);                 // [HP][KC][QO_ROW] T(q*scale)
   T* Os = Qs + HP * KC * Cfg::QO_ROW;                 // [HP][KC][QO_ROW] dO
   float* Lv = reinterpret_cast<float*>(smem + Cfg::QO_BYTES);  // [3][HP][KC]
   unsigned char* tbase = smem + Cfg::QO_BYTES + Cfg::VEC_BYTES + tile * Cfg::TILE_BYTES;
@@ -585,24 +603,26 @@ __global__ __launch_bounds__(256, 1) void bwd_cols_kernel(BwdParams prm) {
                              : float4{0.f, 0.f, 0.f, 0.f};
 
   for (int c0 = 0; c0 < len; c0 += KC) {
-    // ---- stage the chunk's streamed rows: qt, dO (bf16), lse2, D, dob ----
-    if constexpr (BF) {
-      constexpr int PER_ROW = D / 8;
+    // ---- stage the chunk's streamed rows: qt, dO (QOS), lse2, D, dob ----
+    if constexpr (Cfg::QOS) {
+      using V16 = typename VecOf<T>::type;
+      constexpr int VEC = 16 / Cfg::ESZ;
+      constexpr int PER_ROW = D / VEC;
       const int total = H * KC * PER_ROW;
       for (int idx = tid; idx < total; idx += 256) {
         const int dv = idx % PER_ROW;
         const int il = (idx / PER_ROW) % KC;
         const int h = idx / (PER_ROW * KC);
         const int i = c0 + il;
-        bf16x8 qv = VecOf<bf16>::zero(), ov = VecOf<bf16>::zero();
+        V16 qv = VecOf<T>::zero(), ov = VecOf<T>::zero();
         if (i < len) {
-          const bf16x8 raw = *reinterpret_cast<const bf16x8*>(qg + rx.off(h, i, D) + dv * 8);
+          const V16 raw = *reinterpret_cast<const V16*>(qg + rx.off(h, i, D) + dv * VEC);
 #pragma unroll
-          for (int e = 0; e < 8; ++e) qv[e] = (bf16)((float)raw[e] * prm.scale);
-          ov = *reinterpret_cast<const bf16x8*>(dog + ra.off(h, i, D) + dv * 8);
+          for (int e = 0; e < VEC; ++e) qv[e] = (T)((float)raw[e] * prm.scale);
+          ov = *reinterpret_cast<const V16*>(dog + ra.off(h, i, D) + dv * VEC);
         }
-        *reinterpret_cast<bf16x8*>(Qs + (h * KC + il) * Cfg::QO_ROW + dv * 8) = qv;
-        *reinterpret_cast<bf16x8*>(Os + (h * KC + il) * Cfg::QO_ROW + dv * 8) = ov;
+        *reinterpret_cast<V16*>(Qs + (h * KC + il) * Cfg::QO_ROW + dv * VEC) = qv;
+        *reinterpret_cast<V16*>(Os + (h * KC + il) * Cfg::QO_ROW + dv * VEC) = ov;
       }
     }
     for (int idx = tid; idx < H * KC; idx += 256) {
@@ -668,7 +688,7 @@ __global__ __launch_bounds__(256, 1) void bwd_cols_kernel(BwdParams prm) {
         const f32x4 ue = attn ? *reinterpret_cast<const f32x4*>(us) : zero4();
         const f32x4 we = act ? *reinterpret_cast<const f32x4*>(us + HP * 16 * UWR) : zero4();
         KFrag<T, D> qa, oa;  // A = qt_i[d], dO_i[d]: lane n = streamed row 16s + n
-        if constexpr (BF) {
+        if constexpr (Cfg::QOS) {
           qa.load(Qs + (h * KC + 16 * s + n) * Cfg::QO_ROW, g);
           oa.load(Os + (h * KC + 16 * s + n) * Cfg::QO_ROW, g);
         } else {
@@ -704,7 +724,7 @@ __global__ __launch_bounds__(256, 1) void bwd_cols_kernel(BwdParams prm) {
 #pragma unroll
       for (int dt = 0; dt < D / 16; ++dt) {
         JFrag<T, NS> ot, qt;
-        if constexpr (BF) {
+        if constexpr (Cfg::QOS) {
           ot.load_tr(Os + h * KC * Cfg::QO_ROW, Cfg::QO_ROW, 16 * dt, g, n);
           qt.load_tr(Qs + h * KC * Cfg::QO_ROW, Cfg::QO_ROW, 16 * dt, g, n);
         } else {

@@ -44,8 +44,7 @@ struct FwdCfg {
   static constexpr int PAD = 16 / ESZ;   // 16 bytes of padding per LDS row
   // LDS regions. Row strides keep every vector access 16-byte aligned and
   // are padded to spread banks.
-  static constexpr int V_ROW = D + PAD;                    // elements per key row of V
-  static constexpr int V_BYTES = BF ? HP * KC * V_ROW * ESZ : 0;
+  static constexpr int V_ROW = D + PAD;                    // elements per key row of K and V
   static constexpr int E_ROW = C + PAD;                    // elements per (row, key)
   static constexpr int E_TILE = 16 * KC * E_ROW * ESZ;
   static constexpr int U_ROW = KC + 4;                     // fp32 u.E keys per slot
@@ -56,6 +55,16 @@ struct FwdCfg {
   static constexpr int STAGE_TILE = 16 * HP * SLOT;
   static constexpr int A_TILE = HP * 16 * 4;               // alpha[h][row]
   static constexpr int TILE_BYTES = E_TILE + STAGE_TILE + A_TILE;
+  // Staging of each chunk's key rows in LDS by the whole workgroup
+  // (coalesced 16-byte loads): V for bf16. KS (K as well) and float32 V are
+  // kept off: for float32 the staged LDS plan halved the workgroups per CU
+  // at B=256 L=768 H=12 D=32 C=16 (5.29 against 2.85 ms) and changed
+  // nothing at cfg4, so float32 reads K fragments and gathers V transposed
+  // from global memory.
+  static constexpr int KV_ONE = HP * KC * V_ROW * ESZ;
+  static constexpr bool VS = BF;
+  static constexpr bool KS = false;
+  static constexpr int V_BYTES = (VS ? KV_ONE : 0) + (KS ? KV_ONE : 0);  // V, then K
   static constexpr int LDS_BYTES = V_BYTES + TILES * TILE_BYTES;
   static constexpr bool FITS = LDS_BYTES <= 160 * 1024 && HP % NW == 0 && !(BF && NS != 1 && NS != 2);
   static_assert(SLOT % 16 == 0, "slots must stay 16-byte aligned");
@@ -93,6 +102,7 @@ __global__ __launch_bounds__(256, 1) void fwd_kernel(FwdParams prm) {
   }
 
   T* Vs = reinterpret_cast<T*>(smem);
+  T* Ks = Vs + HP * KC * Cfg::V_ROW;  // KS
   unsigned char* tbase = smem + Cfg::V_BYTES + tile * Cfg::TILE_BYTES;
   T* Es = reinterpret_cast<T*>(tbase);                                          // [16][KC][E_ROW]
   float* Sf = reinterpret_cast<float*>(tbase + Cfg::E_TILE);                    // [16][HP] slots
@@ -151,9 +161,10 @@ __global__ __launch_bounds__(256, 1) void fwd_kernel(FwdParams prm) {
   }
 
   for (int j0 = 0; j0 < len; j0 += KC) {
-    // ---- bf16: stage V[h][key][d] (keys past the event are zero) ----
-    if constexpr (Cfg::BF) {
-      constexpr int VEC = 8;
+    // ---- VS / KS: stage V[h][key][d] and K (keys past the event are zero) ----
+    if constexpr (Cfg::VS) {
+      using V16 = typename VecOf<T>::type;
+      constexpr int VEC = 16 / Cfg::ESZ;
       constexpr int PER_ROW = D / VEC;
       const int total = H * KC * PER_ROW;
       for (int idx = tid; idx < total; idx += 256) {
@@ -161,9 +172,13 @@ __global__ __launch_bounds__(256, 1) void fwd_kernel(FwdParams prm) {
         const int key = (idx / PER_ROW) % KC;
         const int h = idx / (PER_ROW * KC);
         const int j = j0 + key;
-        const bf16x8 val = j < len ? *reinterpret_cast<const bf16x8*>(vg + rx.off(h, j, D) + dv * VEC)
-                                   : VecOf<bf16>::zero();
-        *reinterpret_cast<bf16x8*>(Vs + (h * KC + key) * Cfg::V_ROW + dv * VEC) = val;
+        const long off = rx.off(h, j < len ? j : 0, D) + dv * VEC;
+        const V16 val = j < len ? *reinterpret_cast<const V16*>(vg + off) : VecOf<T>::zero();
+        *reinterpret_cast<V16*>(Vs + (h * KC + key) * Cfg::V_ROW + dv * VEC) = val;
+        if constexpr (Cfg::KS) {
+          const V16 kv = j < len ? *reinterpret_cast<const V16*>(kg + off) : VecOf<T>::zero();
+          *reinterpret_cast<V16*>(Ks + (h * KC + key) * Cfg::V_ROW + dv * VEC) = kv;
+        }
       }
     }
 
@@ -204,10 +219,14 @@ __global__ __launch_bounds__(256, 1) void fwd_kernel(FwdParams prm) {
       for (int s = 0; s < NS; ++s) {
         const f32x4 init =
             attn ? *reinterpret_cast<const f32x4*>(Sf + (n * HP + h) * SLOT_F + 16 * s + 4 * g) : zero4();
-        int key = j0 + 16 * s + n;
-        key = key < len ? key : len - 1;
         KFrag<T, D> kf;
-        kf.load(kg + rx.off(h, key, D), g);
+        if constexpr (Cfg::KS) {
+          kf.load(Ks + (h * KC + 16 * s + n) * Cfg::V_ROW, g);
+        } else {
+          int key = j0 + 16 * s + n;
+          key = key < len ? key : len - 1;
+          kf.load(kg + rx.off(h, key, D), g);
+        }
         S[s] = mma_k<D>(kf, qf[hl], init);
       }
       float mx = -INFINITY;
@@ -238,7 +257,7 @@ __global__ __launch_bounds__(256, 1) void fwd_kernel(FwdParams prm) {
 #pragma unroll
       for (int dt = 0; dt < D / 16; ++dt) {
         JFrag<T, NS> vf;
-        if constexpr (Cfg::BF) {
+        if constexpr (Cfg::VS) {
           vf.load_tr(Vs + h * KC * Cfg::V_ROW, Cfg::V_ROW, 16 * dt, g, n);
         } else {
 #pragma unroll
