@@ -43,7 +43,9 @@ FST_PLAN_BWD_T32 = 1 << 23
 FST_PLAN_BWD_T64 = 1 << 24
 FST_PLAN_BWD_KC16 = 1 << 25
 FST_PLAN_BWD_KC32 = 1 << 26
-FST_PLAN_MASK = 0x07FFFF00
+FST_PLAN_BWD_PASS1 = 1 << 27
+FST_PLAN_BWD_PASS2 = 1 << 28
+FST_PLAN_MASK = 0x1FFFFF00
 
 FST_PHASE_WORKLIST = 1
 FST_PHASE_FWD = 2

@@ -18,9 +18,10 @@
 // Two kernels, each the single writer of its outputs (no atomics, fixed
 // loop order => bitwise deterministic):
 //  * rows: workgroups own query rows, same head-owner / row-owner split as
-//    the forward. Pass 1 over the keys forms D; pass 2 recomputes the tile
-//    exactly as pass 1 did and accumulates dq (head-owner), H and G
-//    (row-owner), sigma. The epilogue projects H through W into dq, and
+//    the forward. One pass over the keys forms D online (N / Z over the keys
+//    seen, the accumulators corrected by the P-sums they lack whenever D
+//    moves) and accumulates dq (head-owner), H and G (row-owner), sigma. The
+//    epilogue projects H through W into dq, and
 //    reduces qt (x) H + dO (x) G and dO over the block's rows into per-block
 //    partials of dW and db. u, w~, dob and D go to scratch for the cols
 //    kernel.
@@ -40,8 +41,8 @@ namespace fst {
 // One 16-row MFMA tile (rows = the lane index of the C tile's columns) of
 // P and dP for one head: s = mma(A_s, B_s) + init_s, dP = mma(A_p, B_p) +
 // init_p, both already computed by the caller; this applies masking, the
-// exponential and the dob term. Written once and used by every pass so the
-// arithmetic of P and dP is identical wherever they are recomputed.
+// exponential and the dob term. Written once and used by both kernels so
+// the arithmetic of P and dP is identical wherever they are recomputed.
 __device__ __forceinline__ void finish_p_dp(f32x4& s, f32x4& dp, float lse2, float dob, unsigned valid_mask) {
 #pragma unroll
   for (int r = 0; r < 4; ++r) {
@@ -76,7 +77,8 @@ struct BwdRowsCfg {
   static constexpr int SLOT_2 = SLOT_O > SLOT_HG ? SLOT_O : SLOT_HG;
   static constexpr int SLOT = SLOT_1 > SLOT_2 ? SLOT_1 : SLOT_2;
   static constexpr int STAGE_TILE = 16 * HP * SLOT;
-  static constexpr int TILE_BYTES = E_TILE + STAGE_TILE;
+  static constexpr int DD_BYTES = 16 * HP * 4;  // per (row, head) increments of D
+  static constexpr int TILE_BYTES = E_TILE + STAGE_TILE + DD_BYTES;
   // KVS: each chunk's K and V rows are staged in LDS by the whole workgroup
   // (coalesced 16-byte loads, then row fragments and transposed K read back
   // from LDS); bf16 only. For float32 every head-owner wave loads its K and
@@ -93,7 +95,11 @@ struct BwdRowsCfg {
   static_assert(SLOT % 16 == 0, "slot alignment");
 };
 
-template <typename T, int HP, int D, int C, int NW, int NS>
+// PASSES = 1: one pass over the keys with D formed online; 2: a first pass
+// forms D, the second accumulates with it (no corrections, no sum P k, H
+// and G live only in the second pass: fewer registers at the large
+// layouts).
+template <typename T, int HP, int D, int C, int NW, int NS, int PASSES>
 __global__ __launch_bounds__(256, 1) void bwd_rows_kernel(BwdParams prm) {
   using Cfg = BwdRowsCfg<T, HP, D, C, NW, NS>;
   constexpr bool BF = Cfg::BF;
@@ -132,6 +138,7 @@ __global__ __launch_bounds__(256, 1) void bwd_rows_kernel(BwdParams prm) {
   T* Es = reinterpret_cast<T*>(tbase);
   float* Sf = reinterpret_cast<float*>(tbase + Cfg::E_TILE);
   T* St = reinterpret_cast<T*>(tbase + Cfg::E_TILE);
+  float* Dd = reinterpret_cast<float*>(tbase + Cfg::E_TILE + Cfg::STAGE_TILE);  // [HP][16] increments of D
 
   const T* __restrict__ qg = reinterpret_cast<const T*>(prm.q);
   const T* __restrict__ kg = reinterpret_cast<const T*>(prm.k);
@@ -139,11 +146,18 @@ __global__ __launch_bounds__(256, 1) void bwd_rows_kernel(BwdParams prm) {
   const T* __restrict__ dog = reinterpret_cast<const T*>(prm.dout);
 
   // ---- head-owner state (rows on lane n) ----
+  // PASSES = 1: one pass over the keys. D = N / Z is formed online: after chunk t the
+  // running D_t (N, Z over the keys seen) replaces D_{t-1}, and the
+  // accumulators built with the old value are corrected with the P-sums
+  // they lack (dQ -= dD A2, A2 = sum P k; H -= dD G; sigma -= dD Z), so at
+  // the end each equals its two-pass value for D = N / Z over all keys
+  // (backward.py:371-407 forms D in a first pass). sigma is the sum of the
+  // dS values the products were fed, with the same corrections.
   const int my_row = i0 + n;
   const bool row_ok = my_row < len;
   KFrag<T, D> qf[HW], dof[HW];
-  f32x4 dQ[HW][D / 16];
-  float lse2[HW], dobv[HW], nsum[HW], zsum[HW], dval[HW], sig[HW];
+  f32x4 dQ[HW][D / 16], A2[HW][D / 16];
+  float lse2[HW], dobv[HW], nsum[HW], zsum[HW], dval[HW], sig[HW], zlane[HW];
 #pragma unroll
   for (int hl = 0; hl < HW; ++hl) {
     const int h = ws * HW + hl;
@@ -169,9 +183,9 @@ __global__ __launch_bounds__(256, 1) void bwd_rows_kernel(BwdParams prm) {
     }
     dobv[hl] = group_allsum(part);
     if (g == 0 && ok) prm.dob[ra.vec(h, my_row)] = dobv[hl];
-    nsum[hl] = zsum[hl] = sig[hl] = dval[hl] = 0.f;
+    nsum[hl] = zsum[hl] = sig[hl] = dval[hl] = zlane[hl] = 0.f;
 #pragma unroll
-    for (int dt = 0; dt < D / 16; ++dt) dQ[hl][dt] = zero4();
+    for (int dt = 0; dt < D / 16; ++dt) dQ[hl][dt] = A2[hl][dt] = zero4();
   }
 
   // ---- row-owner state (heads on lane n) ----
@@ -224,7 +238,7 @@ __global__ __launch_bounds__(256, 1) void bwd_rows_kernel(BwdParams prm) {
     pos_i[k2] = use_e ? ra.pos(prm.ev.pos4, row < len ? row : (len > 0 ? len - 1 : 0)) : float4{0.f, 0.f, 0.f, 0.f};
   }
 
-  for (int pass = 0; pass < 2; ++pass) {
+  for (int pass = 0; pass < PASSES; ++pass) {
     for (int j0 = 0; j0 < len; j0 += KC) {
       // ---- KVS: stage K and V rows of the chunk (zero past the event) ----
       if constexpr (Cfg::KVS) {
@@ -276,7 +290,7 @@ __global__ __launch_bounds__(256, 1) void bwd_rows_kernel(BwdParams prm) {
       }
       __syncthreads();
 
-      // ---- head-owner: P, dP (and in pass 2 dS, dq) ----
+      // ---- head-owner: P, dP, online D, dS, dQ ----
 #pragma unroll
       for (int hl = 0; hl < HW; ++hl) {
         const int h = ws * HW + hl;
@@ -305,15 +319,31 @@ __global__ __launch_bounds__(256, 1) void bwd_rows_kernel(BwdParams prm) {
           finish_p_dp(S[s], P_[s], lse2[hl], dobv[hl], vm);
         }
         // S now holds P, P_ holds dP.
-        if (pass == 0) {
+        float nt = 0.f, zt = 0.f;
 #pragma unroll
-          for (int s = 0; s < NS; ++s)
+        for (int s = 0; s < NS; ++s)
 #pragma unroll
-            for (int r = 0; r < 4; ++r) {
-              nsum[hl] = __builtin_fmaf(S[s][r], P_[s][r], nsum[hl]);
-              zsum[hl] += S[s][r];
-            }
+          for (int r = 0; r < 4; ++r) {
+            nt = __builtin_fmaf(S[s][r], P_[s][r], nt);
+            zt += S[s][r];
+          }
+        float dD = 0.f;
+        if constexpr (PASSES == 2) {
+          if (pass == 0) {  // the first pass forms N and Z only
+            nsum[hl] += group_allsum(nt);
+            zsum[hl] += group_allsum(zt);
+            continue;
+          }
         } else {
+          nsum[hl] += group_allsum(nt);
+          zsum[hl] += group_allsum(zt);
+          const float dn = zsum[hl] > 0.f ? nsum[hl] / zsum[hl] : 0.f;
+          dD = dn - dval[hl];
+          dval[hl] = dn;
+          sig[hl] = __builtin_fmaf(-dD, zlane[hl], sig[hl]);
+          zlane[hl] += zt;
+        }
+        {
           f32x4 dS[NS];
 #pragma unroll
           for (int s = 0; s < NS; ++s)
@@ -339,6 +369,10 @@ __global__ __launch_bounds__(256, 1) void bwd_rows_kernel(BwdParams prm) {
                   kt.v[4 * s + r] = j < len ? kg[rx.off(h, j, D) + 16 * dt + n] : 0.f;
                 }
             }
+            if constexpr (PASSES == 1) {
+              dQ[hl][dt] = dQ[hl][dt] - dD * A2[hl][dt];
+              A2[hl][dt] = mma_j(kt, pf, A2[hl][dt]);
+            }
             dQ[hl][dt] = mma_j(kt, dsf, dQ[hl][dt]);
           }
           if (use_e) {
@@ -346,16 +380,18 @@ __global__ __launch_bounds__(256, 1) void bwd_rows_kernel(BwdParams prm) {
             T* tslot = St + (n * HP + h) * SLOT_T;
             pf.store_keys(tslot, g);
             dsf.store_keys(tslot + Cfg::P_ROW, g);
+            if (PASSES == 1 && g == 0) Dd[h * 16 + n] = dD;
           }
         }
       }
       __syncthreads();
 
-      // ---- row-owner (pass 2): H += E^T dS, G += E^T P ----
-      if (pass == 1 && use_e) {
+      // ---- row-owner: H -= dD G; H += E^T dS, G += E^T P (last pass) ----
+      if (use_e && pass == PASSES - 1) {
 #pragma unroll
         for (int ri = 0; ri < RW; ++ri) {
           const int il = ws * RW + ri;
+          const float dd = (PASSES == 1 && n < H) ? Dd[n * 16 + il] : 0.f;
           JFrag<T, NS> pf, dsf;
           if (n < H) {
             const T* tslot = St + (il * HP + n) * SLOT_T;
@@ -369,23 +405,26 @@ __global__ __launch_bounds__(256, 1) void bwd_rows_kernel(BwdParams prm) {
           for (int ct = 0; ct < C / 16; ++ct) {
             JFrag<T, NS> ef;
             ef.load_tr(Es + il * KC * Cfg::E_ROW, Cfg::E_ROW, 16 * ct, g, n);
-            if (attn) Hacc[ri][ct] = mma_j(ef, dsf, Hacc[ri][ct]);
-            if (act) Gacc[ri][ct] = mma_j(ef, pf, Gacc[ri][ct]);
+            if (attn) {
+              if constexpr (PASSES == 1) Hacc[ri][ct] = Hacc[ri][ct] - dd * Gacc[ri][ct];
+              Hacc[ri][ct] = mma_j(ef, dsf, Hacc[ri][ct]);
+            }
+            // G also feeds H's corrections in the one-pass form.
+            if (PASSES == 1 || act) Gacc[ri][ct] = mma_j(ef, pf, Gacc[ri][ct]);
           }
         }
       }
       __syncthreads();
     }
-    if (pass == 0) {
+    if (PASSES == 2 && pass == 0) {
 #pragma unroll
-      for (int hl = 0; hl < HW; ++hl) {
-        const int h = ws * HW + hl;
-        const float nn = group_allsum(nsum[hl]);
-        const float zz = group_allsum(zsum[hl]);
-        dval[hl] = zz > 0.f ? nn / zz : 0.f;
-        if (g == 0 && h < H && row_ok) prm.dsum[ra.vec(h, my_row)] = dval[hl];
-      }
+      for (int hl = 0; hl < HW; ++hl) dval[hl] = zsum[hl] > 0.f ? nsum[hl] / zsum[hl] : 0.f;
     }
+  }
+#pragma unroll
+  for (int hl = 0; hl < HW; ++hl) {
+    const int h = ws * HW + hl;
+    if (g == 0 && h < H && row_ok) prm.dsum[ra.vec(h, my_row)] = dval[hl];
   }
 
   // ---- epilogue: dq = scale (dQ + W H + sigma b) ----
@@ -783,6 +822,16 @@ struct BwdPick {
   static constexpr bool OK = STATIC != 0;
 };
 
+// Passes of the rows kernel's static choice: one where the lane state of
+// the one-pass form stays small ((HP / NW) D + (16 / NW) C <= 256: Q, dO,
+// dQ and sum P k per head, u, w~, H and G per row; at B=256 L=768 H=12
+// D=32 C=16 in float32 one pass took 7.06 against 9.72 ms), two where it
+// would spill (cfg4, D = C = 64: 82.8 against 41.2 ms).
+template <int HP, int D, int C, int NW>
+constexpr int rows_static_passes() {
+  return (HP / NW) * D + (16 / NW) * C <= 256 ? 1 : 2;
+}
+
 template <typename T, int HP, int D, int C, int NW, int NS>
 int bwd_launch_v(const BwdParams& prm, int which, hipStream_t stream, int grid, bool query, int* rows) {
   using R = BwdRowsCfg<T, HP, D, C, NW, NS>;
@@ -793,7 +842,10 @@ int bwd_launch_v(const BwdParams& prm, int which, hipStream_t stream, int grid, 
     } else {
       *rows = R::ROWS;
       if (query) return FST_OK;
-      auto kern = bwd_rows_kernel<T, HP, D, C, NW, NS>;
+      const int passes = (prm.flags & FST_PLAN_BWD_PASS1)   ? 1
+                         : (prm.flags & FST_PLAN_BWD_PASS2) ? 2
+                                                            : rows_static_passes<HP, D, C, NW>();
+      auto kern = passes == 1 ? bwd_rows_kernel<T, HP, D, C, NW, NS, 1> : bwd_rows_kernel<T, HP, D, C, NW, NS, 2>;
       if (hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, R::LDS_BYTES) !=
           hipSuccess)
         return FST_ELAUNCH;
@@ -821,8 +873,9 @@ template <typename T, int HP, int D, int C>
 constexpr int bwd_split_plans() {
   using PR = BwdPick<BwdRowsCfg, T, HP, D, C>;
   using PC = BwdPick<BwdColsCfg, T, HP, D, C>;
-  return split_plans<PR::template F>(FST_PLAN_BWD_T16, FST_PLAN_BWD_KC16) &
-         split_plans<PC::template F>(FST_PLAN_BWD_T16, FST_PLAN_BWD_KC16);
+  return (split_plans<PR::template F>(FST_PLAN_BWD_T16, FST_PLAN_BWD_KC16) &
+          split_plans<PC::template F>(FST_PLAN_BWD_T16, FST_PLAN_BWD_KC16)) |
+         FST_PLAN_BWD_PASS1 | FST_PLAN_BWD_PASS2;
 }
 
 // Launches (or, with query, only checks) the rows (which = 0) or cols

@@ -314,6 +314,7 @@ static const int kPlanGroups[] = {
     FST_PLAN_FWD_T16 | FST_PLAN_FWD_T32 | FST_PLAN_FWD_T64,
     FST_PLAN_BWD_T16 | FST_PLAN_BWD_T32 | FST_PLAN_BWD_T64,
     FST_PLAN_BWD_KC16 | FST_PLAN_BWD_KC32,
+    FST_PLAN_BWD_PASS1 | FST_PLAN_BWD_PASS2,
 };
 
 static int check_common(int dtype, int flags, int B, int H, int L, int T, int D, int C) {

@@ -11,7 +11,8 @@ combination is):
 * bf16 backward cols kernel: two or three workgroups per CU;
 * float32 forward: 16, 32 or 64 query rows per workgroup, 16- or 32-key
   chunks; float32 backward: 16, 32 or 64 rows (keys) per workgroup and
-  16- or 32-key (row) chunks, for the rows and cols kernels together.
+  16- or 32-key (row) chunks, for the rows and cols kernels together, and
+  one or two passes of the rows kernel over the keys.
 
 Without tuning the library runs its static choice per (dtype, H, D, C). With
 tuning on, the first call of a shape times every supported combination of
@@ -57,7 +58,8 @@ _ROWS_GROUPS = ((_lib.FST_PLAN_ROWS_W4, _lib.FST_PLAN_ROWS_W8, _lib.FST_PLAN_ROW
 _COLS_GROUPS = ((_lib.FST_PLAN_COLS_OCC2, _lib.FST_PLAN_COLS_OCC3),)
 # float32 backward groups: they set the rows and the cols kernel together.
 _BWD_GROUPS = ((_lib.FST_PLAN_BWD_T16, _lib.FST_PLAN_BWD_T32, _lib.FST_PLAN_BWD_T64),
-               (_lib.FST_PLAN_BWD_KC16, _lib.FST_PLAN_BWD_KC32))
+               (_lib.FST_PLAN_BWD_KC16, _lib.FST_PLAN_BWD_KC32),
+               (_lib.FST_PLAN_BWD_PASS1, _lib.FST_PLAN_BWD_PASS2))
 
 
 def _bits(groups: Sequence[Sequence[int]]) -> int:
@@ -377,7 +379,8 @@ _NAMES = ((_lib.FST_PLAN_FWD_OCC2, "fwd:occ2"), (_lib.FST_PLAN_FWD_OCC3, "fwd:oc
           (_lib.FST_PLAN_COLS_OCC2, "cols:occ2"), (_lib.FST_PLAN_COLS_OCC3, "cols:occ3"),
           (_lib.FST_PLAN_BWD_T16, "bwd:t16"), (_lib.FST_PLAN_BWD_T32, "bwd:t32"),
           (_lib.FST_PLAN_BWD_T64, "bwd:t64"), (_lib.FST_PLAN_BWD_KC16, "bwd:kc16"),
-          (_lib.FST_PLAN_BWD_KC32, "bwd:kc32"))
+          (_lib.FST_PLAN_BWD_KC32, "bwd:kc32"), (_lib.FST_PLAN_BWD_PASS1, "bwd:pass1"),
+          (_lib.FST_PLAN_BWD_PASS2, "bwd:pass2"))
 
 
 def plan_names(plan: int) -> Optional[str]:

@@ -113,7 +113,11 @@ enum fst_flags {
   /* float32 backward: keys (rows kernel) and rows (cols kernel) per chunk */
   FST_PLAN_BWD_KC16 = 1 << 25,
   FST_PLAN_BWD_KC32 = 1 << 26,
-  FST_PLAN_MASK = 0x07ffff00
+  /* float32 backward rows kernel: passes over the keys (one, with D formed
+   * online and the accumulators corrected as it moves; or two, D first) */
+  FST_PLAN_BWD_PASS1 = 1 << 27,
+  FST_PLAN_BWD_PASS2 = 1 << 28,
+  FST_PLAN_MASK = 0x1fffff00
 };
 
 /* Phases of one operator call, for callers that time or schedule them

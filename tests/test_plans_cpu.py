@@ -16,7 +16,7 @@ BF16_ALL = 0x7FF00  # every bf16 group's bits (forward, rows, cols)
 F32_FWD = _lib.FST_PLAN_FWD_KC16 | _lib.FST_PLAN_FWD_KC32 | _lib.FST_PLAN_FWD_T16 | _lib.FST_PLAN_FWD_T32 \
     | _lib.FST_PLAN_FWD_T64
 F32_BWD = _lib.FST_PLAN_BWD_T16 | _lib.FST_PLAN_BWD_T32 | _lib.FST_PLAN_BWD_T64 | _lib.FST_PLAN_BWD_KC16 \
-    | _lib.FST_PLAN_BWD_KC32
+    | _lib.FST_PLAN_BWD_KC32 | _lib.FST_PLAN_BWD_PASS1 | _lib.FST_PLAN_BWD_PASS2
 GROUPS = [
     _lib.FST_PLAN_FWD_OCC2 | _lib.FST_PLAN_FWD_OCC3,
     _lib.FST_PLAN_ROWS_W4 | _lib.FST_PLAN_ROWS_W8 | _lib.FST_PLAN_ROWS_W8X2,
@@ -26,6 +26,7 @@ GROUPS = [
     _lib.FST_PLAN_FWD_T16 | _lib.FST_PLAN_FWD_T32 | _lib.FST_PLAN_FWD_T64,
     _lib.FST_PLAN_BWD_T16 | _lib.FST_PLAN_BWD_T32 | _lib.FST_PLAN_BWD_T64,
     _lib.FST_PLAN_BWD_KC16 | _lib.FST_PLAN_BWD_KC32,
+    _lib.FST_PLAN_BWD_PASS1 | _lib.FST_PLAN_BWD_PASS2,
 ]
 
 
@@ -51,7 +52,7 @@ def test_plans_of_shapes():
     assert lib.fst_plans(_lib.FST_F32, 4, 16, 16) == F32_FWD | F32_BWD
     assert lib.fst_plans(_lib.FST_F32, 8, 64, 64) == (
         _lib.FST_PLAN_FWD_KC16 | _lib.FST_PLAN_FWD_KC32 | _lib.FST_PLAN_FWD_T16 | _lib.FST_PLAN_FWD_T32
-        | _lib.FST_PLAN_BWD_T16 | _lib.FST_PLAN_BWD_KC16)
+        | _lib.FST_PLAN_BWD_T16 | _lib.FST_PLAN_BWD_KC16 | _lib.FST_PLAN_BWD_PASS1 | _lib.FST_PLAN_BWD_PASS2)
     assert lib.fst_plans(_lib.FST_BF16, 17, 32, 16) == 0
     assert lib.fst_plans(_lib.FST_BF16, 12, 24, 16) == 0
     for dtype in (_lib.FST_BF16, _lib.FST_F32):
@@ -70,7 +71,7 @@ def test_plans_of_shapes():
                         assert mask & ~(F32_FWD | F32_BWD) == 0
                     # the static plan and every offered bit alone are runnable
                     assert lib.fst_plan_supported(dtype, h, d, c, 0)
-                    for b in range(8, 27):
+                    for b in range(8, 29):
                         if mask >> b & 1:
                             assert lib.fst_plan_supported(dtype, h, d, c, 1 << b), (dtype, h, d, c, b)
 
@@ -98,7 +99,10 @@ def test_plan_combinations():
     assert not sup(f32, 12, 32, 16, _lib.FST_PLAN_FWD_OCC2)
     assert not sup(bf, 12, 32, 16, _lib.FST_PLAN_FWD_T32)
     assert not sup(bf, 12, 32, 16, _lib.FST_PLAN_ROWS_W4 | _lib.FST_PLAN_ROWS_W8X2)
-    assert not sup(bf, 12, 32, 16, 1 << 27)
+    assert not sup(bf, 12, 32, 16, 1 << 29)
+    # one or two passes of the float32 rows kernel, with any fitting split
+    assert sup(f32, 8, 64, 64, _lib.FST_PLAN_BWD_PASS1) and sup(f32, 8, 64, 64, _lib.FST_PLAN_BWD_PASS2)
+    assert not sup(bf, 12, 32, 16, _lib.FST_PLAN_BWD_PASS1)
 
 
 @needs_lib
@@ -108,11 +112,11 @@ def test_plan_bits_are_validated():
     base = ws(_lib.FST_BF16, 3, 4, 12, 64, 0, 32, 16)
     assert base > 0
     # the workspace does not depend on the plan
-    for b in range(8, 27):
+    for b in range(8, 29):
         if BF16_ALL >> b & 1:
             assert ws(_lib.FST_BF16, 3 | (1 << b), 4, 12, 64, 0, 32, 16) == base
     base32 = ws(_lib.FST_F32, 3, 4, 4, 64, 0, 16, 16)
-    for b in range(8, 27):
+    for b in range(8, 29):
         if (F32_FWD | F32_BWD) >> b & 1:
             assert ws(_lib.FST_F32, 3 | (1 << b), 4, 4, 64, 0, 16, 16) == base32
     # two variants of one kernel knob
@@ -132,7 +136,7 @@ def test_plan_bits_are_validated():
     assert rc == _lib.FST_EUNSUPPORTED and "plan" in _lib.last_error()
     assert ws(_lib.FST_BF16, 3 | _lib.FST_PLAN_ROWS_W4, 4, 8, 64, 0, 64, 64) == 0
     # bits past the plan field are unknown flags
-    rc = lib.fst_forward(0, 3 | (1 << 27), 1, 12, 8, 0, 32, 16, None, None, None, None, None, None, None,
+    rc = lib.fst_forward(0, 3 | (1 << 29), 1, 12, 8, 0, 32, 16, None, None, None, None, None, None, None,
                          1.0, None, None, None, 0, None)
     assert rc == _lib.FST_EINVAL and "flag" in _lib.last_error()
 
@@ -166,7 +170,7 @@ def test_plan_names_and_fixed_plan():
 
 
 def test_plan_names_cover_every_bit():
-    for b in range(8, 27):
+    for b in range(8, 29):
         assert tune.plan_names(1 << b), b
     assert tune.plan_names(_lib.FST_PLAN_ROWS_W8X2 | _lib.FST_PLAN_ROWS_KV_LDS | _lib.FST_PLAN_FWD_KC32) == \
         "fwd:kc32 rows:w8x2 rows:kvlds"

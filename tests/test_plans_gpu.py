@@ -6,7 +6,8 @@ for every supported combination of them out, lse, dq, dk, dv and the dS row
 sums must equal the static plan's bit for bit, and dW and db (whose fp32
 per-tile partials another wave or tile layout adds in another order) agree
 to fp32 rounding. The key-chunk groups move the online softmax's rescaling
-points and the order of the key sums: a combination with a key-chunk bit is
+points and the order of the key sums, and the float32 rows kernel's pass
+group forms D online or in a first pass: a combination with such a bit is
 held to the float64 oracle at the dtype's tolerance (bf16 2e-2, float32
 1e-4 relative). The tuner, switched on, must pick plans the shape offers (or
 keep the static one) and leave every result as that rule allows.
@@ -30,7 +31,9 @@ if torch.cuda.is_available():
 DEV = "cuda"
 BF, F32 = 0, 1
 TOL = {BF: 2e-2, F32: 1e-4}
-KC_BITS = (1 << 17) | (1 << 18) | (1 << 25) | (1 << 26)  # FST_PLAN_FWD_KC*, FST_PLAN_BWD_KC*
+# Groups whose variants change the order of the arithmetic: FST_PLAN_FWD_KC*,
+# FST_PLAN_BWD_KC*, FST_PLAN_BWD_PASS* (D formed online or in a first pass).
+KC_BITS = (1 << 17) | (1 << 18) | (1 << 25) | (1 << 26) | (1 << 27) | (1 << 28)
 
 # (dtype, heads, dim, channels, lengths, packed, bias flags)
 SHAPES = [
@@ -49,7 +52,7 @@ SHAPES = [
 
 FWD_GROUPS = [(1 << 8, 1 << 9), (1 << 17, 1 << 18), (1 << 19, 1 << 20, 1 << 21)]
 BWD_GROUPS = [(1 << 10, 1 << 11, 1 << 14), (1 << 15, 1 << 16), (1 << 12, 1 << 13),
-              (1 << 22, 1 << 23, 1 << 24), (1 << 25, 1 << 26)]
+              (1 << 22, 1 << 23, 1 << 24), (1 << 25, 1 << 26), (1 << 27, 1 << 28)]
 
 
 def _inputs(dtype, heads, dim, chans, lens, packed, seed):
