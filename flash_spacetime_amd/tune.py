@@ -23,8 +23,8 @@ static choice.
 
 The occupancy, wave, K/V-staging and tile-height variants leave out, lse,
 dq, dk, dv and rowsum unchanged bit for bit (dW and db change only in the
-order their fp32 partial sums are added); the key-chunk variants agree with
-the static choice to rounding. A shape is keyed by the GPU architecture, the
+order their fp32 partial sums are added); the key-chunk and pass variants
+agree with the static choice to rounding. A shape is keyed by the GPU architecture, the
 library version, kind, dtype, H, D, C, the layout and bias flags, and the
 bit lengths of its batch and length (padded) or token count (packed), so the
 ragged batches of one training run share a choice.

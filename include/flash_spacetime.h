@@ -80,7 +80,8 @@ enum fst_flags {
    * and rowsum are the same bit for bit, and dweight / dbias differ only in
    * the order in which their fp32 partial sums are added. The key-chunk
    * groups move the points where the online softmax rescales and the order
-   * of the sums over keys, so their results agree to rounding.
+   * of the sums over keys, and the pass group forms D online or in a first
+   * pass, so their results agree to rounding.
    * No reference counterpart: the reference's Triton kernels take fixed tile
    * constants (_tiles.py), are not autotuned (README.md:86-95), and its
    * launchers' block_m / block_n / num_warps arguments (forward.py:233-236,
