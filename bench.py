@@ -38,14 +38,28 @@ PEAK_BF16_TFLOPS = 2500.0  # MI355X dense bf16 MFMA
 PEAK_HBM_GBS = 8000.0
 
 
+# Position distribution of the synthetic inputs (--pos): "detector" draws the
+# BASELINE configs' x, y, z ~ U(-500, 500), t ~ U(0, 2e4) (every off-diagonal
+# pair saturates the angle clip, so E is nearly constant), "normal" the
+# survey's twin with pos ~ N(0, 1) [.., 4], which exercises E for real.
+POS = "detector"
+
+
+def draw_pos(gen, *lead):
+    """Positions [*lead, 4] from `gen` in the distribution POS names."""
+    if POS == "normal":
+        return torch.randn(*lead, 4, generator=gen)
+    xyz = (torch.rand(*lead, 3, generator=gen) - 0.5) * 1000.0
+    t = torch.rand(*lead, 1, generator=gen) * 2e4
+    return torch.cat([xyz, t], -1)
+
+
 def make_inputs(device):
     gen = torch.Generator().manual_seed(0)
     q = torch.randn(B, H, L, D, generator=gen)
     k = torch.randn(B, H, L, D, generator=gen)
     v = torch.randn(B, H, L, D, generator=gen)
-    xyz = (torch.rand(B, L, 3, generator=gen) - 0.5) * 1000.0
-    t = torch.rand(B, L, 1, generator=gen) * 2e4
-    feats = torch.cat([xyz, t], -1)
+    feats = draw_pos(gen, B, L)
     w = torch.randn(D, C, generator=gen) / C ** 0.5
     bias = torch.randn(D, generator=gen) * 0.02
     lengths = torch.randint(16, L + 1, (B,), generator=gen)
@@ -299,7 +313,7 @@ def run_forward_only(steps, warmup):
         "unit": "ms", "n_gpus": 1, "steps": steps, "warmup": warmup, "ms_per_step": round(ms, 4),
         "higher_is_better": False, "scaling": "weak", "vs_baseline": None, "dtype": "bf16",
         "data": "synthetic (seeded; BASELINE.json configs[1] distributions)",
-        "config": {"workload": WORKLOADS["cfg1"]}, "peak_gib": round(peak, 4),
+        "config": {"workload": WORKLOADS["cfg1"], "positions": POS}, "peak_gib": round(peak, 4),
         "mfma_pct_of_peak": round(100.0 * f_fwd / (ms * 1e-3) / (PEAK_BF16_TFLOPS * 1e12), 3),
     }), flush=True)
 
@@ -433,8 +447,7 @@ def run_other_workload(name, steps, warmup):
         total = int(lens.sum())
         dtype = torch.bfloat16
         shape = (total, h, d)
-        xyz = (torch.rand(total, 3, generator=gen) - 0.5) * 1000.0
-        t = torch.rand(total, 1, generator=gen) * 2e4
+        pos = draw_pos(gen, total)
         cu = torch.zeros(n_ev + 1, dtype=torch.int32)
         cu[1:] = torch.cumsum(lens, 0)
         cu = cu.to(dev)
@@ -444,14 +457,13 @@ def run_other_workload(name, steps, warmup):
         lens = torch.full((bsz,), length, dtype=torch.long)
         dtype = torch.float32 if name == "cfg4-fp32" else torch.bfloat16
         shape = (bsz, h, length, d)
-        xyz = (torch.rand(bsz, length, 3, generator=gen) - 0.5) * 1000.0
-        t = torch.rand(bsz, length, 1, generator=gen) * 2e4
+        pos = draw_pos(gen, bsz, length)
         cu = None
         scale_qk = 30.0
     q = (rn(*shape) * scale_qk).to(dev, dtype)
     k = (rn(*shape) * scale_qk).to(dev, dtype)
     v = rn(*shape).to(dev, dtype)
-    feats = torch.cat([xyz, t], -1).to(dev)
+    feats = pos.to(dev)
     w = (rn(d, c) / c ** 0.5).to(dev)
     bias = (rn(d) * 0.02).to(dev)
     do = rn(*shape).to(dev, dtype)
@@ -485,7 +497,7 @@ def run_other_workload(name, steps, warmup):
         "steps": steps, "warmup": warmup, "ms_per_step": round(ms, 4), "higher_is_better": False,
         "scaling": "weak", "vs_baseline": None, "dtype": "bf16" if dtype == torch.bfloat16 else "fp32",
         "data": "synthetic (seeded; BASELINE.json distributions)",
-        "config": {"workload": WORKLOADS[name], "valid_pairs": sl2},
+        "config": {"workload": WORKLOADS[name], "valid_pairs": sl2, "positions": POS},
         "plan": plan_label(plan),
         "mfma_pct_of_peak": round(100.0 * f_total / (ms * 1e-3) / (peak * 1e12), 3),
         "algorithmic_tflop": round(f_total / 1e12, 4),
@@ -586,10 +598,15 @@ def main():
                          "that rocprof counter runs use to scale FETCH_SIZE / WRITE_SIZE")
     ap.add_argument("--workload", default="cfg2", choices=["cfg2", *WORKLOADS],
                     help="cfg2 (default) is the metric's configuration; the others print a line of their own")
+    ap.add_argument("--pos", choices=["detector", "normal"], default="detector",
+                    help="positions as the BASELINE configs draw them (detector units), or the N(0, 1) twin "
+                         "that exercises the pair embedding")
     ap.add_argument("--autotune", action="store_true",
                     help="time the compiled kernel variants of each shape on its first call (a warm-up "
                          "step) and run the fastest; without it the library's static choice runs")
     args = ap.parse_args()
+    global POS
+    POS = args.pos
     if args.autotune:
         from flash_spacetime_amd import tune
 
@@ -672,12 +689,13 @@ def main():
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "bf16",
-        "data": "synthetic (seeded; BASELINE.json configs[2] distributions)",
+        "data": "synthetic (seeded; BASELINE.json configs[2] distributions)" if POS == "detector" else
+                "synthetic (seeded; configs[2] with positions ~ N(0, 1))",
         "config": {
             "workload": "configs[2]: flash_spacetime_attention fwd+bwd, B=256 L=768 H=12 D=32 C=16 bf16, "
                         "valid lengths U{16..768} (bool key_padding_mask -> seqlens once), W/b fp32",
             "B": B, "L": L, "H": H, "D": D, "C": C,
-            "valid_pairs": flops["sum_l2"],
+            "valid_pairs": flops["sum_l2"], "positions": POS,
         },
         "plan": plan_label(plan),
         "peak_gib": round(peak_gib, 4),
