@@ -45,7 +45,9 @@ FST_PLAN_BWD_KC16 = 1 << 25
 FST_PLAN_BWD_KC32 = 1 << 26
 FST_PLAN_BWD_PASS1 = 1 << 27
 FST_PLAN_BWD_PASS2 = 1 << 28
-FST_PLAN_MASK = 0x1FFFFF00
+FST_PLAN_FWD_W8 = 1 << 29
+FST_PLAN_BWD_W8 = 1 << 30
+FST_PLAN_MASK = 0x7FFFFF00
 
 FST_PHASE_WORKLIST = 1
 FST_PHASE_FWD = 2

@@ -59,12 +59,14 @@ __device__ __forceinline__ void finish_p_dp(f32x4& s, f32x4& dp, float lse2, flo
 template <typename T, int HP, int D, int C, int NW, int NS>
 struct BwdRowsCfg {
   static constexpr bool BF = is_bf16<T>::value;
-  static constexpr int HW = HP / NW, RW = 16 / NW, TILES = 4 / NW, ROWS = 16 * TILES;
+  static constexpr int HW = HP / NW, RW = 16 / NW;
+  static constexpr int WPG = NW > 4 ? NW : 4, THREADS = 64 * WPG;  // waves, threads per workgroup
+  static constexpr int TILES = WPG / NW, ROWS = 16 * TILES;
   static constexpr int KC = 16 * NS;
   static constexpr int ESZ = sizeof(T);
   static constexpr int PAD = 16 / ESZ;
   static constexpr int KV_ROW = D + PAD;
-  static constexpr int DW_BYTES = 4 * (D * C + D) * 4;                  // per-wave dW/db partials
+  static constexpr int DW_BYTES = 4 * (D * C + D) * 4;                  // dW/db partials of four waves
   static constexpr int E_ROW = C + PAD;
   static constexpr int E_TILE = 16 * KC * E_ROW * ESZ;
   static constexpr int U_ROW = KC + 4;   // fp32 per staged u.E / w~.E
@@ -91,7 +93,10 @@ struct BwdRowsCfg {
   static constexpr int KV_BYTES = KVS ? KV_STAGED : 0;                 // K and V
   static constexpr int R0_BYTES = KV_BYTES > DW_BYTES ? KV_BYTES : DW_BYTES;
   static constexpr int LDS_BYTES = R0_BYTES + TILES * TILE_BYTES;
-  static constexpr bool FITS = LDS_BYTES <= 160 * 1024 && HP % NW == 0;
+  // A row-owner wave's RW rows x KC keys: whole embeddings per lane, or
+  // whole groups of four frequencies per lane where lanes share a pair.
+  using EL = EmbedLanes<RW * KC>;
+  static constexpr bool FITS = LDS_BYTES <= 160 * 1024 && HP % NW == 0 && EL::OK && (C / 2 / EL::SPLIT) % 4 == 0;
   static_assert(SLOT % 16 == 0, "slot alignment");
 };
 
@@ -100,8 +105,9 @@ struct BwdRowsCfg {
 // and G live only in the second pass: fewer registers at the large
 // layouts).
 template <typename T, int HP, int D, int C, int NW, int NS, int PASSES>
-__global__ __launch_bounds__(256, 1) void bwd_rows_kernel(BwdParams prm) {
+__global__ __launch_bounds__(64 * (NW > 4 ? NW : 4), 1) void bwd_rows_kernel(BwdParams prm) {
   using Cfg = BwdRowsCfg<T, HP, D, C, NW, NS>;
+  constexpr int NT = Cfg::THREADS;
   constexpr bool BF = Cfg::BF;
   constexpr int HW = Cfg::HW, RW = Cfg::RW, KC = Cfg::KC;
   constexpr int SLOT_F = Cfg::SLOT / 4, SLOT_T = Cfg::SLOT / Cfg::ESZ;
@@ -124,16 +130,16 @@ __global__ __launch_bounds__(256, 1) void bwd_rows_kernel(BwdParams prm) {
   const int row0 = eb.blk * Cfg::ROWS;
   const int i0 = row0 + 16 * tile;
   if (event_refused(prm.ev, eb)) {
-    fill_rows_nan<T, D>(rx, ra, row0, min(row0 + Cfg::ROWS, len), H, tid, 256, reinterpret_cast<T*>(prm.dq),
+    fill_rows_nan<T, D>(rx, ra, row0, min(row0 + Cfg::ROWS, len), H, tid, NT, reinterpret_cast<T*>(prm.dq),
                         prm.rowsum);
     float* part = prm.dw_part + (long)blockIdx.x * (D * C + D);
-    for (int e = tid; e < D * C + D; e += 256) part[e] = __builtin_nanf("");
+    for (int e = tid; e < D * C + D; e += NT) part[e] = __builtin_nanf("");
     return;
   }
 
   T* Ks = reinterpret_cast<T*>(smem);
   T* Vs = Ks + HP * KC * Cfg::KV_ROW;
-  float* Wred = reinterpret_cast<float*>(smem);  // epilogue: [4][D*C + D]
+  float* Wred = reinterpret_cast<float*>(smem);  // epilogue: [4][D*C + D], one slot per wave mod 4
   unsigned char* tbase = smem + Cfg::R0_BYTES + tile * Cfg::TILE_BYTES;
   T* Es = reinterpret_cast<T*>(tbase);
   float* Sf = reinterpret_cast<float*>(tbase + Cfg::E_TILE);
@@ -229,12 +235,14 @@ __global__ __launch_bounds__(256, 1) void bwd_rows_kernel(BwdParams prm) {
 #pragma unroll
     for (int ct = 0; ct < C / 16; ++ct) Hacc[ri][ct] = Gacc[ri][ct] = zero4();
   }
-  constexpr int EPL = RW * KC / 64;
+  using EL = typename Cfg::EL;  // lane slot el -> key el % KC, rows el / KC + (64 / KC) k2
+  constexpr int EPL = EL::EPL;
   constexpr int ESTEP = 64 / KC;
+  const int el = EL::slot(lane), epart = EL::part(lane);
   float4 pos_i[EPL];
 #pragma unroll
   for (int k2 = 0; k2 < EPL; ++k2) {
-    const int row = i0 + ws * RW + lane / KC + ESTEP * k2;
+    const int row = i0 + ws * RW + el / KC + ESTEP * k2;
     pos_i[k2] = use_e ? ra.pos(prm.ev.pos4, row < len ? row : (len > 0 ? len - 1 : 0)) : float4{0.f, 0.f, 0.f, 0.f};
   }
 
@@ -246,7 +254,7 @@ __global__ __launch_bounds__(256, 1) void bwd_rows_kernel(BwdParams prm) {
         constexpr int VEC = 16 / Cfg::ESZ;
         constexpr int PER_ROW = D / VEC;
         const int total = H * KC * PER_ROW;
-        for (int idx = tid; idx < total; idx += 256) {
+        for (int idx = tid; idx < total; idx += NT) {
           const int dv = idx % PER_ROW;
           const int key = (idx / PER_ROW) % KC;
           const int h = idx / (PER_ROW * KC);
@@ -260,13 +268,13 @@ __global__ __launch_bounds__(256, 1) void bwd_rows_kernel(BwdParams prm) {
       }
       // ---- row-owner: embedding, u.E and w~.E staged per (row, head) ----
       if (use_e) {
-        const int key = lane % KC;
+        const int key = el % KC;
         const int j = j0 + key;
         const float4 pj = ra.pos(prm.ev.pos4, j < len ? j : len - 1);
 #pragma unroll
         for (int k2 = 0; k2 < EPL; ++k2) {
-          const int il = ws * RW + lane / KC + ESTEP * k2;
-          write_embedding<T, C>(Es + (il * KC + key) * Cfg::E_ROW, pos_i[k2], pj, prm.freq);
+          const int il = ws * RW + el / KC + ESTEP * k2;
+          write_embedding<T, C, EL::SPLIT>(Es + (il * KC + key) * Cfg::E_ROW, pos_i[k2], pj, prm.freq, epart);
         }
         wave_lds_sync();
 #pragma unroll
@@ -520,19 +528,32 @@ __global__ __launch_bounds__(256, 1) void bwd_rows_kernel(BwdParams prm) {
       }
       __syncthreads();
     }
-    float* wr = Wred + wave * (D * C + D);
+    // Eight waves: waves 4-7 store their partials first, waves 0-3 add
+    // theirs to the slot of the same index (a fixed order).
+    float* wr = Wred + (wave & 3) * (D * C + D);
+    float dbs[D / 16];
 #pragma unroll
-    for (int dt = 0; dt < D / 16; ++dt) {
+    for (int dt = 0; dt < D / 16; ++dt) dbs[dt] = group_allsum(dbl[dt]);
 #pragma unroll
-      for (int ct = 0; ct < C / 16; ++ct)
+    for (int round = Cfg::WPG / 4 - 1; round >= 0; --round) {
+      if (wave >> 2 == round) {
 #pragma unroll
-        for (int r = 0; r < 4; ++r) wr[(16 * dt + 4 * g + r) * C + 16 * ct + n] = dw[dt][ct][r];
-      const float dbs = group_allsum(dbl[dt]);
-      if (g == 0) wr[D * C + 16 * dt + n] = dbs;
+        for (int dt = 0; dt < D / 16; ++dt) {
+#pragma unroll
+          for (int ct = 0; ct < C / 16; ++ct)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+              float* dst = wr + (16 * dt + 4 * g + r) * C + 16 * ct + n;
+              *dst = round == Cfg::WPG / 4 - 1 ? dw[dt][ct][r] : *dst + dw[dt][ct][r];
+            }
+          float* dst = wr + D * C + 16 * dt + n;
+          if (g == 0) *dst = round == Cfg::WPG / 4 - 1 ? dbs[dt] : *dst + dbs[dt];
+        }
+      }
+      __syncthreads();
     }
-    __syncthreads();
     float* part = prm.dw_part + (long)blockIdx.x * (D * C + D);
-    for (int e = tid; e < D * C + D; e += 256) {
+    for (int e = tid; e < D * C + D; e += NT) {
       float acc = 0.f;
 #pragma unroll
       for (int w = 0; w < 4; ++w) acc += Wred[w * (D * C + D) + e];
@@ -540,7 +561,7 @@ __global__ __launch_bounds__(256, 1) void bwd_rows_kernel(BwdParams prm) {
     }
   }
 
-  zero_pad_rows<T>(prm.ev, eb, rx, ra, row0, Cfg::ROWS, D, tid, 256, dqg, prm.rowsum, 1);
+  zero_pad_rows<T>(prm.ev, eb, rx, ra, row0, Cfg::ROWS, D, tid, NT, dqg, prm.rowsum, 1);
 }
 
 // ---------------------------------------------------------------------------
@@ -549,7 +570,9 @@ __global__ __launch_bounds__(256, 1) void bwd_rows_kernel(BwdParams prm) {
 template <typename T, int HP, int D, int C, int NW, int NS>
 struct BwdColsCfg {
   static constexpr bool BF = is_bf16<T>::value;
-  static constexpr int HW = HP / NW, TILES = 4 / NW, KEYS = 16 * TILES;
+  static constexpr int HW = HP / NW;
+  static constexpr int WPG = NW > 4 ? NW : 4, THREADS = 64 * WPG;  // waves, threads per workgroup
+  static constexpr int TILES = WPG / NW, KEYS = 16 * TILES;
   static constexpr int KC = 16 * NS;          // streamed rows per chunk
   static constexpr int RWS = KC / NW;         // streamed rows per pair-owner wave
   static constexpr int ESZ = sizeof(T);
@@ -570,12 +593,17 @@ struct BwdColsCfg {
   static constexpr bool QOS = BF || QO_STAGED + VEC_BYTES + TILES * TILE_BYTES <= 160 * 1024;
   static constexpr int QO_BYTES = QOS ? QO_STAGED : 0;  // qt and dO
   static constexpr int LDS_BYTES = QO_BYTES + VEC_BYTES + TILES * TILE_BYTES;
-  static constexpr bool FITS = LDS_BYTES <= 160 * 1024 && HP % NW == 0 && RWS >= 4 && RWS % 4 == 0;
+  // The pair-owner's RWS rows x 16 keys: whole embeddings per lane, or
+  // whole groups of four frequencies per lane where lanes share a pair.
+  using EL = EmbedLanes<RWS * 16>;
+  static constexpr bool FITS =
+      LDS_BYTES <= 160 * 1024 && HP % NW == 0 && RWS >= 1 && EL::OK && (C / 2 / EL::SPLIT) % 4 == 0;
 };
 
 template <typename T, int HP, int D, int C, int NW, int NS>
-__global__ __launch_bounds__(256, 1) void bwd_cols_kernel(BwdParams prm) {
+__global__ __launch_bounds__(64 * (NW > 4 ? NW : 4), 1) void bwd_cols_kernel(BwdParams prm) {
   using Cfg = BwdColsCfg<T, HP, D, C, NW, NS>;
+  constexpr int NT = Cfg::THREADS;
   constexpr bool BF = Cfg::BF;
   constexpr int HW = Cfg::HW, KC = Cfg::KC, RWS = Cfg::RWS;
   constexpr int UWR = Cfg::UW_ROW;
@@ -599,8 +627,8 @@ __global__ __launch_bounds__(256, 1) void bwd_cols_kernel(BwdParams prm) {
   const int key0 = eb.blk * Cfg::KEYS;
   const int j0t = key0 + 16 * tile;
   if (event_refused(ev, eb)) {
-    fill_rows_nan<T, D>(rx, rx, key0, min(key0 + Cfg::KEYS, len), H, tid, 256, reinterpret_cast<T*>(prm.dk), nullptr);
-    fill_rows_nan<T, D>(rx, rx, key0, min(key0 + Cfg::KEYS, len), H, tid, 256, reinterpret_cast<T*>(prm.dv), nullptr);
+    fill_rows_nan<T, D>(rx, rx, key0, min(key0 + Cfg::KEYS, len), H, tid, NT, reinterpret_cast<T*>(prm.dk), nullptr);
+    fill_rows_nan<T, D>(rx, rx, key0, min(key0 + Cfg::KEYS, len), H, tid, NT, reinterpret_cast<T*>(prm.dv), nullptr);
     return;
   }
 
@@ -648,7 +676,7 @@ __global__ __launch_bounds__(256, 1) void bwd_cols_kernel(BwdParams prm) {
       constexpr int VEC = 16 / Cfg::ESZ;
       constexpr int PER_ROW = D / VEC;
       const int total = H * KC * PER_ROW;
-      for (int idx = tid; idx < total; idx += 256) {
+      for (int idx = tid; idx < total; idx += NT) {
         const int dv = idx % PER_ROW;
         const int il = (idx / PER_ROW) % KC;
         const int h = idx / (PER_ROW * KC);
@@ -664,7 +692,7 @@ __global__ __launch_bounds__(256, 1) void bwd_cols_kernel(BwdParams prm) {
         *reinterpret_cast<V16*>(Os + (h * KC + il) * Cfg::QO_ROW + dv * VEC) = ov;
       }
     }
-    for (int idx = tid; idx < H * KC; idx += 256) {
+    for (int idx = tid; idx < H * KC; idx += NT) {
       const int il = idx % KC, h = idx / KC;
       const int i = c0 + il;
       const bool ok = i < len;
@@ -674,12 +702,14 @@ __global__ __launch_bounds__(256, 1) void bwd_cols_kernel(BwdParams prm) {
     }
     // ---- pair-owner: E of (streamed rows, own keys), u.E and w~.E ----
     if (use_e) {
+      using EL = typename Cfg::EL;  // lane slot el -> key el & 15, rows (el >> 4) + 4 k4
+      const int el = EL::slot(lane), epart = EL::part(lane);
 #pragma unroll
-      for (int k4 = 0; k4 < RWS / 4; ++k4) {
-        const int il = ws * RWS + (lane >> 4) + 4 * k4;
+      for (int k4 = 0; k4 < EL::EPL; ++k4) {
+        const int il = ws * RWS + (el >> 4) + 4 * k4;
         const int i = c0 + il;
         const float4 pi = ra.pos(ev.pos4, i < len ? i : len - 1);
-        write_embedding<T, C>(Es + (il * 16 + pk) * Cfg::E_ROW, pi, pos_j, prm.freq);
+        write_embedding<T, C, EL::SPLIT>(Es + (il * 16 + pk) * Cfg::E_ROW, pi, pos_j, prm.freq, epart);
       }
       wave_lds_sync();
 #pragma unroll
@@ -797,8 +827,8 @@ __global__ __launch_bounds__(256, 1) void bwd_cols_kernel(BwdParams prm) {
       store4<T>(dvg + rx.off(h, my_key, D) + 16 * dt + 4 * g, dV[hl][dt]);
     }
   }
-  zero_pad_rows<T>(ev, eb, rx, rx, key0, Cfg::KEYS, D, tid, 256, dkg, nullptr, 1);
-  zero_pad_rows<T>(ev, eb, rx, rx, key0, Cfg::KEYS, D, tid, 256, dvg, nullptr, 1);
+  zero_pad_rows<T>(ev, eb, rx, rx, key0, Cfg::KEYS, D, tid, NT, dkg, nullptr, 1);
+  zero_pad_rows<T>(ev, eb, rx, rx, key0, Cfg::KEYS, D, tid, NT, dvg, nullptr, 1);
 }
 
 // ---------------------------------------------------------------------------
@@ -826,7 +856,9 @@ struct BwdPick {
 // the one-pass form stays small ((HP / NW) D + (16 / NW) C <= 256: Q, dO,
 // dQ and sum P k per head, u, w~, H and G per row; at B=256 L=768 H=12
 // D=32 C=16 in float32 one pass took 7.06 against 9.72 ms), two where it
-// would spill (cfg4, D = C = 64: 82.8 against 41.2 ms).
+// would spill heavily (cfg4, D = C = 64, four waves: 82.8 against 41.2 ms).
+// Eight waves halve the state: at cfg4 one pass (51 registers spilled)
+// took 22.7 ms against 31.7 for two.
 template <int HP, int D, int C, int NW>
 constexpr int rows_static_passes() {
   return (HP / NW) * D + (16 / NW) * C <= 256 ? 1 : 2;
@@ -849,7 +881,7 @@ int bwd_launch_v(const BwdParams& prm, int which, hipStream_t stream, int grid, 
       if (hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, R::LDS_BYTES) !=
           hipSuccess)
         return FST_ELAUNCH;
-      if (grid > 0) hipLaunchKernelGGL(kern, dim3(grid), dim3(256), R::LDS_BYTES, stream, prm);
+      if (grid > 0) hipLaunchKernelGGL(kern, dim3(grid), dim3(R::THREADS), R::LDS_BYTES, stream, prm);
       return hipGetLastError() == hipSuccess ? FST_OK : FST_ELAUNCH;
     }
   }
@@ -862,7 +894,7 @@ int bwd_launch_v(const BwdParams& prm, int which, hipStream_t stream, int grid, 
     if (hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, K::LDS_BYTES) !=
         hipSuccess)
       return FST_ELAUNCH;
-    if (grid > 0) hipLaunchKernelGGL(kern, dim3(grid), dim3(256), K::LDS_BYTES, stream, prm);
+    if (grid > 0) hipLaunchKernelGGL(kern, dim3(grid), dim3(K::THREADS), K::LDS_BYTES, stream, prm);
     return hipGetLastError() == hipSuccess ? FST_OK : FST_ELAUNCH;
   }
 }
@@ -873,8 +905,8 @@ template <typename T, int HP, int D, int C>
 constexpr int bwd_split_plans() {
   using PR = BwdPick<BwdRowsCfg, T, HP, D, C>;
   using PC = BwdPick<BwdColsCfg, T, HP, D, C>;
-  return (split_plans<PR::template F>(FST_PLAN_BWD_T16, FST_PLAN_BWD_KC16) &
-          split_plans<PC::template F>(FST_PLAN_BWD_T16, FST_PLAN_BWD_KC16)) |
+  return (split_plans<PR::template F>(FST_PLAN_BWD_T16, FST_PLAN_BWD_KC16, FST_PLAN_BWD_W8) &
+          split_plans<PC::template F>(FST_PLAN_BWD_T16, FST_PLAN_BWD_KC16, FST_PLAN_BWD_W8)) |
          FST_PLAN_BWD_PASS1 | FST_PLAN_BWD_PASS2;
 }
 
@@ -896,7 +928,7 @@ int bwd_launch_t(const BwdParams& prm, int which, hipStream_t stream, int grid, 
   if constexpr (!PR::OK || !PC::OK || REFUSED) {
     return FST_EUNSUPPORTED;
   } else {
-    const int nw = plan_nw(prm.flags, bit_index(FST_PLAN_BWD_T16));
+    const int nw = plan_nw(prm.flags, bit_index(FST_PLAN_BWD_T16), bit_index(FST_PLAN_BWD_W8));
     const int ns = plan_ns(prm.flags, bit_index(FST_PLAN_BWD_KC16));
     const int split = which == 0 ? pick_split<PR::template F>(nw, ns, 1) : pick_split<PC::template F>(nw, ns, 1);
     switch (split) {
@@ -906,6 +938,8 @@ int bwd_launch_t(const BwdParams& prm, int which, hipStream_t stream, int grid, 
       case 22: return bwd_launch_v<T, HP, D, C, 2, 2>(prm, which, stream, grid, query, rows);
       case 41: return bwd_launch_v<T, HP, D, C, 4, 1>(prm, which, stream, grid, query, rows);
       case 42: return bwd_launch_v<T, HP, D, C, 4, 2>(prm, which, stream, grid, query, rows);
+      case 81: return bwd_launch_v<T, HP, D, C, 8, 1>(prm, which, stream, grid, query, rows);
+      case 82: return bwd_launch_v<T, HP, D, C, 8, 2>(prm, which, stream, grid, query, rows);
       default: return FST_EUNSUPPORTED;
     }
   }

@@ -311,8 +311,8 @@ static const int kPlanGroups[] = {
     FST_PLAN_COLS_OCC2 | FST_PLAN_COLS_OCC3,
     FST_PLAN_ROWS_KV_REG | FST_PLAN_ROWS_KV_LDS,
     FST_PLAN_FWD_KC16 | FST_PLAN_FWD_KC32,
-    FST_PLAN_FWD_T16 | FST_PLAN_FWD_T32 | FST_PLAN_FWD_T64,
-    FST_PLAN_BWD_T16 | FST_PLAN_BWD_T32 | FST_PLAN_BWD_T64,
+    FST_PLAN_FWD_T16 | FST_PLAN_FWD_T32 | FST_PLAN_FWD_T64 | FST_PLAN_FWD_W8,
+    FST_PLAN_BWD_T16 | FST_PLAN_BWD_T32 | FST_PLAN_BWD_T64 | FST_PLAN_BWD_W8,
     FST_PLAN_BWD_KC16 | FST_PLAN_BWD_KC32,
     FST_PLAN_BWD_PASS1 | FST_PLAN_BWD_PASS2,
 };

@@ -9,9 +9,9 @@
 // sum_j p_ij = 1 folds b out of the value sum, and E (C sin/cos channels of
 // the pair's interval angle) is recomputed per tile and never stored.
 //
-// Work decomposition. A workgroup of four waves owns ROWS query rows of one
-// event, split in 16-row tiles; each tile is served by NW waves (NW in
-// {1, 2, 4}) that split the work two ways:
+// Work decomposition. A workgroup of WPG waves (four, or eight where NW is
+// eight) owns ROWS query rows of one event, split in 16-row tiles; each tile
+// is served by NW waves (NW in {1, 2, 4, 8}) that split the work two ways:
 //  * head-owner role: wave ws of the tile owns heads [ws*HW, (ws+1)*HW) for
 //    all 16 rows -- the per-head products S^T_h = K_h Qt_h^T and
 //    O^T_h += V_h^T P^T_h on 16x16 MFMA tiles with rows on the lanes, and
@@ -37,7 +37,9 @@ struct FwdCfg {
   static constexpr bool BF = is_bf16<T>::value;
   static constexpr int HW = HP / NW;     // heads per head-owner wave
   static constexpr int RW = 16 / NW;     // rows per row-owner wave
-  static constexpr int TILES = 4 / NW;   // 16-row tiles per workgroup
+  static constexpr int WPG = NW > 4 ? NW : 4;  // waves per workgroup
+  static constexpr int THREADS = 64 * WPG;
+  static constexpr int TILES = WPG / NW;  // 16-row tiles per workgroup
   static constexpr int ROWS = 16 * TILES;
   static constexpr int KC = 16 * NS;     // keys per chunk
   static constexpr int ESZ = sizeof(T);
@@ -66,13 +68,18 @@ struct FwdCfg {
   static constexpr bool KS = false;
   static constexpr int V_BYTES = (VS ? KV_ONE : 0) + (KS ? KV_ONE : 0);  // V, then K
   static constexpr int LDS_BYTES = V_BYTES + TILES * TILE_BYTES;
-  static constexpr bool FITS = LDS_BYTES <= 160 * 1024 && HP % NW == 0 && !(BF && NS != 1 && NS != 2);
+  // A row-owner wave's RW rows x KC keys: whole embeddings per lane, or
+  // whole groups of four frequencies per lane where lanes share a pair.
+  using EL = EmbedLanes<RW * KC>;
+  static constexpr bool FITS = LDS_BYTES <= 160 * 1024 && HP % NW == 0 && EL::OK && (C / 2 / EL::SPLIT) % 4 == 0 &&
+                               !(BF && NS != 1 && NS != 2);
   static_assert(SLOT % 16 == 0, "slots must stay 16-byte aligned");
 };
 
 template <typename T, int HP, int D, int C, int NW, int NS>
-__global__ __launch_bounds__(256, 1) void fwd_kernel(FwdParams prm) {
+__global__ __launch_bounds__(64 * (NW > 4 ? NW : 4), 1) void fwd_kernel(FwdParams prm) {
   using Cfg = FwdCfg<T, HP, D, C, NW, NS>;
+  constexpr int NT = Cfg::THREADS;
   constexpr int HW = Cfg::HW, RW = Cfg::RW, KC = Cfg::KC;
   constexpr int SLOT_F = Cfg::SLOT / 4;          // slot stride in floats
   constexpr int SLOT_T = Cfg::SLOT / Cfg::ESZ;   // slot stride in T
@@ -96,7 +103,7 @@ __global__ __launch_bounds__(256, 1) void fwd_kernel(FwdParams prm) {
   const int row0 = eb.blk * Cfg::ROWS;
   const int i0 = row0 + 16 * tile;  // first row of this wave's tile
   if (event_refused(prm.ev, eb)) {
-    fill_rows_nan<T, D>(ra, ra, row0, min(row0 + Cfg::ROWS, len), H, tid, 256, reinterpret_cast<T*>(prm.out),
+    fill_rows_nan<T, D>(ra, ra, row0, min(row0 + Cfg::ROWS, len), H, tid, NT, reinterpret_cast<T*>(prm.out),
                         prm.lse);
     return;
   }
@@ -149,14 +156,16 @@ __global__ __launch_bounds__(256, 1) void fwd_kernel(FwdParams prm) {
 #pragma unroll
     for (int ct = 0; ct < C / 16; ++ct) AE[ri][ct] = zero4();
   }
-  // Pair-embedding assignment: lane -> key (lane % KC), rows spaced by
-  // 64 / KC starting at lane / KC.
-  constexpr int EPL = RW * KC / 64;  // embeddings per lane per chunk
+  // Pair-embedding assignment (EmbedLanes): lane slot el -> key (el % KC),
+  // rows spaced by 64 / KC starting at el / KC.
+  using EL = typename Cfg::EL;
+  constexpr int EPL = EL::EPL;  // embeddings per lane per chunk
   constexpr int ESTEP = 64 / KC;
+  const int el = EL::slot(lane), epart = EL::part(lane);
   float4 pos_i[EPL];
 #pragma unroll
   for (int k2 = 0; k2 < EPL; ++k2) {
-    const int row = i0 + ws * RW + lane / KC + ESTEP * k2;
+    const int row = i0 + ws * RW + el / KC + ESTEP * k2;
     pos_i[k2] = use_e ? ra.pos(prm.ev.pos4, row < len ? row : (len > 0 ? len - 1 : 0)) : float4{0.f, 0.f, 0.f, 0.f};
   }
 
@@ -167,7 +176,7 @@ __global__ __launch_bounds__(256, 1) void fwd_kernel(FwdParams prm) {
       constexpr int VEC = 16 / Cfg::ESZ;
       constexpr int PER_ROW = D / VEC;
       const int total = H * KC * PER_ROW;
-      for (int idx = tid; idx < total; idx += 256) {
+      for (int idx = tid; idx < total; idx += NT) {
         const int dv = idx % PER_ROW;
         const int key = (idx / PER_ROW) % KC;
         const int h = idx / (PER_ROW * KC);
@@ -184,13 +193,13 @@ __global__ __launch_bounds__(256, 1) void fwd_kernel(FwdParams prm) {
 
     // ---- row-owner: embedding of its rows x KC keys, then u.E ----
     if (use_e) {
-      const int key = lane % KC;
+      const int key = el % KC;
       const int j = j0 + key;
       const float4 pj = ra.pos(prm.ev.pos4, j < len ? j : len - 1);
 #pragma unroll
       for (int k2 = 0; k2 < EPL; ++k2) {
-        const int il = ws * RW + lane / KC + ESTEP * k2;
-        write_embedding<T, C>(Es + (il * KC + key) * Cfg::E_ROW, pos_i[k2], pj, prm.freq);
+        const int il = ws * RW + el / KC + ESTEP * k2;
+        write_embedding<T, C, EL::SPLIT>(Es + (il * KC + key) * Cfg::E_ROW, pos_i[k2], pj, prm.freq, epart);
       }
       wave_lds_sync();
       if (attn) {
@@ -350,7 +359,7 @@ __global__ __launch_bounds__(256, 1) void fwd_kernel(FwdParams prm) {
   }
 
   // Padding rows of this block (and past the event for its last block): 0.
-  zero_pad_rows<T>(prm.ev, eb, ra, ra, row0, Cfg::ROWS, D, tid, 256, outg, prm.lse, 1);
+  zero_pad_rows<T>(prm.ev, eb, ra, ra, row0, Cfg::ROWS, D, tid, NT, outg, prm.lse, 1);
 }
 
 // ---------------------------------------------------------------------------
@@ -370,7 +379,7 @@ struct FwdPick {
   static constexpr int NW = STATIC ? STATIC / 10 : 4, NS = STATIC ? STATIC % 10 : 1;
   using Cfg = F<NW, NS>;
   static constexpr bool OK = STATIC != 0;
-  static constexpr int PLANS = OK ? split_plans<F>(FST_PLAN_FWD_T16, FST_PLAN_FWD_KC16) : 0;
+  static constexpr int PLANS = OK ? split_plans<F>(FST_PLAN_FWD_T16, FST_PLAN_FWD_KC16, FST_PLAN_FWD_W8) : 0;
 };
 
 template <typename T, int HP, int D, int C, int NW, int NS>
@@ -385,7 +394,7 @@ int fwd_launch_v(const FwdParams& prm, hipStream_t stream, int grid, bool query,
     if (hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, Cfg::LDS_BYTES) !=
         hipSuccess)
       return FST_ELAUNCH;
-    if (grid > 0) hipLaunchKernelGGL(kern, dim3(grid), dim3(256), Cfg::LDS_BYTES, stream, prm);
+    if (grid > 0) hipLaunchKernelGGL(kern, dim3(grid), dim3(Cfg::THREADS), Cfg::LDS_BYTES, stream, prm);
     return hipGetLastError() == hipSuccess ? FST_OK : FST_ELAUNCH;
   }
 }
@@ -399,7 +408,7 @@ int fwd_launch_t(const FwdParams& prm, hipStream_t stream, int grid, bool query,
   if constexpr (!P::OK) {
     return FST_EUNSUPPORTED;
   } else {
-    const int split = pick_split<P::template F>(plan_nw(prm.flags, bit_index(FST_PLAN_FWD_T16)),
+    const int split = pick_split<P::template F>(plan_nw(prm.flags, bit_index(FST_PLAN_FWD_T16), bit_index(FST_PLAN_FWD_W8)),
                                                 plan_ns(prm.flags, bit_index(FST_PLAN_FWD_KC16)));
     switch (split) {
       case 11: return fwd_launch_v<T, HP, D, C, 1, 1>(prm, stream, grid, query, rows);
@@ -408,6 +417,8 @@ int fwd_launch_t(const FwdParams& prm, hipStream_t stream, int grid, bool query,
       case 22: return fwd_launch_v<T, HP, D, C, 2, 2>(prm, stream, grid, query, rows);
       case 41: return fwd_launch_v<T, HP, D, C, 4, 1>(prm, stream, grid, query, rows);
       case 42: return fwd_launch_v<T, HP, D, C, 4, 2>(prm, stream, grid, query, rows);
+      case 81: return fwd_launch_v<T, HP, D, C, 8, 1>(prm, stream, grid, query, rows);
+      case 82: return fwd_launch_v<T, HP, D, C, 8, 2>(prm, stream, grid, query, rows);
       default: return FST_EUNSUPPORTED;
     }
   }

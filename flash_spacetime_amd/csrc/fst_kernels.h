@@ -306,46 +306,64 @@ __device__ __forceinline__ void project_row(const T* x_row, long hstride, bool v
 // Pair embedding of one (row i, key j) into an LDS row: channel f is
 // sin(x_ij f_f), channel C/2 + f is cos(x_ij f_f) (reference.py:75-84 order).
 // bf16 kernels evaluate the angle in fp32 (the result is rounded to bf16);
-// fp32 kernels evaluate angle and argument reduction in binary64.
-template <typename T, int C>
-__device__ __forceinline__ void write_embedding(T* erow, float4 pi, float4 pj, const FreqTable& ft) {
-  constexpr int F = C / 2;
-  float sv[F], cv[F];
+// fp32 kernels evaluate angle and argument reduction in binary64. With
+// SPLIT > 1, SPLIT lanes share the pair: this one writes the frequencies
+// [part F / SPLIT, (part + 1) F / SPLIT) and their cosines.
+template <typename T, int C, int SPLIT = 1>
+__device__ __forceinline__ void write_embedding(T* erow, float4 pi, float4 pj, const FreqTable& ft, int part = 0) {
+  constexpr int F = C / 2, FP = F / SPLIT;
+  static_assert(FP % 4 == 0, "each lane writes whole groups of four frequencies");
+  const int f0 = SPLIT == 1 ? 0 : part * FP;
+  float sv[FP], cv[FP];
   if constexpr (is_bf16<T>::value) {
     const float x = pair_angle(pi, pj);
 #pragma unroll
-    for (int f = 0; f < F; ++f) sincos_rev<false>(x, ft.ghi[f], ft.glo[f], (ft.reduce_mask >> f) & 1u, sv[f], cv[f]);
+    for (int f = 0; f < FP; ++f)
+      sincos_rev<false>(x, ft.ghi[f0 + f], ft.glo[f0 + f], (ft.reduce_mask >> (f0 + f)) & 1u, sv[f], cv[f]);
   } else {
     const double x = pair_angle_f64(pi, pj);
 #pragma unroll
-    for (int f = 0; f < F; ++f) {
-      const double rev = x * ((double)ft.ghi[f] + (double)ft.glo[f]);
+    for (int f = 0; f < FP; ++f) {
+      const double rev = x * ((double)ft.ghi[f0 + f] + (double)ft.glo[f0 + f]);
       const float r = (float)(rev - __builtin_floor(rev));
       sv[f] = __builtin_amdgcn_sinf(r);
       cv[f] = __builtin_amdgcn_cosf(r);
     }
   }
   if constexpr (is_bf16<T>::value) {
-    static_assert(F % 4 == 0, "C must be a multiple of 8");
 #pragma unroll
-    for (int f = 0; f < F; f += 4) {
+    for (int f = 0; f < FP; f += 4) {
       bf16x4 a, b;
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         a[e] = (bf16)sv[f + e];
         b[e] = (bf16)cv[f + e];
       }
-      *reinterpret_cast<bf16x4*>(erow + f) = a;
-      *reinterpret_cast<bf16x4*>(erow + F + f) = b;
+      *reinterpret_cast<bf16x4*>(erow + f0 + f) = a;
+      *reinterpret_cast<bf16x4*>(erow + F + f0 + f) = b;
     }
   } else {
 #pragma unroll
-    for (int f = 0; f < F; f += 4) {
-      *reinterpret_cast<f32x4*>(erow + f) = f32x4{sv[f], sv[f + 1], sv[f + 2], sv[f + 3]};
-      *reinterpret_cast<f32x4*>(erow + F + f) = f32x4{cv[f], cv[f + 1], cv[f + 2], cv[f + 3]};
+    for (int f = 0; f < FP; f += 4) {
+      *reinterpret_cast<f32x4*>(erow + f0 + f) = f32x4{sv[f], sv[f + 1], sv[f + 2], sv[f + 3]};
+      *reinterpret_cast<f32x4*>(erow + F + f0 + f) = f32x4{cv[f], cv[f + 1], cv[f + 2], cv[f + 3]};
     }
   }
 }
+
+// Lane assignment of a wave's embeddings: NP (row, key) pairs of a chunk
+// per wave. NP >= 64: EPL pairs per lane, lane l taking key l % KC of rows
+// l / KC + (64 / KC) k; NP < 64 (a divisor of 64): SPLIT = 64 / NP lanes
+// per pair, each writing 1 / SPLIT of the frequencies.
+template <int NP>
+struct EmbedLanes {
+  static constexpr bool OK = NP % 64 == 0 || 64 % NP == 0;
+  static constexpr int EPL = NP >= 64 ? NP / 64 : 1;
+  static constexpr int SPLIT = NP >= 64 ? 1 : 64 / NP;
+  // pair slot and frequency part of a lane
+  static __device__ __forceinline__ int slot(int lane) { return SPLIT == 1 ? lane : lane % NP; }
+  static __device__ __forceinline__ int part(int lane) { return SPLIT == 1 ? 0 : lane / NP; }
+};
 
 // Zero the outputs of padding rows [max(row0, len), end) of a padded event,
 // where end is the block's last row, or L for the event's last block
@@ -414,21 +432,22 @@ FST_DECL_BWD(f32_64)
 // ---------------------------------------------------------------------------
 // Plan requests of the first-generation kernels (fst_forward.hip,
 // fst_backward.hip), which come in (NW, NS) splits: NW waves per 16-row tile
-// (16 * 4 / NW rows or keys per workgroup) and 16 * NS keys (or rows) per
-// chunk.
+// (16 * 4 / NW rows or keys per four-wave workgroup; NW = 8 is one 16-row
+// tile in an eight-wave workgroup) and 16 * NS keys (or rows) per chunk.
 // ---------------------------------------------------------------------------
 // (NW, NS) of a plan request for a family of configurations F<NW, NS>
 // (nw, ns = 0: not requested), as 10 NW + NS, or 0 when nothing fits.
-// Preference: the most waves per 16-row tile first (16 rows per workgroup:
-// on gfx950 the smaller workgroups run about twice as fast as 64-row ones,
-// e.g. 2.8 against 5.3 ms for the float32 forward at B=256, L=768, H=12,
-// D=32, C=16), then ns_first keys (or rows) per chunk.
+// Preference: the most waves per 16-row tile first (on gfx950 the 16-row
+// workgroups run about twice as fast as 64-row ones, e.g. 2.8 against 5.3
+// ms for the float32 forward at B=256, L=768, H=12, D=32, C=16: more waves
+// share the tile's work and each holds less), then ns_first keys (or rows)
+// per chunk.
 template <template <int, int> class F>
 constexpr int pick_split(int nw, int ns, int ns_first = 2) {
-  const bool fits[3][2] = {{F<4, 1>::FITS, F<4, 2>::FITS}, {F<2, 1>::FITS, F<2, 2>::FITS},
-                           {F<1, 1>::FITS, F<1, 2>::FITS}};
-  const int nws[3] = {4, 2, 1};
-  for (int w = 0; w < 3; ++w) {
+  const bool fits[4][2] = {{F<8, 1>::FITS, F<8, 2>::FITS}, {F<4, 1>::FITS, F<4, 2>::FITS},
+                           {F<2, 1>::FITS, F<2, 2>::FITS}, {F<1, 1>::FITS, F<1, 2>::FITS}};
+  const int nws[4] = {8, 4, 2, 1};
+  for (int w = 0; w < 4; ++w) {
     if (nw && nws[w] != nw) continue;
     for (int k = 0; k < 2; ++k) {
       const int s = k == 0 ? ns_first : 3 - ns_first;
@@ -441,8 +460,11 @@ constexpr int pick_split(int nw, int ns, int ns_first = 2) {
 
 // The requested (nw, ns) of the plan bits in flags, for the groups starting
 // at bit t (three tile-height bits) and bit k (two key-chunk bits).
-__host__ __device__ inline int plan_nw(int flags, int t) {
-  return (flags >> t) & 1 ? 4 : ((flags >> (t + 1)) & 1 ? 2 : ((flags >> (t + 2)) & 1 ? 1 : 0));
+// t: bit index of the T16 / T32 / T64 triple; w8: bit index of the
+// eight-wave 16-row tile.
+__host__ __device__ inline int plan_nw(int flags, int t, int w8) {
+  return (flags >> w8) & 1 ? 8
+                           : ((flags >> t) & 1 ? 4 : ((flags >> (t + 1)) & 1 ? 2 : ((flags >> (t + 2)) & 1 ? 1 : 0)));
 }
 __host__ __device__ inline int plan_ns(int flags, int k) { return (flags >> k) & 1 ? 1 : ((flags >> (k + 1)) & 1 ? 2 : 0); }
 constexpr int bit_index(int b) { return b <= 1 ? 0 : 1 + bit_index(b >> 1); }
@@ -450,11 +472,12 @@ constexpr int bit_index(int b) { return b <= 1 ? 0 : 1 + bit_index(b >> 1); }
 // The plan bits of a (NW, NS) family: a tile-height bit for each NW and a
 // key-chunk bit for each NS that fits with some value of the other.
 template <template <int, int> class F>
-constexpr int split_plans(int t16, int k16) {
+constexpr int split_plans(int t16, int k16, int w8) {
   int bits = 0;
   const int nws[3] = {4, 2, 1};
   for (int w = 0; w < 3; ++w)
     if (pick_split<F>(nws[w], 0)) bits |= t16 << w;
+  if (pick_split<F>(8, 0)) bits |= w8;
   for (int s = 1; s <= 2; ++s)
     if (pick_split<F>(0, s)) bits |= k16 << (s - 1);
   return bits;

@@ -52,12 +52,12 @@ from . import _lib
 # Plan-bit groups of each kernel (at most one bit of a group per plan).
 _FWD_GROUPS = ((_lib.FST_PLAN_FWD_OCC2, _lib.FST_PLAN_FWD_OCC3),
                (_lib.FST_PLAN_FWD_KC16, _lib.FST_PLAN_FWD_KC32),
-               (_lib.FST_PLAN_FWD_T16, _lib.FST_PLAN_FWD_T32, _lib.FST_PLAN_FWD_T64))
+               (_lib.FST_PLAN_FWD_T16, _lib.FST_PLAN_FWD_T32, _lib.FST_PLAN_FWD_T64, _lib.FST_PLAN_FWD_W8))
 _ROWS_GROUPS = ((_lib.FST_PLAN_ROWS_W4, _lib.FST_PLAN_ROWS_W8, _lib.FST_PLAN_ROWS_W8X2),
                 (_lib.FST_PLAN_ROWS_KV_REG, _lib.FST_PLAN_ROWS_KV_LDS))
 _COLS_GROUPS = ((_lib.FST_PLAN_COLS_OCC2, _lib.FST_PLAN_COLS_OCC3),)
 # float32 backward groups: they set the rows and the cols kernel together.
-_BWD_GROUPS = ((_lib.FST_PLAN_BWD_T16, _lib.FST_PLAN_BWD_T32, _lib.FST_PLAN_BWD_T64),
+_BWD_GROUPS = ((_lib.FST_PLAN_BWD_T16, _lib.FST_PLAN_BWD_T32, _lib.FST_PLAN_BWD_T64, _lib.FST_PLAN_BWD_W8),
                (_lib.FST_PLAN_BWD_KC16, _lib.FST_PLAN_BWD_KC32),
                (_lib.FST_PLAN_BWD_PASS1, _lib.FST_PLAN_BWD_PASS2))
 
@@ -339,10 +339,12 @@ def plan_from_tiles(dtype: int, heads: int, dim: int, channels: int, kind: str,
     height, 16 rows. block_n (keys per inner step) selects the key chunk of
     the forward (16 or 32) and of the float32 backward. num_warps selects the
     bf16 rows kernel's waves per workgroup (4, or 8 in two workgroups per CU
-    where offered, else in one). Each takes the offered value nearest the
-    request (the smaller on a tie), and a combination the shape does not
-    compile drops num_warps, then block_n, then block_m, in that order.
-    num_stages has no counterpart: the kernels' loads run one chunk ahead."""
+    where offered, else in one) and, for float32, the waves of a 16-row
+    tile (4, or 8 where offered; the 32- and 64-row tiles have four waves).
+    Each takes the offered value nearest the request (the smaller on a tie),
+    and a combination the shape does not compile drops num_warps, then
+    block_n, then block_m, in that order. num_stages has no counterpart: the
+    kernels' loads run one chunk ahead."""
     if block_m is None and block_n is None and num_warps is None:
         return None
     mask = plans(dtype, heads, dim, channels)
@@ -358,21 +360,29 @@ def plan_from_tiles(dtype: int, heads: int, dim: int, channels: int, kind: str,
         ((16, _lib.FST_PLAN_BWD_T16), (32, _lib.FST_PLAN_BWD_T32), (64, _lib.FST_PLAN_BWD_T64))
     n_opts = ((16, _lib.FST_PLAN_FWD_KC16), (32, _lib.FST_PLAN_FWD_KC32)) if fwd else \
         ((16, _lib.FST_PLAN_BWD_KC16), (32, _lib.FST_PLAN_BWD_KC32))
-    w8 = _lib.FST_PLAN_ROWS_W8X2 if mask & _lib.FST_PLAN_ROWS_W8X2 else _lib.FST_PLAN_ROWS_W8
-    w_opts = () if fwd else ((4, _lib.FST_PLAN_ROWS_W4), (8, w8))
-    parts = [nearest(block_m, m_opts), nearest(block_n, n_opts), nearest(num_warps, w_opts)]
-    while parts:
-        plan = sum(parts)
+    m, n = nearest(block_m, m_opts), nearest(block_n, n_opts)
+    if dtype == _lib.FST_F32:
+        # num_warps refines the tile-height group: eight waves replace the
+        # 16-row bit, four waves pick it where no height was asked for.
+        t16, w8 = (_lib.FST_PLAN_FWD_T16, _lib.FST_PLAN_FWD_W8) if fwd else \
+            (_lib.FST_PLAN_BWD_T16, _lib.FST_PLAN_BWD_W8)
+        w = nearest(num_warps, ((4, t16), (8, w8)))
+        mw = w8 if w == w8 and m in (0, t16) else (t16 if w == t16 and m == 0 else m)
+        candidates = [mw + n, m + n, m]
+    else:
+        w8 = _lib.FST_PLAN_ROWS_W8X2 if mask & _lib.FST_PLAN_ROWS_W8X2 else _lib.FST_PLAN_ROWS_W8
+        w_opts = () if fwd else ((4, _lib.FST_PLAN_ROWS_W4), (8, w8))
+        candidates = [m + n + nearest(num_warps, w_opts), m + n, m]
+    for plan in candidates:
         if plan == 0 or plan_supported(dtype, heads, dim, channels, plan):
             return plan
-        parts.pop()
     return 0
 
 
 _NAMES = ((_lib.FST_PLAN_FWD_OCC2, "fwd:occ2"), (_lib.FST_PLAN_FWD_OCC3, "fwd:occ3"),
           (_lib.FST_PLAN_FWD_KC16, "fwd:kc16"), (_lib.FST_PLAN_FWD_KC32, "fwd:kc32"),
           (_lib.FST_PLAN_FWD_T16, "fwd:t16"), (_lib.FST_PLAN_FWD_T32, "fwd:t32"),
-          (_lib.FST_PLAN_FWD_T64, "fwd:t64"),
+          (_lib.FST_PLAN_FWD_T64, "fwd:t64"), (_lib.FST_PLAN_FWD_W8, "fwd:w8"),
           (_lib.FST_PLAN_ROWS_W4, "rows:w4"), (_lib.FST_PLAN_ROWS_W8, "rows:w8"),
           (_lib.FST_PLAN_ROWS_W8X2, "rows:w8x2"), (_lib.FST_PLAN_ROWS_KV_REG, "rows:kvreg"),
           (_lib.FST_PLAN_ROWS_KV_LDS, "rows:kvlds"),
@@ -380,7 +390,7 @@ _NAMES = ((_lib.FST_PLAN_FWD_OCC2, "fwd:occ2"), (_lib.FST_PLAN_FWD_OCC3, "fwd:oc
           (_lib.FST_PLAN_BWD_T16, "bwd:t16"), (_lib.FST_PLAN_BWD_T32, "bwd:t32"),
           (_lib.FST_PLAN_BWD_T64, "bwd:t64"), (_lib.FST_PLAN_BWD_KC16, "bwd:kc16"),
           (_lib.FST_PLAN_BWD_KC32, "bwd:kc32"), (_lib.FST_PLAN_BWD_PASS1, "bwd:pass1"),
-          (_lib.FST_PLAN_BWD_PASS2, "bwd:pass2"))
+          (_lib.FST_PLAN_BWD_PASS2, "bwd:pass2"), (_lib.FST_PLAN_BWD_W8, "bwd:w8"))
 
 
 def plan_names(plan: int) -> Optional[str]:

@@ -103,11 +103,13 @@ enum fst_flags {
   /* forward: keys per chunk (bf16 and float32) */
   FST_PLAN_FWD_KC16 = 1 << 17,
   FST_PLAN_FWD_KC32 = 1 << 18,
-  /* float32 forward: query rows per workgroup (tile height) */
+  /* float32 forward: query rows per workgroup (tile height); one group with
+   * FST_PLAN_FWD_W8 */
   FST_PLAN_FWD_T16 = 1 << 19,
   FST_PLAN_FWD_T32 = 1 << 20,
   FST_PLAN_FWD_T64 = 1 << 21,
-  /* float32 backward: rows (rows kernel) and keys (cols kernel) per workgroup */
+  /* float32 backward: rows (rows kernel) and keys (cols kernel) per
+   * workgroup; one group with FST_PLAN_BWD_W8 */
   FST_PLAN_BWD_T16 = 1 << 22,
   FST_PLAN_BWD_T32 = 1 << 23,
   FST_PLAN_BWD_T64 = 1 << 24,
@@ -118,7 +120,11 @@ enum fst_flags {
    * online and the accumulators corrected as it moves; or two, D first) */
   FST_PLAN_BWD_PASS1 = 1 << 27,
   FST_PLAN_BWD_PASS2 = 1 << 28,
-  FST_PLAN_MASK = 0x1fffff00
+  /* float32: a 16-row tile served by eight waves (the T16 tile of four
+   * waves, with each wave's heads and rows halved) */
+  FST_PLAN_FWD_W8 = 1 << 29,
+  FST_PLAN_BWD_W8 = 1 << 30,
+  FST_PLAN_MASK = 0x7fffff00
 };
 
 /* Phases of one operator call, for callers that time or schedule them

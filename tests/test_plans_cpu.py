@@ -14,17 +14,17 @@ needs_lib = pytest.mark.skipif(not _lib.LIB_PATH.exists(),
 
 BF16_ALL = 0x7FF00  # every bf16 group's bits (forward, rows, cols)
 F32_FWD = _lib.FST_PLAN_FWD_KC16 | _lib.FST_PLAN_FWD_KC32 | _lib.FST_PLAN_FWD_T16 | _lib.FST_PLAN_FWD_T32 \
-    | _lib.FST_PLAN_FWD_T64
+    | _lib.FST_PLAN_FWD_T64 | _lib.FST_PLAN_FWD_W8
 F32_BWD = _lib.FST_PLAN_BWD_T16 | _lib.FST_PLAN_BWD_T32 | _lib.FST_PLAN_BWD_T64 | _lib.FST_PLAN_BWD_KC16 \
-    | _lib.FST_PLAN_BWD_KC32 | _lib.FST_PLAN_BWD_PASS1 | _lib.FST_PLAN_BWD_PASS2
+    | _lib.FST_PLAN_BWD_KC32 | _lib.FST_PLAN_BWD_PASS1 | _lib.FST_PLAN_BWD_PASS2 | _lib.FST_PLAN_BWD_W8
 GROUPS = [
     _lib.FST_PLAN_FWD_OCC2 | _lib.FST_PLAN_FWD_OCC3,
     _lib.FST_PLAN_ROWS_W4 | _lib.FST_PLAN_ROWS_W8 | _lib.FST_PLAN_ROWS_W8X2,
     _lib.FST_PLAN_COLS_OCC2 | _lib.FST_PLAN_COLS_OCC3,
     _lib.FST_PLAN_ROWS_KV_REG | _lib.FST_PLAN_ROWS_KV_LDS,
     _lib.FST_PLAN_FWD_KC16 | _lib.FST_PLAN_FWD_KC32,
-    _lib.FST_PLAN_FWD_T16 | _lib.FST_PLAN_FWD_T32 | _lib.FST_PLAN_FWD_T64,
-    _lib.FST_PLAN_BWD_T16 | _lib.FST_PLAN_BWD_T32 | _lib.FST_PLAN_BWD_T64,
+    _lib.FST_PLAN_FWD_T16 | _lib.FST_PLAN_FWD_T32 | _lib.FST_PLAN_FWD_T64 | _lib.FST_PLAN_FWD_W8,
+    _lib.FST_PLAN_BWD_T16 | _lib.FST_PLAN_BWD_T32 | _lib.FST_PLAN_BWD_T64 | _lib.FST_PLAN_BWD_W8,
     _lib.FST_PLAN_BWD_KC16 | _lib.FST_PLAN_BWD_KC32,
     _lib.FST_PLAN_BWD_PASS1 | _lib.FST_PLAN_BWD_PASS2,
 ]
@@ -48,11 +48,14 @@ def test_plans_of_shapes():
     assert lib.fst_plans(_lib.FST_BF16, 8, 64, 64) == (
         _lib.FST_PLAN_FWD_OCC2 | _lib.FST_PLAN_FWD_KC16 | _lib.FST_PLAN_ROWS_W8 | _lib.FST_PLAN_ROWS_KV_REG
         | _lib.FST_PLAN_COLS_OCC2)
-    # float32 (first-generation kernels): tile heights and key chunks.
-    assert lib.fst_plans(_lib.FST_F32, 4, 16, 16) == F32_FWD | F32_BWD
+    # float32 (first-generation kernels): tile heights (eight waves per
+    # 16-row tile where 8 divides the padded heads) and key chunks.
+    assert lib.fst_plans(_lib.FST_F32, 8, 16, 16) == F32_FWD | F32_BWD & ~_lib.FST_PLAN_BWD_T64
+    assert lib.fst_plans(_lib.FST_F32, 4, 16, 16) == F32_FWD & ~_lib.FST_PLAN_FWD_W8 | F32_BWD & ~_lib.FST_PLAN_BWD_W8
     assert lib.fst_plans(_lib.FST_F32, 8, 64, 64) == (
         _lib.FST_PLAN_FWD_KC16 | _lib.FST_PLAN_FWD_KC32 | _lib.FST_PLAN_FWD_T16 | _lib.FST_PLAN_FWD_T32
-        | _lib.FST_PLAN_BWD_T16 | _lib.FST_PLAN_BWD_KC16 | _lib.FST_PLAN_BWD_PASS1 | _lib.FST_PLAN_BWD_PASS2)
+        | _lib.FST_PLAN_FWD_W8 | _lib.FST_PLAN_BWD_T16 | _lib.FST_PLAN_BWD_KC16 | _lib.FST_PLAN_BWD_PASS1
+        | _lib.FST_PLAN_BWD_PASS2 | _lib.FST_PLAN_BWD_W8)
     assert lib.fst_plans(_lib.FST_BF16, 17, 32, 16) == 0
     assert lib.fst_plans(_lib.FST_BF16, 12, 24, 16) == 0
     for dtype in (_lib.FST_BF16, _lib.FST_F32):
@@ -71,7 +74,7 @@ def test_plans_of_shapes():
                         assert mask & ~(F32_FWD | F32_BWD) == 0
                     # the static plan and every offered bit alone are runnable
                     assert lib.fst_plan_supported(dtype, h, d, c, 0)
-                    for b in range(8, 29):
+                    for b in range(8, 31):
                         if mask >> b & 1:
                             assert lib.fst_plan_supported(dtype, h, d, c, 1 << b), (dtype, h, d, c, b)
 
@@ -99,7 +102,10 @@ def test_plan_combinations():
     assert not sup(f32, 12, 32, 16, _lib.FST_PLAN_FWD_OCC2)
     assert not sup(bf, 12, 32, 16, _lib.FST_PLAN_FWD_T32)
     assert not sup(bf, 12, 32, 16, _lib.FST_PLAN_ROWS_W4 | _lib.FST_PLAN_ROWS_W8X2)
-    assert not sup(bf, 12, 32, 16, 1 << 29)
+    assert not sup(bf, 12, 32, 16, _lib.FST_PLAN_FWD_W8)
+    # eight-wave float32 tiles need the padded heads divisible by 8
+    assert sup(f32, 8, 64, 64, _lib.FST_PLAN_FWD_W8) and sup(f32, 8, 64, 64, _lib.FST_PLAN_BWD_W8)
+    assert not sup(f32, 12, 32, 16, _lib.FST_PLAN_FWD_W8)
     # one or two passes of the float32 rows kernel, with any fitting split
     assert sup(f32, 8, 64, 64, _lib.FST_PLAN_BWD_PASS1) and sup(f32, 8, 64, 64, _lib.FST_PLAN_BWD_PASS2)
     assert not sup(bf, 12, 32, 16, _lib.FST_PLAN_BWD_PASS1)
@@ -112,12 +118,12 @@ def test_plan_bits_are_validated():
     base = ws(_lib.FST_BF16, 3, 4, 12, 64, 0, 32, 16)
     assert base > 0
     # the workspace does not depend on the plan
-    for b in range(8, 29):
+    for b in range(8, 31):
         if BF16_ALL >> b & 1:
             assert ws(_lib.FST_BF16, 3 | (1 << b), 4, 12, 64, 0, 32, 16) == base
     base32 = ws(_lib.FST_F32, 3, 4, 4, 64, 0, 16, 16)
-    for b in range(8, 29):
-        if (F32_FWD | F32_BWD) >> b & 1:
+    for b in range(8, 31):
+        if lib.fst_plans(_lib.FST_F32, 4, 16, 16) >> b & 1:
             assert ws(_lib.FST_F32, 3 | (1 << b), 4, 4, 64, 0, 16, 16) == base32
     # two variants of one kernel knob
     rc = lib.fst_forward(0, 3 | _lib.FST_PLAN_FWD_OCC2 | _lib.FST_PLAN_FWD_OCC3, 1, 12, 8, 0, 32, 16, None,
@@ -136,7 +142,7 @@ def test_plan_bits_are_validated():
     assert rc == _lib.FST_EUNSUPPORTED and "plan" in _lib.last_error()
     assert ws(_lib.FST_BF16, 3 | _lib.FST_PLAN_ROWS_W4, 4, 8, 64, 0, 64, 64) == 0
     # bits past the plan field are unknown flags
-    rc = lib.fst_forward(0, 3 | (1 << 29), 1, 12, 8, 0, 32, 16, None, None, None, None, None, None, None,
+    rc = lib.fst_forward(0, 3 | -(1 << 31), 1, 12, 8, 0, 32, 16, None, None, None, None, None, None, None,
                          1.0, None, None, None, 0, None)
     assert rc == _lib.FST_EINVAL and "flag" in _lib.last_error()
 
@@ -170,7 +176,7 @@ def test_plan_names_and_fixed_plan():
 
 
 def test_plan_names_cover_every_bit():
-    for b in range(8, 29):
+    for b in range(8, 31):
         assert tune.plan_names(1 << b), b
     assert tune.plan_names(_lib.FST_PLAN_ROWS_W8X2 | _lib.FST_PLAN_ROWS_KV_LDS | _lib.FST_PLAN_FWD_KC32) == \
         "fwd:kc32 rows:w8x2 rows:kvlds"
@@ -211,6 +217,12 @@ def test_tile_arguments_map_to_plans():
     assert p(f32, 4, 16, 16, "fwd", block_m=32, block_n=32) == _lib.FST_PLAN_FWD_T32 | _lib.FST_PLAN_FWD_KC32
     assert p(f32, 4, 16, 16, "bwd", block_m=64, block_n=16) == _lib.FST_PLAN_BWD_T64 | _lib.FST_PLAN_BWD_KC16
     assert p(f32, 4, 16, 16, "fwd", block_m=64, block_n=32) == _lib.FST_PLAN_FWD_T64  # 64 x 32 does not fit
+    # float32: num_warps=8 asks for the eight-wave 16-row tile, 4 for four
+    assert p(f32, 8, 64, 64, "fwd", num_warps=8) == _lib.FST_PLAN_FWD_W8
+    assert p(f32, 8, 64, 64, "bwd", block_m=16, num_warps=8) == _lib.FST_PLAN_BWD_W8
+    assert p(f32, 8, 64, 64, "bwd", num_warps=4) == _lib.FST_PLAN_BWD_T16
+    assert p(f32, 8, 64, 64, "fwd", block_m=32, num_warps=8) == _lib.FST_PLAN_FWD_T32
+    assert p(f32, 12, 32, 16, "fwd", num_warps=8) == _lib.FST_PLAN_FWD_T16  # 8 does not divide 12
     # a combination not compiled drops block_n (then block_m)
     assert p(f32, 8, 64, 64, "fwd", block_m=32, block_n=32) == _lib.FST_PLAN_FWD_T32
     assert p(f32, 8, 64, 64, "fwd", block_m=64) == _lib.FST_PLAN_FWD_T32

@@ -48,11 +48,13 @@ SHAPES = [
     (F32, 4, 16, 16, [70, 33], False, (True, True)),
     (F32, 12, 32, 16, [80, 33, 1], True, (True, True)),
     (F32, 8, 64, 64, [48, 21], False, (True, True)),
+    (F32, 16, 32, 16, [70, 33], True, (True, True)),       # eight waves, two heads each
+    (F32, 8, 32, 16, [90, 17, 1], False, (True, False)),   # eight waves, lanes sharing an embedding
 ]
 
-FWD_GROUPS = [(1 << 8, 1 << 9), (1 << 17, 1 << 18), (1 << 19, 1 << 20, 1 << 21)]
+FWD_GROUPS = [(1 << 8, 1 << 9), (1 << 17, 1 << 18), (1 << 19, 1 << 20, 1 << 21, 1 << 29)]
 BWD_GROUPS = [(1 << 10, 1 << 11, 1 << 14), (1 << 15, 1 << 16), (1 << 12, 1 << 13),
-              (1 << 22, 1 << 23, 1 << 24), (1 << 25, 1 << 26), (1 << 27, 1 << 28)]
+              (1 << 22, 1 << 23, 1 << 24, 1 << 30), (1 << 25, 1 << 26), (1 << 27, 1 << 28)]
 
 
 def _inputs(dtype, heads, dim, chans, lens, packed, seed):
