@@ -105,6 +105,7 @@ __global__ __launch_bounds__(256, OCC) void fwd2_kernel(FwdParams prm) {
   f32x4 O[HW][NQ];
   float lsum[HW];  // this lane group's part of the row sum
   float mref[HW];
+  float thr[HW];   // (mref + 2^8 headroom) in the logits' natural-log units
   // The prologue's loads (q, W, the projected rows, positions, then the
   // first chunk's operands) are all issued before the first of them is used,
   // from clamped rows and without branches, so none waits for another.
@@ -217,6 +218,7 @@ __global__ __launch_bounds__(256, OCC) void fwd2_kernel(FwdParams prm) {
     for (int q = 0; q < NQ; ++q) O[hl][q] = zero4();
     lsum[hl] = 0.f;
     mref[hl] = -INFINITY;
+    thr[hl] = -INFINITY;
   }
   bf16x4 uf[4][NCT];
   f32x4 AE[4][NCT];
@@ -281,20 +283,22 @@ __global__ __launch_bounds__(256, OCC) void fwd2_kernel(FwdParams prm) {
       }
     }
     // A row's reference m moves only when some key of the chunk exceeds it by
-    // more than 2^8; each lane compares its own logits with the threshold,
-    // and only then is the row maximum formed across the lane groups.
+    // more than 2^8; each lane compares the largest margin of its own logits
+    // over the threshold, and only then is the row maximum formed across the
+    // lane groups.
     float mx[HW], alpha[HW];
-    bool need_any = false;
+    float margin = -INFINITY;
 #pragma unroll
     for (int hl = 0; hl < HW; ++hl) {
-      const float thr = (mref[hl] + kRescaleLog2) * kLn2;
+      float m = S[hl][0][0];
 #pragma unroll
       for (int s = 0; s < NS; ++s)
 #pragma unroll
-        for (int r = 0; r < 4; ++r) need_any |= S[hl][s][r] > thr;
+        for (int r = (s == 0 ? 1 : 0); r < 4; ++r) m = fmaxf(m, S[hl][s][r]);
+      margin = fmaxf(margin, m - thr[hl]);
       alpha[hl] = 1.f;
     }
-    const bool rescale = __builtin_amdgcn_ballot_w64(need_any) != 0;
+    const bool rescale = __builtin_amdgcn_ballot_w64(margin > 0.f) != 0;
     if (rescale) {
 #pragma unroll
       for (int hl = 0; hl < HW; ++hl) {
@@ -307,6 +311,7 @@ __global__ __launch_bounds__(256, OCC) void fwd2_kernel(FwdParams prm) {
         const float mnew = mx[hl] > mref[hl] + kRescaleLog2 ? mx[hl] : mref[hl];
         alpha[hl] = exp2f_fast(mref[hl] - mnew);
         mref[hl] = mnew;
+        thr[hl] = (mnew + kRescaleLog2) * kLn2;
 #pragma unroll
         for (int q = 0; q < NQ; ++q) O[hl][q] = O[hl][q] * alpha[hl];
         lsum[hl] *= alpha[hl];
