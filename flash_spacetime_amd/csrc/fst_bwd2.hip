@@ -537,17 +537,21 @@ __global__ __launch_bounds__(64 * NW, WPE) void bwd_rows2_kernel(BwdParams prm) 
   if constexpr (KL) wait_vmem();
 
   // ---- epilogue: sigma, D, dq = scale (dQ + W H + sigma b) ----
-  // W (d on the lanes, the slots of H on the k index) and b, loaded before
-  // the first barrier.
-  float wdq[NQ][NCT][4], bq[NQ][4];
+  // W (d on the lanes, the slots of H on the k index) as bf16 parts, and b,
+  // loaded before the first barrier.
+  bf16x4 wdh[NQ][NCT], wdl[NQ][NCT];
+  float bq[NQ][4];
   if (attn) {
 #pragma unroll
     for (int q = 0; q < NQ; ++q) {
       const int dn = DT::dmap(q, n >> 2, n & 3);
 #pragma unroll
-      for (int ct = 0; ct < NCT; ++ct)
+      for (int ct = 0; ct < NCT; ++ct) {
+        f32x4 wq;
 #pragma unroll
-        for (int sp = 0; sp < 4; ++sp) wdq[q][ct][sp] = prm.weight[dn * C + slot_channel<C>(16 * ct + 4 * g + sp)];
+        for (int sp = 0; sp < 4; ++sp) wq[sp] = prm.weight[dn * C + slot_channel<C>(16 * ct + 4 * g + sp)];
+        split4(wq, wdh[q][ct], wdl[q][ct]);
+      }
 #pragma unroll
       for (int r = 0; r < 4; ++r) bq[q][r] = prm.bias ? prm.bias[DT::dmap(q, g, r)] : 0.f;
     }
@@ -562,6 +566,14 @@ __global__ __launch_bounds__(64 * NW, WPE) void bwd_rows2_kernel(BwdParams prm) 
       if (prm.rowsum) prm.rowsum[ra.vec(h, my_row)] = sig[hl];
     }
   }
+  // W H on bf16 MFMA over the two parts of each factor (W and H to 16 bits).
+  bf16x4 hh[RPW][NCT], hlo[RPW][NCT];
+  if (attn) {
+#pragma unroll
+    for (int r = 0; r < RPW; ++r)
+#pragma unroll
+      for (int ct = 0; ct < NCT; ++ct) split4(Hacc[r][ct], hh[r][ct], hlo[r][ct]);
+  }
 #pragma unroll
   for (int q = 0; q < NQ; ++q) {
     if (attn) {
@@ -570,9 +582,7 @@ __global__ __launch_bounds__(64 * NW, WPE) void bwd_rows2_kernel(BwdParams prm) 
       for (int r = 0; r < RPW; ++r) {
         f32x4 acc = zero4();
 #pragma unroll
-        for (int ct = 0; ct < NCT; ++ct)
-#pragma unroll
-          for (int sp = 0; sp < 4; ++sp) acc = mfma_f32(wdq[q][ct][sp], Hacc[r][ct][sp], acc);
+        for (int ct = 0; ct < NCT; ++ct) acc = mma_split(wdh[q][ct], wdl[q][ct], hh[r][ct], hlo[r][ct], acc);
         *reinterpret_cast<f32x4*>(stU + stage_off(g, row0 + r, n)) = acc;
       }
       __syncthreads();
@@ -609,7 +619,7 @@ __global__ __launch_bounds__(64 * NW, WPE) void bwd_rows2_kernel(BwdParams prm) 
 
   // ---- dW / db partial of this tile: sum over its rows and heads ----
   // dW[d, channel(slot)] += sum_(row, head) A[d, (row, head)] B[(row, head), slot]
-  // on fp32 MFMA: A = qt (then dO) with d on the lanes, read from the tile's
+  // on bf16 MFMA: A = qt (then dO) with d on the lanes, read from the tile's
   // rows staged by the head-owners ([row][head][D], zeros for invalid rows
   // and heads); B = H (then G) with the slot on the lanes, staged one channel
   // step at a time as [row][head][16 slots].
@@ -641,19 +651,27 @@ __global__ __launch_bounds__(64 * NW, WPE) void bwd_rows2_kernel(BwdParams prm) 
           if (n < HP)
             *reinterpret_cast<f32x4*>(HGs + ((row0 + r) * HP + n) * 16 + 4 * g) = op == 0 ? Hacc[r][ct] : Gacc[r][ct];
         __syncthreads();
+        // One 16x16x16 product per head quad s4: k-slot 4g + e is the pair
+        // (row row0 + e, head 4 s4 + g) (e < RPW; the rest zero), A = the
+        // staged bf16 rows (exact), B = H or G in two bf16 parts.
 #pragma unroll
-        for (int r = 0; r < RPW; ++r) {
-          const int il = row0 + r;
+        for (int s4 = 0; s4 < HP / 4; ++s4) {
+          const int h = 4 * s4 + g;
+          f32x4 bv = zero4();
 #pragma unroll
-          for (int s4 = 0; s4 < HP / 4; ++s4) {
-            const int h = 4 * s4 + g;
-            const float b = HGs[(il * HP + h) * 16 + n];
+          for (int e = 0; e < RPW && e < 4; ++e) bv[e] = HGs[((row0 + e) * HP + h) * 16 + n];
+          bf16x4 bh, bl;
+          split4(bv, bh, bl);
 #pragma unroll
-            for (int q = 0; q < NQ; ++q) {
-              const float a = (float)Xs[(il * HP + h) * D + 16 * q + n];
-              if (op == 1 && ct == 0) dbl[q] += a;
-              dw[q][ct] = mfma_f32(a, b, dw[q][ct]);
+          for (int q = 0; q < NQ; ++q) {
+            bf16x4 av{};
+#pragma unroll
+            for (int e = 0; e < RPW && e < 4; ++e) {
+              av[e] = Xs[((row0 + e) * HP + h) * D + 16 * q + n];
+              if (op == 1 && ct == 0) dbl[q] += (float)av[e];
             }
+            dw[q][ct] = mfma_x16(av, bl, dw[q][ct]);
+            dw[q][ct] = mfma_x16(av, bh, dw[q][ct]);
           }
         }
         __syncthreads();

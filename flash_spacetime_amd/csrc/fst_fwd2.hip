@@ -430,22 +430,35 @@ __global__ __launch_bounds__(256, OCC) void fwd2_kernel(FwdParams prm) {
   // read transposed from LDS, DTiles::dmap otherwise.
   auto omap = [&](int q, int gg, int r) { return VL ? 16 * q + 4 * gg + r : DT::dmap(q, gg, r); };
   // One head-dim tile per round: the row-owner forms o2^T_i[d, h] =
-  // sum_slot W[d, channel(slot)] A^T_i[slot, h] on fp32 MFMA (lane n of the
-  // A operand is the tile's feature omap(q, n/4, n%4)) and stages it; the
-  // head-owner forms out = (O + o2) / l + b in place.
+  // sum_slot W[d, channel(slot)] A^T_i[slot, h] on bf16 MFMA over the two
+  // parts of each factor (W and A to 16 bits; lane n of the W operand is the
+  // tile's feature omap(q, n/4, n%4)) and stages it; the head-owner forms
+  // out = (O + o2) / l + b in place.
+  bf16x4 aeh[4][NCT], ael[4][NCT];
+  if (act) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+#pragma unroll
+      for (int ct = 0; ct < NCT; ++ct) split4(AE[r][ct], aeh[r][ct], ael[r][ct]);
+  }
 #pragma unroll
   for (int q = 0; q < NQ; ++q) {
     if (act) {
-      __syncthreads();  // previous round (or the last chunk) done with the stage
       const int dn = omap(q, n >> 2, n & 3);
+      bf16x4 wh[NCT], wl[NCT];
+#pragma unroll
+      for (int ct = 0; ct < NCT; ++ct) {
+        f32x4 wq;
+#pragma unroll
+        for (int sp = 0; sp < 4; ++sp) wq[sp] = prm.weight[dn * C + slot_channel<C>(16 * ct + 4 * g + sp)];
+        split4(wq, wh[ct], wl[ct]);
+      }
+      __syncthreads();  // previous round (or the last chunk) done with the stage
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         f32x4 acc = zero4();
 #pragma unroll
-        for (int ct = 0; ct < NCT; ++ct)
-#pragma unroll
-          for (int sp = 0; sp < 4; ++sp)
-            acc = mfma_f32(prm.weight[dn * C + slot_channel<C>(16 * ct + 4 * g + sp)], AE[r][ct][sp], acc);
+        for (int ct = 0; ct < NCT; ++ct) acc = mma_split(wh[ct], wl[ct], aeh[r][ct], ael[r][ct], acc);
         *reinterpret_cast<f32x4*>(stage + stage_off(g, 4 * w + r, n)) = acc;
       }
       __syncthreads();

@@ -222,16 +222,28 @@ __device__ __forceinline__ void zero_tile_rows(const EventSpec& ev, const RowAdd
     for (int idx = tid; idx < H * nr; idx += NT) vec[rv.vec(idx / nr, first + idx % nr)] = 0.f;
 }
 
-// The W operand of project_slots: lane (g, n) holds W[Qd g + s][channel(16
-// ct + n)], loaded once and shared by every row a kernel projects.
+// The W operand of project_loaded, split into bf16 parts hi = bf16(W) and
+// lo = bf16(W - hi) (W to 16 significant bits): lane (g, n) holds W[Qd g +
+// i][channel(16 ct + n)] for its Qd = D / 4 features i, in steps of 8 (16x16x32
+// products) where Qd is a multiple of 8, else of 4 (16x16x16). Loaded once
+// and shared by every row a kernel projects.
 template <int D, int C>
 struct WSlots {
-  float v[D / 4][C / 16];
+  static constexpr int Qd = D / 4, STEP = Qd % 8 == 0 ? 8 : 4, NST = Qd / STEP;
+  using V = std::conditional_t<STEP == 8, bf16x8, bf16x4>;
+  V hi[C / 16][NST], lo[C / 16][NST];
   __device__ __forceinline__ void load(const float* __restrict__ W, int g, int n) {
 #pragma unroll
-    for (int s = 0; s < D / 4; ++s)
+    for (int ct = 0; ct < C / 16; ++ct)
 #pragma unroll
-      for (int ct = 0; ct < C / 16; ++ct) v[s][ct] = W[((D / 4) * g + s) * C + slot_channel<C>(16 * ct + n)];
+      for (int st = 0; st < NST; ++st)
+#pragma unroll
+        for (int e = 0; e < STEP; ++e) {
+          const float wv = W[(Qd * g + STEP * st + e) * C + slot_channel<C>(16 * ct + n)];
+          const bf16 h = (bf16)wv;
+          hi[ct][st][e] = h;
+          lo[ct][st][e] = (bf16)(wv - (float)h);
+        }
   }
 };
 
@@ -251,23 +263,49 @@ struct SlotRow {
   }
 };
 
-// u = bf16(x @ W[:, channel(slot)]) for the heads of one row, x = row * mult
-// (q * scale or dO): fp32 MFMA with the head on lane n (heads >= H or an
-// invalid row give zeros); lane (g, n = h) receives slots 16 ct + 4 g .. +3.
+// u = bf16(mult (x @ W[:, channel(slot)])) for the heads of one row (x =
+// q with mult = scale, or dO with mult = 1): bf16 MFMA over x (exact in bf16)
+// and W's two parts, accumulated in fp32, so the product keeps W to 16 bits
+// before the one rounding to bf16; the head is on lane n (heads >= H or an
+// invalid row give zeros) and lane (g, n = h) receives slots 16 ct + 4 g .. +3.
 template <int D, int C>
 __device__ __forceinline__ void project_loaded(const SlotRow<D>& xr, bool ok, float mult, const WSlots<D, C>& wv,
                                             bf16x4* out) {
-  constexpr int VW = SlotRow<D>::VW;
-  float xv[D / 4];
-#pragma unroll
-  for (int s = 0; s < D / 4; ++s) xv[s] = ok ? (float)xr.x[s / VW][s % VW] * mult : 0.f;
+  using WS = WSlots<D, C>;
+  static_assert(SlotRow<D>::VW == WS::STEP, "one SlotRow vector per product step");
 #pragma unroll
   for (int ct = 0; ct < C / 16; ++ct) {
     f32x4 a = zero4();
 #pragma unroll
-    for (int s = 0; s < D / 4; ++s) a = mfma_f32(wv.v[s][ct], xv[s], a);
-    out[ct] = pack4(a);
+    for (int st = 0; st < WS::NST; ++st) {
+      const typename WS::V x = ok ? xr.x[st] : typename WS::V{};
+      if constexpr (WS::STEP == 8) {
+        a = mfma_x32(wv.hi[ct][st], x, a);
+        a = mfma_x32(wv.lo[ct][st], x, a);
+      } else {
+        a = mfma_x16(wv.hi[ct][st], x, a);
+        a = mfma_x16(wv.lo[ct][st], x, a);
+      }
+    }
+    out[ct] = pack4(a * mult);
   }
+}
+
+// fp32 quad -> bf16 parts hi = bf16(x), lo = bf16(x - hi) (x to 16 bits).
+__device__ __forceinline__ void split4(const f32x4& x, bf16x4& hi, bf16x4& lo) {
+  hi = pack4(x);
+  f32x4 r;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) r[e] = x[e] - (float)hi[e];
+  lo = pack4(r);
+}
+
+// C += A B over 16 k-slots (16x16x16 operand layouts) with A and B given as
+// bf16 parts: three products, lo x lo (below 2^-16 of the result) dropped.
+__device__ __forceinline__ f32x4 mma_split(bf16x4 ah, bf16x4 al, bf16x4 bh, bf16x4 bl, f32x4 c) {
+  c = mfma_x16(al, bh, c);
+  c = mfma_x16(ah, bl, c);
+  return mfma_x16(ah, bh, c);
 }
 
 // Load and project one row; xrow points at head 0 of the row, hstride is the
