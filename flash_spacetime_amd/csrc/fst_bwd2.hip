@@ -74,12 +74,12 @@ struct Rows2Cfg {
   static constexpr int REGION = (KC / 4) * 16 * 16 * 16;  // one fp32 term of KC keys per (row, 16 head slots)
   static constexpr int SCAL_BYTES = 16 * 17 * 4;
   static constexpr int MAIN = E_BYTES + 2 * REGION + SCAL_BYTES;
-  // Epilogue: the tile's qt (or dO) rows, then four dW / db partials (one per
+  // Epilogue: the tile's qt and dO rows, then four dW / db partials (one per
   // wave, or per pair of waves w, w + 4) in the same bytes; one channel step
-  // of H (or G) after them.
+  // of H (or G) after them, each wave's rows its own.
   static constexpr int DW_BYTES = 4 * (D * C + D) * 4;
   static constexpr int XS_BYTES = 16 * HP * D * 2;
-  static constexpr int X_DW = DW_BYTES > XS_BYTES ? DW_BYTES : XS_BYTES;
+  static constexpr int X_DW = DW_BYTES > 2 * XS_BYTES ? DW_BYTES : 2 * XS_BYTES;
   static constexpr int HG_BYTES = 16 * HP * 16 * 4;
   static constexpr int EPI = X_DW + HG_BYTES;
   static constexpr int LDS_BYTES = MAIN > EPI ? MAIN : EPI;  // dynamic
@@ -619,10 +619,11 @@ __global__ __launch_bounds__(64 * NW, WPE) void bwd_rows2_kernel(BwdParams prm) 
 
   // ---- dW / db partial of this tile: sum over its rows and heads ----
   // dW[d, channel(slot)] += sum_(row, head) A[d, (row, head)] B[(row, head), slot]
-  // on bf16 MFMA: A = qt (then dO) with d on the lanes, read from the tile's
-  // rows staged by the head-owners ([row][head][D], zeros for invalid rows
-  // and heads); B = H (then G) with the slot on the lanes, staged one channel
-  // step at a time as [row][head][16 slots].
+  // on bf16 MFMA, each wave over its own rows: A = qt (then dO) with d on the
+  // lanes, read from the tile's rows that the head-owners stage ([op][row]
+  // [head][D], zeros for invalid rows and heads: the one exchange between
+  // waves); B = H (then G) with the slot on the lanes, which the wave stages
+  // for itself one channel step at a time as [row][head][16 slots].
   __syncthreads();
   float* Wred = reinterpret_cast<float*>(smem);  // after the products, over Xs
   bf16* Xs = reinterpret_cast<bf16*>(smem);
@@ -642,15 +643,26 @@ __global__ __launch_bounds__(64 * NW, WPE) void bwd_rows2_kernel(BwdParams prm) 
 #pragma unroll
       for (int hl = 0; hl < HW; ++hl) {
         const int h = head(hl);
-        if (h < HP) (op == 0 ? qf[hl] : dof[hl]).store(Xs + (n * HP + h) * D, g);
+        if (h < HP) (op == 0 ? qf[hl] : dof[hl]).store(Xs + op * 16 * HP * D + (n * HP + h) * D, g);
       }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int op = 0; op < 2; ++op) {
+      if (!(op == 0 ? attn : act)) continue;
+      const bf16* Xo = Xs + op * 16 * HP * D;
 #pragma unroll
       for (int ct = 0; ct < NCT; ++ct) {
+        // The wave's own rows, exchanged between its lanes: wave_lds_sync
+        // (a compiler fence and an LDS wait) orders the stores after the
+        // previous step's reads and before this step's, in place of a
+        // workgroup barrier.
+        wave_lds_sync();
 #pragma unroll
         for (int r = 0; r < RPW; ++r)
           if (n < HP)
             *reinterpret_cast<f32x4*>(HGs + ((row0 + r) * HP + n) * 16 + 4 * g) = op == 0 ? Hacc[r][ct] : Gacc[r][ct];
-        __syncthreads();
+        wave_lds_sync();
         // One 16x16x16 product per head quad s4: k-slot 4g + e is the pair
         // (row row0 + e, head 4 s4 + g) (e < RPW; the rest zero), A = the
         // staged bf16 rows (exact), B = H or G in two bf16 parts.
@@ -667,16 +679,16 @@ __global__ __launch_bounds__(64 * NW, WPE) void bwd_rows2_kernel(BwdParams prm) 
             bf16x4 av{};
 #pragma unroll
             for (int e = 0; e < RPW && e < 4; ++e) {
-              av[e] = Xs[((row0 + e) * HP + h) * D + 16 * q + n];
+              av[e] = Xo[((row0 + e) * HP + h) * D + 16 * q + n];
               if (op == 1 && ct == 0) dbl[q] += (float)av[e];
             }
             dw[q][ct] = mfma_x16(av, bl, dw[q][ct]);
             dw[q][ct] = mfma_x16(av, bh, dw[q][ct]);
           }
         }
-        __syncthreads();
       }
     }
+    __syncthreads();  // every wave done with Xs before the partials overwrite it
     // Four partials: wave w's (w < 4), then with eight waves wave w + 4's
     // added to slot w in a second round (a fixed order of additions).
     float* wr = Wred + (w & 3) * DCW;
