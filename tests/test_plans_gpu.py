@@ -50,6 +50,8 @@ SHAPES = [
     (F32, 8, 64, 64, [48, 21], False, (True, True)),
     (F32, 16, 32, 16, [70, 33], True, (True, True)),       # eight waves, two heads each
     (F32, 8, 32, 16, [90, 17, 1], False, (True, False)),   # eight waves, lanes sharing an embedding
+    (F32, 7, 32, 16, [70, 33], False, (True, True)),       # eight waves, one owning only a padded head
+    (F32, 13, 16, 32, [60, 21], True, (False, True)),      # eight waves over 16 padded heads
 ]
 
 FWD_GROUPS = [(1 << 8, 1 << 9), (1 << 17, 1 << 18), (1 << 19, 1 << 20, 1 << 21, 1 << 29)]
