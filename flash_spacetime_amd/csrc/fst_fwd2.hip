@@ -11,8 +11,8 @@
 //    O^T_h += V_h^T P^T_h on 16x16 MFMA tiles with the 16 rows on the lanes,
 //    the online softmax and its row sums l (fp32, per lane group, summed
 //    across the groups at the end);
-//  * row-owner of rows 4w .. 4w+3: u of its rows (fp32 MFMA projection), the
-//    embedding E of its rows x the chunk's keys, computed directly in the
+//  * row-owner of rows 4w .. 4w+3: u of its rows (bf16 MFMA over W in two
+//    parts), the embedding E of its rows x the chunk's keys, computed in the
 //    operand layout of the u.E product (UE^T_i = E_i U_i^T, heads on the
 //    lanes) and kept in LDS for A^T_i += E_i^T P_i^T (A = sum_j p_ij E_ij).
 // The roles meet in LDS: u.E goes row-owner -> head-owner (fp32), P and the
@@ -225,7 +225,7 @@ __global__ __launch_bounds__(256, OCC) void fwd2_kernel(FwdParams prm) {
 #pragma unroll
   for (int r = 0; r < 4; ++r) {
     if (attn) {
-      // u^T[slot][h] = sum_d W[d][channel(slot)] qt[h][d] on fp32 MFMA.
+      // u^T[slot][h] = scale sum_d W[d][channel(slot)] q[h][d] (project_loaded).
       project_loaded<D, C>(xq[r], i0 + 4 * w + r < len && n < H, prm.scale, wv, uf[r]);
     } else {
 #pragma unroll
