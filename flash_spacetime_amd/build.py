@@ -36,6 +36,13 @@ DTYPES = {"bf16": "bf16", "f32": "float"}
 HEAD_DIMS = (16, 32, 48, 64)
 
 
+# The bf16 tile rows kernel is built in a unit of its own with the machine
+# scheduler's max-ilp strategy (cfg2's rows kernel 0.891 -> 0.873 ms); the
+# strategy slowed the cols kernel by up to a third at other shapes and the
+# float32 forward by 11 %, so every other unit keeps the default.
+ROWS_SCHED = ["-mllvm", "--amdgpu-sched-strategy=max-ilp"]
+
+
 def _units():
     units = [("capi", CSRC / "fst_capi.hip", [])]
     for tag, ctype in DTYPES.items():
@@ -43,7 +50,11 @@ def _units():
             name = f"{tag}_{d}"
             defs = [f"-DFST_T={ctype}", f"-DFST_D={d}", f"-DFST_NAME={name}"]
             units.append((f"fwd_{name}", CSRC / "fst_fwd_inst.hip", defs))
-            units.append((f"bwd_{name}", CSRC / "fst_bwd_inst.hip", defs))
+            if tag == "bf16":
+                units.append((f"bwdr_{name}", CSRC / "fst_bwd_inst.hip", defs + ["-DFST_BWD_PART=1"] + ROWS_SCHED))
+                units.append((f"bwd_{name}", CSRC / "fst_bwd_inst.hip", defs + ["-DFST_BWD_PART=2"]))
+            else:
+                units.append((f"bwd_{name}", CSRC / "fst_bwd_inst.hip", defs))
     return [u for u in units if u[1].exists()]
 
 

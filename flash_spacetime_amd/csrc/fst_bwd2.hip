@@ -1172,15 +1172,24 @@ int bwd2_launch_cols(const BwdParams& prm, hipStream_t stream, int g8, bool quer
 // (which = 1) kernel variant the plan bits of prm.flags name. For the rows
 // kernel HP is the rows head padding, which the library rounds to a
 // multiple of 8 when the eight-wave, one-workgroup plan (static or chosen)
-// runs.
+// runs. FST_BWD_PART: the kernels a translation unit instantiates (0 both,
+// 1 the rows kernel, 2 the cols kernel), so the rows kernel can be built
+// with its own scheduler options; the launcher has internal linkage, as
+// its body depends on the part.
+#ifndef FST_BWD_PART
+#define FST_BWD_PART 0
+#endif
 template <int HP, int D, int C>
-int bwd2_launch_t(const BwdParams& prm, int which, hipStream_t stream, int grid, bool query) {
+static int bwd2_launch_t(const BwdParams& prm, int which, hipStream_t stream, int grid, bool query) {
   using P = Bwd2Pick<HP, D, C>;
   // The grid is rounded up to a multiple of 64 for the XCD schedules
   // (tile_block); logical blocks past the work list exit at once.
   const int g8 = grid > 0 ? (grid + 63) & ~63 : 0;
   const int f = prm.flags;
   if (which == 0) {
+#if FST_BWD_PART == 2
+    return FST_EUNSUPPORTED;
+#else
     const bool kl = f & FST_PLAN_ROWS_KV_LDS;
     const int waves = (f & FST_PLAN_ROWS_W4)     ? 1
                       : (f & FST_PLAN_ROWS_W8)   ? 2
@@ -1203,7 +1212,11 @@ int bwd2_launch_t(const BwdParams& prm, int which, hipStream_t stream, int grid,
       if constexpr (P::KL_W8X2) return bwd2_launch_rows<HP, D, C, 8, 4, true>(prm, stream, g8, query);
     }
     return FST_EUNSUPPORTED;
+#endif
   }
+#if FST_BWD_PART == 1
+  return FST_EUNSUPPORTED;
+#else
   if constexpr (!P::CC::FITS) {
     return FST_EUNSUPPORTED;
   } else {
@@ -1214,6 +1227,7 @@ int bwd2_launch_t(const BwdParams& prm, int which, hipStream_t stream, int grid,
     }
     return bwd2_launch_cols<HP, D, C, 2>(prm, stream, g8, query);
   }
+#endif
 }
 
 }  // namespace fst

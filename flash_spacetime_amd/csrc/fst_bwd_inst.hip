@@ -1,6 +1,9 @@
 // Instantiates the backward kernels for one (dtype, D) over every head
 // padding HP in {4, 8, 12, 16} and channel count C in {16, 32, 48, 64}.
-// Built once per (dtype, D) with -DFST_T, -DFST_D and -DFST_NAME.
+// Built once per (dtype, D) with -DFST_T, -DFST_D and -DFST_NAME; for bf16
+// twice, with -DFST_BWD_PART=1 (the tile rows kernel, bwd2_rows_dispatch_*,
+// built with the machine scheduler's max-ilp strategy) and =2 (everything
+// else).
 #include "fst_backward.hip"
 #include "fst_bwd2.hip"
 
@@ -13,6 +16,31 @@
 
 namespace fst {
 
+// The bf16 tile rows kernel of (HP, C): launched (or, with query, checked)
+// from its own translation unit (FST_BWD_PART = 1).
+int FST_CAT(bwd2_rows_dispatch_, FST_NAME)(const BwdParams& prm, int HP, int C, hipStream_t stream, int grid,
+                                           bool query);
+
+#if FST_BWD_PART == 1
+int FST_CAT(bwd2_rows_dispatch_, FST_NAME)(const BwdParams& prm, int HP, int C, hipStream_t stream, int grid,
+                                           bool query) {
+#define FST_CASE(HPV, CV)                                                      \
+  if (HP == HPV && C == CV) {                                                  \
+    if constexpr (Bwd2Pick<HPV, FST_D, CV>::OK)                                \
+      return bwd2_launch_t<HPV, FST_D, CV>(prm, 0, stream, grid, query);       \
+    return FST_EUNSUPPORTED;                                                   \
+  }
+#define FST_CASES(HPV) FST_CASE(HPV, 16) FST_CASE(HPV, 32) FST_CASE(HPV, 48) FST_CASE(HPV, 64)
+  FST_CASES(4)
+  FST_CASES(8)
+  FST_CASES(12)
+  FST_CASES(16)
+#undef FST_CASES
+#undef FST_CASE
+  return FST_EUNSUPPORTED;
+}
+#else
+
 int FST_CAT(bwd_dispatch_, FST_NAME)(const BwdParams& prm, int which, int HP, int C, hipStream_t stream, int grid,
                                      bool query, int* rows) {
   // bf16 runs the 16-row / 16-key tile kernels (fst_bwd2.hip) wherever their
@@ -23,6 +51,9 @@ int FST_CAT(bwd_dispatch_, FST_NAME)(const BwdParams& prm, int which, int HP, in
   if (HP == HPV && C == CV) {                                                  \
     if constexpr (is_bf16<FST_T>::value && Bwd2Pick<HPV, FST_D, CV>::OK) {     \
       *rows = 16;                                                              \
+      if constexpr (FST_BWD_PART == 2) {                                       \
+        if (which == 0) return FST_CAT(bwd2_rows_dispatch_, FST_NAME)(prm, HP, C, stream, grid, query); \
+      }                                                                        \
       return bwd2_launch_t<HPV, FST_D, CV>(prm, which, stream, grid, query);   \
     } else {                                                                   \
       return bwd_launch_t<FST_T, HPV, FST_D, CV>(prm, which, stream, grid, query, rows); \
@@ -75,5 +106,7 @@ int FST_CAT(bwd_plans_, FST_NAME)(int HP, int C) {
 #undef FST_CASE
   return 0;
 }
+
+#endif  // FST_BWD_PART
 
 }  // namespace fst
