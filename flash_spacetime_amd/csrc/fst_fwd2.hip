@@ -105,7 +105,6 @@ __global__ __launch_bounds__(256, OCC) void fwd2_kernel(FwdParams prm) {
   f32x4 O[HW][NQ];
   float lsum[HW];  // this lane group's part of the row sum
   float mref[HW];
-  float thr[HW];   // (mref + 2^8 headroom) in the logits' natural-log units
   // The prologue's loads (q, W, the projected rows, positions, then the
   // first chunk's operands) are all issued before the first of them is used,
   // from clamped rows and without branches, so none waits for another.
@@ -218,7 +217,6 @@ __global__ __launch_bounds__(256, OCC) void fwd2_kernel(FwdParams prm) {
     for (int q = 0; q < NQ; ++q) O[hl][q] = zero4();
     lsum[hl] = 0.f;
     mref[hl] = -INFINITY;
-    thr[hl] = -INFINITY;
   }
   bf16x4 uf[4][NCT];
   f32x4 AE[4][NCT];
@@ -283,22 +281,26 @@ __global__ __launch_bounds__(256, OCC) void fwd2_kernel(FwdParams prm) {
       }
     }
     // A row's reference m moves only when some key of the chunk exceeds it by
-    // more than 2^8; each lane compares the largest margin of its own logits
-    // over the threshold, and only then is the row maximum formed across the
-    // lane groups.
+    // more than 2^8. X holds the exponents of the chunk's probabilities against
+    // the current reference; each lane tests the largest of its own, and only
+    // then is the row maximum formed across the lane groups. (On the first
+    // chunk the reference is -inf and every valid key's X is +inf.)
     float mx[HW], alpha[HW];
+    f32x4 X[HW][NS];
     float margin = -INFINITY;
 #pragma unroll
     for (int hl = 0; hl < HW; ++hl) {
-      float m = S[hl][0][0];
+      const float mb = mref[hl];
 #pragma unroll
       for (int s = 0; s < NS; ++s)
 #pragma unroll
-        for (int r = (s == 0 ? 1 : 0); r < 4; ++r) m = fmaxf(m, S[hl][s][r]);
-      margin = fmaxf(margin, m - thr[hl]);
+        for (int r = 0; r < 4; ++r) {
+          X[hl][s][r] = __builtin_fmaf(S[hl][s][r], kLog2e, -mb);
+          margin = fmaxf(margin, X[hl][s][r]);
+        }
       alpha[hl] = 1.f;
     }
-    const bool rescale = __builtin_amdgcn_ballot_w64(margin > 0.f) != 0;
+    const bool rescale = __builtin_amdgcn_ballot_w64(margin > kRescaleLog2) != 0;
     if (rescale) {
 #pragma unroll
       for (int hl = 0; hl < HW; ++hl) {
@@ -311,7 +313,10 @@ __global__ __launch_bounds__(256, OCC) void fwd2_kernel(FwdParams prm) {
         const float mnew = mx[hl] > mref[hl] + kRescaleLog2 ? mx[hl] : mref[hl];
         alpha[hl] = exp2f_fast(mref[hl] - mnew);
         mref[hl] = mnew;
-        thr[hl] = (mnew + kRescaleLog2) * kLn2;
+#pragma unroll
+        for (int s = 0; s < NS; ++s)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) X[hl][s][r] = __builtin_fmaf(S[hl][s][r], kLog2e, -mnew);
 #pragma unroll
         for (int q = 0; q < NQ; ++q) O[hl][q] = O[hl][q] * alpha[hl];
         lsum[hl] *= alpha[hl];
@@ -320,13 +325,12 @@ __global__ __launch_bounds__(256, OCC) void fwd2_kernel(FwdParams prm) {
     JFrag<bf16, NS> pf[HW];
 #pragma unroll
     for (int hl = 0; hl < HW; ++hl) {
-      const float mb = mref[hl];
       float ls = lsum[hl];
 #pragma unroll
       for (int s = 0; s < NS; ++s)
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-          S[hl][s][r] = exp2f_fast(__builtin_fmaf(S[hl][s][r], kLog2e, -mb));
+          S[hl][s][r] = exp2f_fast(X[hl][s][r]);
           ls += S[hl][s][r];
         }
       lsum[hl] = ls;
