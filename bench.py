@@ -145,7 +145,7 @@ def kernel_times(inp, seqlens, iters=10, cu=None, plan=0, flags=(True, True)):
     bws = lib.fst_backward_workspace_bytes(*dims)
     bwork = torch.empty(bws, device=dev, dtype=torch.uint8)
     bargs = (P(prep.q), P(prep.k), P(prep.v), P(prep.pos4), P(prep.weight), P(prep.bias), P(prep.lens), P(lse),
-             P(do), prep.scale, P(dq), P(dk), P(dv), P(dw), P(db), None, P(bwork), bws, sh)
+             P(do), P(out), prep.scale, P(dq), P(dk), P(dv), P(dw), P(db), None, P(bwork), bws, sh)
     _lib.check(lib.fst_forward_phases(_lib.FST_PHASE_FWD, *dims, *fargs), "fwd")
     _lib.check(lib.fst_backward_phases(_lib.FST_BWD_ALL, *dims, *bargs), "bwd")
     torch.cuda.synchronize(dev)

@@ -81,7 +81,7 @@ SIGNATURES = {
     "fst_backward_workspace_bytes": (_sz, [_i, _i, _i, _i, _i, _i, _i, _i]),
     "fst_backward": (
         _i,
-        [_i, _i, _i, _i, _i, _i, _i, _i, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _f,
+        [_i, _i, _i, _i, _i, _i, _i, _i, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _f,
          _vp, _vp, _vp, _vp, _vp, _vp, _vp, _sz, _vp],
     ),
     "fst_forward_phases": (
@@ -90,7 +90,7 @@ SIGNATURES = {
     ),
     "fst_backward_phases": (
         _i,
-        [_i, _i, _i, _i, _i, _i, _i, _i, _i, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _f,
+        [_i, _i, _i, _i, _i, _i, _i, _i, _i, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _f,
          _vp, _vp, _vp, _vp, _vp, _vp, _vp, _sz, _vp],
     ),
     "fst_max_event_len": (_i, [_i, _i, _i, _i, _i]),

@@ -26,12 +26,15 @@ def _same_layout(a: Tensor, b: Tensor) -> bool:
 
 def _run_backward(dims, q, k, v, pos4, w32, b32, lens, lse, grad_out, scale, vec_shape,
                   rowsum: Optional[Tensor] = None, out_like: Optional[Tensor] = None,
-                  grads: Optional[Tuple[Tensor, Tensor, Tensor]] = None):
+                  grads: Optional[Tuple[Tensor, Tensor, Tensor]] = None, out: Optional[Tensor] = None):
     """Launch the backward. grad_out is brought into the layout of `out_like`
     (default q: contiguous, or token-major when the flags say so; empty_like
     keeps a dense view's strides); dq, dk, dv are written into `grads` when
     given (the slots of one interleaved gradient tensor), else into tensors
-    laid out like q, k, v."""
+    laid out like q, k, v. `out`, the forward's output, is handed to the
+    kernels where it has grad_out's final shape, dtype and layout (the bf16
+    rows kernel takes its reference D from it); otherwise it is left out,
+    which changes nothing but the kernel's schedule of D updates."""
     if grad_out.shape != q.shape:
         raise ValueError(f"grad_out must have the shape of the output {tuple(q.shape)}")
     interleaved = bool(dims[1] & _lib.FST_QKV_INTERLEAVED)
@@ -51,11 +54,14 @@ def _run_backward(dims, q, k, v, pos4, w32, b32, lens, lse, grad_out, scale, vec
     groups = head_groups(dims[0], dims[3], dims[6], dims[7])
     if len(groups) > 1:
         return _run_backward_grouped(groups, dims, q, k, v, pos4, w32, b32, lens, lse, grad_out, scale,
-                                     rowsum, grads)
+                                     rowsum, grads, out)
     like = q if out_like is None else out_like
     do = grad_out.to(q.dtype)
     if not _same_layout(do, like):
         do = torch.empty_like(like).copy_(do)
+    if out is not None and not (out.shape == do.shape and out.dtype == do.dtype and out.device == do.device
+                                and _same_layout(out, do)):
+        out = None
     if grads is not None:
         dq, dk, dv = grads
     else:
@@ -77,7 +83,7 @@ def _run_backward(dims, q, k, v, pos4, w32, b32, lens, lse, grad_out, scale, vec
         return lib.fst_backward_phases(
             phases, dims[0], flags, *dims[2:],
             _lib.ptr(q), _lib.ptr(k), _lib.ptr(v), _lib.ptr(pos4), _lib.ptr(w32), _lib.ptr(b32),
-            _lib.ptr(lens), _lib.ptr(lse), _lib.ptr(do), scale,
+            _lib.ptr(lens), _lib.ptr(lse), _lib.ptr(do), _lib.ptr(out), scale,
             _lib.ptr(dq), _lib.ptr(dk), _lib.ptr(dv), _lib.ptr(dw), _lib.ptr(db), _lib.ptr(rs),
             _lib.ptr(ws), ws_bytes, _lib.stream_handle(q.device),
         )
@@ -91,7 +97,8 @@ def _run_backward(dims, q, k, v, pos4, w32, b32, lens, lse, grad_out, scale, vec
     return dq, dk, dv, dw, db
 
 
-def _run_backward_grouped(groups, dims, q, k, v, pos4, w32, b32, lens, lse, grad_out, scale, rowsum, grads):
+def _run_backward_grouped(groups, dims, q, k, v, pos4, w32, b32, lens, lse, grad_out, scale, rowsum, grads,
+                          out=None):
     """The backward one head group at a time (head_groups): each group's
     operands as contiguous tensors, its gradients copied into the full ones,
     dW and db summed over the groups in order."""
@@ -109,7 +116,8 @@ def _run_backward_grouped(groups, dims, q, k, v, pos4, w32, b32, lens, lse, grad
         rs_g = torch.empty_like(lse_g) if rowsum is not None else None
         sub = (dims[0], flags, dims[2], h1 - h0) + tuple(dims[4:])
         g_dq, g_dk, g_dv, g_dw, g_db = _run_backward(sub, part(q), part(k), part(v), pos4, w32, b32, lens,
-                                                     lse_g, part(do), scale, tuple(lse_g.shape), rowsum=rs_g)
+                                                     lse_g, part(do), scale, tuple(lse_g.shape), rowsum=rs_g,
+                                                     out=None if out is None else part(out))
         dq[:, h0:h1].copy_(g_dq)
         dk[:, h0:h1].copy_(g_dk)
         dv[:, h0:h1].copy_(g_dv)
@@ -140,6 +148,7 @@ def flash_spacetime_backward(
     num_stages: Optional[int] = None,
     cu_seqlens: Optional[Tensor] = None,
     rowsum: Optional[Tensor] = None,
+    out: Optional[Tensor] = None,
 ) -> Tuple[Tensor, Tensor, Tensor, Tensor, Optional[Tensor]]:
     """Deterministic backward from the saved lse; returns (dq, dk, dv, dW, db).
 
@@ -153,20 +162,24 @@ def flash_spacetime_backward(
     each the nearest offered value; None (the default here; the reference
     defaults to 16, 16, 8) keeps the library's tuned or static choice, and
     num_stages is accepted with no counterpart (loads run one chunk ahead).
+    `out` (optional, no reference counterpart) is the forward's output: with
+    it the bf16 rows kernel forms dS against a reference D taken from it and
+    corrects to its own D = sum P dP / sum P once, after the last key chunk;
+    the gradients agree with those without it up to rounding.
     """
     del num_stages
     if q.dtype == torch.float16:  # the bf16 path, as the forward launcher runs it
         dq, dk, dv, dw, db = flash_spacetime_backward(
             *_bf16(q, k, v), feats, weight, bias, seqlens, lse, grad_out.to(torch.bfloat16), scale,
             use_attn_bias, use_activation_bias, block_m=block_m, block_n=block_n, num_warps=num_warps,
-            cu_seqlens=cu_seqlens, rowsum=rowsum)
+            cu_seqlens=cu_seqlens, rowsum=rowsum, out=None if out is None else out.to(torch.bfloat16))
         return dq.to(q.dtype), dk.to(q.dtype), dv.to(q.dtype), dw, db
     prep = _Prepared(q, k, v, feats, weight, bias, seqlens, scale, use_attn_bias,
                      use_activation_bias, cu_seqlens)
     with tune.tile_request(block_m, block_n, num_warps):
         dq, dk, dv, dw, db = _run_backward(
             prep.dims(), prep.q, prep.k, prep.v, prep.pos4, prep.weight, prep.bias, prep.lens,
-            _vec_in_layout(lse, prep.token_major), grad_out, prep.scale, prep.vec_shape(), rowsum,
+            _vec_in_layout(lse, prep.token_major), grad_out, prep.scale, prep.vec_shape(), rowsum, out=out,
         )
     return (
         dq,

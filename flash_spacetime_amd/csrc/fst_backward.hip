@@ -338,13 +338,16 @@ __global__ __launch_bounds__(64 * (NW > 4 ? NW : 4), 1) void bwd_rows_kernel(Bwd
         float dD = 0.f;
         if constexpr (PASSES == 2) {
           if (pass == 0) {  // the first pass forms N and Z only
-            nsum[hl] += group_allsum(nt);
-            zsum[hl] += group_allsum(zt);
+            group_allsum2(nt, zt);
+            nsum[hl] += nt;
+            zsum[hl] += zt;
             continue;
           }
         } else {
-          nsum[hl] += group_allsum(nt);
-          zsum[hl] += group_allsum(zt);
+          float ns = nt, zs = zt;  // zt stays this lane's part
+          group_allsum2(ns, zs);
+          nsum[hl] += ns;
+          zsum[hl] += zs;
           const float dn = zsum[hl] > 0.f ? nsum[hl] / zsum[hl] : 0.f;
           dD = dn - dval[hl];
           dval[hl] = dn;

@@ -99,7 +99,7 @@ struct Rows2Cfg {
                                (!KL || (D % 32 == 0 && KC == 16 && LDS_BYTES + KV_BYTES <= LDS_CAP));
 };
 
-template <int HP, int D, int C, int KC, int HB, int FL, int NW, int WPE, bool KLV>
+template <int HP, int D, int C, int KC, int HB, int FL, int NW, int WPE, bool KLV, bool ORF>
 __global__ __launch_bounds__(64 * NW, WPE) void bwd_rows2_kernel(BwdParams prm) {
   using Cfg = Rows2Cfg<HP, D, C, KC, NW, WPE, KLV>;
   using ET = ETile<C, KC>;
@@ -169,9 +169,11 @@ __global__ __launch_bounds__(64 * NW, WPE) void bwd_rows2_kernel(BwdParams prm) 
   // ---- head-owner state (lane n = row i0 + n) ----
   const int my_row = i0 + n;
   const bool row_ok = my_row < len;
-  KFrag<bf16, D> qf[HW], dof[HW];
+  KFrag<bf16, D> qf[HW], dof[HW], of[ORF ? HW : 1];
   f32x4 dQ[HW][NQ], A2[HW][NQ];
-  float lse2[HW], Nn[HW], Zz[HW], Dc[HW];  // Dc: the running D - dob
+  // Dc: D - dob, the running value (ORF: the reference value until the end).
+  // ORF: Nn, Zz hold this lane's parts until the end.
+  float lse2[HW], Nn[HW], Zz[HW], Dc[HW];
   // Loads from a clamped row and head, without branches, so that no load
   // waits for the one before it; invalid rows and heads are zeroed below.
   const int rc = row_ok ? my_row : last;
@@ -180,6 +182,7 @@ __global__ __launch_bounds__(64 * NW, WPE) void bwd_rows2_kernel(BwdParams prm) 
     const int hc = min(head(hl), H - 1);
     qf[hl].load(qg + rx.off(hc, rc, D), g);
     dof[hl].load(dog + ra.off(hc, rc, D), g);
+    if constexpr (ORF) of[hl].load(reinterpret_cast<const bf16*>(prm.out) + ra.off(hc, rc, D), g);
     lse2[hl] = prm.lse[ra.vec(hc, rc)];
   }
 
@@ -293,6 +296,14 @@ __global__ __launch_bounds__(64 * NW, WPE) void bwd_rows2_kernel(BwdParams prm) 
       for (int t = 0; t < KFrag<bf16, D>::N16; ++t) *reinterpret_cast<bf16x4*>(qd + 16 * t + 4 * g) = qf[hl].x16[t];
     }
     Nn[hl] = Zz[hl] = Dc[hl] = 0.f;
+    if constexpr (ORF) {
+      // The reference D - dob from the forward's output: dO . (out - [V] b),
+      // the same sum over the keys up to the output's rounding. dS is formed
+      // against it and the accumulators are corrected to N / Z once, after
+      // the last chunk.
+      const float part = ok ? dof[hl].dot_minus(of[hl], act ? prm.bias : nullptr, g) : 0.f;
+      Dc[hl] = group_allsum(part);
+    }
 #pragma unroll
     for (int q = 0; q < NQ; ++q) dQ[hl][q] = A2[hl][q] = zero4();
   }
@@ -334,6 +345,10 @@ __global__ __launch_bounds__(64 * NW, WPE) void bwd_rows2_kernel(BwdParams prm) 
 #pragma unroll
       for (int s = 0; s < NS; ++s) group_gather(pair_angle_unit(pos_i, pj[s]), xg[s]);
       if constexpr (!KL) issue_pos(j0 + KC);
+      // Each (row, subtile)'s u.E and w~.E are stored after the next one's
+      // embedding is formed, which covers the products' latency.
+      f32x4 ue_p = zero4(), we_p = zero4();
+      int so_p = 0;
 #pragma unroll
       for (int r = 0; r < RPW; ++r)
 #pragma unroll
@@ -344,21 +359,25 @@ __global__ __launch_bounds__(64 * NW, WPE) void bwd_rows2_kernel(BwdParams prm) 
             ef[ct] = embed_step<C>(xg[s][r], fa[ct], fb[ct], ct);
             ET::store(Es, row0 + r, ct, 16 * s + n, g, ef[ct]);
           }
+          if (r + s > 0) {
+            if (attn) *reinterpret_cast<f32x4*>(stU + so_p) = ue_p;
+            if (act) *reinterpret_cast<f32x4*>(stW + so_p) = we_p;
+          }
           // Lanes of heads past HP fill padding slots nobody reads.
-          const int so = stage_off(4 * s + g, row0 + r, n);
+          so_p = stage_off(4 * s + g, row0 + r, n);
           if (attn) {
-            f32x4 ue = zero4();
+            ue_p = zero4();
 #pragma unroll
-            for (int ct = 0; ct < NCT; ++ct) ue = mfma_x16(ef[ct], uf[r][ct], ue);
-            *reinterpret_cast<f32x4*>(stU + so) = ue;
+            for (int ct = 0; ct < NCT; ++ct) ue_p = mfma_x16(ef[ct], uf[r][ct], ue_p);
           }
           if (act) {
-            f32x4 we = zero4();
+            we_p = zero4();
 #pragma unroll
-            for (int ct = 0; ct < NCT; ++ct) we = mfma_x16(ef[ct], wf[r][ct], we);
-            *reinterpret_cast<f32x4*>(stW + so) = we;
+            for (int ct = 0; ct < NCT; ++ct) we_p = mfma_x16(ef[ct], wf[r][ct], we_p);
           }
         }
+      if (attn) *reinterpret_cast<f32x4*>(stU + so_p) = ue_p;
+      if (act) *reinterpret_cast<f32x4*>(stW + so_p) = we_p;
     }
     __syncthreads();  // u.E, w~.E staged
 
@@ -403,7 +422,7 @@ __global__ __launch_bounds__(64 * NW, WPE) void bwd_rows2_kernel(BwdParams prm) 
 #pragma unroll
       for (int b = 0; b < NB; ++b) {
         const int hl = hb + b < HW ? hb + b : HW - 1;
-        float a = -0.f, z = -0.f;
+        float a = ORF ? Nn[hl] : -0.f, z = ORF ? Zz[hl] : -0.f;
 #pragma unroll
         for (int s = 0; s < NS; ++s)
 #pragma unroll
@@ -422,11 +441,18 @@ __global__ __launch_bounds__(64 * NW, WPE) void bwd_rows2_kernel(BwdParams prm) 
       for (int b = 0; b < NB; ++b) {
         const int hl = hb + b;
         if (hl >= nh) continue;
-        Nn[hl] += group_allsum(nt[b]);
-        Zz[hl] += group_allsum(zt[b]);
-        const float dn = Zz[hl] > 0.f ? Nn[hl] * __builtin_amdgcn_rcpf(Zz[hl]) : 0.f;
-        dD[b] = dn - Dc[hl];
-        Dc[hl] = dn;
+        if constexpr (ORF) {
+          Nn[hl] = nt[b];
+          Zz[hl] = zt[b];
+          dD[b] = 0.f;
+        } else {
+          group_allsum2(nt[b], zt[b]);
+          Nn[hl] += nt[b];
+          Zz[hl] += zt[b];
+          const float dn = Zz[hl] > 0.f ? Nn[hl] * __builtin_amdgcn_rcpf(Zz[hl]) : 0.f;
+          dD[b] = dn - Dc[hl];
+          Dc[hl] = dn;
+        }
       }
       JFrag<bf16, NS> pf[NB], dsf[NB];
 #pragma unroll
@@ -453,7 +479,7 @@ __global__ __launch_bounds__(64 * NW, WPE) void bwd_rows2_kernel(BwdParams prm) 
             kt.v = cat8(transpose_x16(DT::part(kf[hl][0], q), id), transpose_x16(DT::part(kf[hl][1], q), id));
           else
             kt.v = transpose_x16(DT::part(kf[hl][0], q), id);
-          dQ[hl][q] = dQ[hl][q] - dD[b] * A2[hl][q];
+          if constexpr (!ORF) dQ[hl][q] = dQ[hl][q] - dD[b] * A2[hl][q];
           A2[hl][q] = mma_j(kt, pf[b], A2[hl][q]);
           dQ[hl][q] = mma_j(kt, dsf[b], dQ[hl][q]);
         }
@@ -478,7 +504,7 @@ __global__ __launch_bounds__(64 * NW, WPE) void bwd_rows2_kernel(BwdParams prm) 
             *reinterpret_cast<bf16x4*>(stU + so) = pv;
             *reinterpret_cast<bf16x4*>(stW + so) = dv;
           }
-          *reinterpret_cast<float*>(scal + scal_off(n, h)) = dD[b];  // the same value from every lane group
+          if constexpr (!ORF) *reinterpret_cast<float*>(scal + scal_off(n, h)) = dD[b];  // the same value from every lane group
         }
       }
     }
@@ -498,7 +524,7 @@ __global__ __launch_bounds__(64 * NW, WPE) void bwd_rows2_kernel(BwdParams prm) 
         // Lanes of padded heads (n >= H) read some other slot of the row:
         // finite values whose columns of H and G are never used.
         const int hn = n < HP ? n : HP - 1;
-        const float dd = *reinterpret_cast<const float*>(scal + scal_off(il, n));
+        const float dd = ORF ? 0.f : *reinterpret_cast<const float*>(scal + scal_off(il, n));
         JFrag<bf16, NS> pr, dr;
 #pragma unroll
         for (int s = 0; s < NS; ++s) {
@@ -519,7 +545,7 @@ __global__ __launch_bounds__(64 * NW, WPE) void bwd_rows2_kernel(BwdParams prm) 
           else
             et.v = ET::load_tr(Es, il, ct, 0, g, n);
           if (attn) {
-            Hacc[r][ct] = Hacc[r][ct] - dd * Gacc[r][ct];
+            if constexpr (!ORF) Hacc[r][ct] = Hacc[r][ct] - dd * Gacc[r][ct];
             Hacc[r][ct] = mma_j(et, dr, Hacc[r][ct]);
           }
           Gacc[r][ct] = mma_j(et, pr, Gacc[r][ct]);
@@ -535,6 +561,33 @@ __global__ __launch_bounds__(64 * NW, WPE) void bwd_rows2_kernel(BwdParams prm) 
   // KL: the loads of the chunk past the last finish before the workgroup
   // ends.
   if constexpr (KL) wait_vmem();
+
+  if constexpr (ORF) {
+    // D = N / Z over all keys; dQ and H, built against the reference value,
+    // take the P sums they lack: dQ -= (D - Dref) sum P k, H -= (D - Dref) G.
+    float dD[HW];
+#pragma unroll
+    for (int hl = 0; hl < HW; ++hl) {
+      group_allsum2(Nn[hl], Zz[hl]);
+      const float dn = Zz[hl] > 0.f ? Nn[hl] * __builtin_amdgcn_rcpf(Zz[hl]) : 0.f;
+      dD[hl] = dn - Dc[hl];
+      Dc[hl] = dn;
+#pragma unroll
+      for (int q = 0; q < NQ; ++q) dQ[hl][q] = dQ[hl][q] - dD[hl] * A2[hl][q];
+    }
+    if (use_e && attn) {
+#pragma unroll
+      for (int hl = 0; hl < HW; ++hl)
+        if (hl < nh) *reinterpret_cast<float*>(scal + scal_off(n, head(hl))) = dD[hl];
+      __syncthreads();
+#pragma unroll
+      for (int r = 0; r < RPW; ++r) {
+        const float dd = *reinterpret_cast<const float*>(scal + scal_off(row0 + r, n));
+#pragma unroll
+        for (int ct = 0; ct < NCT; ++ct) Hacc[r][ct] = Hacc[r][ct] - dd * Gacc[r][ct];
+      }
+    }
+  }
 
   // ---- epilogue: sigma, D, dq = scale (dQ + W H + sigma b) ----
   // W (d on the lanes, the slots of H on the k index) as bf16 parts, and b,
@@ -1139,8 +1192,13 @@ int bwd2_launch_rows(const BwdParams& prm, hipStream_t stream, int g8, bool quer
     return FST_EUNSUPPORTED;
   } else {
     if (query) return FST_OK;
-    auto kern = (prm.flags & 3) == 3 ? bwd_rows2_kernel<HP, D, C, P::KC, P::HB, 3, NW, WPE, KL>
-                                     : bwd_rows2_kernel<HP, D, C, P::KC, P::HB, -1, NW, WPE, KL>;
+    // With the forward's output the rows kernel forms dS against a reference
+    // D from it and corrects once at the end; without, D is formed online.
+    const bool fb = (prm.flags & 3) == 3;
+    auto kern = prm.out ? (fb ? bwd_rows2_kernel<HP, D, C, P::KC, P::HB, 3, NW, WPE, KL, true>
+                              : bwd_rows2_kernel<HP, D, C, P::KC, P::HB, -1, NW, WPE, KL, true>)
+                        : (fb ? bwd_rows2_kernel<HP, D, C, P::KC, P::HB, 3, NW, WPE, KL, false>
+                              : bwd_rows2_kernel<HP, D, C, P::KC, P::HB, -1, NW, WPE, KL, false>);
     if (hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, Cfg::LDS_BYTES) !=
         hipSuccess)
       return FST_ELAUNCH;

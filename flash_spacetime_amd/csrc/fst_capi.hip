@@ -693,8 +693,8 @@ size_t fst_backward_workspace_bytes(int dtype, int flags, int B, int H, int L, i
 
 int fst_backward_phases(int phases, int dtype, int flags, int B, int H, int L, int T, int D, int C, const void* q,
                         const void* k, const void* v, const float* pos4, const float* weight, const float* bias,
-                        const int32_t* lens, const float* lse, const void* grad_out, float scale, void* dq, void* dk,
-                        void* dv, float* dweight, float* dbias, float* rowsum, void* workspace,
+                        const int32_t* lens, const float* lse, const void* grad_out, const void* out, float scale,
+                        void* dq, void* dk, void* dv, float* dweight, float* dbias, float* rowsum, void* workspace,
                         size_t workspace_bytes, void* stream) {
   g_last_error[0] = 0;
   if (phases & ~FST_BWD_ALL) return fail(FST_EINVAL, "unknown backward phase bits 0x%x", phases);
@@ -757,6 +757,7 @@ int fst_backward_phases(int phases, int dtype, int flags, int B, int H, int L, i
   prm.k = k;
   prm.v = v;
   prm.dout = grad_out;
+  prm.out = dtype == FST_BF16 ? out : nullptr;
   prm.weight = weight;
   prm.bias = bias;
   prm.lse = lse;
@@ -802,10 +803,11 @@ int fst_backward_phases(int phases, int dtype, int flags, int B, int H, int L, i
 
 int fst_backward(int dtype, int flags, int B, int H, int L, int T, int D, int C, const void* q, const void* k,
                  const void* v, const float* pos4, const float* weight, const float* bias, const int32_t* lens,
-                 const float* lse, const void* grad_out, float scale, void* dq, void* dk, void* dv, float* dweight,
-                 float* dbias, float* rowsum, void* workspace, size_t workspace_bytes, void* stream) {
+                 const float* lse, const void* grad_out, const void* out, float scale, void* dq, void* dk, void* dv,
+                 float* dweight, float* dbias, float* rowsum, void* workspace, size_t workspace_bytes, void* stream) {
   return fst_backward_phases(FST_BWD_ALL, dtype, flags, B, H, L, T, D, C, q, k, v, pos4, weight, bias, lens, lse,
-                             grad_out, scale, dq, dk, dv, dweight, dbias, rowsum, workspace, workspace_bytes, stream);
+                             grad_out, out, scale, dq, dk, dv, dweight, dbias, rowsum, workspace, workspace_bytes,
+                             stream);
 }
 
 }  // extern "C"

@@ -98,6 +98,22 @@ __device__ __forceinline__ float group_allsum(float x) {
   return __uint_as_float(b[0]) + __uint_as_float(b[1]);
 }
 
+// Two sums at once, with the additions of group_allsum in the same order:
+// the first swap gives lanes 0-31 the half sums of x and lanes 32-63 those of
+// y, the second completes both, and a last swap hands each value to every
+// lane (three swaps where two group_allsum calls take four and two copies).
+__device__ __forceinline__ void group_allsum2(float& x, float& y) {
+  auto a = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(y), false, false);
+  const float c = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+  const unsigned uc = __float_as_uint(c);
+  auto b = __builtin_amdgcn_permlane16_swap(uc, uc, false, false);
+  const float e = __uint_as_float(b[0]) + __uint_as_float(b[1]);
+  const unsigned ue = __float_as_uint(e);
+  auto d = __builtin_amdgcn_permlane32_swap(ue, ue, false, false);
+  x = __uint_as_float(d[0]);
+  y = __uint_as_float(d[1]);
+}
+
 // Orders this wave's LDS accesses: everything issued before completes
 // before anything after is issued (LDS executes a wave's requests in order).
 __device__ __forceinline__ void wave_lds_sync() {
@@ -162,6 +178,21 @@ struct KFrag<bf16, K> {
   __device__ __forceinline__ void load_scaled(const bf16* p, int g, float scale) {
     load(p, g);
     scale_by(scale);
+  }
+  // This lane's part of sum_k x_k (o_k - b_k) over the row (b nullable).
+  __device__ __forceinline__ float dot_minus(const KFrag& o, const float* b, int g) const {
+    float a = 0.f;
+#pragma unroll
+    for (int t = 0; t < N32; ++t)
+#pragma unroll
+      for (int e = 0; e < 8; ++e)
+        a = __builtin_fmaf((float)x32[t][e], (float)o.x32[t][e] - (b ? b[32 * t + 8 * g + e] : 0.f), a);
+#pragma unroll
+    for (int t = 0; t < N16; ++t)
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        a = __builtin_fmaf((float)x16[t][e], (float)o.x16[t][e] - (b ? b[16 * t + 4 * g + e] : 0.f), a);
+    return a;
   }
 };
 

@@ -162,6 +162,7 @@ struct BwdParams {
   const float* weight;  // [D, C]
   const float* bias;    // [D] or null
   const float* lse;     // [rows]
+  const void* out;      // the forward's output, laid out as dout (nullable; bf16 rows kernel)
   // scratch written by the rows kernel, read by the cols kernel
   void* u;              // [rows, C] T
   void* wt;             // [rows, C] T

@@ -328,6 +328,24 @@ def flash_spacetime_forward(
         return _run_forward(prep)
 
 
+def _keep_output(ctx: Any, out: Tensor) -> None:
+    """Keep a detached alias of the forward's output and its version for the
+    backward, which hands it to the bf16 rows kernel as the source of its
+    reference D (the output is usually alive anyway: it is the op's result).
+    A detached alias holds no graph, so no reference cycle forms."""
+    ctx.out_alias = out.detach()
+    ctx.out_version = out._version
+
+
+def _kept_output(ctx: Any) -> Optional[Tensor]:
+    """The kept output, unless it was modified in place after the forward
+    (then the kernel forms D online instead; either way D is its own)."""
+    alias = getattr(ctx, "out_alias", None)
+    if alias is None or alias._version != ctx.out_version:
+        return None
+    return alias
+
+
 class _FlashSpacetimeAttention(torch.autograd.Function):
     """Fused forward and deterministic HIP backward (forward.py:349-478)."""
 
@@ -351,9 +369,10 @@ class _FlashSpacetimeAttention(torch.autograd.Function):
         prep = _Prepared(q, k, v, feats, weight, bias, seqlens, scale, use_attn_bias,
                          use_activation_bias, cu_seqlens)
         out, lse = _run_forward(prep)
-        # Only inputs and the LSE are kept: the backward forms its own softmax
-        # row sums and never needs the output (forward.py:381-388).
+        # The inputs and the LSE are saved as the reference saves them
+        # (forward.py:381-388); the backward forms its own softmax row sums.
         ctx.save_for_backward(prep.q, prep.k, prep.v, prep.pos4, prep.lens, lse)
+        _keep_output(ctx, out)
         ctx.prep_meta = (prep.weight, prep.bias, weight.dtype,
                          None if bias is None else bias.dtype)
         ctx.dims = prep.dims()
@@ -375,7 +394,8 @@ class _FlashSpacetimeAttention(torch.autograd.Function):
         q, k, v, pos4, lens, lse = ctx.saved_tensors
         w32, b32, w_dtype, b_dtype = ctx.prep_meta
         dq, dk, dv, dw, db = _run_backward(
-            ctx.dims, q, k, v, pos4, w32, b32, lens, lse, grad_out, ctx.scale, ctx.vec_shape
+            ctx.dims, q, k, v, pos4, w32, b32, lens, lse, grad_out, ctx.scale, ctx.vec_shape,
+            out=_kept_output(ctx),
         )
         use_attn_bias, use_activation_bias = ctx.flags
         proj_used = use_attn_bias or use_activation_bias
@@ -541,6 +561,7 @@ class _FlashSpacetimeAttentionQKV(torch.autograd.Function):
                          use_activation_bias, cu_seqlens, interleaved=True)
         out, lse = _run_forward(prep)
         ctx.save_for_backward(qkv, prep.pos4, prep.lens, lse)
+        _keep_output(ctx, out)
         ctx.prep_meta = (prep.weight, prep.bias, weight.dtype, None if bias is None else bias.dtype)
         ctx.dims = prep.dims()
         ctx.scale = prep.scale
@@ -565,7 +586,7 @@ class _FlashSpacetimeAttentionQKV(torch.autograd.Function):
             like = torch.empty(b, length, h, d, device=qkv.device, dtype=qkv.dtype).transpose(1, 2)
         _, _, _, dw, db = _run_backward(
             ctx.dims, q, k, v, pos4, w32, b32, lens, lse, g, ctx.scale, ctx.vec_shape,
-            out_like=like, grads=_qkv_views(dqkv, ctx.packed),
+            out_like=like, grads=_qkv_views(dqkv, ctx.packed), out=_kept_output(ctx),
         )
         use_attn_bias, use_activation_bias = ctx.flags
         proj_used = use_attn_bias or use_activation_bias

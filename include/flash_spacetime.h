@@ -215,14 +215,21 @@ size_t fst_backward_workspace_bytes(int dtype, int flags, int B, int H, int L, i
  * dweight [D, C] and, when bias != NULL, dbias [D] (all float32 for the
  * weight-side). rowsum (nullable, float32 like lse) receives sum_j dS_ij,
  * which the normalised softmax row term makes zero up to rounding.
+ * out (nullable) is the forward's output, laid out as grad_out. With bf16
+ * operands the rows kernel then forms dS against a reference D taken from it
+ * (dO . (out - b), b with FST_ACT_BIAS) and corrects its sums to the
+ * in-kernel D = sum P dP / sum P once, after its last key chunk, instead of
+ * after every chunk; D itself, and so every gradient up to rounding, is the
+ * same either way. Ignored for float32.
  * Replaces flash_spacetime_backward (reference backward.py:488-630): the
  * host prologue (:526-556), both Triton kernels (:589-598) and the host
- * epilogue (:600-630). */
+ * epilogue (:600-630); `out` has no counterpart there (the reference's
+ * launcher does not take the output). */
 int fst_backward(int dtype, int flags, int B, int H, int L, int T, int D, int C,
                  const void* q, const void* k, const void* v, const float* pos4,
                  const float* weight, const float* bias, const int32_t* lens,
-                 const float* lse, const void* grad_out, float scale, void* dq,
-                 void* dk, void* dv, float* dweight, float* dbias, float* rowsum,
+                 const float* lse, const void* grad_out, const void* out, float scale,
+                 void* dq, void* dk, void* dv, float* dweight, float* dbias, float* rowsum,
                  void* workspace, size_t workspace_bytes, void* stream);
 
 /* fst_backward restricted to the given phases (FST_PHASE_WORKLIST,
@@ -234,7 +241,7 @@ int fst_backward_phases(int phases, int dtype, int flags, int B, int H, int L, i
                         int C, const void* q, const void* k, const void* v,
                         const float* pos4, const float* weight, const float* bias,
                         const int32_t* lens, const float* lse, const void* grad_out,
-                        float scale, void* dq, void* dk, void* dv, float* dweight,
+                        const void* out, float scale, void* dq, void* dk, void* dv, float* dweight,
                         float* dbias, float* rowsum, void* workspace,
                         size_t workspace_bytes, void* stream);
 

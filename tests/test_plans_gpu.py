@@ -80,12 +80,13 @@ def _inputs(dtype, heads, dim, chans, lens, packed, seed):
     return q, k, v, do, feats, w, b, sl, cu
 
 
-def _run(args, flags):
+def _run(args, flags, with_out=False):
     q, k, v, do, feats, w, b, sl, cu = (x.to(DEV) if x is not None else None for x in args)
     kw = dict(use_attn_bias=flags[0], use_activation_bias=flags[1], cu_seqlens=cu)
     out, lse = flash_spacetime_forward(q, k, v, feats, w, b, sl, **kw)
     rowsum = torch.zeros_like(lse)
-    grads = flash_spacetime_backward(q, k, v, feats, w, b, sl, lse, do, rowsum=rowsum, **kw)
+    grads = flash_spacetime_backward(q, k, v, feats, w, b, sl, lse, do, rowsum=rowsum,
+                                     out=out if with_out else None, **kw)
     torch.cuda.synchronize()
     return out, lse, rowsum, grads
 
@@ -121,16 +122,21 @@ def _same(got, base):
     return all(r is None or rel_err(g, r) <= 1e-5 for g, r in zip(got[3][3:], base[3][3:]))
 
 
+@pytest.mark.parametrize("with_out", [False, True], ids=["online_d", "reference_d"])
 @pytest.mark.parametrize("case", range(len(SHAPES)))
-def test_every_plan_matches_the_static_plan(case):
+def test_every_plan_matches_the_static_plan(case, with_out):
     """Fully specified plans (one bit in every offered group) of one kernel
     family, classed by their key-chunk bits: plans of one class agree bit for
     bit, each class is within the dtype's tolerance of the float64 oracle,
-    and the static plan is bit for bit one of the classes."""
+    and the static plan is bit for bit one of the classes. with_out: the
+    backward is given the forward's output (the bf16 rows kernel's
+    reference D; float32 ignores it)."""
     dtype, heads, dim, chans, lens, packed, flags = SHAPES[case]
+    if with_out and dtype == F32:
+        pytest.skip("float32 kernels do not read the output")
     args = _inputs(dtype, heads, dim, chans, lens, packed, 100 + case)
     tune.set_autotune(False)
-    base = _run(args, flags)
+    base = _run(args, flags, with_out)
     ref = _oracle(args, flags, packed)
     valid = None if packed else \
         oracle.valid_row_mask(len(lens), max(lens), torch.tensor(lens))[:, None, :, None].to(DEV)
@@ -139,7 +145,7 @@ def test_every_plan_matches_the_static_plan(case):
         for plan in _full_combos(dtype, heads, dim, chans, groups):
             print(f"plan {tune.plan_names(plan)}", flush=True)
             with tune.fixed_plan(plan):
-                got = _run(args, flags)
+                got = _run(args, flags, with_out)
             kc = plan & KC_BITS
             if kc in classes:
                 assert _same(got, classes[kc][1]), f"{tune.plan_names(plan)} vs {tune.plan_names(classes[kc][0])}"

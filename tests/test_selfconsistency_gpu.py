@@ -21,8 +21,10 @@ size bounds |sum_j dS_ij| as the products saw it.
 
 Bound. With bf16 round-to-nearest (unit roundoff 2^-8), each dS value fed
 to a product is P_j (dP_j - D_c) with D_c the row term at the time (a
-P-weighted mean of dP over a subset of the keys, so within [min dP, max dP])
-and each correction uses bf16 P_j; the final D lies in the same range. So
+P-weighted mean of dP over a subset of the keys, so within [min dP, max dP];
+or, when the forward's output is passed, dO . (out - b), the final D up to
+the output's rounding) and each correction uses bf16 P_j; the final D lies
+in the same range. So
 
     |sigma_i| <= 2^-8 * (A_i + 4 M_i) + fp32 accumulation
     A_i = sum_j P_j |dP_j - D_i|,   M_i = max_j |dP_j - D_i|
@@ -72,11 +74,14 @@ def _constant_key_inputs(batch, length, heads, dim, chans, lens, seed, qk_scale)
     return q, k, v, feats, w, b, torch.tensor(lens, dtype=torch.int32), do
 
 
-def _check(batch, length, heads, dim, chans, lens, seed, qk_scale, rows_per_event):
+def _check(batch, length, heads, dim, chans, lens, seed, qk_scale, rows_per_event, with_out):
     q, k, v, feats, w, b, sl, do = _constant_key_inputs(batch, length, heads, dim, chans, lens, seed, qk_scale)
     g = lambda x: x.to(DEV)
     out, lse = flash_spacetime_forward(g(q), g(k), g(v), g(feats), g(w), g(b), g(sl))
-    dq, dk, dv, dw, db = flash_spacetime_backward(g(q), g(k), g(v), g(feats), g(w), g(b), g(sl), lse, g(do))
+    # with_out: the rows kernel's reference D comes from the forward's output
+    # and its sums are corrected once at the end; else D is formed online.
+    dq, dk, dv, dw, db = flash_spacetime_backward(g(q), g(k), g(v), g(feats), g(w), g(b), g(sl), lse, g(do),
+                                                  out=out if with_out else None)
     torch.cuda.synchronize()
     dq = dq.double().cpu()
     assert torch.isfinite(dq).all()
@@ -117,12 +122,17 @@ def _check(batch, length, heads, dim, chans, lens, seed, qk_scale, rows_per_even
           f"/ 7-std bound = {worst_s:.3e}")
 
 
-def test_rowsum_via_dq_cfg2_shape():
+WITH_OUT = pytest.mark.parametrize("with_out", [False, True], ids=["online_d", "reference_d"])
+
+
+@WITH_OUT
+def test_rowsum_via_dq_cfg2_shape(with_out):
     gen = torch.Generator().manual_seed(5)
     lens = torch.randint(16, 769, (256,), generator=gen).tolist()
     lens[0], lens[1] = 768, 16
-    _check(256, 768, 12, 32, 16, lens, 50, 1.0, rows_per_event=8)
+    _check(256, 768, 12, 32, 16, lens, 50, 1.0, rows_per_event=8, with_out=with_out)
 
 
-def test_rowsum_via_dq_cfg4_x30():
-    _check(8, 4096, 8, 64, 64, [4096] * 8, 60, 30.0, rows_per_event=48)
+@WITH_OUT
+def test_rowsum_via_dq_cfg4_x30(with_out):
+    _check(8, 4096, 8, 64, 64, [4096] * 8, 60, 30.0, rows_per_event=48, with_out=with_out)
