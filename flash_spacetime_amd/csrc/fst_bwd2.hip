@@ -21,7 +21,12 @@
 // accumulator equals its value for D = N / Z over all keys, the same N and Z
 // that give sigma = N - D Z; a fully peaked row (all mass on one key) has
 // D_t = dP of that key from its chunk on, so its dS vanishes as in the
-// two-pass form (backward.py:371-407). The row constant dob never enters a
+// two-pass form (backward.py:371-407). Given the forward's output, dS is
+// formed against a fixed reference instead, D_ref = dO . (out - [V] b) (D up
+// to the output's rounding), each lane keeps its part of N and Z, and the
+// correction is made once after the last chunk with D = N / Z: dQ -= (D -
+// D_ref) sum P k, H -= (D - D_ref) G. Either way D is the kernel's own N / Z.
+// The row constant dob never enters a
 // pair: with dP~ = dP - dob, D - dob = sum P dP~ / sum P and dS = P (dP~ -
 // (D - dob)), so the kernel forms D - dob directly. It writes qt, u, w~ and
 // D - dob for the cols kernel and a per-tile dW / db partial.
