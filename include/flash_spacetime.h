@@ -214,7 +214,12 @@ size_t fst_backward_workspace_bytes(int dtype, int flags, int B, int H, int L, i
 /* Deterministic backward from the saved lse. Writes dq, dk, dv (pad rows 0),
  * dweight [D, C] and, when bias != NULL, dbias [D] (all float32 for the
  * weight-side). rowsum (nullable, float32 like lse) receives sum_j dS_ij,
- * which the normalised softmax row term makes zero up to rounding.
+ * which the normalised softmax row term makes zero up to rounding: float32
+ * sums the dS values its products were fed (corrections included); bf16
+ * writes N - D Z from the float32 sums N = sum P dP, Z = sum P that define
+ * D = N / Z, which is zero up to one rounding by construction and so says
+ * nothing about the bf16 dS values (the tests measure those through dq with
+ * every key of an event equal).
  * out (nullable) is the forward's output, laid out as grad_out. With bf16
  * operands the rows kernel then forms dS against a reference D taken from it
  * (dO . (out - b), b with FST_ACT_BIAS) and corrects its sums to the
