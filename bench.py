@@ -114,10 +114,12 @@ def plan_label(plan):
     return tune.plan_names(plan) if plan else "static"
 
 
-def kernel_times(inp, seqlens, iters=10, cu=None, plan=0, flags=(True, True)):
+def kernel_times(inp, seqlens, iters=10, cu=None, plan=0, flags=(True, True), with_out=True):
     """Average duration of each launch, timed with HIP events on the stream the
     library launches on (torch's current stream), one phase at a time, with
-    the FST_PLAN_* bits `plan` (0: the library's static choice)."""
+    the FST_PLAN_* bits `plan` (0: the library's static choice). with_out:
+    the backward is given the forward's output, as the autograd op gives it
+    (its rows kernel's reference D); else it forms D online."""
     from flash_spacetime_amd import _lib
     from flash_spacetime_amd.forward import _Prepared
 
@@ -145,7 +147,8 @@ def kernel_times(inp, seqlens, iters=10, cu=None, plan=0, flags=(True, True)):
     bws = lib.fst_backward_workspace_bytes(*dims)
     bwork = torch.empty(bws, device=dev, dtype=torch.uint8)
     bargs = (P(prep.q), P(prep.k), P(prep.v), P(prep.pos4), P(prep.weight), P(prep.bias), P(prep.lens), P(lse),
-             P(do), P(out), prep.scale, P(dq), P(dk), P(dv), P(dw), P(db), None, P(bwork), bws, sh)
+             P(do), P(out) if with_out else None, prep.scale, P(dq), P(dk), P(dv), P(dw), P(db), None, P(bwork),
+             bws, sh)
     _lib.check(lib.fst_forward_phases(_lib.FST_PHASE_FWD, *dims, *fargs), "fwd")
     _lib.check(lib.fst_backward_phases(_lib.FST_BWD_ALL, *dims, *bargs), "bwd")
     torch.cuda.synchronize(dev)
