@@ -307,7 +307,10 @@ __global__ __launch_bounds__(64 * NW, WPE) void bwd_rows2_kernel(BwdParams prm) 
       // against it and the accumulators are corrected to N / Z once, after
       // the last chunk.
       const float part = ok ? dof[hl].dot_minus(of[hl], act ? prm.bias : nullptr, g) : 0.f;
-      Dc[hl] = group_allsum(part);
+      // Any finite reference gives the same D; a non-finite one (an output
+      // that is not this forward's) falls back to 0.
+      const float dref = group_allsum(part);
+      Dc[hl] = __builtin_isfinite(dref) ? dref : 0.f;
     }
 #pragma unroll
     for (int q = 0; q < NQ; ++q) dQ[hl][q] = A2[hl][q] = zero4();

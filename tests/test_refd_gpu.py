@@ -155,3 +155,26 @@ def test_varlen_autograd_reference_d():
                                        b.double().cpu(), do.double().cpu(), None, cu_seqlens=case["cu"])
     for leaf, e in zip(leaves, ref[:3]):
         assert rel_err(leaf.grad.cpu(), e) <= 2e-2
+
+
+def test_nonfinite_output_is_not_used():
+    """An output with non-finite values (not this forward's) is not a usable
+    reference: the kernel falls back to 0 for it, and the gradients stay
+    finite and within the bf16 tolerance of the float64 ones."""
+    case = make_padded(2, 96, 12, 32, 16, seed=95)
+    for key in ("q", "k", "v"):
+        case[key] = case[key].to(BF).double()
+    q, k, v = (case[x].to(DEV, BF) for x in ("q", "k", "v"))
+    feats, sl = case["feats"].to(DEV), case["seqlens"].to(DEV)
+    w, b = case["weight"].float().to(DEV), case["bias"].float().to(DEV)
+    out, lse = flash_spacetime_forward(q, k, v, feats, w, b, sl)
+    do = torch.randn(q.shape, generator=torch.Generator().manual_seed(8)).to(BF)
+    bad = torch.full_like(out, float("nan"))
+    bad[:, :, 1::2] = float("inf")
+    got = flash_spacetime_backward(q, k, v, feats, w, b, sl, lse, do.to(DEV), out=bad)
+    valid = oracle.valid_row_mask(q.shape[0], q.shape[2], case["seqlens"])[:, None, :, None]
+    ref = oracle.backward_fp64_chunked(case["q"], case["k"], case["v"], case["feats"], w.double().cpu(),
+                                       b.double().cpu(), do.double() * valid, case["seqlens"])
+    for name, a, e in zip(("dq", "dk", "dv", "dW", "db"), got, ref):
+        assert torch.isfinite(a).all(), name
+        assert rel_err(a.cpu(), e) <= 2e-2, name
