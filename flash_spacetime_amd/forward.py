@@ -331,8 +331,10 @@ def flash_spacetime_forward(
 def _keep_output(ctx: Any, out: Tensor) -> None:
     """Keep a detached alias of the forward's output and its version for the
     backward, which hands it to the bf16 rows kernel as the source of its
-    reference D (the output is usually alive anyway: it is the op's result).
-    A detached alias holds no graph, so no reference cycle forms."""
+    reference D (the output is usually alive anyway: it is the op's result;
+    for float16 operands it is the bf16 output the float16 result is
+    converted from, held until the backward). A detached alias holds no
+    graph, so no reference cycle forms."""
     ctx.out_alias = out.detach()
     ctx.out_version = out._version
 
