@@ -20,6 +20,10 @@ with the oracle one at a time (`oracle.event_rows_fp64`):
   whichever is larger (at logits of O(1e4) that evaluation's dq is off by
   ~2e-4);
 
+The whole-batch backwards are given the forward's output (the path the
+autograd op takes) and so are the cfg3 / cfg4 block backwards; the cfg2
+event's dW / db backward is not (D formed online), so both of the rows
+kernel's D schedules are held to the oracle at these sizes;
 plus size-independent properties over the whole batch: finite results,
 padding rows exactly zero, bitwise determinism, the padded result equal to
 the packed one. (The kernel's `rowsum` output is formed from the same fp32
@@ -61,9 +65,14 @@ def _inputs_padded(batch, length, heads, dim, chans, lens, seed, dtype, qk_scale
 
 
 def _fwd_bwd(q, k, v, feats, w, b, seqlens=None, cu=None, do=None):
+    # The backward gets the forward's output, as the autograd op gives it
+    # (the bf16 rows kernel's reference D); so do the second backwards below
+    # where a row's dq is compared bit for bit with this one's, and the cfg2
+    # one runs without it (D formed online).
     out, lse = flash_spacetime_forward(q, k, v, feats, w, b, seqlens, cu_seqlens=cu)
     rowsum = torch.full(lse.shape, float("nan"), device=DEV)
-    grads = flash_spacetime_backward(q, k, v, feats, w, b, seqlens, lse, do, cu_seqlens=cu, rowsum=rowsum)
+    grads = flash_spacetime_backward(q, k, v, feats, w, b, seqlens, lse, do, cu_seqlens=cu, rowsum=rowsum,
+                                     out=out)
     torch.cuda.synchronize()
     return out, lse, grads, rowsum
 
@@ -243,7 +252,7 @@ def test_cfg3_full_size():
         _check_block(q, k, v, feats, w, b, out, grads[0], do, n, rows, packed_tok0=t0)
     do_m = torch.zeros_like(do)
     do_m[t0:t0 + 128] = do[t0:t0 + 128]
-    grads_m = flash_spacetime_backward(q, k, v, feats, w, b, None, lse, do_m, cu_seqlens=cu)
+    grads_m = flash_spacetime_backward(q, k, v, feats, w, b, None, lse, do_m, cu_seqlens=cu, out=out)
     torch.cuda.synchronize()
     _check_masked_grads(q, k, v, feats, w, b, grads_m, do_m, n, (0, 128), packed_tok0=t0)
     # dq of the block does not depend on other rows' dO.
@@ -267,7 +276,7 @@ def test_cfg4_full_size(dtype):
         _check_block(q, k, v, feats, w, b, out, grads[0], do, ev, rows, tol=tol, eager_dtype=eager_dtype)
     do_m = torch.zeros_like(do)
     do_m[3, :, 2048:2176] = do[3, :, 2048:2176]
-    grads_m = flash_spacetime_backward(q, k, v, feats, w, b, sl, lse, do_m)
+    grads_m = flash_spacetime_backward(q, k, v, feats, w, b, sl, lse, do_m, out=out)
     torch.cuda.synchronize()
     _check_masked_grads(q, k, v, feats, w, b, grads_m, do_m, ev, (2048, 2176), tol=tol, eager_dtype=eager_dtype)
     assert torch.equal(grads_m[0][3, :, 2048:2176], grads[0][3, :, 2048:2176])
