@@ -383,6 +383,10 @@ __global__ __launch_bounds__(64 * NW, WPE) void bwd_rows2_kernel(BwdParams prm) 
 #pragma unroll
             for (int ct = 0; ct < NCT; ++ct) we_p = mfma_x16(ef[ct], wf[r][ct], we_p);
           }
+          // One (row, subtile) at a time: left free, the scheduler
+          // interleaves the rows' embeddings and products into an order that
+          // measured 4 % slower (likewise between head batches below).
+          __builtin_amdgcn_sched_barrier(0);
         }
       if (attn) *reinterpret_cast<f32x4*>(stU + so_p) = ue_p;
       if (act) *reinterpret_cast<f32x4*>(stW + so_p) = we_p;
@@ -515,6 +519,7 @@ __global__ __launch_bounds__(64 * NW, WPE) void bwd_rows2_kernel(BwdParams prm) 
           if constexpr (!ORF) *reinterpret_cast<float*>(scal + scal_off(n, h)) = dD[b];  // the same value from every lane group
         }
       }
+      __builtin_amdgcn_sched_barrier(0);
     }
     if constexpr (!KL) issue(j0 + KC);
     __syncthreads();  // P, dS and D increments staged
@@ -1081,6 +1086,9 @@ __global__ __launch_bounds__(256, OCC) void bwd_cols2_kernel(BwdParams prm) {
       }
       pf[hl].from_tiles(S[hl]);
       dsf[hl].from_tiles(dP[hl]);
+      // One head's P and dS at a time (2 % faster than the scheduler's own
+      // interleaving of the heads).
+      __builtin_amdgcn_sched_barrier(0);
     }
 #pragma unroll
     for (int hl = 0; hl < HW; ++hl) {
