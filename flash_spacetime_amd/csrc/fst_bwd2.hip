@@ -1087,10 +1087,11 @@ __global__ __launch_bounds__(256, OCC) void bwd_cols2_kernel(BwdParams prm) {
       pf[hl].from_tiles(S[hl]);
       dsf[hl].from_tiles(dP[hl]);
       // One head's P and dS at a time where a wave owns three heads or more
-      // and D <= 48 (H = 12, D = 32: 2-3 % faster than the scheduler's own
-      // interleaving of the heads; at D = 64 it measured 18-21 % slower, and
-      // 3 % slower at two heads of D = 32).
-      if constexpr (HW >= 3 && D <= 48) __builtin_amdgcn_sched_barrier(0);
+      // and D <= 48, and at D = 48 (H = 12, D = 32: 2-3 % faster than the
+      // scheduler's own interleaving of the heads; H = 8, D = 48: 0-2 %; at
+      // D = 64 it measured 18-21 % slower, and 3 % slower at two heads of
+      // D = 32).
+      if constexpr ((HW >= 3 && D <= 48) || D == 48) __builtin_amdgcn_sched_barrier(0);
     }
 #pragma unroll
     for (int hl = 0; hl < HW; ++hl) {
