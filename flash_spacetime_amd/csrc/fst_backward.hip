@@ -13,7 +13,11 @@
 // Forming D from the very P and dP that build dS makes sigma (the row sum of
 // dS) vanish by construction (backward.py:371-407); normalising by sum P
 // makes it invariant to an O(1) mismatch between the saved LSE and the
-// recomputed logits at large logits.
+// recomputed logits at large logits. The same mismatch scales a row's P by a
+// common factor (the forward's fp32 lse of a logit of O(1e4) is rounded to
+// ~1e-3), which the gradients would carry: the rows kernel divides its
+// accumulators by Z = sum P, and the cols kernel recomputes P / Z with log2 Z
+// (lse_z) subtracted after the exponent's fma, where it is not rounded away.
 //
 // Two kernels, each the single writer of its outputs (no atomics, fixed
 // loop order => bitwise deterministic):
@@ -432,16 +436,38 @@ __global__ __launch_bounds__(64 * (NW > 4 ? NW : 4), 1) void bwd_rows_kernel(Bwd
       for (int hl = 0; hl < HW; ++hl) dval[hl] = zsum[hl] > 0.f ? nsum[hl] / zsum[hl] : 0.f;
     }
   }
+  // P / Z: every accumulator divided by the row's Z (dQ and sigma here, H
+  // and G through the per-tile D slots, free after the key loop).
+  float rz[HW];
 #pragma unroll
   for (int hl = 0; hl < HW; ++hl) {
     const int h = ws * HW + hl;
-    if (g == 0 && h < H && row_ok) prm.dsum[ra.vec(h, my_row)] = dval[hl];
+    rz[hl] = zsum[hl] > 0.f ? 1.f / zsum[hl] : 1.f;
+#pragma unroll
+    for (int dt = 0; dt < D / 16; ++dt) dQ[hl][dt] = dQ[hl][dt] * rz[hl];
+    if (g == 0 && h < H && row_ok) {
+      prm.dsum[ra.vec(h, my_row)] = dval[hl];
+      prm.lse_z[ra.vec(h, my_row)] = zsum[hl] > 0.f ? log2f(zsum[hl]) : 0.f;
+    }
+    if (use_e && g == 0) Dd[h * 16 + n] = rz[hl];
+  }
+  if (use_e) {
+    __syncthreads();
+#pragma unroll
+    for (int ri = 0; ri < RW; ++ri) {
+      const float zr = n < H ? Dd[n * 16 + ws * RW + ri] : 1.f;
+#pragma unroll
+      for (int ct = 0; ct < C / 16; ++ct) {
+        Hacc[ri][ct] = Hacc[ri][ct] * zr;
+        Gacc[ri][ct] = Gacc[ri][ct] * zr;
+      }
+    }
   }
 
   // ---- epilogue: dq = scale (dQ + W H + sigma b) ----
 #pragma unroll
   for (int hl = 0; hl < HW; ++hl) {
-    sig[hl] = group_allsum(sig[hl]);
+    sig[hl] = group_allsum(sig[hl]) * rz[hl];
     const int h = ws * HW + hl;
     if (prm.rowsum && g == 0 && h < H && row_ok) prm.rowsum[ra.vec(h, my_row)] = sig[hl];
   }
@@ -581,7 +607,7 @@ struct BwdColsCfg {
   static constexpr int ESZ = sizeof(T);
   static constexpr int PAD = 16 / ESZ;
   static constexpr int QO_ROW = D + PAD;
-  static constexpr int VEC_BYTES = 3 * HP * KC * 4;                     // lse2, D, dob
+  static constexpr int VEC_BYTES = 4 * HP * KC * 4;                     // lse2, D, dob, log2 Z
   static constexpr int E_ROW = C + PAD;
   static constexpr int E_TILE = KC * 16 * E_ROW * ESZ;                   // [row][key][c]
   static constexpr int UW_ROW = KC + 4;                                 // fp32 rows per (head, key)
@@ -637,7 +663,7 @@ __global__ __launch_bounds__(64 * (NW > 4 ? NW : 4), 1) void bwd_cols_kernel(Bwd
 
   T* Qs = reinterpret_cast<T*>(smem);                 // [HP][KC][QO_ROW] T(q*scale)
   T* Os = Qs + HP * KC * Cfg::QO_ROW;                 // [HP][KC][QO_ROW] dO
-  float* Lv = reinterpret_cast<float*>(smem + Cfg::QO_BYTES);  // [3][HP][KC]
+  float* Lv = reinterpret_cast<float*>(smem + Cfg::QO_BYTES);  // [4][HP][KC]
   unsigned char* tbase = smem + Cfg::QO_BYTES + Cfg::VEC_BYTES + tile * Cfg::TILE_BYTES;
   T* Es = reinterpret_cast<T*>(tbase);                               // [KC][16][E_ROW]
   float* UWs = reinterpret_cast<float*>(tbase + Cfg::E_TILE);        // [2][HP][16][UW_ROW]
@@ -702,6 +728,7 @@ __global__ __launch_bounds__(64 * (NW > 4 ? NW : 4), 1) void bwd_cols_kernel(Bwd
       Lv[idx] = ok ? prm.lse[ra.vec(h, i)] * kLog2e : 0.f;
       Lv[HP * KC + idx] = ok ? prm.dsum[ra.vec(h, i)] : 0.f;
       Lv[2 * HP * KC + idx] = (ok && act && prm.bias) ? prm.dob[ra.vec(h, i)] : 0.f;
+      Lv[3 * HP * KC + idx] = ok ? prm.lse_z[ra.vec(h, i)] : 0.f;
     }
     // ---- pair-owner: E of (streamed rows, own keys), u.E and w~.E ----
     if (use_e) {
@@ -772,7 +799,7 @@ __global__ __launch_bounds__(64 * (NW > 4 ? NW : 4), 1) void bwd_cols_kernel(Bwd
         S[s] = mma_k<D>(qa, kf[hl], ue);
         dP[s] = mma_k<D>(oa, vf[hl], we);
         unsigned vm = 0;
-        f32x4 lse4, d4, dob4;
+        f32x4 lse4, d4, dob4, z4;
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
           const int il = 16 * s + 4 * g + r;
@@ -780,11 +807,13 @@ __global__ __launch_bounds__(64 * (NW > 4 ? NW : 4), 1) void bwd_cols_kernel(Bwd
           lse4[r] = Lv[h * KC + il];
           d4[r] = Lv[HP * KC + h * KC + il];
           dob4[r] = Lv[2 * HP * KC + h * KC + il];
+          z4[r] = Lv[3 * HP * KC + h * KC + il];
         }
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
           const bool ok = (vm >> r) & 1u;
-          const float p = exp2f_fast(__builtin_fmaf(S[s][r], kLog2e, -lse4[r]));
+          // P / Z, as the rows kernel's accumulators hold it.
+          const float p = exp2f_fast(__builtin_fmaf(S[s][r], kLog2e, -lse4[r]) - z4[r]);
           S[s][r] = ok ? p : 0.f;
           dP[s][r] = dP[s][r] + dob4[r];
           dS[s][r] = S[s][r] * (dP[s][r] - d4[r]);

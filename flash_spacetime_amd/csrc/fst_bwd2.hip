@@ -26,6 +26,10 @@
 // to the output's rounding), each lane keeps its part of N and Z, and the
 // correction is made once after the last chunk with D = N / Z: dQ -= (D -
 // D_ref) sum P k, H -= (D - D_ref) G. Either way D is the kernel's own N / Z.
+// Every accumulator is then divided by Z (P / Z instead of P: the forward's
+// rounded lse leaves a common factor on a row's P, which Z measures), and
+// the cols kernel recomputes the same normalised P from lse_z = lse log2 e
+// + log2 Z.
 // The row constant dob never enters a
 // pair: with dP~ = dP - dob, D - dob = sum P dP~ / sum P and dS = P (dP~ -
 // (D - dob)), so the kernel forms D - dob directly. It writes qt, u, w~ and
@@ -77,7 +81,9 @@ struct Rows2Cfg {
   static constexpr int WG_PER_CU = 4 * WPE / NW;
   static constexpr int E_BYTES = ETile<C, KC>::BYTES;
   static constexpr int REGION = (KC / 4) * 16 * 16 * 16;  // one fp32 term of KC keys per (row, 16 head slots)
-  static constexpr int SCAL_BYTES = 16 * 17 * 4;
+  // Two per-(row, head slot) scalars: the increments of D (scal_off), and
+  // after the key loop the row's 1 / Z (the same offsets in the second half).
+  static constexpr int SCAL_BYTES = 2 * 16 * 17 * 4;
   static constexpr int MAIN = E_BYTES + 2 * REGION + SCAL_BYTES;
   // Epilogue: the tile's qt and dO rows, then four dW / db partials (one per
   // wave, or per pair of waves w, w + 4) in the same bytes; one channel step
@@ -118,6 +124,7 @@ __global__ __launch_bounds__(64 * NW, WPE) void bwd_rows2_kernel(BwdParams prm) 
   unsigned char* stU = smem + Cfg::E_BYTES;  // u.E, then P
   unsigned char* stW = stU + Cfg::REGION;    // w~.E + dob, then dS
   unsigned char* scal = stW + Cfg::REGION;   // increments of D
+  unsigned char* scal_z = scal + 16 * 17 * 4;  // 1 / Z, after the key loop
   __shared__ __align__(16) unsigned char kv_lds[KL ? Cfg::KV_BYTES : 16];
   unsigned char* kvt = kv_lds;  // KL: [K, V][head][part] QoTile blocks of the chunk
 
@@ -575,12 +582,16 @@ __global__ __launch_bounds__(64 * NW, WPE) void bwd_rows2_kernel(BwdParams prm) 
   // ends.
   if constexpr (KL) wait_vmem();
 
-  if constexpr (ORF) {
-    // D = N / Z over all keys; dQ and H, built against the reference value,
-    // take the P sums they lack: dQ -= (D - Dref) sum P k, H -= (D - Dref) G.
-    float dD[HW];
+  // D = N / Z over all keys. ORF: dQ and H, built against the reference
+  // value, take the P sums they lack: dQ -= (D - Dref) sum P k, H -= (D -
+  // Dref) G. Then every accumulator is divided by Z: P = exp(s - lse) with
+  // the forward's rounded lse carries a common factor per row (Z = sum P
+  // = 1 up to that rounding, ~1e-3 off at logits of O(1e4)), which P / Z
+  // removes; the cols kernel recomputes P / Z from lse_z.
+  float dD[HW], rz[HW];
 #pragma unroll
-    for (int hl = 0; hl < HW; ++hl) {
+  for (int hl = 0; hl < HW; ++hl) {
+    if constexpr (ORF) {
       group_allsum2(Nn[hl], Zz[hl]);
       const float dn = Zz[hl] > 0.f ? Nn[hl] * __builtin_amdgcn_rcpf(Zz[hl]) : 0.f;
       dD[hl] = dn - Dc[hl];
@@ -588,16 +599,33 @@ __global__ __launch_bounds__(64 * NW, WPE) void bwd_rows2_kernel(BwdParams prm) 
 #pragma unroll
       for (int q = 0; q < NQ; ++q) dQ[hl][q] = dQ[hl][q] - dD[hl] * A2[hl][q];
     }
-    if (use_e && attn) {
+    rz[hl] = Zz[hl] > 0.f ? 1.f / Zz[hl] : 1.f;
 #pragma unroll
-      for (int hl = 0; hl < HW; ++hl)
-        if (hl < nh) *reinterpret_cast<float*>(scal + scal_off(n, head(hl))) = dD[hl];
-      __syncthreads();
+    for (int q = 0; q < NQ; ++q) dQ[hl][q] = dQ[hl][q] * rz[hl];
+  }
+  if (use_e) {
 #pragma unroll
-      for (int r = 0; r < RPW; ++r) {
-        const float dd = *reinterpret_cast<const float*>(scal + scal_off(row0 + r, n));
+    for (int hl = 0; hl < HW; ++hl)
+      if (hl < nh) {
+        if (ORF && attn) *reinterpret_cast<float*>(scal + scal_off(n, head(hl))) = dD[hl];
+        *reinterpret_cast<float*>(scal_z + scal_off(n, head(hl))) = rz[hl];
+      }
+    __syncthreads();
+    // Lanes of padded heads (n >= HP) read some other slot: finite values in
+    // columns of H and G that are never used.
+    const int hn = n < HP ? n : HP - 1;
+#pragma unroll
+    for (int r = 0; r < RPW; ++r) {
+      const float zr = *reinterpret_cast<const float*>(scal_z + scal_off(row0 + r, hn));
+      if (ORF && attn) {
+        const float dd = *reinterpret_cast<const float*>(scal + scal_off(row0 + r, hn));
 #pragma unroll
         for (int ct = 0; ct < NCT; ++ct) Hacc[r][ct] = Hacc[r][ct] - dd * Gacc[r][ct];
+      }
+#pragma unroll
+      for (int ct = 0; ct < NCT; ++ct) {
+        Hacc[r][ct] = Hacc[r][ct] * zr;
+        Gacc[r][ct] = Gacc[r][ct] * zr;
       }
     }
   }
@@ -625,10 +653,12 @@ __global__ __launch_bounds__(64 * NW, WPE) void bwd_rows2_kernel(BwdParams prm) 
   float sig[HW];
 #pragma unroll
   for (int hl = 0; hl < HW; ++hl) {
-    sig[hl] = Nn[hl] - Dc[hl] * Zz[hl];
+    sig[hl] = (Nn[hl] - Dc[hl] * Zz[hl]) * rz[hl];
     const int h = head(hl);
     if (g == 0 && row_ok && h < H) {
       prm.dsum[ra.vec(h, my_row)] = Dc[hl];  // D - dob: the cols kernel's dS = P (dP~ - (D - dob))
+      // The cols kernel's exponent offset: its P is exp2(s log2 e - lse_z) = P / Z.
+      prm.lse_z[ra.vec(h, my_row)] = lse2[hl] + (Zz[hl] > 0.f ? __builtin_amdgcn_logf(Zz[hl]) : 0.f);
       if (prm.rowsum) prm.rowsum[ra.vec(h, my_row)] = sig[hl];
     }
   }
@@ -891,7 +921,7 @@ __global__ __launch_bounds__(256, OCC) void bwd_cols2_kernel(BwdParams prm) {
   const Buf qbuf(reinterpret_cast<const bf16*>(prm.qt) + ebase, ebytes);
   const Buf obuf(reinterpret_cast<const bf16*>(prm.dout) + ebase, ebytes);
   const unsigned vbytes = (unsigned)((ev.tokmajor ? (long)len * ra.ts : (long)H * ra.hs) * 4);
-  const Buf lbuf(prm.lse + ra.base_row, vbytes), dbuf(prm.dsum + ra.base_row, vbytes);
+  const Buf lbuf(prm.lse_z + ra.base_row, vbytes), dbuf(prm.dsum + ra.base_row, vbytes);
   // u / w~ in the row-group layout the rows kernel writes (uw_off): the
   // event's groups start at 4 x its first tile in the rows work list.
   const long ggrp = uw_group_elems(H, NCT);
@@ -907,7 +937,8 @@ __global__ __launch_bounds__(256, OCC) void bwd_cols2_kernel(BwdParams prm) {
     qvo[hl] = (int)(min(w * HW + hl, H - 1) * ra.hs * D * 2) + n * rowb + kfrag_goff<D>(g);
 
   KFrag<bf16, D> qr[QL ? 1 : HW][NS], orw[QL ? 1 : HW][NS];
-  // Per-row scalars (lse * log2 e and D - dob) of the next chunk: thread t
+  // Per-row scalars (the rows kernel's lse_z = lse log2 e + log2 Z, so that
+  // P = exp2(s log2 e - lse_z) is normalised, and D - dob) of the next chunk: thread t
   // loads item t of the chunk's RC x H values of each (coalesced), and writes
   // it to LDS at the start of that chunk; the head-owners read four rows at a
   // time (one 16-byte broadcast read).
@@ -1036,7 +1067,7 @@ __global__ __launch_bounds__(256, OCC) void bwd_cols2_kernel(BwdParams prm) {
     }
     if constexpr (!QL) issue_rows(i0c + RC);
     if (sc_ok) {
-      rsc[sc_h * RC + sc_r] = i0c + sc_r < len ? sc_lraw * kLog2e : INFINITY;  // rows past the event: P = 0
+      rsc[sc_h * RC + sc_r] = i0c + sc_r < len ? sc_lraw : INFINITY;  // rows past the event: P = 0
       rsc[16 * RC + sc_h * RC + sc_r] = sc_draw;
     }
     if constexpr (QL) wait_vmem();  // this wave's direct-to-LDS rows have landed

@@ -434,7 +434,7 @@ __global__ __launch_bounds__(256) void fill_zero_kernel(float* p, int n) {
 struct BwdLayout {
   int rows_r, rows_c;   // rows (keys) per workgroup of the rows / cols kernels
   long grid_r, grid_c;
-  size_t off_bc_r, off_bc_c, off_u, off_wt, off_qt, off_dob, off_dsum, off_part, off_seg, total;
+  size_t off_bc_r, off_bc_c, off_u, off_wt, off_qt, off_dob, off_dsum, off_lsez, off_part, off_seg, total;
   long nseg;  // stage-1 runs of the dW reduction
 };
 
@@ -469,6 +469,8 @@ static int bwd_layout(int dtype, int flags, int B, int H, int L, int T, int D, i
   lay.off_dob = off;
   off += align_up((size_t)rows * H * 4, 256);
   lay.off_dsum = off;
+  off += align_up((size_t)rows * H * 4, 256);
+  lay.off_lsez = off;
   off += align_up((size_t)rows * H * 4, 256);
   // The dW / db partials (one per rows-kernel workgroup) are sized for
   // 16-row workgroups, the smallest of any plan, so that the workspace a
@@ -766,6 +768,7 @@ int fst_backward_phases(int phases, int dtype, int flags, int B, int H, int L, i
   prm.qt = ws + lay.off_qt;
   prm.dob = reinterpret_cast<float*>(ws + lay.off_dob);
   prm.dsum = reinterpret_cast<float*>(ws + lay.off_dsum);
+  prm.lse_z = reinterpret_cast<float*>(ws + lay.off_lsez);
   prm.dw_part = reinterpret_cast<float*>(ws + lay.off_part);
   prm.dq = dq;
   prm.dk = dk;

@@ -169,6 +169,12 @@ struct BwdParams {
   void* qt;             // [rows, D] T: bf16(q * scale) (written by the bf16 rows kernel)
   float* dob;           // [rows]
   float* dsum;          // [rows]
+  // [rows] the rows kernel's sum of P per row, Z, for the cols kernel's P / Z:
+  // bf16, the log2-domain LSE of the normalised P, lse log2(e) + log2 Z;
+  // float32, log2 Z alone (at logits of O(1e4) the sum would round away the
+  // correction, so the float32 cols kernel subtracts it after the exponent's
+  // fma).
+  float* lse_z;
   float* dw_part;       // [blocks, D, C]
   float* db_part;       // [blocks, D]
   // outputs
