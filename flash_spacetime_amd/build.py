@@ -43,8 +43,20 @@ HEAD_DIMS = (16, 32, 48, 64)
 ROWS_SCHED = ["-mllvm", "--amdgpu-sched-strategy=max-ilp"]
 
 
+def source_hash() -> str:
+    """First 12 hex digits of the SHA-256 of every kernel source: the build id
+    fst_version reports (the tuner's plan cache keys on it)."""
+    import hashlib
+
+    h = hashlib.sha256()
+    for p in sorted(CSRC.glob("*.h")) + sorted(CSRC.glob("*.hip")):
+        h.update(p.name.encode())
+        h.update(p.read_bytes())
+    return h.hexdigest()[:12]
+
+
 def _units():
-    units = [("capi", CSRC / "fst_capi.hip", [])]
+    units = [("capi", CSRC / "fst_capi.hip", [f'-DFST_BUILD_ID="{source_hash()}"'])]
     for tag, ctype in DTYPES.items():
         for d in HEAD_DIMS:
             name = f"{tag}_{d}"

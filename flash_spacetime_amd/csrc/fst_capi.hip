@@ -494,7 +494,10 @@ extern "C" {
 
 const char* fst_last_error(void) { return g_last_error; }
 
-const char* fst_version(void) { return "flash-spacetime-gfx950 0.1.0"; }
+#ifndef FST_BUILD_ID
+#define FST_BUILD_ID "unknown"
+#endif
+const char* fst_version(void) { return "flash-spacetime-gfx950 0.3.0 abi 2 build " FST_BUILD_ID; }
 
 void fst_frequencies(int C, float* out) {
   if (C > 0 && C <= 64 && C % 2 == 0 && out) frequencies(C, out);
@@ -635,12 +638,24 @@ constexpr int kMaxDevices = 64;
 static void* g_scratch_ptr[kMaxDevices];
 static std::mutex g_scratch_mu;
 
-// The device address of `scratch` on the current device (nullptr and an
-// error message on failure).
-static void* scratch_on_current_device() {
-  int dev = -1;
+// The device address of `scratch` on the device of `stream`, which must be
+// the current device: hipGetSymbolAddress resolves the current device's copy
+// (nullptr and an error message on failure, with *rc the status to return).
+static void* scratch_for_stream(hipStream_t stream, int* rc) {
+  int dev = -1, sdev = -1;
+  *rc = FST_ELAUNCH;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices) {
     fail(FST_ELAUNCH, "no current HIP device (or device index %d beyond %d)", dev, kMaxDevices);
+    return nullptr;
+  }
+  if (hipStreamGetDevice(stream, &sdev) != hipSuccess) {
+    fail(FST_ELAUNCH, "hipStreamGetDevice failed");
+    return nullptr;
+  }
+  if (sdev != dev) {
+    *rc = FST_EINVAL;
+    fail(FST_EINVAL, "the stream belongs to device %d but device %d is current: make the stream's device current",
+         sdev, dev);
     return nullptr;
   }
   std::lock_guard<std::mutex> lock(g_scratch_mu);
@@ -673,8 +688,9 @@ int fst_forward_noalloc(int dtype, int flags, int B, int H, int L, int T, int D,
                                           need, sizeof(scratch));
   const bool packed = flags & FST_PACKED;
   if (B == 0 || (packed ? (long)T : (long)B * L) == 0) return FST_OK;
-  void* ws = scratch_on_current_device();
-  if (!ws) return FST_ELAUNCH;
+  int src = FST_OK;
+  void* ws = scratch_for_stream(reinterpret_cast<hipStream_t>(stream), &src);
+  if (!ws) return src;
   return fst_forward_phases(FST_FWD_ALL, dtype, flags, B, H, L, T, D, C, q, k, v, pos4, weight, bias, lens, scale,
                             out, lse, ws, sizeof(scratch), stream);
 }

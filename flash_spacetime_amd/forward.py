@@ -13,8 +13,11 @@ tensor raises.
 
 from __future__ import annotations
 
+import contextlib
 import copy
 import os
+import threading
+import weakref
 from typing import Any, List, Optional, Tuple
 
 import torch
@@ -328,24 +331,54 @@ def flash_spacetime_forward(
         return _run_forward(prep)
 
 
-def _keep_output(ctx: Any, out: Tensor) -> None:
-    """Keep a detached alias of the forward's output and its version for the
-    backward, which hands it to the bf16 rows kernel as the source of its
-    reference D (the output is usually alive anyway: it is the op's result;
-    for float16 operands it is the bf16 output the float16 result is
-    converted from, held until the backward). A detached alias holds no
-    graph, so no reference cycle forms."""
-    ctx.out_alias = out.detach()
-    ctx.out_version = out._version
+_TEMPORARY_OUTPUT = threading.local()
 
 
-def _kept_output(ctx: Any) -> Optional[Tensor]:
-    """The kept output, unless it was modified in place after the forward
-    (then the kernel forms D online instead; either way D is its own)."""
-    alias = getattr(ctx, "out_alias", None)
-    if alias is None or alias._version != ctx.out_version:
+@contextlib.contextmanager
+def _output_is_temporary():
+    """Calls inside convert or scatter the op's output into another tensor
+    (float16 results, masks with holes): their backward keeps nothing of the
+    output, and the rows kernel forms D online."""
+    prev = getattr(_TEMPORARY_OUTPUT, "on", False)
+    _TEMPORARY_OUTPUT.on = True
+    try:
+        yield
+    finally:
+        _TEMPORARY_OUTPUT.on = prev
+
+
+def _keep_output(ctx: Any, out: Tensor, returned: Optional[Tensor] = None) -> List[Tensor]:
+    """What of the forward's output the backward keeps, to be appended to the
+    tensors saved for backward: the bf16 rows kernel takes its reference D
+    from it. It goes through save_for_backward (so saved-tensor hooks, such as
+    offloading or checkpointing, handle it like any saved tensor) as `.data`,
+    an alias with a version counter of its own, so that modifying the output
+    in place does not make the backward fail as it would for a saved output.
+    A weak reference to the tensor the caller receives (`returned`, default
+    `out`) and its version tell the backward whether the caller modified it
+    since; nothing is kept where the output is a temporary of the op."""
+    if getattr(_TEMPORARY_OUTPUT, "on", False):
+        ctx.out_ref = None
+        return []
+    ret = out if returned is None else returned
+    ctx.out_ref = weakref.ref(ret)
+    ctx.out_version = ret._version
+    return [out.data]
+
+
+def _kept_output(ctx: Any, kept: Tuple[Tensor, ...]) -> Optional[Tensor]:
+    """The kept output (the saved tensors past the inputs and lse), or None
+    where nothing was kept or the caller modified the output in place since
+    the forward; then the kernel forms D online. Either way D is the kernel's
+    own N / Z, so the gradients do not depend on which (a caller that
+    modified the output and then dropped it leaves the modified values as the
+    reference, which moves only roundings)."""
+    if not kept:
         return None
-    return alias
+    ret = None if ctx.out_ref is None else ctx.out_ref()
+    if ret is not None and ret._version != ctx.out_version:
+        return None
+    return kept[0]
 
 
 class _FlashSpacetimeAttention(torch.autograd.Function):
@@ -373,8 +406,7 @@ class _FlashSpacetimeAttention(torch.autograd.Function):
         out, lse = _run_forward(prep)
         # The inputs and the LSE are saved as the reference saves them
         # (forward.py:381-388); the backward forms its own softmax row sums.
-        ctx.save_for_backward(prep.q, prep.k, prep.v, prep.pos4, prep.lens, lse)
-        _keep_output(ctx, out)
+        ctx.save_for_backward(prep.q, prep.k, prep.v, prep.pos4, prep.lens, lse, *_keep_output(ctx, out))
         ctx.prep_meta = (prep.weight, prep.bias, weight.dtype,
                          None if bias is None else bias.dtype)
         ctx.dims = prep.dims()
@@ -393,11 +425,11 @@ class _FlashSpacetimeAttention(torch.autograd.Function):
             )
         from .backward import _run_backward
 
-        q, k, v, pos4, lens, lse = ctx.saved_tensors
+        q, k, v, pos4, lens, lse, *kept = ctx.saved_tensors
         w32, b32, w_dtype, b_dtype = ctx.prep_meta
         dq, dk, dv, dw, db = _run_backward(
             ctx.dims, q, k, v, pos4, w32, b32, lens, lse, grad_out, ctx.scale, ctx.vec_shape,
-            out=_kept_output(ctx),
+            out=_kept_output(ctx, kept),
         )
         use_attn_bias, use_activation_bias = ctx.flags
         proj_used = use_attn_bias or use_activation_bias
@@ -437,8 +469,10 @@ def flash_spacetime_attention(
     a mask with holes runs the packed kernels on the gathered valid tokens.
     """
     if q.dtype == _HALF:
-        return flash_spacetime_attention(*_bf16(q, k, v), feats, weight, bias, seqlens, scale, use_attn_bias,
-                                         use_activation_bias, key_padding_mask=key_padding_mask).to(_HALF)
+        with _output_is_temporary():
+            out = flash_spacetime_attention(*_bf16(q, k, v), feats, weight, bias, seqlens, scale, use_attn_bias,
+                                            use_activation_bias, key_padding_mask=key_padding_mask)
+        return out.to(_HALF)
     mask = key_padding_mask
     if mask is None and seqlens is not None and seqlens.dim() == 2:
         mask = seqlens
@@ -474,8 +508,9 @@ def _attention_scattered(q, k, v, feats, weight, bias, valid, scale, use_attn_bi
     cu = torch.zeros(b + 1, dtype=torch.int32, device=q.device)
     cu[1:] = torch.cumsum(counts, 0, dtype=torch.int32)
     rows = lambda x: x.transpose(1, 2)[valid]  # [T, H, D], events and tokens in order
-    out = flash_spacetime_attention_varlen(rows(q), rows(k), rows(v), feats[valid], weight, bias, cu, scale,
-                                           use_attn_bias, use_activation_bias)
+    with _output_is_temporary():  # scattered into the padded result below
+        out = flash_spacetime_attention_varlen(rows(q), rows(k), rows(v), feats[valid], weight, bias, cu, scale,
+                                               use_attn_bias, use_activation_bias)
     full = out.new_zeros(b, length, h, d).index_put((valid,), out)
     # Heads-first view of the token-major result when q was one, else
     # contiguous [B, H, L, D].
@@ -507,8 +542,10 @@ def flash_spacetime_attention_varlen(
     offsets), and the output is a jagged tensor with the same offsets.
     """
     if q.dtype == _HALF:
-        return flash_spacetime_attention_varlen(*_bf16(q, k, v), feats, weight, bias, cu_seqlens, scale,
-                                                use_attn_bias, use_activation_bias).to(_HALF)
+        with _output_is_temporary():
+            out = flash_spacetime_attention_varlen(*_bf16(q, k, v), feats, weight, bias, cu_seqlens, scale,
+                                                   use_attn_bias, use_activation_bias)
+        return out.to(_HALF)
     if q.is_nested:
         if not (k.is_nested and v.is_nested):
             raise ValueError("q, k and v must all be nested tensors, or none of them")
@@ -562,21 +599,21 @@ class _FlashSpacetimeAttentionQKV(torch.autograd.Function):
         prep = _Prepared(q, k, v, feats, weight, bias, seqlens, scale, use_attn_bias,
                          use_activation_bias, cu_seqlens, interleaved=True)
         out, lse = _run_forward(prep)
-        ctx.save_for_backward(qkv, prep.pos4, prep.lens, lse)
-        _keep_output(ctx, out)
+        ret = out if packed else out.transpose(1, 2)  # [T, H, D] / [B, L, H, D], dense
+        ctx.save_for_backward(qkv, prep.pos4, prep.lens, lse, *_keep_output(ctx, out, ret))
         ctx.prep_meta = (prep.weight, prep.bias, weight.dtype, None if bias is None else bias.dtype)
         ctx.dims = prep.dims()
         ctx.scale = prep.scale
         ctx.packed = packed
         ctx.flags = (use_attn_bias, use_activation_bias)
         ctx.vec_shape = prep.vec_shape()
-        return out if packed else out.transpose(1, 2)  # [T, H, D] / [B, L, H, D], dense
+        return ret
 
     @staticmethod
     def backward(ctx: Any, grad_out: Tensor) -> Tuple[Optional[Tensor], ...]:  # type: ignore[override]
         from .backward import _run_backward
 
-        qkv, pos4, lens, lse = ctx.saved_tensors
+        qkv, pos4, lens, lse, *kept = ctx.saved_tensors
         w32, b32, w_dtype, b_dtype = ctx.prep_meta
         q, k, v = _qkv_views(qkv, ctx.packed)
         dqkv = torch.empty_like(qkv)
@@ -588,7 +625,7 @@ class _FlashSpacetimeAttentionQKV(torch.autograd.Function):
             like = torch.empty(b, length, h, d, device=qkv.device, dtype=qkv.dtype).transpose(1, 2)
         _, _, _, dw, db = _run_backward(
             ctx.dims, q, k, v, pos4, w32, b32, lens, lse, g, ctx.scale, ctx.vec_shape,
-            out_like=like, grads=_qkv_views(dqkv, ctx.packed), out=_kept_output(ctx),
+            out_like=like, grads=_qkv_views(dqkv, ctx.packed), out=_kept_output(ctx, kept),
         )
         use_attn_bias, use_activation_bias = ctx.flags
         proj_used = use_attn_bias or use_activation_bias
@@ -629,9 +666,11 @@ def flash_spacetime_attention_qkv(
     (forward.py:481-501).
     """
     if qkv.dtype == _HALF:
-        return flash_spacetime_attention_qkv(qkv.to(torch.bfloat16), feats, weight, bias, seqlens, scale,
-                                             use_attn_bias, use_activation_bias, cu_seqlens=cu_seqlens,
-                                             key_padding_mask=key_padding_mask).to(_HALF)
+        with _output_is_temporary():
+            out = flash_spacetime_attention_qkv(qkv.to(torch.bfloat16), feats, weight, bias, seqlens, scale,
+                                                use_attn_bias, use_activation_bias, cu_seqlens=cu_seqlens,
+                                                key_padding_mask=key_padding_mask)
+        return out.to(_HALF)
     if cu_seqlens is not None:
         if qkv.dim() != 4 or qkv.shape[1] != 3:
             raise ValueError(f"packed qkv must be [T, 3, H, D], got {tuple(qkv.shape)}")
@@ -654,10 +693,11 @@ def flash_spacetime_attention_qkv(
                 raise ValueError(f"feats must be [B, L, F>=4], got {tuple(feats.shape)}")
             cu = torch.zeros(b + 1, dtype=torch.int32, device=qkv.device)
             cu[1:] = torch.cumsum(valid.sum(1, dtype=torch.int32), 0, dtype=torch.int32)
-            out = _FlashSpacetimeAttentionQKV.apply(
-                qkv[valid], feats[valid], weight, bias, None, scale, use_attn_bias,
-                use_activation_bias, cu,
-            )
+            with _output_is_temporary():  # scattered into the padded result below
+                out = _FlashSpacetimeAttentionQKV.apply(
+                    qkv[valid], feats[valid], weight, bias, None, scale, use_attn_bias,
+                    use_activation_bias, cu,
+                )
             return out.new_zeros(b, length, *out.shape[1:]).index_put((valid,), out)
         seqlens = valid.sum(1, dtype=torch.int32)
     return _FlashSpacetimeAttentionQKV.apply(

@@ -295,11 +295,12 @@ def forward_plan(dims: Tuple[int, ...], run: Callable[[int], int]) -> int:
 
 def backward_plan(dims: Tuple[int, ...], run: Callable[[int, int], int]) -> int:
     """Plan bits for a backward call; `run(phases, flags)` launches those
-    phases of the backward with those flags and returns the status. The rows
-    kernel's groups are timed first (after one work-list phase), then the
-    cols kernel's, which reads what the rows kernel wrote; the float32
-    groups, which set both kernels, are timed over the two together. The
-    caller's own launch follows with the chosen plan."""
+    phases of the backward with those flags and returns the status. The
+    float32 groups, which set both kernels and their rows per workgroup, are
+    timed over the two together, each run with its own work list; then the
+    rows kernel's groups (after one work-list phase for the plan so far), then
+    the cols kernel's, which reads what the rows kernel wrote. The caller's
+    own launch follows with the chosen plan."""
     tiled = _tiled("bwd", dims)
     if tiled is not None:
         return tiled
@@ -315,9 +316,12 @@ def backward_plan(dims: Tuple[int, ...], run: Callable[[int, int], int]) -> int:
         return 0
     what = "flash_spacetime_backward (tuning)"
     rows, cols, both = (_combos(dims, g) for g in (_ROWS_GROUPS, _COLS_GROUPS, _BWD_GROUPS))
-    if rows or cols or both:
-        _lib.check(run(_lib.FST_PHASE_WORKLIST, dims[1]), what)
-    plan = _fastest(lambda f: run(_lib.FST_PHASE_BWD_ROWS | _lib.FST_PHASE_BWD_COLS, f), both, dims[1], what)
+    # The float32 groups change the rows per workgroup, which the work list
+    # is built for: each of their timed runs builds its own.
+    plan = _fastest(lambda f: run(_lib.FST_PHASE_WORKLIST | _lib.FST_PHASE_BWD_ROWS | _lib.FST_PHASE_BWD_COLS, f),
+                    both, dims[1], what)
+    if rows or cols:
+        _lib.check(run(_lib.FST_PHASE_WORKLIST, dims[1] | plan), what)
     r = _fastest(lambda f: run(_lib.FST_PHASE_BWD_ROWS, f), rows, dims[1] | plan, what)
     plan |= r
     if cols and not rows:  # the cols kernel reads the rows kernel's scratch

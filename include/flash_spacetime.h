@@ -188,9 +188,10 @@ int fst_forward(int dtype, int flags, int B, int H, int L, int T, int D, int C,
  * harnesses that forbid hipMalloc). No counterpart in the reference. The
  * work list lives in a file-scope device array of the library sized for at
  * most 65536 events (B > 65536 returns FST_EUNSUPPORTED); each GPU holds its
- * own copy, about 1 MiB, until the process ends. The first call on a device
- * resolves the array's address there (with the stream's device current);
- * no call allocates, frees or synchronises. Every call on one GPU shares
+ * own copy, about 1 MiB, until the process ends. The stream's device must
+ * be the current device (else FST_EINVAL): the first call on a device
+ * resolves the array's address there, and every call uses the current
+ * device's copy. No call allocates, frees or synchronises. Every call on one GPU shares
  * that GPU's array, so calls that overlap on one GPU (concurrent streams or
  * threads) race: serialise them. Results are bitwise those of fst_forward. */
 int fst_forward_noalloc(int dtype, int flags, int B, int H, int L, int T, int D, int C,
@@ -265,7 +266,12 @@ void fst_frequencies(int C, float* out);
 /* Message of the last failed call on this thread ("" if none). */
 const char* fst_last_error(void);
 
-/* Library version string. */
+/* Library version string, "flash-spacetime-gfx950 <major>.<minor>.<patch>
+ * abi <n> build <id>", id a hash of the kernel sources. The abi number changes with every change of an entry point's
+ * arguments or of what a caller must provide (workspace sizes are always
+ * queried, so a larger workspace is not an ABI change): abi 2 added the
+ * forward's output to fst_backward / fst_backward_phases (the argument
+ * `out`, before `scale`). */
 const char* fst_version(void);
 
 #ifdef __cplusplus

@@ -29,7 +29,7 @@ class BuildWithKernels(build_py):
 
 setup(
     name="flash-spacetime-amd",
-    version="0.1.0",
+    version="0.3.0",
     description="flash-spacetime attention on MI355X (gfx950): hand-written HIP kernels behind the "
                 "reference's operator API",
     long_description=(ROOT / "README.md").read_text(),

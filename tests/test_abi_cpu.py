@@ -17,6 +17,7 @@ import oracle
 import flash_spacetime_amd
 from flash_spacetime_amd import _lib
 from flash_spacetime_amd import reference as spec_api
+from flash_spacetime_amd.build import source_hash
 
 HEADER = Path(__file__).resolve().parents[1] / "include" / "flash_spacetime.h"
 
@@ -43,7 +44,13 @@ def test_library_exports_every_declared_symbol():
     lib = _lib.load()
     for name in _declared_functions():
         assert hasattr(lib, name), name
-    assert lib.fst_version().decode().startswith("flash-spacetime-gfx950")
+    version = lib.fst_version().decode()
+    assert version.startswith("flash-spacetime-gfx950 ")
+    # the ABI number of the header this binding was written for (fst_backward
+    # takes the forward's output before `scale`), and the build of these sources
+    m = re.fullmatch(r"flash-spacetime-gfx950 \d+\.\d+\.\d+ abi (\d+) build ([0-9a-f]{12})", version)
+    assert m and m.group(1) == "2", version
+    assert m.group(2) == source_hash(), "the library was built from other sources than these"
 
 
 @needs_lib

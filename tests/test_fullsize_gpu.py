@@ -43,7 +43,8 @@ pytestmark = pytest.mark.gpu
 
 if torch.cuda.is_available():
     from flash_spacetime_amd import (
-        flash_spacetime_attention_varlen, flash_spacetime_backward, flash_spacetime_forward,
+        flash_spacetime_attention, flash_spacetime_attention_varlen, flash_spacetime_backward,
+        flash_spacetime_forward,
     )
 
 DEV = "cuda"
@@ -289,3 +290,34 @@ def test_cfg4_full_size(dtype):
     torch.testing.assert_close(out_p, pk(out), atol=atol, rtol=rtol)
     for a, c in zip(grads_p[:3], grads[:3]):
         assert rel_err(a, pk(c)) <= (1e-2 if dtype == torch.bfloat16 else 1e-4)
+
+
+def test_cfg2_peak_memory_linear_in_length():
+    """cfg2's fwd+bwd step (autograd op, bool key_padding_mask, bf16, B=256,
+    H=12, D=32, C=16, lengths U{16..L}) allocates memory linear in L: the
+    peak above the resident inputs at L = 384, 768, 1536 is within 1.1x of
+    proportional (the reference's test_varlen.py:251-282 measures its packed
+    op the same way). Nothing O(L^2) is held: eager R alone at L = 1536
+    would take 256 * 1536^2 * 32 * 2 bytes = 36 GiB."""
+    per_l = {}
+    for length in (384, 768, 1536):
+        gen = torch.Generator().manual_seed(11)
+        lens = torch.randint(16, length + 1, (256,), generator=gen).tolist()
+        q, k, v, feats, w, b, sl, do = _inputs_padded(256, length, 12, 32, 16, lens, 11, torch.bfloat16)
+        mask = torch.arange(length, device=DEV)[None, :] >= sl[:, None].long()
+        leaves = [x.requires_grad_(True) for x in (q, k, v)]
+        wl, bl = w.requires_grad_(True), b.requires_grad_(True)
+        torch.cuda.synchronize()
+        torch.cuda.reset_peak_memory_stats()
+        base = torch.cuda.memory_allocated()
+        out = flash_spacetime_attention(*leaves, feats, wl, bl, key_padding_mask=mask)
+        out.backward(do)
+        torch.cuda.synchronize()
+        peak = torch.cuda.max_memory_allocated() - base
+        per_l[length] = peak / length
+        print(f"L={length}: peak {peak / 2**30:.3f} GiB above the inputs", flush=True)
+        assert torch.isfinite(out).all() and all(torch.isfinite(x.grad).all() for x in leaves)
+        del q, k, v, out, leaves, do, wl, bl
+    ratios = [per_l[n] / per_l[768] for n in per_l]
+    assert max(ratios) / min(ratios) <= 1.1, per_l
+    assert per_l[768] * 768 < 1.0 * 2**30  # cfg2 itself: under 1 GiB above the inputs

@@ -48,8 +48,17 @@ def test_half_padded_op_runs_the_bf16_path():
                                            case["seqlens"])
     vm = valid.cpu().expand(ref.shape)
     assert rel_err(out.double().cpu()[vm], ref[vm]) <= 2e-2
-    for g, r in zip(grads, ref_grads):
+    # The float16 result is converted from a temporary bf16 output, which the
+    # op does not keep alive for its backward: the rows kernel forms D online,
+    # as the bf16 backward does without the forward's output (same N / Z,
+    # the schedule's own roundings).
+    bq, bk, bv = (case[n].to(DEV, torch.float16).to(torch.bfloat16) for n in ("q", "k", "v"))
+    _, ref_lse = flash_spacetime_forward(bq, bk, bv, feats, w, b, sl)
+    online = flash_spacetime_backward(bq, bk, bv, feats, w, b, sl, ref_lse,
+                                      gw.to(DEV, torch.float16).to(torch.bfloat16))
+    for g, r, r_out in zip(grads, online[:3], ref_grads):
         assert torch.equal(g, r.to(torch.float16))
+        assert rel_err(g.double().cpu(), r_out.double().cpu()) <= 2e-2
 
 
 def test_half_launchers_packed_and_qkv():

@@ -178,3 +178,43 @@ def test_nonfinite_output_is_not_used():
     for name, a, e in zip(("dq", "dk", "dv", "dW", "db"), got, ref):
         assert torch.isfinite(a).all(), name
         assert rel_err(a.cpu(), e) <= 2e-2, name
+
+
+def test_kept_output_goes_through_saved_tensor_hooks():
+    """The output the backward keeps is a saved tensor like the inputs:
+    saved-tensor hooks (here counting and offloading, as save_on_cpu does)
+    see it, and the gradients are bit for bit those of the plain run. The
+    float16 op, whose result is converted from a temporary bf16 output, keeps
+    nothing of it."""
+    case = make_padded(2, 80, 12, 32, 16, seed=98)
+    feats, sl = case["feats"].to(DEV), case["seqlens"].to(DEV)
+    w, b = case["weight"].float().to(DEV), case["bias"].float().to(DEV)
+    do = torch.randn(case["q"].shape, generator=torch.Generator().manual_seed(8)).to(DEV, BF)
+
+    leaves = _leaves(case)
+    flash_spacetime_attention(*leaves, feats, w, b, sl).backward(do)
+    plain = [x.grad for x in leaves]
+
+    packed = []
+
+    def pack(t):
+        packed.append((tuple(t.shape), t.dtype))
+        return t.to("cpu")
+
+    def unpack(t):
+        return t.to(DEV)
+
+    leaves = _leaves(case)
+    with torch.autograd.graph.saved_tensors_hooks(pack, unpack):
+        o = flash_spacetime_attention(*leaves, feats, w, b, sl)
+    o.backward(do)
+    assert (tuple(o.shape), BF) in packed[6:], packed  # after q, k, v, pos, lengths, lse
+    for leaf, g in zip(leaves, plain):
+        assert torch.equal(leaf.grad, g)
+
+    packed.clear()
+    half = [case[x].to(DEV, torch.float16).requires_grad_(True) for x in ("q", "k", "v")]
+    with torch.autograd.graph.saved_tensors_hooks(pack, unpack):
+        o = flash_spacetime_attention(*half, feats, w, b, sl)
+    o.backward(do.to(torch.float16))
+    assert not any(s == tuple(o.shape) and d == BF for s, d in packed[6:]), packed

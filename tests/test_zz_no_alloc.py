@@ -81,3 +81,75 @@ def test_noalloc_forward_rejects_too_many_events():
     rc = lib.fst_forward_noalloc(_lib.FST_BF16, 3, 65537, 12, 16, 0, 32, 16, *([None] * 7), 1.0, None, None,
                                  _lib.stream_handle(torch.device(DEV)))
     assert rc == _lib.FST_EUNSUPPORTED and "65536" in _lib.last_error()
+
+
+def test_noalloc_forward_under_graph_capture():
+    """Captured after one eager call: every replay bitwise equal to fst_forward,
+    with eager work between the replays, and a second, smaller captured call
+    after the first graph's replays."""
+    lib = _lib.load()
+    for batch, length, seed in ((32, 200, 3), (4, 40, 4)):
+        prep = _case(batch, length, seed, False)
+        want_out, want_lse = _reference_forward(lib, prep)
+        _noalloc_forward(lib, prep)  # eager warm-up on this stream
+        torch.cuda.synchronize()
+        out, lse = torch.empty_like(prep.q), prep.empty_vec()
+        graph = torch.cuda.CUDAGraph()
+        stream = torch.cuda.Stream()
+        stream.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(stream):
+            with torch.cuda.graph(graph, stream=stream):
+                rc = lib.fst_forward_noalloc(*prep.dims(), *_args(prep), _lib.ptr(out), _lib.ptr(lse),
+                                             _lib.stream_handle(prep.device))
+        torch.cuda.current_stream().wait_stream(stream)
+        _lib.check(rc, "fst_forward_noalloc (captured)")
+        for rep in range(3):
+            out.zero_()
+            lse.fill_(float("nan"))
+            graph.replay()
+            torch.cuda.synchronize()
+            print(f"replay {rep}: B={batch} L={length}", flush=True)
+            assert torch.equal(out, want_out) and torch.equal(lse, want_lse)
+            _reference_forward(lib, _case(3, 30, 9, False))  # eager work between replays
+            torch.cuda.synchronize()
+
+
+_FIRST_CALL_CAPTURED = r"""
+import sys, torch
+sys.path.insert(0, sys.argv[1])
+from tests.test_zz_no_alloc import _case, _args, _reference_forward
+from flash_spacetime_amd import _lib
+lib = _lib.load()
+prep = _case(16, 100, 5, False)
+want_out, want_lse = _reference_forward(lib, prep)
+torch.cuda.synchronize()
+out, lse = torch.empty_like(prep.q), prep.empty_vec()
+graph = torch.cuda.CUDAGraph()
+stream = torch.cuda.Stream()
+stream.wait_stream(torch.cuda.current_stream())
+with torch.cuda.stream(stream):
+    with torch.cuda.graph(graph, stream=stream):
+        rc = lib.fst_forward_noalloc(*prep.dims(), *_args(prep), _lib.ptr(out), _lib.ptr(lse),
+                                     _lib.stream_handle(prep.device))
+torch.cuda.current_stream().wait_stream(stream)
+_lib.check(rc, "first fst_forward_noalloc call, captured")
+for _ in range(2):
+    graph.replay()
+    torch.cuda.synchronize()
+    assert torch.equal(out, want_out) and torch.equal(lse, want_lse)
+print("first captured call ok", flush=True)
+"""
+
+
+def test_noalloc_forward_first_call_captured():
+    """The first call on a device (where the scratch address is resolved) made
+    under graph capture, in a fresh process of its own."""
+    import os
+    import subprocess
+    import sys
+
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    res = subprocess.run([sys.executable, "-c", _FIRST_CALL_CAPTURED, root], capture_output=True, text=True,
+                         timeout=100)
+    print(res.stdout[-2000:], res.stderr[-2000:], flush=True)
+    assert res.returncode == 0 and "first captured call ok" in res.stdout
