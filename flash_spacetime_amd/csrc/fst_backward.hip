@@ -949,15 +949,8 @@ template <typename T, int HP, int D, int C>
 int bwd_launch_t(const BwdParams& prm, int which, hipStream_t stream, int grid, bool query, int* rows) {
   using PR = BwdPick<BwdRowsCfg, T, HP, D, C>;
   using PC = BwdPick<BwdColsCfg, T, HP, D, C>;
-  // float32 with D = 16 and C >= 48 is refused: on gfx950 the dW / db
-  // partials of these rows-kernel instances came out wrong and different from
-  // run to run (every other float32 shape is exact and bitwise repeatable;
-  // an -O1 build of the same source changed the C = 48 result), so the shape
-  // is reported unsupported rather than computed. The reference itself takes
-  // only C == D (forward.py:258-265).
-  constexpr bool REFUSED = !is_bf16<T>::value && D == 16 && C >= 48;
   *rows = 0;
-  if constexpr (!PR::OK || !PC::OK || REFUSED) {
+  if constexpr (!PR::OK || !PC::OK) {
     return FST_EUNSUPPORTED;
   } else {
     const int nw = plan_nw(prm.flags, bit_index(FST_PLAN_BWD_T16), bit_index(FST_PLAN_BWD_W8));

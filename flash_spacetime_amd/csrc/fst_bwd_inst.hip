@@ -85,8 +85,7 @@ static int bwd_plans_at() {
     if constexpr (P::KL_W4 || P::KL_W8X2) plans |= FST_PLAN_ROWS_KV_LDS;
     return plans;
   } else {
-    constexpr bool REFUSED = !is_bf16<FST_T>::value && FST_D == 16 && C >= 48;
-    if constexpr (REFUSED || !BwdPick<BwdRowsCfg, FST_T, HP, FST_D, C>::OK ||
+    if constexpr (!BwdPick<BwdRowsCfg, FST_T, HP, FST_D, C>::OK ||
                   !BwdPick<BwdColsCfg, FST_T, HP, FST_D, C>::OK)
       return 0;
     else

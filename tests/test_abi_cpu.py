@@ -249,13 +249,13 @@ def test_sanitised_offsets_fit_the_tile_slots(seed):
 
 
 @needs_lib
-def test_fp32_d16_wide_channels_refused():
-    """float32 with D = 16 and C >= 48 is refused (its backward's dW partials
-    were wrong on gfx950); bf16 runs those shapes on the tile kernels, and
-    float32 takes every other (D, C)."""
+def test_every_head_and_channel_width_supported():
+    """Both dtypes take every (D, C) in {16, 32, 48, 64}^2 at every head count
+    one call covers (float32 at D = C = 64: up to 8), including float32 with
+    D = 16 and C >= 48."""
     lib = _lib.load()
-    for c in (48, 64):
-        assert lib.fst_supported(_lib.FST_F32, 4, 16, c) == 0
-        assert lib.fst_supported(_lib.FST_BF16, 4, 16, c) == 1
-    for d, c in ((16, 16), (16, 32), (32, 48), (32, 64), (48, 64), (64, 16)):
-        assert lib.fst_supported(_lib.FST_F32, 4, d, c) == 1
+    for dt in (_lib.FST_F32, _lib.FST_BF16):
+        for d in (16, 32, 48, 64):
+            for c in (16, 32, 48, 64):
+                for h in (1, 4, 8):
+                    assert lib.fst_supported(dt, h, d, c) == 1, (dt, h, d, c)

@@ -99,6 +99,8 @@ FP32_SHAPES = [
     (3, 130, 12, 32, 16, 101),
     (2, 96, 8, 64, 64, 102),
     (4, 57, 4, 32, 48, 103),
+    (4, 57, 4, 16, 48, 103),
+    (3, 44, 6, 16, 64, 104),
     (3, 44, 16, 16, 32, 105),
 ]
 

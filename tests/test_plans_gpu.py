@@ -52,6 +52,9 @@ SHAPES = [
     (F32, 8, 32, 16, [90, 17, 1], False, (True, False)),   # eight waves, lanes sharing an embedding
     (F32, 7, 32, 16, [70, 33], False, (True, True)),       # eight waves, one owning only a padded head
     (F32, 13, 16, 32, [60, 21], True, (False, True)),      # eight waves over 16 padded heads
+    (F32, 4, 16, 48, [57, 30, 1], False, (True, True)),    # D = 16 with wide C: every variant
+    (F32, 6, 16, 64, [45, 20], True, (True, True)),
+    (F32, 16, 16, 48, [40, 17], False, (True, False)),
 ]
 
 FWD_GROUPS = [(1 << 8, 1 << 9), (1 << 17, 1 << 18), (1 << 19, 1 << 20, 1 << 21, 1 << 29)]
