@@ -7,7 +7,9 @@ declared in include/flash_spacetime.h. Usage: python -m flash_spacetime_amd.buil
 
 from __future__ import annotations
 
+import json
 import os
+import re
 import shutil
 import subprocess
 import sys
@@ -70,16 +72,40 @@ def _units():
     return [u for u in units if u[1].exists()]
 
 
+RESOURCES = BUILD / "kernel_resources.json"
+_REMARK = re.compile(r"remark:\s+(Function Name|VGPRs|AGPRs|ScratchSize \[bytes/lane\]|Occupancy \[waves/SIMD\]"
+                     r"|LDS Size \[bytes/block\]): (\S+)")
+_KEYS = {"VGPRs": "vgpr", "AGPRs": "agpr", "ScratchSize [bytes/lane]": "scratch_bytes",
+         "Occupancy [waves/SIMD]": "waves_per_simd", "LDS Size [bytes/block]": "static_lds_bytes"}
+
+
+def _resources(text):
+    """Per-kernel register, scratch and occupancy figures from the compiler's
+    kernel-resource-usage remarks of one unit (the code object's own counts)."""
+    out, cur = {}, None
+    for line in text.splitlines():
+        m = _REMARK.search(line)
+        if not m:
+            continue
+        key, val = m.group(1), m.group(2)
+        if key == "Function Name":
+            cur = out.setdefault(val, {})
+        elif cur is not None:
+            cur[_KEYS[key]] = int(val)
+    return out
+
+
 def _compile(unit):
     name, src, defs = unit
     obj = BUILD / f"{name}.o"
-    cmd = [HIPCC, *FLAGS, *defs, "-c", str(src), "-o", str(obj)]
+    cmd = [HIPCC, *FLAGS, *defs, "-c", str(src), "-o", str(obj), "-Rpass-analysis=kernel-resource-usage"]
     res = subprocess.run(cmd, capture_output=True, text=True)
+    text = res.stdout + res.stderr
     out = "\n".join(
-        line for line in (res.stdout + res.stderr).splitlines()
-        if "packed-fp32-ops" not in line
+        line for line in text.splitlines()
+        if "packed-fp32-ops" not in line and "-Rpass-analysis=kernel-resource-usage" not in line
     )
-    return name, obj, res.returncode, out
+    return name, obj, res.returncode, out, _resources(text)
 
 
 def build(jobs: int | None = None, verbose: bool = False) -> Path:
@@ -90,11 +116,15 @@ def build(jobs: int | None = None, verbose: bool = False) -> Path:
     with ThreadPoolExecutor(max_workers=jobs) as pool:
         results = list(pool.map(_compile, units))
     failed = [r for r in results if r[2] != 0]
-    for name, _, rc, out in results:
+    for name, _, rc, out, _ in results:
         if out.strip() and (verbose or rc != 0):
             print(f"--- {name} ---\n{out}", file=sys.stderr)
     if failed:
         raise RuntimeError("hipcc failed for: " + ", ".join(r[0] for r in failed))
+    resources = {}
+    for r in results:
+        resources.update(r[4])
+    RESOURCES.write_text(json.dumps(resources, indent=0, sort_keys=True))
     tmp = LIB.with_suffix(".so.tmp")
     cmd = [HIPCC, f"--offload-arch={ARCH}", "-shared", "-o", str(tmp), *(str(r[1]) for r in results)]
     res = subprocess.run(cmd, capture_output=True, text=True)

@@ -61,15 +61,6 @@
 #ifndef FST_ROWS_KC
 #define FST_ROWS_KC 16
 #endif
-#ifndef FST_ROWS_WPE
-#define FST_ROWS_WPE 2
-#endif
-#ifndef FST_ROWS_W8X2_WPE
-#define FST_ROWS_W8X2_WPE 4
-#endif
-#ifndef FST_ROWS_KC8
-#define FST_ROWS_KC8 16
-#endif
 
 namespace fst {
 
@@ -1226,8 +1217,7 @@ struct Bwd2Pick {
   static constexpr bool LIGHT = rows_wave_load(HP, D, C) < 160;
   static constexpr bool ROWS_W4 = Rows2Cfg<HP, D, C, KC, 4>::FITS && LIGHT;
   static constexpr bool ROWS_W8 = HP % 8 == 0 && Rows2Cfg<HP, D, C, KC, 8>::FITS;
-  static constexpr int KC8 = FST_ROWS_KC8;
-  static constexpr bool ROWS_W8X2 = Rows2Cfg<HP, D, C, KC8, 8, FST_ROWS_W8X2_WPE>::FITS && LIGHT;
+  static constexpr bool ROWS_W8X2 = Rows2Cfg<HP, D, C, KC, 8, 4>::FITS && LIGHT;
   static constexpr bool KL_W4 = ROWS_W4 && Rows2Cfg<HP, D, C, KC, 4, 2, true>::FITS;
   static constexpr bool KL_W8X2 = ROWS_W8X2 && Rows2Cfg<HP, D, C, KC, 8, 4, true>::FITS;
   using CC = Cols2Cfg<HP, D, C, RC>;
@@ -1244,10 +1234,10 @@ struct Bwd2Pick {
   static constexpr int COLS_STATIC = COLS_OCC3 ? 3 : 2;
 };
 
-template <int HP, int D, int C, int NW, int WPE, bool KL, int KCX = FST_ROWS_KC>
+template <int HP, int D, int C, int NW, int WPE, bool KL>
 int bwd2_launch_rows(const BwdParams& prm, hipStream_t stream, int g8, bool query) {
   using P = Bwd2Pick<HP, D, C>;
-  using Cfg = Rows2Cfg<HP, D, C, KCX, NW, WPE, KL>;
+  using Cfg = Rows2Cfg<HP, D, C, P::KC, NW, WPE, KL>;
   if constexpr (!Cfg::FITS) {
     return FST_EUNSUPPORTED;
   } else {
@@ -1255,10 +1245,10 @@ int bwd2_launch_rows(const BwdParams& prm, hipStream_t stream, int g8, bool quer
     // With the forward's output the rows kernel forms dS against a reference
     // D from it and corrects once at the end; without, D is formed online.
     const bool fb = (prm.flags & 3) == 3;
-    auto kern = prm.out ? (fb ? bwd_rows2_kernel<HP, D, C, KCX, P::HB, 3, NW, WPE, KL, true>
-                              : bwd_rows2_kernel<HP, D, C, KCX, P::HB, -1, NW, WPE, KL, true>)
-                        : (fb ? bwd_rows2_kernel<HP, D, C, KCX, P::HB, 3, NW, WPE, KL, false>
-                              : bwd_rows2_kernel<HP, D, C, KCX, P::HB, -1, NW, WPE, KL, false>);
+    auto kern = prm.out ? (fb ? bwd_rows2_kernel<HP, D, C, P::KC, P::HB, 3, NW, WPE, KL, true>
+                              : bwd_rows2_kernel<HP, D, C, P::KC, P::HB, -1, NW, WPE, KL, true>)
+                        : (fb ? bwd_rows2_kernel<HP, D, C, P::KC, P::HB, 3, NW, WPE, KL, false>
+                              : bwd_rows2_kernel<HP, D, C, P::KC, P::HB, -1, NW, WPE, KL, false>);
     if (hipFuncSetAttribute((const void*)kern, hipFuncAttributeMaxDynamicSharedMemorySize, Cfg::LDS_BYTES) !=
         hipSuccess)
       return FST_ELAUNCH;
@@ -1315,7 +1305,7 @@ static int bwd2_launch_t(const BwdParams& prm, int which, hipStream_t stream, in
                                                  : P::ROWS_STATIC;
     if (waves == 1) {
       if constexpr (P::ROWS_W4) {
-        if (!kl) return bwd2_launch_rows<HP, D, C, 4, FST_ROWS_WPE, false>(prm, stream, g8, query);
+        if (!kl) return bwd2_launch_rows<HP, D, C, 4, 2, false>(prm, stream, g8, query);
         if constexpr (P::KL_W4) return bwd2_launch_rows<HP, D, C, 4, 2, true>(prm, stream, g8, query);
       }
       return FST_EUNSUPPORTED;
@@ -1326,7 +1316,7 @@ static int bwd2_launch_t(const BwdParams& prm, int which, hipStream_t stream, in
       return FST_EUNSUPPORTED;
     }
     if constexpr (P::ROWS_W8X2) {
-      if (!kl) return bwd2_launch_rows<HP, D, C, 8, FST_ROWS_W8X2_WPE, false, P::KC8>(prm, stream, g8, query);
+      if (!kl) return bwd2_launch_rows<HP, D, C, 8, 4, false>(prm, stream, g8, query);
       if constexpr (P::KL_W8X2) return bwd2_launch_rows<HP, D, C, 8, 4, true>(prm, stream, g8, query);
     }
     return FST_EUNSUPPORTED;

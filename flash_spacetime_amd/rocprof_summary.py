@@ -222,8 +222,8 @@ def main():
 
     traffic = {}
     lines = ["| kernel | launches | avg duration (us) | timing-loop avg (us) | FETCH_SIZE (KiB) | WRITE_SIZE (KiB) "
-             "| HBM bytes / launch (scaled) | grid | VGPR | AGPR | LDS (B) |",
-             "|---|---|---|---|---|---|---|---|---|---|---|"]
+             "| HBM bytes / launch (scaled) | grid | LDS (B) |",
+             "|---|---|---|---|---|---|---|---|---|"]
     for ph in ("fwd", "bwd_rows", "bwd_cols", "bwd_reduce_seg", "bwd_reduce_final", "worklist", "worklist_sort"):
         if ph not in stats:
             continue
@@ -239,7 +239,7 @@ def main():
         lines.append(f"| {ph} | {stats[ph]['calls']} | {stats[ph]['avg_us']:.1f} | {lp} | "
                      f"{'' if fk is None else f'{fk:.0f}'} | {'' if wk is None else f'{wk:.0f}'} | "
                      f"{'' if nbytes is None else f'{nbytes:.4g}'} | {m.get('Grid_Size', '')} | "
-                     f"{m.get('VGPR_Count', '')} | {m.get('Accum_VGPR_Count', '')} | {m.get('LDS_Block_Size', '')} |")
+                     f"{m.get('LDS_Block_Size', '')} |")
     md = "\n".join([
         *(["Command:", "", "```", args.command, "```", ""] if args.command else []),
         f"Calibration: fp32 multiply-by-1 over {args.calib_bytes / 2 ** 30:.2f} GiB read + the same written: "
