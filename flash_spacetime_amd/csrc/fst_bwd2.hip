@@ -857,6 +857,7 @@ __global__ __launch_bounds__(256, OCC) void bwd_cols2_kernel(BwdParams prm) {
   EventSpec ev = prm.ev;
   ev.blkcum = prm.blkcum_cols;
   ev.scum = prm.scum_cols;
+  ev.vp = nullptr;  // the interleaved schedule (the padding-last one is the rows kernel's)
   EventBlock eb;
   if (!tile_block(ev, blockIdx.x, eb)) return;
   const int len = eb.len;

@@ -200,6 +200,51 @@ __device__ void sanitize_steps(const int32_t* cu, int B, int T, int32_t* cus, in
   if (t == 0) *status = bad;
 }
 
+// Exclusive prefix sums of val(i), i < n, into out[0 .. n] (out[0] = 0);
+// one workgroup, chunks of 1024 with a carry.
+template <typename F>
+__device__ void scan_steps(int n, F val, int32_t* out, int* buf, int& carry) {
+  const int t = threadIdx.x;
+  if (t == 0) {
+    carry = 0;
+    out[0] = 0;
+  }
+  __syncthreads();
+  for (int base = 0; base < n; base += 1024) {
+    const int i = base + t;
+    buf[t] = i < n ? val(i) : 0;
+    __syncthreads();
+    for (int off = 1; off < 1024; off <<= 1) {
+      const int add = t >= off ? buf[t - off] : 0;
+      __syncthreads();
+      buf[t] += add;
+      __syncthreads();
+    }
+    if (i < n) out[i + 1] = carry + buf[t];
+    __syncthreads();
+    if (t == 1023) carry += buf[1023];
+    __syncthreads();
+  }
+}
+
+// The padding-last schedule's prefix sums (EventSpec::vp): valid 16-row tiles
+// of the padded events in XCD order, entry x S + j for XCD x's j-th event
+// (rank 8 j + (j odd ? 7 - x : x), as tile_block deals them), 0 past the
+// events; an empty event keeps one tile (its zero dW / db slot).
+__device__ void valid_tiles_steps(const EventSpec& ev, const int32_t* perm, int32_t* vp, int* buf, int& carry) {
+  const int B = ev.B, S = (B + 7) >> 3;
+  scan_steps(
+      8 * S,
+      [&](int idx) {
+        const int x = idx / S, j = idx - x * S, r = 8 * j + ((j & 1) ? 7 - x : x);
+        if (r >= B) return 0;
+        int tok0, len;
+        event_range(ev, perm[r], tok0, len);
+        return len > 0 ? (len + 15) >> 4 : 1;
+      },
+      vp, buf, carry);
+}
+
 // The work list of one operator call in one launch (one workgroup, steps
 // separated by barriers, which also order the global writes of perm before
 // their reads): for packed events the sanitised offsets and the call status
@@ -210,7 +255,7 @@ __device__ void sanitize_steps(const int32_t* cu, int B, int T, int32_t* cus, in
 __global__ __launch_bounds__(1024) void worklist_kernel(const int32_t* lens, int packed, int B, int L, int T,
                                                         int rows_a, int32_t* blk_a, int rows_b, int32_t* blk_b,
                                                         int32_t* perm, int32_t* scum_a, int32_t* scum_b,
-                                                        int32_t* cus, int32_t* status) {
+                                                        int32_t* cus, int32_t* status, int32_t* vp) {
   extern __shared__ int keys[];
   __shared__ int buf[1024];
   __shared__ int carry;
@@ -232,11 +277,12 @@ __global__ __launch_bounds__(1024) void worklist_kernel(const int32_t* lens, int
   __syncthreads();
   if (scum_a) blkcum_steps(ev, rows_a, perm, scum_a, buf, carry);
   if (scum_b) blkcum_steps(ev, rows_b, perm, scum_b, buf, carry);
+  if (vp && !packed) valid_tiles_steps(ev, perm, vp, buf, carry);
 }
 
 static int launch_worklist(const int32_t* lens, bool packed, int B, int L, int T, int rows_a, int32_t* blk_a,
                            int rows_b, int32_t* blk_b, int32_t* perm, int32_t* scum_a, int32_t* scum_b,
-                           int32_t* cus, int32_t* status, hipStream_t st) {
+                           int32_t* cus, int32_t* status, hipStream_t st, int32_t* vp = nullptr) {
   int p2 = 1;
   while (p2 < B && p2 < kSortMax) p2 <<= 1;
   const int lds = B > kSortMax ? 0 : p2 * (int)sizeof(int);
@@ -244,7 +290,8 @@ static int launch_worklist(const int32_t* lens, bool packed, int B, int L, int T
                           kSortMax * (int)sizeof(int)) != hipSuccess)
     return FST_ELAUNCH;
   hipLaunchKernelGGL(worklist_kernel, dim3(1), dim3(1024), lds, st, lens, packed ? 1 : 0, B, L, T, rows_a, blk_a,
-                     rows_b, blk_b, perm, packed ? scum_a : nullptr, packed ? scum_b : nullptr, cus, status);
+                     rows_b, blk_b, perm, packed ? scum_a : nullptr, packed ? scum_b : nullptr, cus, status,
+                     packed ? nullptr : vp);
   return hipGetLastError() == hipSuccess ? FST_OK : FST_ELAUNCH;
 }
 
@@ -434,7 +481,7 @@ __global__ __launch_bounds__(256) void fill_zero_kernel(float* p, int n) {
 struct BwdLayout {
   int rows_r, rows_c;   // rows (keys) per workgroup of the rows / cols kernels
   long grid_r, grid_c;
-  size_t off_bc_r, off_bc_c, off_u, off_wt, off_qt, off_dob, off_dsum, off_lsez, off_part, off_seg, total;
+  size_t off_bc_r, off_bc_c, off_vp, off_u, off_wt, off_qt, off_dob, off_dsum, off_lsez, off_part, off_seg, total;
   long nseg;  // stage-1 runs of the dW reduction
 };
 
@@ -457,6 +504,9 @@ static int bwd_layout(int dtype, int flags, int B, int H, int L, int T, int D, i
   off += blkcum_bytes(B);
   lay.off_bc_c = off;
   off += blkcum_bytes(B);
+  // The rows kernel's padding-last schedule (bf16, padded).
+  lay.off_vp = off;
+  off += align_up((size_t)(8 * ((B + 7) / 8) + 1) * sizeof(int32_t), 256);
   // u and w~ hold whole 16-row tiles of each event (the bf16 kernels' row-group
   // layout): at most B ceil(L / 16) tiles padded, T / 16 + B packed.
   const long rows_uw = packed ? ((long)(T + 15) / 16 + B) * 16 : (long)B * ((L + 15) / 16) * 16;
@@ -744,9 +794,12 @@ int fst_backward_phases(int phases, int dtype, int flags, int B, int H, int L, i
 
   unsigned char* ws = reinterpret_cast<unsigned char*>(workspace);
   const WorkList wr = worklist_at(ws + lay.off_bc_r, B), wc = worklist_at(ws + lay.off_bc_c, B);
+  // The bf16 rows kernel's padding-last schedule (16-row tiles, padded events).
+  int32_t* vp = (dtype == FST_BF16 && !packed && lay.rows_r == 16) ? reinterpret_cast<int32_t*>(ws + lay.off_vp)
+                                                                    : nullptr;
   if (phases & FST_PHASE_WORKLIST) {
     if (launch_worklist(lens, packed, B, L, T, lay.rows_r, wr.blkcum, lay.rows_c, wc.blkcum, wr.perm, wr.scum,
-                        wc.scum, wr.cus, wr.status, st) != FST_OK)
+                        wc.scum, wr.cus, wr.status, st, vp) != FST_OK)
       return fail(FST_ELAUNCH, "work-list kernel launch failed");
   }
 
@@ -756,6 +809,7 @@ int fst_backward_phases(int phases, int dtype, int flags, int B, int H, int L, i
   prm.ev.blkcum = wr.blkcum;
   prm.ev.perm = wr.perm;
   prm.ev.scum = packed ? wr.scum : nullptr;
+  prm.ev.vp = vp;
   prm.ev.status = wr.status;
   prm.ev.max_len = max_event_len(dtype, flags, H, D, C);
   prm.ev.pos4 = reinterpret_cast<const float4*>(pos4);

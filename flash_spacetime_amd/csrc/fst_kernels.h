@@ -16,6 +16,10 @@ struct EventSpec {
   const int32_t* blkcum;  // [B+1] prefix sums of row blocks per event
   const int32_t* perm;    // [B] events by decreasing length (the tile kernels' schedules)
   const int32_t* scum;    // [B+1] packed: prefix sums of row blocks in perm order (or null)
+  // [8 ceil(B / 8) + 1] padded: prefix sums of the valid (not padding-only)
+  // 16-row tiles over the events in XCD order (entry x S + j: XCD x's j-th
+  // event, S = ceil(B / 8)), for tile_block's padding-last schedule; or null.
+  const int32_t* vp;
   const float4* pos4;     // [B*L] or [T] (x, y, z, t) fp32
   const int32_t* status;  // the work list's verdict on the call's lengths: 0 = well formed (or null)
   int B, H, L, T, packed;
