@@ -398,7 +398,7 @@ __global__ __launch_bounds__(64 * NW, WPE) void bwd_rows2_kernel(BwdParams prm) 
       if (attn) *reinterpret_cast<f32x4*>(stU + so_p) = ue_p;
       if (act) *reinterpret_cast<f32x4*>(stW + so_p) = we_p;
     }
-    __syncthreads();  // u.E, w~.E staged
+    lds_barrier();  // u.E, w~.E staged
 
     // ---- head-owner: P, dP, online D, dS, dQ (phase by phase over batches
     // of HB heads, so the heads' dependency chains overlap) ----
@@ -529,11 +529,11 @@ __global__ __launch_bounds__(64 * NW, WPE) void bwd_rows2_kernel(BwdParams prm) 
       __builtin_amdgcn_sched_barrier(0);
     }
     if constexpr (!KL) issue(j0 + KC);
-    __syncthreads();  // P, dS and D increments staged
+    lds_barrier();  // P, dS and D increments staged
     // KL: the next chunk's positions go out here, its K and V loads at the
-    // end of the chunk: a barrier's release fence waits for loads into LDS,
-    // and so does every transposing LDS read the compiler cannot tell apart
-    // from their destination (the E reads below).
+    // end of the chunk: every transposing LDS read the compiler cannot tell
+    // apart from their destination (the E reads below) waits for loads into
+    // LDS in flight.
     if constexpr (KL) issue_pos(j0 + KC);
 
     // ---- row-owner: H -= dD G; H += E^T dS; G += E^T P ----
@@ -1071,8 +1071,10 @@ __global__ __launch_bounds__(256, OCC) void bwd_cols2_kernel(BwdParams prm) {
       rsc[sc_h * RC + sc_r] = i0c + sc_r < len ? sc_lraw : INFINITY;  // rows past the event: P = 0
       rsc[16 * RC + sc_h * RC + sc_r] = sc_draw;
     }
-    if constexpr (QL) wait_vmem();  // this wave's direct-to-LDS rows have landed
-    __syncthreads();  // u.E, w~.E, the row scalars (and the qt / dO rows) staged
+    lds_barrier();  // u.E, w~.E and the row scalars staged
+    // QL: this wave's own direct-to-LDS qt / dO rows (read by it alone) have
+    // landed; waited for after the barrier, before the next rows' loads.
+    if constexpr (QL) wait_vmem();
     if constexpr (QL) issue_rows(i0c + RC);
 
     // ---- head-owner: P, dS, dV^T += dO^T P, dK^T += Qt^T dS ----

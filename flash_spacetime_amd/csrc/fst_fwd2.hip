@@ -17,7 +17,9 @@
 //    lanes) and kept in LDS for A^T_i += E_i^T P_i^T (A = sum_j p_ij E_ij).
 // The roles meet in LDS: u.E goes row-owner -> head-owner (fp32), P and the
 // rescale factors head-owner -> row-owner; E is private to the wave that
-// computed it. Two barriers per key chunk.
+// computed it. Two barriers per key chunk, LDS-only (lds_barrier): a
+// workgroup fence there would also wait for the V rows' direct loads in
+// flight.
 //
 // K comes from global memory in row-major operand layout. Where the LDS plan
 // allows (D a multiple of 32), each chunk's V rows go straight to LDS by
@@ -264,7 +266,7 @@ __global__ __launch_bounds__(256, OCC) void fwd2_kernel(FwdParams prm) {
           __builtin_amdgcn_sched_barrier(0);
         }
     }
-    __syncthreads();  // u.E staged
+    lds_barrier();  // u.E staged
 
     // ---- head-owner: logits, online softmax, P V (phase by phase over the
     // wave's heads, so the heads' dependency chains overlap) ----
@@ -376,7 +378,7 @@ __global__ __launch_bounds__(256, OCC) void fwd2_kernel(FwdParams prm) {
       rflag[w] = rescale ? 1 : 0;
     }
     issue(j0 + KC);
-    __syncthreads();  // P and rescale factors staged
+    lds_barrier();  // P and rescale factors staged
 
     // ---- row-owner: A = alpha A + E^T P ----
     if (act) {

@@ -443,6 +443,13 @@ struct LdsFrag {
 // Completion of this wave's outstanding buffer loads (including loads into
 // LDS), ordered against every later memory access of the wave.
 __device__ __forceinline__ void wait_vmem() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+// Workgroup barrier for exchanges through LDS: this wave's LDS accesses are
+// complete before it. Unlike __syncthreads() it does not wait for the wave's
+// outstanding buffer loads, loads into LDS included (the compiler's
+// workgroup release fence waits for all of those when any load into LDS is
+// in flight); a wave reads what its own loads put in LDS only after waiting
+// for them itself.
+__device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 
 // ---------------------------------------------------------------------------
 // LDS layouts.
