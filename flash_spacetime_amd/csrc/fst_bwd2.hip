@@ -239,8 +239,10 @@ __global__ __launch_bounds__(64 * NW, WPE) void bwd_rows2_kernel(BwdParams prm) 
   // KL: lane l of a block load fetches the quarter QoTile keeps in slot l;
   // keys past the event are clamped to its last key (their P is zero).
   const int kl_r = lane >> 2, kl_c = (lane & 3) ^ QoTile::swz(kl_r);
-  auto issue = [&](int jn) __attribute__((always_inline)) {
-    const bool full = jn + KC <= len;
+  // NF: chunk jn is known to be whole (no clamped keys), so its addresses
+  // need no selects.
+  auto issue = [&](int jn, auto nf_tag) __attribute__((always_inline)) {
+    const bool full = decltype(nf_tag)::value || jn + KC <= len;
     if constexpr (KL) {
       const int rel = full ? kl_r * rowb : min(jn + kl_r, last) * rowb;
       const int soff = full ? jn * rowb : 0;
@@ -272,18 +274,23 @@ __global__ __launch_bounds__(64 * NW, WPE) void bwd_rows2_kernel(BwdParams prm) 
   };
   // Key positions run one chunk further ahead: they are needed first thing
   // in a chunk.
-  auto issue_pos = [&](int jn) __attribute__((always_inline)) {
+  auto issue_pos = [&](int jn, auto nf_tag) __attribute__((always_inline)) {
     if (use_e) {
 #pragma unroll
-      for (int s = 0; s < NS; ++s) pj[s] = pbuf.ldf4(min(jn + 16 * s + n, last) * 16, 0);
+      for (int s = 0; s < NS; ++s) {
+        if constexpr (decltype(nf_tag)::value)
+          pj[s] = pbuf.ldf4((16 * s + n) * 16, jn * 16);
+        else
+          pj[s] = pbuf.ldf4(min(jn + 16 * s + n, last) * 16, 0);
+      }
     }
   };
   // Every chunk issues the same loads in the same order (positions, then K
   // and V; past the last chunk they reread clamped keys), so the wait at the
   // top of a chunk covers the positions only and E is formed while K and V
   // are still in flight.
-  issue_pos(0);
-  issue(0);
+  issue_pos(0, std::false_type{});
+  issue(0, std::false_type{});
 
   // ---- prologue stores ----
   bf16* qtg = reinterpret_cast<bf16*>(prm.qt);
@@ -352,14 +359,15 @@ __global__ __launch_bounds__(64 * NW, WPE) void bwd_rows2_kernel(BwdParams prm) 
     for (int ct = 0; ct < NCT; ++ct) Hacc[r][ct] = Gacc[r][ct] = zero4();
   }
 
-  auto chunk = [&](int j0, auto tail_tag) __attribute__((always_inline)) {
+  // next_tag: the next chunk is whole (its prefetch addresses need no clamps).
+  auto chunk = [&](int j0, auto tail_tag, auto next_tag) __attribute__((always_inline)) {
     constexpr bool TAIL = decltype(tail_tag)::value;
     // ---- row-owner: E, u.E and w~.E of rows row0 .. row0 + RPW - 1 ----
     if (use_e) {
       float xg[NS][4];
 #pragma unroll
       for (int s = 0; s < NS; ++s) group_gather(pair_angle_unit(pos_i, pj[s]), xg[s]);
-      if constexpr (!KL) issue_pos(j0 + KC);
+      if constexpr (!KL) issue_pos(j0 + KC, next_tag);
       // Each (row, subtile)'s u.E and w~.E are stored after the next one's
       // embedding is formed, which covers the products' latency.
       f32x4 ue_p = zero4(), we_p = zero4();
@@ -528,13 +536,13 @@ __global__ __launch_bounds__(64 * NW, WPE) void bwd_rows2_kernel(BwdParams prm) 
       }
       __builtin_amdgcn_sched_barrier(0);
     }
-    if constexpr (!KL) issue(j0 + KC);
+    if constexpr (!KL) issue(j0 + KC, next_tag);
     lds_barrier();  // P, dS and D increments staged
     // KL: the next chunk's positions go out here, its K and V loads at the
     // end of the chunk: every transposing LDS read the compiler cannot tell
     // apart from their destination (the E reads below) waits for loads into
     // LDS in flight.
-    if constexpr (KL) issue_pos(j0 + KC);
+    if constexpr (KL) issue_pos(j0 + KC, next_tag);
 
     // ---- row-owner: H -= dD G; H += E^T dS; G += E^T P ----
     if (use_e) {
@@ -572,12 +580,16 @@ __global__ __launch_bounds__(64 * NW, WPE) void bwd_rows2_kernel(BwdParams prm) 
         }
       }
     }
-    if constexpr (KL) issue(j0 + KC);
+    if constexpr (KL) issue(j0 + KC, next_tag);
   };
 
   int j0 = 0;
-  for (; j0 + KC <= len; j0 += KC) chunk(j0, std::false_type{});
-  if (j0 < len) chunk(j0, std::true_type{});
+  for (; j0 + 2 * KC <= len; j0 += KC) chunk(j0, std::false_type{}, std::true_type{});
+  if (j0 + KC <= len) {
+    chunk(j0, std::false_type{}, std::false_type{});
+    j0 += KC;
+  }
+  if (j0 < len) chunk(j0, std::true_type{}, std::false_type{});
   // KL: the loads of the chunk past the last finish before the workgroup
   // ends.
   if constexpr (KL) wait_vmem();
@@ -974,9 +986,12 @@ __global__ __launch_bounds__(256, OCC) void bwd_cols2_kernel(BwdParams prm) {
       }
     }
   };
-  auto issue = [&](int in) __attribute__((always_inline)) {
+  // NF: chunk `in` is known to be whole (no clamped rows), so its addresses
+  // need no selects or clamps.
+  auto issue = [&](int in, auto nf_tag) __attribute__((always_inline)) {
+    constexpr bool NF = decltype(nf_tag)::value;
     if constexpr (!QL) {
-      const bool full = in + RC <= len;
+      const bool full = NF || in + RC <= len;
 #pragma unroll
       for (int hl = 0; hl < HW; ++hl) {
 #pragma unroll
@@ -988,7 +1003,11 @@ __global__ __launch_bounds__(256, OCC) void bwd_cols2_kernel(BwdParams prm) {
         }
       }
     }
-    {
+    if constexpr (NF) {
+      const int vo = (int)(sc_hc * ra.hs + sc_r * ra.ts) * 4, so = (int)(in * ra.ts) * 4;
+      sc_lraw = lbuf.ldf(vo, so);
+      sc_draw = dbuf.ldf(vo, so);
+    } else {
       const int vo = (int)(ra.vec(sc_hc, min(in + sc_r, last)) - ra.base_row) * 4;
       sc_lraw = lbuf.ldf(vo, 0);
       sc_draw = dbuf.ldf(vo, 0);
@@ -997,27 +1016,32 @@ __global__ __launch_bounds__(256, OCC) void bwd_cols2_kernel(BwdParams prm) {
   // Row positions and the u / w~ rows of the row-owner part run one chunk
   // further ahead: they are needed first thing in a chunk.
   bf16x4 ur[RGW][4][NCT], wr[RGW][4][NCT];
-  auto issue_rows = [&](int in) __attribute__((always_inline)) {
+  auto issue_rows = [&](int in, auto nf_tag) __attribute__((always_inline)) {
+    constexpr bool NF = decltype(nf_tag)::value;
     if (use_e) {
 #pragma unroll
       for (int q2 = 0; q2 < RGW; ++q2) {
         const int rg = RGW * w + q2;
-        prow[q2] = pbuf.ldf4(min(in + 4 * rg + g, last) * 16, 0);
+        if constexpr (NF)
+          prow[q2] = pbuf.ldf4((4 * rg + g) * 16, in * 16);
+        else
+          prow[q2] = pbuf.ldf4(min(in + 4 * rg + g, last) * 16, 0);
         // Groups past the event reread its last group: their rows carry
         // P = 0 (lse = +inf) in the head-owner part.
-        const int go = (int)(min((in >> 2) + rg, glast) * ggrp);
+        const int go = NF ? (int)(rg * ggrp) : (int)(min((in >> 2) + rg, glast) * ggrp);
+        const int gso = NF ? (int)((in >> 2) * ggrp) * 2 : 0;
 #pragma unroll
         for (int half = 0; half < 2; ++half)
 #pragma unroll
           for (int ct = 0; ct < NCT; ++ct) {
             const int co = (go + uw_off(half, ct, n, g, 0, H, NCT)) * 2;
             if (attn) {
-              const bf16x8 v = ubuf.ld128(co, 0);
+              const bf16x8 v = ubuf.ld128(co, gso);
               ur[q2][2 * half][ct] = lo4(v);
               ur[q2][2 * half + 1][ct] = hi4(v);
             }
             if (act) {
-              const bf16x8 v = wbuf.ld128(co, 0);
+              const bf16x8 v = wbuf.ld128(co, gso);
               wr[q2][2 * half][ct] = lo4(v);
               wr[q2][2 * half + 1][ct] = hi4(v);
             }
@@ -1028,10 +1052,11 @@ __global__ __launch_bounds__(256, OCC) void bwd_cols2_kernel(BwdParams prm) {
   // Every chunk issues the same loads in the same order (the row-owner's
   // rows, then the head-owner's; past the last chunk they reread clamped
   // rows), so each phase waits only for the loads it uses.
-  issue_rows(0);
-  issue(0);
+  issue_rows(0, std::false_type{});
+  issue(0, std::false_type{});
 
-  auto chunk = [&](int i0c, auto tail_tag) __attribute__((always_inline)) {
+  // next_tag: the next chunk is whole (its prefetch addresses need no clamps).
+  auto chunk = [&](int i0c, auto tail_tag, auto next_tag) __attribute__((always_inline)) {
     constexpr bool TAIL = decltype(tail_tag)::value;
     issue_qo(i0c);  // lands during the row-owner part
     // ---- row-owner: u_i E_i^T and w~_i E_i^T for its row groups ----
@@ -1066,7 +1091,7 @@ __global__ __launch_bounds__(256, OCC) void bwd_cols2_kernel(BwdParams prm) {
         }
       }
     }
-    if constexpr (!QL) issue_rows(i0c + RC);
+    if constexpr (!QL) issue_rows(i0c + RC, next_tag);
     if (sc_ok) {
       rsc[sc_h * RC + sc_r] = i0c + sc_r < len ? sc_lraw : INFINITY;  // rows past the event: P = 0
       rsc[16 * RC + sc_h * RC + sc_r] = sc_draw;
@@ -1075,7 +1100,7 @@ __global__ __launch_bounds__(256, OCC) void bwd_cols2_kernel(BwdParams prm) {
     // QL: this wave's own direct-to-LDS qt / dO rows (read by it alone) have
     // landed; waited for after the barrier, before the next rows' loads.
     if constexpr (QL) wait_vmem();
-    if constexpr (QL) issue_rows(i0c + RC);
+    if constexpr (QL) issue_rows(i0c + RC, next_tag);
 
     // ---- head-owner: P, dS, dV^T += dO^T P, dK^T += Qt^T dS ----
     f32x4 S[HW][NS], dP[HW][NS];
@@ -1148,13 +1173,17 @@ __global__ __launch_bounds__(256, OCC) void bwd_cols2_kernel(BwdParams prm) {
       }
     }
     (void)TAIL;
-    issue(i0c + RC);
+    issue(i0c + RC, next_tag);
     __syncthreads();  // the stage is read; the next chunk may overwrite it
   };
 
   int i0c = 0;
-  for (; i0c + RC <= len; i0c += RC) chunk(i0c, std::false_type{});
-  if (i0c < len) chunk(i0c, std::true_type{});
+  for (; i0c + 2 * RC <= len; i0c += RC) chunk(i0c, std::false_type{}, std::true_type{});
+  if (i0c + RC <= len) {
+    chunk(i0c, std::false_type{}, std::false_type{});
+    i0c += RC;
+  }
+  if (i0c < len) chunk(i0c, std::true_type{}, std::false_type{});
 
   // ---- store dk, dv (lane n = key) ----
   // With the tiles in LDS (QL) accumulator q holds features 16 q + 4 g + r

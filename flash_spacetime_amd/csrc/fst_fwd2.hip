@@ -165,8 +165,10 @@ __global__ __launch_bounds__(256, OCC) void fwd2_kernel(FwdParams prm) {
   // are still in flight.
   KFrag<bf16, D> kf[HW][NS], vf[VL ? 1 : HW][NS];
   float4 pj[NS];
-  auto issue = [&](int jn) __attribute__((always_inline)) {
-    const bool full = jn + KC <= len;
+  // NF: chunk jn is known to be whole (no clamped keys), so its addresses
+  // need no selects.
+  auto issue = [&](int jn, auto nf_tag) __attribute__((always_inline)) {
+    const bool full = decltype(nf_tag)::value || jn + KC <= len;
 #pragma unroll
     for (int hl = 0; hl < HW; ++hl) {
 #pragma unroll
@@ -200,14 +202,19 @@ __global__ __launch_bounds__(256, OCC) void fwd2_kernel(FwdParams prm) {
   };
   // Key positions run one chunk further ahead: they are needed first thing
   // in a chunk.
-  auto issue_pos = [&](int jn) __attribute__((always_inline)) {
+  auto issue_pos = [&](int jn, auto nf_tag) __attribute__((always_inline)) {
     if (use_e) {
 #pragma unroll
-      for (int s = 0; s < NS; ++s) pj[s] = pbuf.ldf4(min(jn + 16 * s + n, last) * 16, 0);
+      for (int s = 0; s < NS; ++s) {
+        if constexpr (decltype(nf_tag)::value)
+          pj[s] = pbuf.ldf4((16 * s + n) * 16, jn * 16);
+        else
+          pj[s] = pbuf.ldf4(min(jn + 16 * s + n, last) * 16, 0);
+      }
     }
   };
-  issue_pos(0);
-  issue(0);
+  issue_pos(0, std::false_type{});
+  issue(0, std::false_type{});
 
 #pragma unroll
   for (int hl = 0; hl < HW; ++hl) {
@@ -235,7 +242,8 @@ __global__ __launch_bounds__(256, OCC) void fwd2_kernel(FwdParams prm) {
     for (int ct = 0; ct < NCT; ++ct) AE[r][ct] = zero4();
   }
 
-  auto chunk = [&](int j0, auto tail_tag) __attribute__((always_inline)) {
+  // next_tag: the next chunk is whole (its prefetch addresses need no clamps).
+  auto chunk = [&](int j0, auto tail_tag, auto next_tag) __attribute__((always_inline)) {
     constexpr bool TAIL = decltype(tail_tag)::value;
     issue_v(j0);  // lands during the row-owner part
 
@@ -244,7 +252,7 @@ __global__ __launch_bounds__(256, OCC) void fwd2_kernel(FwdParams prm) {
       float xg[NS][4];
 #pragma unroll
       for (int s = 0; s < NS; ++s) group_gather(pair_angle_unit(pos_i, pj[s]), xg[s]);
-      issue_pos(j0 + KC);
+      issue_pos(j0 + KC, next_tag);
 #pragma unroll
       for (int r = 0; r < 4; ++r)
 #pragma unroll
@@ -377,7 +385,7 @@ __global__ __launch_bounds__(256, OCC) void fwd2_kernel(FwdParams prm) {
       }
       rflag[w] = rescale ? 1 : 0;
     }
-    issue(j0 + KC);
+    issue(j0 + KC, next_tag);
     lds_barrier();  // P and rescale factors staged
 
     // ---- row-owner: A = alpha A + E^T P ----
@@ -422,8 +430,12 @@ __global__ __launch_bounds__(256, OCC) void fwd2_kernel(FwdParams prm) {
   };
 
   int j0 = 0;
-  for (; j0 + KC <= len; j0 += KC) chunk(j0, std::false_type{});
-  if (j0 < len) chunk(j0, std::true_type{});
+  for (; j0 + 2 * KC <= len; j0 += KC) chunk(j0, std::false_type{}, std::true_type{});
+  if (j0 + KC <= len) {
+    chunk(j0, std::false_type{}, std::false_type{});
+    j0 += KC;
+  }
+  if (j0 < len) chunk(j0, std::true_type{}, std::false_type{});
 
   // ---- epilogue ----
   float inv_l[HW];
