@@ -147,7 +147,10 @@ __global__ __launch_bounds__(64 * NW, WPE) void bwd_rows2_kernel(BwdParams prm) 
   // empty padded event owns one slot, written as zeros); tiles of padding
   // rows past an event's last tile own none.
   const int nbv = len > 0 ? (len + 15) / 16 : (prm.ev.packed ? 0 : 1);
-  float* part = eb.blk < nbv ? prm.dw_part + (long)(prm.ev.blkcum[eb.b] + eb.blk) * DCW : nullptr;
+  // The tile's slot in the work list (read once: after the prologue's
+  // stores it would be read again, waiting for every load before it).
+  const long tslot = (long)prm.ev.blkcum[eb.b] + eb.blk;
+  float* part = eb.blk < nbv ? prm.dw_part + tslot * DCW : nullptr;
   if (event_refused(prm.ev, eb)) {
     fill_rows_nan<bf16, D>(rx, ra, i0, min(i0 + 16, len), H, tid, NT, dqg, prm.rowsum);
     if (part)
@@ -196,6 +199,29 @@ __global__ __launch_bounds__(64 * NW, WPE) void bwd_rows2_kernel(BwdParams prm) 
     dof[hl].load(dog + ra.off(hc, rc, D), g);
     if constexpr (ORF) of[hl].load(reinterpret_cast<const bf16*>(prm.out) + ra.off(hc, rc, D), g);
     lse2[hl] = prm.lse[ra.vec(hc, rc)];
+  }
+  // ORF: the bias slots of the reference D, loaded once with the other
+  // prologue loads (read after the prologue's stores, they would be loaded
+  // again for every head, each time after every load before them).
+  float bsl[ORF ? KFrag<bf16, D>::SLOTS : 1];
+  if constexpr (ORF) {
+    // Buffer loads, without branches: an empty range (no bias, or the bias
+    // off) reads as zeros.
+    using KF = KFrag<bf16, D>;
+    const Buf bb(prm.bias, act && prm.bias ? D * 4 : 0);
+#pragma unroll
+    for (int t = 0; t < KF::N32; ++t)
+#pragma unroll
+      for (int e = 0; e < 8; e += 4) {
+        const float4 v = bb.ldf4((32 * t + 8 * g + e) * 4, 0);
+        bsl[8 * t + e] = v.x, bsl[8 * t + e + 1] = v.y, bsl[8 * t + e + 2] = v.z, bsl[8 * t + e + 3] = v.w;
+      }
+#pragma unroll
+    for (int t = 0; t < KF::N16; ++t) {
+      const float4 v = bb.ldf4((16 * t + 4 * g) * 4, 0);
+      float* o = bsl + 8 * KF::N32 + 4 * t;
+      o[0] = v.x, o[1] = v.y, o[2] = v.z, o[3] = v.w;
+    }
   }
 
   // ---- row-owner state: rows i0 + row0 + r (r < RPW), heads on lane n ----
@@ -298,14 +324,15 @@ __global__ __launch_bounds__(64 * NW, WPE) void bwd_rows2_kernel(BwdParams prm) 
   for (int hl = 0; hl < HW; ++hl) {
     const int h = head(hl);
     const bool ok = h < H && row_ok;
-    if (ok) {
-      qf[hl].scale_by(prm.scale);
-    } else {
-      qf[hl].zero();
-      dof[hl].zero();
-    }
+    // Without branches: loads whose values a branch alone uses would be sunk
+    // into it by the compiler, each then waited for with every load before it.
+    qf[hl].scale_by(prm.scale);
+    qf[hl].keep_if(ok);
+    dof[hl].keep_if(ok);
     // Invalid rows get lse = +inf, so their P (and dS) are exactly zero.
-    lse2[hl] = ok ? lse2[hl] * kLog2e : INFINITY;
+    // (Added rather than selected: a select of the loaded value is turned
+    // into a branch that the load is sunk into.)
+    lse2[hl] = __builtin_fmaf(lse2[hl], kLog2e, ok ? 0.f : INFINITY);
     if (ok) {
       // qt for the cols kernel: the same bf16 values the logits use.
       bf16* qd = qtg + ra.off(h, my_row, D);
@@ -320,7 +347,7 @@ __global__ __launch_bounds__(64 * NW, WPE) void bwd_rows2_kernel(BwdParams prm) 
       // the same sum over the keys up to the output's rounding. dS is formed
       // against it and the accumulators are corrected to N / Z once, after
       // the last chunk.
-      const float part = ok ? dof[hl].dot_minus(of[hl], act ? prm.bias : nullptr, g) : 0.f;
+      const float part = dof[hl].dot_minus_slots(of[hl], bsl);  // 0 for invalid rows (dO zeroed)
       // Any finite reference gives the same D; a non-finite one (an output
       // that is not this forward's) falls back to 0.
       const float dref = group_allsum(part);
@@ -334,7 +361,7 @@ __global__ __launch_bounds__(64 * NW, WPE) void bwd_rows2_kernel(BwdParams prm) 
   // u and w~ of the row group go to the cols kernel's scratch; rows past the
   // event are written as zeros, so every row of a group the cols kernel
   // reads is defined.
-  const long uwg = ((long)prm.ev.blkcum[eb.b] + eb.blk) * 4 + (row0 >> 2);
+  const long uwg = tslot * 4 + (row0 >> 2);
   bf16* ug = reinterpret_cast<bf16*>(prm.u) + uwg * uw_group_elems(H, NCT);
   bf16* wtg = reinterpret_cast<bf16*>(prm.wt) + uwg * uw_group_elems(H, NCT);
 #pragma unroll
@@ -362,12 +389,16 @@ __global__ __launch_bounds__(64 * NW, WPE) void bwd_rows2_kernel(BwdParams prm) 
   // next_tag: the next chunk is whole (its prefetch addresses need no clamps).
   auto chunk = [&](int j0, auto tail_tag, auto next_tag) __attribute__((always_inline)) {
     constexpr bool TAIL = decltype(tail_tag)::value;
+    // No prefetch past the last chunk (its loads would only hold the
+    // epilogue back).
+    const bool more = decltype(next_tag)::value || j0 + KC < len;
     // ---- row-owner: E, u.E and w~.E of rows row0 .. row0 + RPW - 1 ----
     if (use_e) {
       float xg[NS][4];
 #pragma unroll
       for (int s = 0; s < NS; ++s) group_gather(pair_angle_unit(pos_i, pj[s]), xg[s]);
-      if constexpr (!KL) issue_pos(j0 + KC, next_tag);
+      if constexpr (!KL)
+        if (more) issue_pos(j0 + KC, next_tag);
       // Each (row, subtile)'s u.E and w~.E are stored after the next one's
       // embedding is formed, which covers the products' latency.
       f32x4 ue_p = zero4(), we_p = zero4();
@@ -536,13 +567,15 @@ __global__ __launch_bounds__(64 * NW, WPE) void bwd_rows2_kernel(BwdParams prm) 
       }
       __builtin_amdgcn_sched_barrier(0);
     }
-    if constexpr (!KL) issue(j0 + KC, next_tag);
+    if constexpr (!KL)
+      if (more) issue(j0 + KC, next_tag);
     lds_barrier();  // P, dS and D increments staged
     // KL: the next chunk's positions go out here, its K and V loads at the
     // end of the chunk: every transposing LDS read the compiler cannot tell
     // apart from their destination (the E reads below) waits for loads into
     // LDS in flight.
-    if constexpr (KL) issue_pos(j0 + KC, next_tag);
+    if constexpr (KL)
+      if (more) issue_pos(j0 + KC, next_tag);
 
     // ---- row-owner: H -= dD G; H += E^T dS; G += E^T P ----
     if (use_e) {
@@ -580,7 +613,8 @@ __global__ __launch_bounds__(64 * NW, WPE) void bwd_rows2_kernel(BwdParams prm) 
         }
       }
     }
-    if constexpr (KL) issue(j0 + KC, next_tag);
+    if constexpr (KL)
+      if (more) issue(j0 + KC, next_tag);
   };
 
   int j0 = 0;
@@ -1058,6 +1092,9 @@ __global__ __launch_bounds__(256, OCC) void bwd_cols2_kernel(BwdParams prm) {
   // next_tag: the next chunk is whole (its prefetch addresses need no clamps).
   auto chunk = [&](int i0c, auto tail_tag, auto next_tag) __attribute__((always_inline)) {
     constexpr bool TAIL = decltype(tail_tag)::value;
+    // No prefetch past the last chunk (its loads would only hold the
+    // epilogue back).
+    const bool more = decltype(next_tag)::value || i0c + RC < len;
     issue_qo(i0c);  // lands during the row-owner part
     // ---- row-owner: u_i E_i^T and w~_i E_i^T for its row groups ----
     if (use_e) {
@@ -1091,7 +1128,8 @@ __global__ __launch_bounds__(256, OCC) void bwd_cols2_kernel(BwdParams prm) {
         }
       }
     }
-    if constexpr (!QL) issue_rows(i0c + RC, next_tag);
+    if constexpr (!QL)
+      if (more) issue_rows(i0c + RC, next_tag);
     if (sc_ok) {
       rsc[sc_h * RC + sc_r] = i0c + sc_r < len ? sc_lraw : INFINITY;  // rows past the event: P = 0
       rsc[16 * RC + sc_h * RC + sc_r] = sc_draw;
@@ -1100,7 +1138,8 @@ __global__ __launch_bounds__(256, OCC) void bwd_cols2_kernel(BwdParams prm) {
     // QL: this wave's own direct-to-LDS qt / dO rows (read by it alone) have
     // landed; waited for after the barrier, before the next rows' loads.
     if constexpr (QL) wait_vmem();
-    if constexpr (QL) issue_rows(i0c + RC, next_tag);
+    if constexpr (QL)
+      if (more) issue_rows(i0c + RC, next_tag);
 
     // ---- head-owner: P, dS, dV^T += dO^T P, dK^T += Qt^T dS ----
     f32x4 S[HW][NS], dP[HW][NS];
@@ -1173,7 +1212,7 @@ __global__ __launch_bounds__(256, OCC) void bwd_cols2_kernel(BwdParams prm) {
       }
     }
     (void)TAIL;
-    issue(i0c + RC, next_tag);
+    if (more) issue(i0c + RC, next_tag);
     __syncthreads();  // the stage is read; the next chunk may overwrite it
   };
 

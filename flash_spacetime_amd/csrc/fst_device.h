@@ -140,6 +140,21 @@ struct KFrag<bf16, K> {
   bf16x8 x32[N32 > 0 ? N32 : 1];
   bf16x4 x16[N16 > 0 ? N16 : 1];
 
+  // Zero unless ok, without a branch (selects on the 32-bit words).
+  __device__ __forceinline__ void keep_if(bool ok) {
+    typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
+    typedef unsigned u32x2 __attribute__((ext_vector_type(2)));
+#pragma unroll
+    for (int t = 0; t < N32; ++t) {
+      const u32x4 v = __builtin_bit_cast(u32x4, x32[t]);
+      x32[t] = __builtin_bit_cast(bf16x8, ok ? v : u32x4{0u, 0u, 0u, 0u});
+    }
+#pragma unroll
+    for (int t = 0; t < N16; ++t) {
+      const u32x2 v = __builtin_bit_cast(u32x2, x16[t]);
+      x16[t] = __builtin_bit_cast(bf16x4, ok ? v : u32x2{0u, 0u});
+    }
+  }
   __device__ __forceinline__ void zero() {
 #pragma unroll
     for (int t = 0; t < N32; ++t)
@@ -179,19 +194,21 @@ struct KFrag<bf16, K> {
     load(p, g);
     scale_by(scale);
   }
-  // This lane's part of sum_k x_k (o_k - b_k) over the row (b nullable).
-  __device__ __forceinline__ float dot_minus(const KFrag& o, const float* b, int g) const {
+  // Per-lane feature slots (as dot_minus_slots takes them): N32 groups of
+  // 8 (features 32t + 8g ..), then N16 groups of 4 (features 16t + 4g ..).
+  static constexpr int SLOTS = N32 * 8 + N16 * 4;
+  // This lane's part of sum_k x_k (o_k - b_k) over the row, b in slots.
+  __device__ __forceinline__ float dot_minus_slots(const KFrag& o, const float* bs) const {
     float a = 0.f;
 #pragma unroll
     for (int t = 0; t < N32; ++t)
 #pragma unroll
-      for (int e = 0; e < 8; ++e)
-        a = __builtin_fmaf((float)x32[t][e], (float)o.x32[t][e] - (b ? b[32 * t + 8 * g + e] : 0.f), a);
+      for (int e = 0; e < 8; ++e) a = __builtin_fmaf((float)x32[t][e], (float)o.x32[t][e] - bs[8 * t + e], a);
 #pragma unroll
     for (int t = 0; t < N16; ++t)
 #pragma unroll
       for (int e = 0; e < 4; ++e)
-        a = __builtin_fmaf((float)x16[t][e], (float)o.x16[t][e] - (b ? b[16 * t + 4 * g + e] : 0.f), a);
+        a = __builtin_fmaf((float)x16[t][e], (float)o.x16[t][e] - bs[N32 * 8 + 4 * t + e], a);
     return a;
   }
 };

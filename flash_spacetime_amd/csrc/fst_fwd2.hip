@@ -218,10 +218,10 @@ __global__ __launch_bounds__(256, OCC) void fwd2_kernel(FwdParams prm) {
 
 #pragma unroll
   for (int hl = 0; hl < HW; ++hl) {
-    if (row_ok)
-      qf[hl].scale_by(prm.scale);
-    else
-      qf[hl].zero();
+    // Without a branch: the compiler would sink the q loads into it, each
+    // then waited for with every load before it.
+    qf[hl].scale_by(prm.scale);
+    qf[hl].keep_if(row_ok);
 #pragma unroll
     for (int q = 0; q < NQ; ++q) O[hl][q] = zero4();
     lsum[hl] = 0.f;
@@ -252,7 +252,9 @@ __global__ __launch_bounds__(256, OCC) void fwd2_kernel(FwdParams prm) {
       float xg[NS][4];
 #pragma unroll
       for (int s = 0; s < NS; ++s) group_gather(pair_angle_unit(pos_i, pj[s]), xg[s]);
-      issue_pos(j0 + KC, next_tag);
+      // No prefetch past the last chunk (its loads would only hold the
+      // epilogue back).
+      if (decltype(next_tag)::value || j0 + KC < len) issue_pos(j0 + KC, next_tag);
 #pragma unroll
       for (int r = 0; r < 4; ++r)
 #pragma unroll
@@ -385,7 +387,7 @@ __global__ __launch_bounds__(256, OCC) void fwd2_kernel(FwdParams prm) {
       }
       rflag[w] = rescale ? 1 : 0;
     }
-    issue(j0 + KC, next_tag);
+    if (decltype(next_tag)::value || j0 + KC < len) issue(j0 + KC, next_tag);
     lds_barrier();  // P and rescale factors staged
 
     // ---- row-owner: A = alpha A + E^T P ----
@@ -438,6 +440,38 @@ __global__ __launch_bounds__(256, OCC) void fwd2_kernel(FwdParams prm) {
   if (j0 < len) chunk(j0, std::true_type{}, std::false_type{});
 
   // ---- epilogue ----
+  // O's accumulator q holds features omap(q, g, r): 16 q + 4 g + r when V was
+  // read transposed from LDS, DTiles::dmap otherwise (four consecutive
+  // features either way).
+  auto omap = [&](int q, int gg, int r) { return VL ? 16 * q + 4 * gg + r : DT::dmap(q, gg, r); };
+  // The epilogue's operands are loaded first, ahead of the lse stores (the
+  // compiler would issue them only after those, on the epilogue's chain):
+  // b, by buffer loads whose range is empty, reading zeros, when there is no
+  // b, and W as two bf16 parts per head-dim tile (lane n of the W operand is
+  // the tile's feature omap(q, n/4, n%4)) where those take few registers
+  // (NQ NCT <= 2; otherwise each round loads its own).
+  constexpr bool WPRE = NQ * NCT <= 2;
+  bf16x4 wh[NQ][NCT], wl[NQ][NCT];
+  f32x4 bq[NQ];
+  auto load_w = [&](int q) __attribute__((always_inline)) {
+    const int dn = omap(q, n >> 2, n & 3);
+#pragma unroll
+    for (int ct = 0; ct < NCT; ++ct) {
+      f32x4 wq;
+#pragma unroll
+      for (int sp = 0; sp < 4; ++sp) wq[sp] = prm.weight[dn * C + slot_channel<C>(16 * ct + 4 * g + sp)];
+      split4(wq, wh[q][ct], wl[q][ct]);
+    }
+  };
+  if (act) {
+    const Buf bb(prm.bias, prm.bias ? D * 4 : 0);
+#pragma unroll
+    for (int q = 0; q < NQ; ++q) {
+      if constexpr (WPRE) load_w(q);
+      const float4 b4 = bb.ldf4(omap(q, g, 0) * 4, 0);
+      bq[q] = f32x4{b4.x, b4.y, b4.z, b4.w};
+    }
+  }
   float inv_l[HW];
 #pragma unroll
   for (int hl = 0; hl < HW; ++hl) {
@@ -447,14 +481,10 @@ __global__ __launch_bounds__(256, OCC) void fwd2_kernel(FwdParams prm) {
     if (g == 0 && row_ok && h < H) prm.lse[ra.vec(h, my_row)] = mref[hl] * kLn2 + __logf(l);
   }
 
-  // O's accumulator q holds features omap(q, g, r): 16 q + 4 g + r when V was
-  // read transposed from LDS, DTiles::dmap otherwise.
-  auto omap = [&](int q, int gg, int r) { return VL ? 16 * q + 4 * gg + r : DT::dmap(q, gg, r); };
   // One head-dim tile per round: the row-owner forms o2^T_i[d, h] =
   // sum_slot W[d, channel(slot)] A^T_i[slot, h] on bf16 MFMA over the two
-  // parts of each factor (W and A to 16 bits; lane n of the W operand is the
-  // tile's feature omap(q, n/4, n%4)) and stages it; the head-owner forms
-  // out = (O + o2) / l + b in place.
+  // parts of each factor (W and A to 16 bits) and stages it; the head-owner
+  // forms out = (O + o2) / l + b in place.
   bf16x4 aeh[4][NCT], ael[4][NCT];
   if (act) {
 #pragma unroll
@@ -465,21 +495,13 @@ __global__ __launch_bounds__(256, OCC) void fwd2_kernel(FwdParams prm) {
 #pragma unroll
   for (int q = 0; q < NQ; ++q) {
     if (act) {
-      const int dn = omap(q, n >> 2, n & 3);
-      bf16x4 wh[NCT], wl[NCT];
-#pragma unroll
-      for (int ct = 0; ct < NCT; ++ct) {
-        f32x4 wq;
-#pragma unroll
-        for (int sp = 0; sp < 4; ++sp) wq[sp] = prm.weight[dn * C + slot_channel<C>(16 * ct + 4 * g + sp)];
-        split4(wq, wh[ct], wl[ct]);
-      }
+      if constexpr (!WPRE) load_w(q);
       __syncthreads();  // previous round (or the last chunk) done with the stage
 #pragma unroll
       for (int r = 0; r < 4; ++r) {
         f32x4 acc = zero4();
 #pragma unroll
-        for (int ct = 0; ct < NCT; ++ct) acc = mma_split(wh[ct], wl[ct], aeh[r][ct], ael[r][ct], acc);
+        for (int ct = 0; ct < NCT; ++ct) acc = mma_split(wh[q][ct], wl[q][ct], aeh[r][ct], ael[r][ct], acc);
         *reinterpret_cast<f32x4*>(stage + stage_off(g, 4 * w + r, n)) = acc;
       }
       __syncthreads();
@@ -489,10 +511,7 @@ __global__ __launch_bounds__(256, OCC) void fwd2_kernel(FwdParams prm) {
       f32x4 o = O[hl][q];
       if (act) o = o + *reinterpret_cast<const f32x4*>(stage + stage_off(g, n, w * HW + hl));
       o = o * inv_l[hl];
-      if (act && prm.bias) {
-#pragma unroll
-        for (int r = 0; r < 4; ++r) o[r] += prm.bias[omap(q, g, r)];
-      }
+      if (act) o = o + bq[q];
       O[hl][q] = o;
     }
   }
