@@ -87,17 +87,33 @@ __device__ void fill_rows_nan(const RowAddr& ra, const RowAddr& rv, int r0, int 
     for (int idx = tid; idx < H * nr; idx += nthreads) vec[rv.vec(idx / nr, r0 + idx % nr)] = __builtin_nanf("");
 }
 
-// Work item of workgroup w: binary search of blkcum (blkcum[0] == 0).
+// Largest i in [0, n) with key(i) <= t, for key nondecreasing in i and
+// key(0) <= t. Each round the wave reads 64 evenly spaced entries of the
+// range left (one load per lane) and the count of those at or below t
+// (a ballot) narrows it to one gap: one round for n <= 64, two for n <= 4096,
+// where a binary search would chain log2 n dependent loads. The result is
+// the same in every lane of the wave.
+template <typename F>
+__device__ __forceinline__ int wave_last_le(int n, int t, F key) {
+  const int lane = threadIdx.x & 63;
+  int lo = 0, len = n;
+  while (len > 1) {
+    const int step = (len + 63) >> 6;
+    const int i = lo + lane * step;
+    const bool le = i < lo + len && key(i) <= t;
+    const int c = __builtin_popcountll(__builtin_amdgcn_ballot_w64(le));
+    const int nlo = lo + (c - 1) * step;
+    len = min(step, lo + len - nlo);
+    lo = nlo;
+  }
+  return __builtin_amdgcn_readfirstlane(lo);
+}
+
+// Work item of workgroup w: the event whose blocks hold w (blkcum[0] == 0).
 __device__ __forceinline__ bool locate_block(const EventSpec& ev, int w, EventBlock& eb) {
   if (w >= ev.blkcum[ev.B]) return false;
-  int lo = 0, hi = ev.B;
-  while (hi - lo > 1) {
-    const int mid = (lo + hi) >> 1;
-    if (ev.blkcum[mid] <= w)
-      lo = mid;
-    else
-      hi = mid;
-  }
+  const int32_t* bc = ev.blkcum;
+  const int lo = wave_last_le(ev.B, w, [&](int i) { return bc[i]; });
   eb.b = lo;
   eb.blk = w - ev.blkcum[lo];
   event_range(ev, lo, eb.tok0, eb.len);

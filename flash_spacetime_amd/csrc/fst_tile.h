@@ -181,14 +181,8 @@ __device__ __forceinline__ bool tile_block(const EventSpec& ev, int w, EventBloc
     const int x = w & 7, k = w >> 3;
     const int t = (((k >> 3) << 3) + x) * 8 + (k & 7);
     if (t >= ev.scum[ev.B]) return false;
-    int lo = 0, hi = ev.B;
-    while (hi - lo > 1) {
-      const int mid = (lo + hi) >> 1;
-      if (ev.scum[mid] <= t)
-        lo = mid;
-      else
-        hi = mid;
-    }
+    const int32_t* sc = ev.scum;
+    const int lo = wave_last_le(ev.B, t, [&](int i) { return sc[i]; });
     eb.b = ev.perm[lo];
     eb.blk = t - ev.scum[lo];
     event_range(ev, eb.b, eb.tok0, eb.len);
@@ -207,15 +201,7 @@ __device__ __forceinline__ bool tile_block(const EventSpec& ev, int w, EventBloc
     const int32_t* v = ev.vp + x * S;
     const int base = v[0], tv = v[S] - base;
     if (k < tv) {
-      int lo = 0, hi = S;  // v[lo] - base <= k < v[hi] - base
-      while (hi - lo > 1) {
-        const int mid = (lo + hi) >> 1;
-        if (v[mid] - base <= k)
-          lo = mid;
-        else
-          hi = mid;
-      }
-      j = lo;
+      j = wave_last_le(S, k + base, [&](int i) { return v[i]; });  // v[j] - base <= k < v[j + 1] - base
       blk = k - (v[j] - base);
     } else {
       const int q = k - tv, jb = ev.B >> 3;
@@ -223,15 +209,8 @@ __device__ __forceinline__ bool tile_block(const EventSpec& ev, int w, EventBloc
       // partial group's rank when it exists.
       const int jr = jb + ((((jb & 1) ? 7 - x : x) < (ev.B & 7)) ? 1 : 0);
       if (q >= jr * nb - tv) return false;
-      int lo = 0, hi = jr;  // padding tiles of events < lo <= q < those of events < hi
-      while (hi - lo > 1) {
-        const int mid = (lo + hi) >> 1;
-        if (mid * nb - (v[mid] - base) <= q)
-          lo = mid;
-        else
-          hi = mid;
-      }
-      j = lo;
+      // padding tiles of the events before j <= q < those of the events up to j
+      j = wave_last_le(jr, q - base, [&](int i) { return i * nb - v[i]; });
       blk = (v[j + 1] - v[j]) + (q - (j * nb - (v[j] - base)));
     }
   } else {
