@@ -1198,8 +1198,8 @@ __global__ __launch_bounds__(256, OCC) void bwd_cols2_kernel(BwdParams prm) {
         JFrag<bf16, NS> ot, qt;
         if constexpr (QL) {
           const int h = w * HW + hl;
-          ot.v = QoTile::tr_frag(qo + ((1 * HP + h) * NP + (q >> 1)) * 1024, q, g, n);
-          qt.v = QoTile::tr_frag(qo + ((0 * HP + h) * NP + (q >> 1)) * 1024, q, g, n);
+          ot.v = QoTile::tr_frag_dmap(qo + ((1 * HP + h) * NP + (q >> 1)) * 1024, q, g, n);
+          qt.v = QoTile::tr_frag_dmap(qo + ((0 * HP + h) * NP + (q >> 1)) * 1024, q, g, n);
         } else if constexpr (NS == 2) {
           ot.v = cat8(transpose_x16(DT::part(orw[hl][0], q), id), transpose_x16(DT::part(orw[hl][1], q), id));
           qt.v = cat8(transpose_x16(DT::part(qr[hl][0], q), id), transpose_x16(DT::part(qr[hl][1], q), id));
@@ -1225,9 +1225,9 @@ __global__ __launch_bounds__(256, OCC) void bwd_cols2_kernel(BwdParams prm) {
   if (i0c < len) chunk(i0c, std::true_type{}, std::false_type{});
 
   // ---- store dk, dv (lane n = key) ----
-  // With the tiles in LDS (QL) accumulator q holds features 16 q + 4 g + r
-  // (the transposed reads' order); otherwise DTiles::dmap's, 8 consecutive
-  // features per lane group across the accumulator pair 2t, 2t + 1.
+  // Accumulator q holds features DTiles::dmap(q, g, r) (with the tiles in LDS
+  // (QL) the transposed reads' order): where D is a multiple of 32, 8
+  // consecutive features per lane group across the accumulator pair 2t, 2t + 1.
   if (key_ok) {
 #pragma unroll
     for (int hl = 0; hl < HW; ++hl) {
@@ -1235,13 +1235,7 @@ __global__ __launch_bounds__(256, OCC) void bwd_cols2_kernel(BwdParams prm) {
       if (h >= H) continue;
       bf16* krow = dkg + rx.off(h, my_key, D);
       bf16* vrow = dvg + rx.off(h, my_key, D);
-      if constexpr (QL) {
-#pragma unroll
-        for (int q = 0; q < NQ; ++q) {
-          *reinterpret_cast<bf16x4*>(krow + 16 * q + 4 * g) = pack4(dK[hl][q]);
-          *reinterpret_cast<bf16x4*>(vrow + 16 * q + 4 * g) = pack4(dV[hl][q]);
-        }
-      } else if constexpr (DT::X32) {
+      if constexpr (DT::X32) {
 #pragma unroll
         for (int t = 0; t < NQ / 2; ++t) {
           *reinterpret_cast<bf16x8*>(krow + DT::dmap(2 * t, g, 0)) = cat8(pack4(dK[hl][2 * t]), pack4(dK[hl][2 * t + 1]));

@@ -361,7 +361,7 @@ __global__ __launch_bounds__(256, OCC) void fwd2_kernel(FwdParams prm) {
       for (int q = 0; q < NQ; ++q) {
         JFrag<bf16, NS> vt;
         if constexpr (VL)
-          vt.v = QoTile::tr_frag(vtile + ((w * HW + hl) * NP + (q >> 1)) * 1024, q, g, n);
+          vt.v = QoTile::tr_frag_dmap(vtile + ((w * HW + hl) * NP + (q >> 1)) * 1024, q, g, n);
         else if constexpr (NS == 2)
           vt.v = cat8(transpose_x16(DT::part(vf[hl][0], q), id), transpose_x16(DT::part(vf[hl][1], q), id));
         else
@@ -440,10 +440,10 @@ __global__ __launch_bounds__(256, OCC) void fwd2_kernel(FwdParams prm) {
   if (j0 < len) chunk(j0, std::true_type{}, std::false_type{});
 
   // ---- epilogue ----
-  // O's accumulator q holds features omap(q, g, r): 16 q + 4 g + r when V was
-  // read transposed from LDS, DTiles::dmap otherwise (four consecutive
-  // features either way).
-  auto omap = [&](int q, int gg, int r) { return VL ? 16 * q + 4 * gg + r : DT::dmap(q, gg, r); };
+  // O's accumulator q holds features omap(q, g, r) = DTiles::dmap(q, g, r)
+  // (V read transposed from LDS in that order where VL): four consecutive
+  // features, eight across the pair 2t, 2t + 1 where D is a multiple of 32.
+  auto omap = [&](int q, int gg, int r) { return DT::dmap(q, gg, r); };
   // The epilogue's operands are loaded first, ahead of the lse stores (the
   // compiler would issue them only after those, on the epilogue's chain):
   // b, by buffer loads whose range is empty, reading zeros, when there is no
@@ -521,10 +521,7 @@ __global__ __launch_bounds__(256, OCC) void fwd2_kernel(FwdParams prm) {
       const int h = w * HW + hl;
       if (h >= H) continue;
       bf16* orow = outg + ra.off(h, my_row, D);
-      if constexpr (VL) {
-#pragma unroll
-        for (int q = 0; q < NQ; ++q) *reinterpret_cast<bf16x4*>(orow + 16 * q + 4 * g) = pack4(O[hl][q]);
-      } else if constexpr (DT::X32) {
+      if constexpr (DT::X32) {
 #pragma unroll
         for (int t = 0; t < NQ / 2; ++t)
           *reinterpret_cast<bf16x8*>(orow + DT::dmap(2 * t, g, 0)) = cat8(pack4(O[hl][2 * t]), pack4(O[hl][2 * t + 1]));
