@@ -716,29 +716,43 @@ __global__ __launch_bounds__(64 * NW, WPE) void bwd_rows2_kernel(BwdParams prm) 
 #pragma unroll
       for (int ct = 0; ct < NCT; ++ct) split4(Hacc[r][ct], hh[r][ct], hlo[r][ct]);
   }
+  // Two head-dim tiles per exchange, staged in the u.E and w~.E regions.
+  constexpr int QR = NQ >= 2 ? 2 : 1;
 #pragma unroll
-  for (int q = 0; q < NQ; ++q) {
+  for (int q0 = 0; q0 < NQ; q0 += QR) {
     if (attn) {
       __syncthreads();  // the stage is free (last chunk, or previous round)
 #pragma unroll
-      for (int r = 0; r < RPW; ++r) {
-        f32x4 acc = zero4();
+      for (int qq = 0; qq < QR; ++qq) {
+        const int q = q0 + qq;
+        if (q >= NQ) break;
+        unsigned char* st = qq == 0 ? stU : stW;
 #pragma unroll
-        for (int ct = 0; ct < NCT; ++ct) acc = mma_split(wdh[q][ct], wdl[q][ct], hh[r][ct], hlo[r][ct], acc);
-        *reinterpret_cast<f32x4*>(stU + stage_off(g, row0 + r, n)) = acc;
+        for (int r = 0; r < RPW; ++r) {
+          f32x4 acc = zero4();
+#pragma unroll
+          for (int ct = 0; ct < NCT; ++ct) acc = mma_split(wdh[q][ct], wdl[q][ct], hh[r][ct], hlo[r][ct], acc);
+          *reinterpret_cast<f32x4*>(st + stage_off(g, row0 + r, n)) = acc;
+        }
       }
       __syncthreads();
     }
 #pragma unroll
-    for (int hl = 0; hl < HW; ++hl) {
-      const int h = head(hl);
-      f32x4 o = dQ[hl][q];
-      if (attn && h < H) {
-        o = o + *reinterpret_cast<const f32x4*>(stU + stage_off(g, n, h));
+    for (int qq = 0; qq < QR; ++qq) {
+      const int q = q0 + qq;
+      if (q >= NQ) break;
+      const unsigned char* st = qq == 0 ? stU : stW;
 #pragma unroll
-        for (int r = 0; r < 4; ++r) o[r] = __builtin_fmaf(sig[hl], bq[q][r], o[r]);
+      for (int hl = 0; hl < HW; ++hl) {
+        const int h = head(hl);
+        f32x4 o = dQ[hl][q];
+        if (attn && h < H) {
+          o = o + *reinterpret_cast<const f32x4*>(st + stage_off(g, n, h));
+#pragma unroll
+          for (int r = 0; r < 4; ++r) o[r] = __builtin_fmaf(sig[hl], bq[q][r], o[r]);
+        }
+        dQ[hl][q] = o * prm.scale;
       }
-      dQ[hl][q] = o * prm.scale;
     }
   }
   if (row_ok) {
