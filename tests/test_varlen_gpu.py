@@ -64,6 +64,34 @@ def test_varlen_matches_padded(lengths, flags, dtype):
     torch.testing.assert_close(out_v, _unpad(out_p, lengths), atol=atol, rtol=rtol)
 
 
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16], ids=["fp32", "bf16"])
+def test_many_events_packed_matches_padded(dtype):
+    """5000 short events, fwd+bwd: the packed work list's event lookup takes
+    three rounds of the wave-wide search (more than 64 x 64 events), the
+    padded bf16 rows kernel's two; both layouts agree on every event."""
+    gen = torch.Generator().manual_seed(5000)
+    lengths = torch.randint(1, 25, (5000,), generator=gen).tolist()
+    case = make_packed(lengths, 2, 16, 16, seed_of("many", dtype))
+    dev = "cuda"
+    packed = {k: case[k].to(dev, dtype).requires_grad_(True) for k in ("q", "k", "v")}
+    padded = {k: _pad(case[k], lengths).to(dev, dtype).requires_grad_(True) for k in ("q", "k", "v")}
+    w, b = case["weight"].to(dev, dtype), case["bias"].to(dev, dtype)
+    out_v = flash_spacetime_attention_varlen(packed["q"], packed["k"], packed["v"], case["feats"].to(dev), w, b,
+                                             case["cu"].to(dev))
+    out_p = flash_spacetime_attention(padded["q"], padded["k"], padded["v"], _pad(case["feats"], lengths, True).to(dev),
+                                      w, b, torch.tensor(lengths, device=dev))
+    gen_do = torch.Generator().manual_seed(5001)
+    do = torch.randn(out_v.shape, generator=gen_do, dtype=torch.float64)
+    out_v.backward(do.to(dev, dtype))
+    out_p.backward(_pad(do, lengths).to(dev, dtype))
+    atol, rtol = (2e-2, 1e-2) if dtype is torch.bfloat16 else (1e-5, 1e-4)
+    torch.testing.assert_close(out_v, _unpad(out_p, lengths), atol=atol, rtol=rtol)
+    bound = 1e-2 if dtype is torch.bfloat16 else 1e-5
+    for key in ("q", "k", "v"):
+        err = rel_err(packed[key].grad, _unpad(padded[key].grad, lengths))
+        assert err <= bound, f"grad {key}: relative error {err:.2e}"
+
+
 @pytest.mark.parametrize("lengths", LENGTH_MIXES[2:], ids=lambda l: "-".join(map(str, l)))
 @pytest.mark.parametrize("flags", FLAGS[:2], ids=["attn1act1", "attn1act0"])
 def test_varlen_matches_oracle(lengths, flags):
