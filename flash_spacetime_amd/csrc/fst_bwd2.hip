@@ -438,6 +438,8 @@ __global__ __launch_bounds__(64 * NW, WPE) void bwd_rows2_kernel(BwdParams prm) 
       if (act) *reinterpret_cast<f32x4*>(stW + so_p) = we_p;
     }
     lds_barrier();  // u.E, w~.E staged
+    // Wave priority by phase: row-owner phase 1, head-owner phase 0 (-1 %).
+    __builtin_amdgcn_s_setprio(0);
 
     // ---- head-owner: P, dP, online D, dS, dQ (phase by phase over batches
     // of HB heads, so the heads' dependency chains overlap) ----
@@ -569,6 +571,7 @@ __global__ __launch_bounds__(64 * NW, WPE) void bwd_rows2_kernel(BwdParams prm) 
     }
     if constexpr (!KL)
       if (more) issue(j0 + KC, next_tag);
+    __builtin_amdgcn_s_setprio(1);
     lds_barrier();  // P, dS and D increments staged
     // KL: the next chunk's positions go out here, its K and V loads at the
     // end of the chunk: every transposing LDS read the compiler cannot tell
@@ -1149,6 +1152,8 @@ __global__ __launch_bounds__(256, OCC) void bwd_cols2_kernel(BwdParams prm) {
       rsc[16 * RC + sc_h * RC + sc_r] = sc_draw;
     }
     lds_barrier();  // u.E, w~.E and the row scalars staged
+    // Wave priority by phase: head-owner phase 1, row-owner phase 0 (-1.7 %).
+    __builtin_amdgcn_s_setprio(1);
     // QL: this wave's own direct-to-LDS qt / dO rows (read by it alone) have
     // landed; waited for after the barrier, before the next rows' loads.
     if constexpr (QL) wait_vmem();
@@ -1227,6 +1232,7 @@ __global__ __launch_bounds__(256, OCC) void bwd_cols2_kernel(BwdParams prm) {
     }
     (void)TAIL;
     if (more) issue(i0c + RC, next_tag);
+    __builtin_amdgcn_s_setprio(0);
     __syncthreads();  // the stage is read; the next chunk may overwrite it
   };
 

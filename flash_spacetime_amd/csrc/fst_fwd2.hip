@@ -277,6 +277,9 @@ __global__ __launch_bounds__(256, OCC) void fwd2_kernel(FwdParams prm) {
         }
     }
     lds_barrier();  // u.E staged
+    // Wave priority by phase: the row-owner phase (its MFMAs feed the next
+    // chunk's u.E) runs at 1, the head-owner phase at 0 (-2 % forward).
+    __builtin_amdgcn_s_setprio(0);
 
     // ---- head-owner: logits, online softmax, P V (phase by phase over the
     // wave's heads, so the heads' dependency chains overlap) ----
@@ -388,6 +391,7 @@ __global__ __launch_bounds__(256, OCC) void fwd2_kernel(FwdParams prm) {
       rflag[w] = rescale ? 1 : 0;
     }
     if (decltype(next_tag)::value || j0 + KC < len) issue(j0 + KC, next_tag);
+    __builtin_amdgcn_s_setprio(1);
     lds_barrier();  // P and rescale factors staged
 
     // ---- row-owner: A = alpha A + E^T P ----
