@@ -97,6 +97,30 @@ struct BwdRowsCfg {
   static constexpr int KV_BYTES = KVS ? KV_STAGED : 0;                 // K and V
   static constexpr int R0_BYTES = KV_BYTES > DW_BYTES ? KV_BYTES : DW_BYTES;
   static constexpr int LDS_BYTES = R0_BYTES + TILES * TILE_BYTES;
+  // UL (float32): the row-owner's u and w~ fragments (C values per row and
+  // head) live in region R0 during the key loop instead of registers; R0
+  // holds the dW reduction only after the loop. Where it fits (HP = 8, D = C
+  // = 64: 64 KB of R0's 66.5) it frees 16 C / 64 VGPRs per row of a wave.
+  static constexpr int UW_BYTES = 2 * ROWS * HP * C * 4;
+  static constexpr bool UL = !BF && !KVS && UW_BYTES <= R0_BYTES;
+  // KE (K and V from global memory): a chunk's K and V fragments and its
+  // transposed K are loaded at the start of the chunk, so they land during
+  // the row-owner part instead of being waited for by the head-owner (B=256
+  // L=768 H=12 D=32 C=16 in float32: rows kernel 6.91 -> 6.47 ms). They hold
+  // 3/4 HW D more registers per lane over the row-owner part: on for the
+  // static splits (16-key chunks; eight waves, or four where 8 does not
+  // divide HP) where the lane-state estimate (HP / NW) D + (16 / NW) C plus
+  // those stays within what compiled without spills on gfx950: 148 with
+  // eight waves (256 registers per lane), 264 (one pass) or 312 (two
+  // passes) with four (512); off elsewhere (cfg4, H = 8, D = C = 64, eight
+  // waves: 112 bytes spilled per lane; 32-key chunks and the four-wave plan
+  // variants at HP = 8, 16 spill too).
+  static constexpr int KE_STATE = HW * D + RW * C + 3 * HW * D / 4;
+  template <int PASSES>
+  static constexpr bool ke() {
+    return !KVS && NS == 1 &&
+           (NW == 8 ? KE_STATE <= 148 : NW == 4 && HP % 8 != 0 ? KE_STATE <= (PASSES == 1 ? 264 : 312) : false);
+  }
   // A row-owner wave's RW rows x KC keys: whole embeddings per lane, or
   // whole groups of four frequencies per lane where lanes share a pair.
   using EL = EmbedLanes<RW * KC>;
@@ -113,6 +137,7 @@ __global__ __launch_bounds__(64 * (NW > 4 ? NW : 4), 1) void bwd_rows_kernel(Bwd
   using Cfg = BwdRowsCfg<T, HP, D, C, NW, NS>;
   constexpr int NT = Cfg::THREADS;
   constexpr bool BF = Cfg::BF;
+  constexpr bool KE = Cfg::template ke<PASSES>();
   constexpr int HW = Cfg::HW, RW = Cfg::RW, KC = Cfg::KC;
   constexpr int SLOT_F = Cfg::SLOT / 4, SLOT_T = Cfg::SLOT / Cfg::ESZ;
   extern __shared__ __align__(16) unsigned char smem[];
@@ -239,6 +264,37 @@ __global__ __launch_bounds__(64 * (NW > 4 ? NW : 4), 1) void bwd_rows_kernel(Bwd
 #pragma unroll
     for (int ct = 0; ct < C / 16; ++ct) Hacc[ri][ct] = Gacc[ri][ct] = zero4();
   }
+  // UL: [u, w~][row of the workgroup][channel tile][lane group][head] f32x4,
+  // written and read by the row's own wave. Lanes of padded heads (n >= HP)
+  // read head HP - 1's slot: they only feed output columns that are never
+  // stored.
+  float* Ul = reinterpret_cast<float*>(smem);
+  const int hn = n < HP ? n : HP - 1;
+  auto ul_off = [&](int op, int ri, int ct) {
+    const int il = 16 * tile + ws * RW + ri;
+    return ((((op * Cfg::ROWS + il) * (C / 16) + ct) * 4 + g) * HP + hn) * 4;
+  };
+  if constexpr (Cfg::UL) {
+#pragma unroll
+    for (int ri = 0; ri < RW; ++ri)
+#pragma unroll
+      for (int ct = 0; ct < C / 16; ++ct)
+        if (n < HP) {
+          *reinterpret_cast<f32x4*>(Ul + ul_off(0, ri, ct)) = uf[ri].v[ct];
+          *reinterpret_cast<f32x4*>(Ul + ul_off(1, ri, ct)) = wf[ri].v[ct];
+        }
+    wave_lds_sync();
+  }
+  auto row_frag = [&](int op, int ri) __attribute__((always_inline)) {
+    if constexpr (Cfg::UL) {
+      CFrag<T, C> f;
+#pragma unroll
+      for (int ct = 0; ct < C / 16; ++ct) f.v[ct] = *reinterpret_cast<const f32x4*>(Ul + ul_off(op, ri, ct));
+      return f;
+    } else {
+      return op == 0 ? uf[ri] : wf[ri];
+    }
+  };
   using EL = typename Cfg::EL;  // lane slot el -> key el % KC, rows el / KC + (64 / KC) k2
   constexpr int EPL = EL::EPL;
   constexpr int ESTEP = 64 / KC;
@@ -270,6 +326,34 @@ __global__ __launch_bounds__(64 * (NW > 4 ? NW : 4), 1) void bwd_rows_kernel(Bwd
           *reinterpret_cast<V16*>(Vs + (h * KC + key) * Cfg::KV_ROW + dv * VEC) = vv;
         }
       }
+      // ---- KE: the head-owner's K, V and transposed K of the chunk, loaded
+      // from clamped keys (padded heads read head H - 1); keys past the
+      // event are zeroed in the transposed K after the load ----
+      constexpr int KH = KE ? HW : 1;
+      KFrag<T, D> kfe[KH][NS], vfe[KH][NS];
+      JFrag<T, NS> kte[KH][D / 16];
+      if constexpr (KE) {
+#pragma unroll
+        for (int hl = 0; hl < HW; ++hl) {
+          const int hc = min(ws * HW + hl, H - 1);
+#pragma unroll
+          for (int s = 0; s < NS; ++s) {
+            const int key = min(j0 + 16 * s + n, len - 1);
+            kfe[hl][s].load(kg + rx.off(hc, key, D), g);
+            vfe[hl][s].load(vg + rx.off(hc, key, D), g);
+          }
+#pragma unroll
+          for (int dt = 0; dt < D / 16; ++dt)
+#pragma unroll
+            for (int s = 0; s < NS; ++s)
+#pragma unroll
+              for (int r = 0; r < 4; ++r) {
+                const int j = j0 + 16 * s + 4 * g + r;
+                const T x = kg[rx.off(hc, min(j, len - 1), D) + 16 * dt + n];
+                kte[hl][dt].v[4 * s + r] = j < len ? (float)x : 0.f;
+              }
+        }
+      }
       // ---- row-owner: embedding, u.E and w~.E staged per (row, head) ----
       if (use_e) {
         const int key = el % KC;
@@ -290,11 +374,11 @@ __global__ __launch_bounds__(64 * (NW > 4 ? NW : 4), 1) void bwd_rows_kernel(Bwd
             ef.load(Es + (il * KC + 16 * s + n) * Cfg::E_ROW, g);
             float* slot = Sf + (il * HP + n) * SLOT_F;
             if (attn) {
-              const f32x4 ue = mma_c<C>(ef, uf[ri], zero4());
+              const f32x4 ue = mma_c<C>(ef, row_frag(0, ri), zero4());
               if (n < H) *reinterpret_cast<f32x4*>(slot + 16 * s + 4 * g) = ue;
             }
             if (act) {
-              const f32x4 we = mma_c<C>(ef, wf[ri], zero4());
+              const f32x4 we = mma_c<C>(ef, row_frag(1, ri), zero4());
               if (n < H) *reinterpret_cast<f32x4*>(slot + Cfg::U_ROW + 16 * s + 4 * g) = we;
             }
           }
@@ -317,9 +401,11 @@ __global__ __launch_bounds__(64 * (NW > 4 ? NW : 4), 1) void bwd_rows_kernel(Bwd
           if constexpr (Cfg::KVS) {
             kf.load(Ks + (h * KC + 16 * s + n) * Cfg::KV_ROW, g);
             vf.load(Vs + (h * KC + 16 * s + n) * Cfg::KV_ROW, g);
+          } else if constexpr (KE) {
+            kf = kfe[hl][s];
+            vf = vfe[hl][s];
           } else {
-            int key = j0 + 16 * s + n;
-            key = key < len ? key : len - 1;
+            const int key = min(j0 + 16 * s + n, len - 1);
             kf.load(kg + rx.off(h, key, D), g);
             vf.load(vg + rx.off(h, key, D), g);
           }
@@ -360,13 +446,19 @@ __global__ __launch_bounds__(64 * (NW > 4 ? NW : 4), 1) void bwd_rows_kernel(Bwd
         }
         {
           f32x4 dS[NS];
+          {
+            // sigma sums the rounded dS the products are fed: no fused
+            // multiply-add here, whatever the surrounding code's layout (the
+            // compiler's fusing otherwise differed between plan variants).
+#pragma clang fp contract(off)
 #pragma unroll
-          for (int s = 0; s < NS; ++s)
+            for (int s = 0; s < NS; ++s)
 #pragma unroll
-            for (int r = 0; r < 4; ++r) {
-              dS[s][r] = S[s][r] * (P_[s][r] - dval[hl]);
-              sig[hl] += dS[s][r];
-            }
+              for (int r = 0; r < 4; ++r) {
+                dS[s][r] = S[s][r] * (P_[s][r] - dval[hl]);
+                sig[hl] += dS[s][r];
+              }
+          }
           JFrag<T, NS> dsf, pf;
           dsf.from_tiles(dS);
           pf.from_tiles(S);
@@ -375,6 +467,8 @@ __global__ __launch_bounds__(64 * (NW > 4 ? NW : 4), 1) void bwd_rows_kernel(Bwd
             JFrag<T, NS> kt;
             if constexpr (Cfg::KVS) {
               kt.load_tr(Ks + h * KC * Cfg::KV_ROW, Cfg::KV_ROW, 16 * dt, g, n);
+            } else if constexpr (KE) {
+              kt = kte[hl][dt];
             } else {
 #pragma unroll
               for (int s = 0; s < NS; ++s)
