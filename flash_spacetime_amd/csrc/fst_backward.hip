@@ -792,9 +792,83 @@ __global__ __launch_bounds__(64 * (NW > 4 ? NW : 4), 1) void bwd_cols_kernel(Bwd
   const float4 pos_j = use_e ? ra.pos(ev.pos4, j0t + pk < len ? j0t + pk : (len > 0 ? len - 1 : 0))
                              : float4{0.f, 0.f, 0.f, 0.f};
 
+  // PF (float32 with QOS): the next chunk's qt / dO rows and per-row scalars
+  // are loaded into registers (from clamped rows) while this chunk runs and
+  // written to LDS at the start of the next, instead of being loaded and
+  // waited for there: cfg4 cols 19.72 -> 19.24 ms, B=256 L=768 H=12 D=32
+  // C=16 8.49 -> 8.13 ms. Only where the LDS plan already allows one
+  // workgroup per CU (over 80 KB): elsewhere the registers cost a workgroup
+  // per CU (H = 8, D = 32, C = 16: 0.79 -> 1.07 ms; H = 4: 0.50 -> 0.58),
+  // and not past HW D = 128 (spills).
+  constexpr bool PF = Cfg::QOS && !BF && HW * D <= 128 && Cfg::LDS_BYTES > 80 * 1024;
+  using V16 = typename VecOf<T>::type;
+  constexpr int VEC = 16 / Cfg::ESZ;
+  constexpr int PER_ROW = D / VEC;
+  constexpr int QIT = PF ? (HP * KC * PER_ROW + NT - 1) / NT : 1;  // rows' 16-byte items per thread
+  constexpr int LIT = PF ? (HP * KC + NT - 1) / NT : 1;            // per-row scalars per thread
+  V16 qraw[QIT], oraw[QIT];
+  float lraw[LIT][4];
+  auto prefetch = [&](int c) __attribute__((always_inline)) {
+#pragma unroll
+    for (int it = 0; it < QIT; ++it) {
+      const int idx = tid + it * NT;
+      if (idx < H * KC * PER_ROW) {
+        const int dv = idx % PER_ROW, il = (idx / PER_ROW) % KC, h = idx / (PER_ROW * KC);
+        const int i = min(c + il, len - 1);
+        qraw[it] = *reinterpret_cast<const V16*>(qg + rx.off(h, i, D) + dv * VEC);
+        oraw[it] = *reinterpret_cast<const V16*>(dog + ra.off(h, i, D) + dv * VEC);
+      }
+    }
+#pragma unroll
+    for (int it = 0; it < LIT; ++it) {
+      const int idx = tid + it * NT;
+      if (idx < H * KC) {
+        const int il = idx % KC, h = idx / KC;
+        const long v = ra.vec(h, min(c + il, len - 1));
+        lraw[it][0] = prm.lse[v];
+        lraw[it][1] = prm.dsum[v];
+        lraw[it][2] = (act && prm.bias) ? prm.dob[v] : 0.f;
+        lraw[it][3] = prm.lse_z[v];
+      }
+    }
+  };
+  if constexpr (PF) prefetch(0);
+
   for (int c0 = 0; c0 < len; c0 += KC) {
+    if constexpr (PF) {
+      // ---- PF: stage the prefetched rows (zero past the event), then load
+      // the next chunk's ----
+#pragma unroll
+      for (int it = 0; it < QIT; ++it) {
+        const int idx = tid + it * NT;
+        if (idx < H * KC * PER_ROW) {
+          const int dv = idx % PER_ROW, il = (idx / PER_ROW) % KC, h = idx / (PER_ROW * KC);
+          const bool ok = c0 + il < len;
+          V16 qv = VecOf<T>::zero(), ov = VecOf<T>::zero();
+          if (ok) {
+#pragma unroll
+            for (int e = 0; e < VEC; ++e) qv[e] = (T)((float)qraw[it][e] * prm.scale);
+            ov = oraw[it];
+          }
+          *reinterpret_cast<V16*>(Qs + (h * KC + il) * Cfg::QO_ROW + dv * VEC) = qv;
+          *reinterpret_cast<V16*>(Os + (h * KC + il) * Cfg::QO_ROW + dv * VEC) = ov;
+        }
+      }
+#pragma unroll
+      for (int it = 0; it < LIT; ++it) {
+        const int idx = tid + it * NT;
+        if (idx < H * KC) {
+          const bool ok = c0 + idx % KC < len;
+          Lv[idx] = ok ? lraw[it][0] * kLog2e : 0.f;
+          Lv[HP * KC + idx] = ok ? lraw[it][1] : 0.f;
+          Lv[2 * HP * KC + idx] = ok ? lraw[it][2] : 0.f;
+          Lv[3 * HP * KC + idx] = ok ? lraw[it][3] : 0.f;
+        }
+      }
+      if (c0 + KC < len) prefetch(c0 + KC);
+    }
     // ---- stage the chunk's streamed rows: qt, dO (QOS), lse2, D, dob ----
-    if constexpr (Cfg::QOS) {
+    if constexpr (Cfg::QOS && !PF) {
       using V16 = typename VecOf<T>::type;
       constexpr int VEC = 16 / Cfg::ESZ;
       constexpr int PER_ROW = D / VEC;
@@ -815,7 +889,7 @@ __global__ __launch_bounds__(64 * (NW > 4 ? NW : 4), 1) void bwd_cols_kernel(Bwd
         *reinterpret_cast<V16*>(Os + (h * KC + il) * Cfg::QO_ROW + dv * VEC) = ov;
       }
     }
-    for (int idx = tid; idx < H * KC; idx += NT) {
+    for (int idx = tid; !PF && idx < H * KC; idx += NT) {
       const int il = idx % KC, h = idx / KC;
       const int i = c0 + il;
       const bool ok = i < len;
