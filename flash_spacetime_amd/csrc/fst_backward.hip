@@ -103,23 +103,26 @@ struct BwdRowsCfg {
   // = 64: 64 KB of R0's 66.5) it frees 16 C / 64 VGPRs per row of a wave.
   static constexpr int UW_BYTES = 2 * ROWS * HP * C * 4;
   static constexpr bool UL = !BF && !KVS && UW_BYTES <= R0_BYTES;
-  // KE (K and V from global memory): a chunk's K and V fragments and its
-  // transposed K are loaded at the start of the chunk, so they land during
-  // the row-owner part instead of being waited for by the head-owner (B=256
-  // L=768 H=12 D=32 C=16 in float32: rows kernel 6.91 -> 6.47 ms). They hold
-  // 3/4 HW D more registers per lane over the row-owner part: on for the
-  // static splits (16-key chunks; eight waves, or four where 8 does not
-  // divide HP) where the lane-state estimate (HP / NW) D + (16 / NW) C plus
-  // those stays within what compiled without spills on gfx950: 148 with
-  // eight waves (256 registers per lane), 264 (one pass) or 312 (two
-  // passes) with four (512); off elsewhere (cfg4, H = 8, D = C = 64, eight
-  // waves: 112 bytes spilled per lane; 32-key chunks and the four-wave plan
-  // variants at HP = 8, 16 spill too).
-  static constexpr int KE_STATE = HW * D + RW * C + 3 * HW * D / 4;
+  // KE (K from global memory): a chunk's transposed K (the dQ product's
+  // operand, gathered element by element) is loaded at the start of the
+  // chunk, so it lands during the row-owner part instead of being waited for
+  // by the head-owner (B=256 L=768 H=12 D=32 C=16 in float32: rows kernel
+  // 6.38 -> 6.08 ms; cfg4 20.07 -> 19.66 ms). Issuing the K and V row
+  // fragments early as well measured slower there (6.47 ms) and needs three
+  // times the registers. It holds HW D / 4 more registers per lane over the
+  // row-owner part: on for the static splits (16-key chunks; eight waves, or
+  // four where 8 does not divide HP) where the lane-state estimate (HP / NW)
+  // D + (16 / NW) C plus those stays within what compiled without new
+  // spills on gfx950: 148 with eight waves (256 registers per lane), 244
+  // (one pass) or 312 (two passes) with four (512); and for cfg4's split
+  // (eight waves of one head, u / w~ in LDS), faster although it spills
+  // three registers.
+  static constexpr int KE_STATE = HW * D + RW * C + HW * D / 4;
   template <int PASSES>
   static constexpr bool ke() {
     return !KVS && NS == 1 &&
-           (NW == 8 ? KE_STATE <= 148 : NW == 4 && HP % 8 != 0 ? KE_STATE <= (PASSES == 1 ? 264 : 312) : false);
+           (NW == 8 ? KE_STATE <= 148 || (UL && HW == 1)
+                    : NW == 4 && HP % 8 != 0 ? KE_STATE <= (PASSES == 1 ? 244 : 312) : false);
   }
   // A row-owner wave's RW rows x KC keys: whole embeddings per lane, or
   // whole groups of four frequencies per lane where lanes share a pair.
@@ -326,22 +329,15 @@ __global__ __launch_bounds__(64 * (NW > 4 ? NW : 4), 1) void bwd_rows_kernel(Bwd
           *reinterpret_cast<V16*>(Vs + (h * KC + key) * Cfg::KV_ROW + dv * VEC) = vv;
         }
       }
-      // ---- KE: the head-owner's K, V and transposed K of the chunk, loaded
-      // from clamped keys (padded heads read head H - 1); keys past the
-      // event are zeroed in the transposed K after the load ----
+      // ---- KE: the head-owner's transposed K of the chunk, loaded from
+      // clamped keys (padded heads read head H - 1) and zeroed past the
+      // event after the load ----
       constexpr int KH = KE ? HW : 1;
-      KFrag<T, D> kfe[KH][NS], vfe[KH][NS];
       JFrag<T, NS> kte[KH][D / 16];
       if constexpr (KE) {
 #pragma unroll
         for (int hl = 0; hl < HW; ++hl) {
           const int hc = min(ws * HW + hl, H - 1);
-#pragma unroll
-          for (int s = 0; s < NS; ++s) {
-            const int key = min(j0 + 16 * s + n, len - 1);
-            kfe[hl][s].load(kg + rx.off(hc, key, D), g);
-            vfe[hl][s].load(vg + rx.off(hc, key, D), g);
-          }
 #pragma unroll
           for (int dt = 0; dt < D / 16; ++dt)
 #pragma unroll
@@ -401,9 +397,6 @@ __global__ __launch_bounds__(64 * (NW > 4 ? NW : 4), 1) void bwd_rows_kernel(Bwd
           if constexpr (Cfg::KVS) {
             kf.load(Ks + (h * KC + 16 * s + n) * Cfg::KV_ROW, g);
             vf.load(Vs + (h * KC + 16 * s + n) * Cfg::KV_ROW, g);
-          } else if constexpr (KE) {
-            kf = kfe[hl][s];
-            vf = vfe[hl][s];
           } else {
             const int key = min(j0 + 16 * s + n, len - 1);
             kf.load(kg + rx.off(h, key, D), g);
