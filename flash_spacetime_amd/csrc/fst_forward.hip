@@ -68,6 +68,12 @@ struct FwdCfg {
   static constexpr bool KS = false;
   static constexpr int V_BYTES = (VS ? KV_ONE : 0) + (KS ? KV_ONE : 0);  // V, then K
   static constexpr int LDS_BYTES = V_BYTES + TILES * TILE_BYTES;
+  // VE (float32): each head's V columns are gathered before its logits
+  // instead of right before P V, where the LDS plan already keeps one
+  // workgroup per CU (over 80 KB): cfg4 forward 11.52 -> 11.10 ms; where the
+  // registers cost a workgroup per CU it lost (B=256 L=768 H=12 D=32 C=16:
+  // 2.87 -> 3.75 ms; H = 8, D = 32: 0.53 -> 0.60).
+  static constexpr bool VE = !VS && LDS_BYTES > 80 * 1024;
   // A row-owner wave's RW rows x KC keys: whole embeddings per lane, or
   // whole groups of four frequencies per lane where lanes share a pair.
   using EL = EmbedLanes<RW * KC>;
@@ -223,6 +229,22 @@ __global__ __launch_bounds__(64 * (NW > 4 ? NW : 4), 1) void fwd_kernel(FwdParam
     for (int hl = 0; hl < HW; ++hl) {
       const int h = ws * HW + hl;
       if (h >= H) continue;
+      // VE: this head's V columns (gathered element by element from clamped
+      // keys, zeroed past the event) are loaded before its logits, so they
+      // land during the logits product and the softmax.
+      JFrag<T, NS> vfe[Cfg::VE ? D / 16 : 1];
+      if constexpr (Cfg::VE) {
+#pragma unroll
+        for (int dt = 0; dt < D / 16; ++dt)
+#pragma unroll
+          for (int s = 0; s < NS; ++s)
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+              const int j = j0 + 16 * s + 4 * g + r;
+              const T x = vg[rx.off(h, min(j, len - 1), D) + 16 * dt + n];
+              vfe[dt].v[4 * s + r] = j < len ? (float)x : 0.f;
+            }
+      }
       f32x4 S[NS];
 #pragma unroll
       for (int s = 0; s < NS; ++s) {
@@ -268,6 +290,8 @@ __global__ __launch_bounds__(64 * (NW > 4 ? NW : 4), 1) void fwd_kernel(FwdParam
         JFrag<T, NS> vf;
         if constexpr (Cfg::VS) {
           vf.load_tr(Vs + h * KC * Cfg::V_ROW, Cfg::V_ROW, 16 * dt, g, n);
+        } else if constexpr (Cfg::VE) {
+          vf = vfe[dt];
         } else {
 #pragma unroll
           for (int s = 0; s < NS; ++s)
