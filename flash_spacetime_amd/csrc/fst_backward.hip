@@ -709,6 +709,16 @@ struct BwdColsCfg {
   static constexpr bool QOS = BF || QO_STAGED + VEC_BYTES + TILES * TILE_BYTES <= 160 * 1024;
   static constexpr int QO_BYTES = QOS ? QO_STAGED : 0;  // qt and dO
   static constexpr int LDS_BYTES = QO_BYTES + VEC_BYTES + TILES * TILE_BYTES;
+  // ER (float32, C a multiple of 32, HP <= 8): the pair-owner forms E in
+  // registers in the products' operand layout (embed_cfrag) instead of
+  // through LDS, and its rows' u and w~ go straight to the E tile's LDS
+  // (wave-private [row][u, w~][head][C + 4] blocks, loaded by direct loads
+  // issued a phase ahead) instead of being loaded from global memory where
+  // they are used. The blocks take 2 HP / 16 of the E tile.
+  static constexpr int UWL_ROW = (C + 4) * 4;                 // bytes per (row, op, head)
+  static constexpr int UWL_SLOTS = HP * UWL_ROW / 16;         // 16-byte slots per (row, op)
+  static constexpr int UWL_LOADS = (UWL_SLOTS + 63) / 64;     // direct loads per (row, op)
+  static constexpr bool ER = !BF && C % 32 == 0 && TILES == 1 && 2 * HP <= 16;
   // The pair-owner's RWS rows x 16 keys: whole embeddings per lane, or
   // whole groups of four frequencies per lane where lanes share a pair.
   using EL = EmbedLanes<RWS * 16>;
@@ -827,7 +837,49 @@ __global__ __launch_bounds__(64 * (NW > 4 ? NW : 4), 1) void bwd_cols_kernel(Bwd
   };
   if constexpr (PF) prefetch(0);
 
+  // ---- ER: this wave's streamed rows' u and w~ go to its blocks of the E
+  // tile by direct loads, [row][u, w~][head][C + 4] (the pad slot of a head
+  // repeats its last quad; heads past H and rows past the event are clamped,
+  // feeding only outputs that are never used), and the rows' positions to
+  // registers, a phase before they are used ----
+  constexpr bool ER = Cfg::ER;
+  unsigned char* ul = reinterpret_cast<unsigned char*>(Es) + ws * RWS * 2 * Cfg::UWL_SLOTS * 16;
+  float4 pin[ER ? RWS : 1];
+  const long uw_base = ra.off(0, 0, C);
+  const unsigned uw_bytes = (unsigned)(((long)(H - 1) * ra.hs + (long)(len > 0 ? len - 1 : 0) * ra.ts + 1) * C * 4);
+  const __amdgpu_buffer_rsrc_t urs = __builtin_amdgcn_make_buffer_rsrc(const_cast<T*>(ug + uw_base), (short)0, (int)uw_bytes, 0x00020000);
+  const __amdgpu_buffer_rsrc_t wrs = __builtin_amdgcn_make_buffer_rsrc(const_cast<T*>(wg_ + uw_base), (short)0, (int)uw_bytes, 0x00020000);
+  auto issue_uw = [&](int c) __attribute__((always_inline)) {
+    if constexpr (ER) {
+      constexpr int SPH = Cfg::UWL_ROW / 16;  // slots per head
+#pragma unroll
+      for (int ri = 0; ri < RWS; ++ri) {
+        const int i = min(c + ws * RWS + ri, len - 1);
+        pin[ri] = ra.pos(ev.pos4, i);
+#pragma unroll
+        for (int t = 0; t < Cfg::UWL_LOADS; ++t) {
+          const int sl = 64 * t + lane;
+          const int h = min(sl / SPH, H - 1), q = min(sl % SPH, C / 4 - 1);
+          const int voff = (int)(((long)h * ra.hs + (long)i * ra.ts) * C + 4 * q) * 4;
+          if (sl < Cfg::UWL_SLOTS) {
+            if (attn)
+              __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                  urs, (__attribute__((address_space(3))) void*)(ul + ((2 * ri) * Cfg::UWL_SLOTS + 64 * t) * 16), 16, voff, 0, 0, 0);
+            if (act)
+              __builtin_amdgcn_raw_ptr_buffer_load_lds(
+                  wrs, (__attribute__((address_space(3))) void*)(ul + ((2 * ri + 1) * Cfg::UWL_SLOTS + 64 * t) * 16), 16, voff, 0, 0, 0);
+          }
+        }
+      }
+    }
+  };
+  if constexpr (ER)
+    if (use_e) issue_uw(0);
+
   for (int c0 = 0; c0 < len; c0 += KC) {
+    // ER: this chunk's u / w~ blocks (and, with PF, the prefetched rows)
+    // have landed.
+    if constexpr (ER) wait_vmem();
     if constexpr (PF) {
       // ---- PF: stage the prefetched rows (zero past the event), then load
       // the next chunk's ----
@@ -892,7 +944,33 @@ __global__ __launch_bounds__(64 * (NW > 4 ? NW : 4), 1) void bwd_cols_kernel(Bwd
       Lv[3 * HP * KC + idx] = ok ? prm.lse_z[ra.vec(h, i)] : 0.f;
     }
     // ---- pair-owner: E of (streamed rows, own keys), u.E and w~.E ----
-    if (use_e) {
+    if constexpr (ER) {
+      if (use_e) {
+        const int hn = n < HP ? n : HP - 1;
+#pragma unroll
+        for (int ri = 0; ri < RWS; ++ri) {
+          const int il = ws * RWS + ri;
+          const CFrag<T, C> ef = embed_cfrag<C>(pin[ri], pos_j, prm.freq, g);  // B = E_i[c, j]: lane n = key
+#pragma unroll
+          for (int op = 0; op < 2; ++op) {
+            if (!(op == 0 ? attn : act)) continue;
+            CFrag<T, C> af;  // A = u_i[h, c] (w~_i): lane n = head
+            const unsigned char* blk = ul + (2 * ri + op) * Cfg::UWL_SLOTS * 16 + hn * Cfg::UWL_ROW;
+#pragma unroll
+            for (int ct = 0; ct < C / 16; ++ct) af.v[ct] = *reinterpret_cast<const f32x4*>(blk + (16 * ct + 4 * g) * 4);
+            const f32x4 ue = mma_c<C>(af, ef, zero4());  // [h = 4g + r][j = n]
+#pragma unroll
+            for (int r = 0; r < 4; ++r)
+              if (4 * g + r < H) UWs[op * HP * 16 * UWR + ((4 * g + r) * 16 + n) * UWR + il] = ue[r];
+          }
+        }
+        // The blocks are read: the next chunk's rows may overwrite them.
+        if (c0 + KC < len) {
+          wave_lds_sync();
+          issue_uw(c0 + KC);
+        }
+      }
+    } else if (use_e) {
       using EL = typename Cfg::EL;  // lane slot el -> key el & 15, rows (el >> 4) + 4 k4
       const int el = EL::slot(lane), epart = EL::part(lane);
 #pragma unroll

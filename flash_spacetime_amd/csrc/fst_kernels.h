@@ -225,6 +225,10 @@ struct VecOf<float> {
 
 __device__ __forceinline__ float exp2f_fast(float x) { return __builtin_amdgcn_exp2f(x); }
 
+// Completion of this wave's outstanding buffer loads (including loads into
+// LDS), ordered against every later memory access of the wave.
+__device__ __forceinline__ void wait_vmem() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+
 // Four consecutive output elements from an fp32 quad.
 template <typename T>
 __device__ __forceinline__ void store4(T* p, const f32x4& v);
@@ -287,6 +291,30 @@ struct CFrag<float, C> {
     for (int ct = 0; ct < C / 16; ++ct) v[ct] = acc[ct];
   }
 };
+
+// The float32 embedding of one pair formed straight in the channel layout of
+// CFrag (lane group g: channels 16 ct + 4 g + r), with write_embedding's
+// arithmetic: channel c < C / 2 is the sine of frequency c, channel C / 2 + c
+// its cosine. With C a multiple of 32 a lane's channels are the sines and
+// cosines of the same C / 8 frequencies.
+template <int C>
+__device__ __forceinline__ CFrag<float, C> embed_cfrag(float4 pi, float4 pj, const FreqTable& ft, int g) {
+  static_assert(C % 32 == 0, "each lane holds the sine and cosine of its frequencies");
+  constexpr int FT = C / 32;  // sine channel tiles
+  const double x = pair_angle_f64(pi, pj);
+  CFrag<float, C> e;
+#pragma unroll
+  for (int ct = 0; ct < FT; ++ct)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int f = 16 * ct + 4 * g + r;
+      const double rev = x * ((double)ft.ghi[f] + (double)ft.glo[f]);
+      const float rr = (float)(rev - __builtin_floor(rev));
+      e.v[ct][r] = __builtin_amdgcn_sinf(rr);
+      e.v[FT + ct][r] = __builtin_amdgcn_cosf(rr);
+    }
+  return e;
+}
 
 template <int C>
 __device__ __forceinline__ f32x4 mma_c(const CFrag<bf16, C>& a, const CFrag<bf16, C>& b, f32x4 c) {

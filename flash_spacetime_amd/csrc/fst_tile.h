@@ -419,9 +419,6 @@ struct LdsFrag {
   }
 };
 
-// Completion of this wave's outstanding buffer loads (including loads into
-// LDS), ordered against every later memory access of the wave.
-__device__ __forceinline__ void wait_vmem() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
 // Workgroup barrier for exchanges through LDS: this wave's LDS accesses are
 // complete before it. Unlike __syncthreads() it does not wait for the wave's
 // outstanding buffer loads, loads into LDS included (the compiler's
