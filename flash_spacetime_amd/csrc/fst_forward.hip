@@ -175,6 +175,12 @@ __global__ __launch_bounds__(64 * (NW > 4 ? NW : 4), 1) void fwd_kernel(FwdParam
     pos_i[k2] = use_e ? ra.pos(prm.ev.pos4, row < len ? row : (len > 0 ? len - 1 : 0)) : float4{0.f, 0.f, 0.f, 0.f};
   }
 
+  // PP: key positions run a chunk ahead, as the embedding needs them first
+  // thing in a chunk (B=256 L=768 H=12 D=32 C=16 in float32: 2.87 -> 2.83
+  // ms); only for the four-wave tiles without VE: the eight-wave ones lost a
+  // workgroup per CU (H = 8, D = 32: 0.52 -> 0.62 ms) or spilled (cfg4).
+  constexpr bool PP = NW == 4 && !Cfg::VE;
+  float4 pjn = use_e ? ra.pos(prm.ev.pos4, min(el % KC, len - 1)) : float4{0.f, 0.f, 0.f, 0.f};
   for (int j0 = 0; j0 < len; j0 += KC) {
     // ---- VS / KS: stage V[h][key][d] and K (keys past the event are zero) ----
     if constexpr (Cfg::VS) {
@@ -200,8 +206,8 @@ __global__ __launch_bounds__(64 * (NW > 4 ? NW : 4), 1) void fwd_kernel(FwdParam
     // ---- row-owner: embedding of its rows x KC keys, then u.E ----
     if (use_e) {
       const int key = el % KC;
-      const int j = j0 + key;
-      const float4 pj = ra.pos(prm.ev.pos4, j < len ? j : len - 1);
+      const float4 pj = PP ? pjn : ra.pos(prm.ev.pos4, min(j0 + key, len - 1));
+      if (PP && j0 + KC < len) pjn = ra.pos(prm.ev.pos4, min(j0 + KC + key, len - 1));
 #pragma unroll
       for (int k2 = 0; k2 < EPL; ++k2) {
         const int il = ws * RW + el / KC + ESTEP * k2;
