@@ -312,7 +312,7 @@ __global__ __launch_bounds__(64 * (NW > 4 ? NW : 4), 1) void bwd_rows_kernel(Bwd
   // Key positions run a chunk ahead (the next pass's first chunk after the
   // last): the embedding needs them first thing in a chunk (B=256 L=768 H=12
   // D=32 C=16 in float32: 6.06 -> 5.67 ms; cfg4 19.69 -> 19.27 ms).
-  float4 pjn = use_e ? ra.pos(prm.ev.pos4, min(el % KC, len - 1)) : float4{0.f, 0.f, 0.f, 0.f};
+  float4 pjn = use_e && len > 0 ? ra.pos(prm.ev.pos4, min(el % KC, len - 1)) : float4{0.f, 0.f, 0.f, 0.f};
   for (int pass = 0; pass < PASSES; ++pass) {
     for (int j0 = 0; j0 < len; j0 += KC) {
       // ---- KVS: stage K and V rows of the chunk (zero past the event) ----
@@ -839,7 +839,10 @@ __global__ __launch_bounds__(64 * (NW > 4 ? NW : 4), 1) void bwd_cols_kernel(Bwd
       }
     }
   };
-  if constexpr (PF) prefetch(0);
+  // (Padded events of length 0 get one workgroup, for their padding rows:
+  // nothing is loaded for them.)
+  if constexpr (PF)
+    if (len > 0) prefetch(0);
 
   // ---- ER: this wave's streamed rows' u and w~ go to its blocks of the E
   // tile by direct loads, [row][u, w~][head][C + 4] (the pad slot of a head
@@ -878,7 +881,7 @@ __global__ __launch_bounds__(64 * (NW > 4 ? NW : 4), 1) void bwd_cols_kernel(Bwd
     }
   };
   if constexpr (ER)
-    if (use_e) issue_uw(0);
+    if (use_e && len > 0) issue_uw(0);
 
   for (int c0 = 0; c0 < len; c0 += KC) {
     // ER: this chunk's u / w~ blocks (and, with PF, the prefetched rows)

@@ -180,7 +180,7 @@ __global__ __launch_bounds__(64 * (NW > 4 ? NW : 4), 1) void fwd_kernel(FwdParam
   // ms); only for the four-wave tiles without VE: the eight-wave ones lost a
   // workgroup per CU (H = 8, D = 32: 0.52 -> 0.62 ms) or spilled (cfg4).
   constexpr bool PP = NW == 4 && !Cfg::VE;
-  float4 pjn = use_e ? ra.pos(prm.ev.pos4, min(el % KC, len - 1)) : float4{0.f, 0.f, 0.f, 0.f};
+  float4 pjn = PP && use_e && len > 0 ? ra.pos(prm.ev.pos4, min(el % KC, len - 1)) : float4{0.f, 0.f, 0.f, 0.f};
   for (int j0 = 0; j0 < len; j0 += KC) {
     // ---- VS / KS: stage V[h][key][d] and K (keys past the event are zero) ----
     if constexpr (Cfg::VS) {

@@ -80,3 +80,34 @@ def test_padded_single_token_events(dtype):
     zero_tol = 1e-3 if dtype == torch.bfloat16 else 1e-5
     assert q.grad.float().abs().max() <= zero_tol and k.grad.float().abs().max() <= zero_tol
     torch.testing.assert_close(v.grad.float(), torch.ones(v.shape, device=DEV), atol=tol, rtol=tol)
+
+
+@pytest.mark.parametrize("dtype", DTYPES, ids=["bf16", "fp32"])
+@pytest.mark.parametrize("heads,dim,chans", [(8, 64, 64), (12, 32, 16)], ids=["h8d64c64", "h12d32c16"])
+def test_padded_empty_events_beside_others(dtype, heads, dim, chans):
+    """Empty events first and last in a padded batch, at the shapes whose
+    float32 kernels prefetch rows, positions and u / w~ ahead of a chunk (the
+    prefetches of an empty event's single workgroup must not run): the empty
+    events' outputs and gradients are exact zeros, and the other event's out,
+    dq, dk and dv are bitwise those of the same event run alone."""
+    length = 40
+    gen = torch.Generator().manual_seed(7)
+    q, k, v = (torch.randn(3, heads, length, dim, generator=gen).to(DEV, dtype) for _ in range(3))
+    feats = torch.randn(3, length, 4, generator=gen).to(DEV)
+    do = torch.randn(3, heads, length, dim, generator=gen).to(DEV, dtype)
+    w, b = _params(dim, chans)
+
+    def run(sl, lens):
+        leaves = [t[sl].detach().clone().requires_grad_(True) for t in (q, k, v)]
+        out = flash_spacetime_attention(*leaves, feats[sl], w, b, torch.tensor(lens, dtype=torch.int32, device=DEV))
+        out.backward(do[sl])
+        torch.cuda.synchronize()
+        return out.detach(), [t.grad for t in leaves]
+
+    out, grads = run(slice(0, 3), [0, 33, 0])
+    for e in (0, 2):
+        assert (out[e] == 0).all() and all((g[e] == 0).all() for g in grads)
+    out1, grads1 = run(slice(1, 2), [33])
+    assert torch.equal(out[1:2], out1)
+    for g, g1 in zip(grads, grads1):
+        assert torch.equal(g[1:2], g1)
