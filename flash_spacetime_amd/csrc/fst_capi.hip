@@ -272,11 +272,20 @@ __global__ __launch_bounds__(1024) void worklist_kernel(const int32_t* lens, int
   ev.L = L;
   ev.T = T;
   blkcum_steps(ev, rows_a, nullptr, blk_a, buf, carry);
-  if (blk_b) blkcum_steps(ev, rows_b, nullptr, blk_b, buf, carry);
+  // The second family's lists equal the first's when its blocks are as tall
+  // (the bf16 backward: 16 rows and 16 keys): copied instead of rescanned.
+  const bool same = rows_b == rows_a;
+  if (blk_b && !same) blkcum_steps(ev, rows_b, nullptr, blk_b, buf, carry);
   sort_steps(ev, perm, keys);
   __syncthreads();
   if (scum_a) blkcum_steps(ev, rows_a, perm, scum_a, buf, carry);
-  if (scum_b) blkcum_steps(ev, rows_b, perm, scum_b, buf, carry);
+  if (scum_b && !same) blkcum_steps(ev, rows_b, perm, scum_b, buf, carry);
+  if (same) {
+    for (int i = threadIdx.x; i <= B; i += blockDim.x) {
+      if (blk_b) blk_b[i] = blk_a[i];
+      if (scum_b) scum_b[i] = scum_a[i];
+    }
+  }
   if (vp && !packed) valid_tiles_steps(ev, perm, vp, buf, carry);
 }
 
