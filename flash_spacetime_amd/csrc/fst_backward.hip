@@ -100,7 +100,8 @@ struct BwdRowsCfg {
   // UL (float32): the row-owner's u and w~ fragments (C values per row and
   // head) live in region R0 during the key loop instead of registers; R0
   // holds the dW reduction only after the loop. Where it fits (HP = 8, D = C
-  // = 64: 64 KB of R0's 66.5) it frees 16 C / 64 VGPRs per row of a wave.
+  // = 64: 64 KB of R0's 66.5) it frees C / 2 VGPRs per row of a wave (64 at
+  // cfg4's two rows per wave).
   static constexpr int UW_BYTES = 2 * ROWS * HP * C * 4;
   static constexpr bool UL = !BF && !KVS && UW_BYTES <= R0_BYTES;
   // KE (K from global memory): a chunk's transposed K (the dQ product's
