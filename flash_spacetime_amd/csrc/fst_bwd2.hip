@@ -89,7 +89,13 @@ struct Rows2Cfg {
   // wave, or per pair of waves w, w + 4) in the same bytes; one channel step
   // of H (or G) after them, each wave's rows its own.
   static constexpr int DW_BYTES = 4 * (D * C + D) * 4;
-  static constexpr int XS_BYTES = 16 * HP * D * 2;
+  // The rows are staged [op][head][16 rows of XS_RS + pad] (bf16): the dW
+  // products read four rows of one head and feature per lane with one
+  // transposing read, and these strides put lane groups 0 and 1 (2 and 3),
+  // which share an LDS phase, on disjoint banks.
+  static constexpr int XS_RS = D == 64 ? 80 : D;                     // row stride
+  static constexpr int XS_HS = 16 * XS_RS + (D == 32 ? 16 : 64);     // head stride
+  static constexpr int XS_BYTES = HP * XS_HS * 2;
   static constexpr int X_DW = DW_BYTES > 2 * XS_BYTES ? DW_BYTES : 2 * XS_BYTES;
   static constexpr int HG_BYTES = 16 * HP * 16 * 4;
   static constexpr int EPI = X_DW + HG_BYTES;
@@ -802,14 +808,14 @@ __global__ __launch_bounds__(64 * NW, WPE) void bwd_rows2_kernel(BwdParams prm) 
 #pragma unroll
       for (int hl = 0; hl < HW; ++hl) {
         const int h = head(hl);
-        if (h < HP) (op == 0 ? qf[hl] : dof[hl]).store(Xs + op * 16 * HP * D + (n * HP + h) * D, g);
+        if (h < HP) (op == 0 ? qf[hl] : dof[hl]).store(Xs + (op * HP + h) * Cfg::XS_HS + n * Cfg::XS_RS, g);
       }
     }
     __syncthreads();
 #pragma unroll
     for (int op = 0; op < 2; ++op) {
       if (!(op == 0 ? attn : act)) continue;
-      const bf16* Xo = Xs + op * 16 * HP * D;
+      const bf16* Xo = Xs + op * HP * Cfg::XS_HS;
 #pragma unroll
       for (int ct = 0; ct < NCT; ++ct) {
         // The wave's own rows, exchanged between its lanes: wave_lds_sync
@@ -835,12 +841,15 @@ __global__ __launch_bounds__(64 * NW, WPE) void bwd_rows2_kernel(BwdParams prm) 
           split4(bv, bh, bl);
 #pragma unroll
           for (int q = 0; q < NQ; ++q) {
-            bf16x4 av{};
+            // Lane n of the group receives rows row0 .. row0 + 3 of feature
+            // 16 q + n; source lane n supplies row row0 + n / 4 (clamped to
+            // the wave's rows: the others meet zero slots of B), features
+            // 16 q + 4 (n % 4) .. + 3.
+            const bf16* src = Xo + h * Cfg::XS_HS + (row0 + min(n >> 2, RPW - 1)) * Cfg::XS_RS + 16 * q + 4 * (n & 3);
+            const bf16x4 av = __builtin_amdgcn_ds_read_tr16_b64_v4bf16((lds_bf16x4*)(src));
+            if (op == 1 && ct == 0)
 #pragma unroll
-            for (int e = 0; e < RPW && e < 4; ++e) {
-              av[e] = Xo[((row0 + e) * HP + h) * D + 16 * q + n];
-              if (op == 1 && ct == 0) dbl[q] += (float)av[e];
-            }
+              for (int e = 0; e < RPW && e < 4; ++e) dbl[q] += (float)av[e];
             dw[q][ct] = mfma_x16(av, bl, dw[q][ct]);
             dw[q][ct] = mfma_x16(av, bh, dw[q][ct]);
           }
