@@ -73,38 +73,61 @@ static void freq_table(int C, FreqTable& ft) {
   }
 }
 
+// Inclusive scan of x over the work list's 1024 threads under op (a sum or a
+// max; 0 is the identity for the values scanned here): within each wave by
+// lane shuffles, then each thread combines the totals of the waves before it
+// (broadcast LDS reads after one barrier). total receives the workgroup's
+// result. wsum (16 ints) is reused: the caller puts a barrier between calls.
+template <typename Op>
+__device__ int block_scan(int x, int* wsum, int& total, Op op) {
+  const int lane = threadIdx.x & 63, wv = threadIdx.x >> 6;
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+    const int o = __shfl_up(x, off);
+    if (lane >= off) x = op(x, o);
+  }
+  if (lane == 63) wsum[wv] = x;
+  __syncthreads();
+  int pre = 0;
+  total = 0;
+#pragma unroll
+  for (int k = 0; k < 16; ++k) {
+    const int s = wsum[k];
+    if (k < wv) pre = op(pre, s);
+    total = op(total, s);
+  }
+  return op(pre, x);
+}
+
+// Exclusive prefix sums of val(i), i < n, into out[0 .. n] (out[0] = 0);
+// one workgroup, chunks of 1024 with a carry.
+template <typename F>
+__device__ void scan_steps(int n, F val, int32_t* out, int* wsum) {
+  const int t = threadIdx.x;
+  if (t == 0) out[0] = 0;
+  int carry = 0;
+  for (int base = 0; base < n; base += 1024) {
+    const int i = base + t;
+    int total;
+    const int inc = block_scan(i < n ? val(i) : 0, wsum, total, [](int a, int c) { return a + c; });
+    if (i < n) out[i + 1] = carry + inc;
+    carry += total;
+    __syncthreads();
+  }
+}
+
 // Number of row blocks of each event and their prefix sum, over the events
 // in index order, or in the order perm gives when not null; one workgroup.
 // Padded events always get one block so that their padding rows are zeroed.
-__device__ void blkcum_steps(const EventSpec& ev, int rows, const int32_t* perm, int32_t* blkcum, int* buf,
-                             int& carry) {
-  const int t = threadIdx.x;
-  if (t == 0) {
-    carry = 0;
-    blkcum[0] = 0;
-  }
-  __syncthreads();
-  for (int base = 0; base < ev.B; base += 1024) {
-    const int b = base + t;
-    int nb = 0;
-    if (b < ev.B) {
-      int tok0, len;
-      event_range(ev, perm ? perm[b] : b, tok0, len);
-      nb = len > 0 ? (len + rows - 1) / rows : (ev.packed ? 0 : 1);
-    }
-    buf[t] = nb;
-    __syncthreads();
-    for (int off = 1; off < 1024; off <<= 1) {
-      const int add = t >= off ? buf[t - off] : 0;
-      __syncthreads();
-      buf[t] += add;
-      __syncthreads();
-    }
-    if (b < ev.B) blkcum[b + 1] = carry + buf[t];
-    __syncthreads();
-    if (t == 1023) carry += buf[1023];
-    __syncthreads();
-  }
+__device__ void blkcum_steps(const EventSpec& ev, int rows, const int32_t* perm, int32_t* blkcum, int* wsum) {
+  scan_steps(
+      ev.B,
+      [&](int b) {
+        int tok0, len;
+        event_range(ev, perm ? perm[b] : b, tok0, len);
+        return len > 0 ? (len + rows - 1) / rows : (ev.packed ? 0 : 1);
+      },
+      blkcum, wsum);
 }
 
 // Schedule of the tile kernels: the events ordered by decreasing valid
@@ -169,12 +192,9 @@ __device__ void sort_steps(const EventSpec& ev, int32_t* perm, int* keys) {
 // kernels then write NaN into every event's rows instead of computing.
 // cu[B] < T is allowed: tokens past cu[B] belong to no event and are left
 // unwritten.
-__device__ void sanitize_steps(const int32_t* cu, int B, int T, int32_t* cus, int32_t* status, int* buf,
-                               int& carry) {
+__device__ void sanitize_steps(const int32_t* cu, int B, int T, int32_t* cus, int32_t* status, int* wsum) {
   const int t = threadIdx.x;
-  int bad = 0;
-  if (t == 0) carry = 0;
-  __syncthreads();
+  int bad = 0, carry = 0;
   for (int base = 0; base <= B; base += 1024) {
     const int b = base + t;
     int x = 0;
@@ -183,55 +203,21 @@ __device__ void sanitize_steps(const int32_t* cu, int B, int T, int32_t* cus, in
       if (b == 0 ? x != 0 : x < cu[b - 1]) bad = 1;
       if (b == B && x > T) bad = 1;
     }
-    buf[t] = x;
-    __syncthreads();
-    for (int off = 1; off < 1024; off <<= 1) {
-      const int o = t >= off ? buf[t - off] : 0;
-      __syncthreads();
-      buf[t] = max(buf[t], o);
-      __syncthreads();
-    }
-    if (b <= B) cus[b] = min(max(carry, buf[t]), T);
-    __syncthreads();
-    if (t == 1023) carry = max(carry, buf[1023]);
+    int total;
+    const int inc = block_scan(x, wsum, total, [](int a, int c) { return max(a, c); });
+    if (b <= B) cus[b] = min(max(carry, inc), T);
+    carry = max(carry, total);
     __syncthreads();
   }
   bad = __syncthreads_or(bad);
   if (t == 0) *status = bad;
 }
 
-// Exclusive prefix sums of val(i), i < n, into out[0 .. n] (out[0] = 0);
-// one workgroup, chunks of 1024 with a carry.
-template <typename F>
-__device__ void scan_steps(int n, F val, int32_t* out, int* buf, int& carry) {
-  const int t = threadIdx.x;
-  if (t == 0) {
-    carry = 0;
-    out[0] = 0;
-  }
-  __syncthreads();
-  for (int base = 0; base < n; base += 1024) {
-    const int i = base + t;
-    buf[t] = i < n ? val(i) : 0;
-    __syncthreads();
-    for (int off = 1; off < 1024; off <<= 1) {
-      const int add = t >= off ? buf[t - off] : 0;
-      __syncthreads();
-      buf[t] += add;
-      __syncthreads();
-    }
-    if (i < n) out[i + 1] = carry + buf[t];
-    __syncthreads();
-    if (t == 1023) carry += buf[1023];
-    __syncthreads();
-  }
-}
-
 // The padding-last schedule's prefix sums (EventSpec::vp): valid 16-row tiles
 // of the padded events in XCD order, entry x S + j for XCD x's j-th event
 // (rank 8 j + (j odd ? 7 - x : x), as tile_block deals them), 0 past the
 // events; an empty event keeps one tile (its zero dW / db slot).
-__device__ void valid_tiles_steps(const EventSpec& ev, const int32_t* perm, int32_t* vp, int* buf, int& carry) {
+__device__ void valid_tiles_steps(const EventSpec& ev, const int32_t* perm, int32_t* vp, int* wsum) {
   const int B = ev.B, S = (B + 7) >> 3;
   scan_steps(
       8 * S,
@@ -242,7 +228,7 @@ __device__ void valid_tiles_steps(const EventSpec& ev, const int32_t* perm, int3
         event_range(ev, perm[r], tok0, len);
         return len > 0 ? (len + 15) >> 4 : 1;
       },
-      vp, buf, carry);
+      vp, wsum);
 }
 
 // The work list of one operator call in one launch (one workgroup, steps
@@ -257,10 +243,9 @@ __global__ __launch_bounds__(1024) void worklist_kernel(const int32_t* lens, int
                                                         int32_t* perm, int32_t* scum_a, int32_t* scum_b,
                                                         int32_t* cus, int32_t* status, int32_t* vp) {
   extern __shared__ int keys[];
-  __shared__ int buf[1024];
-  __shared__ int carry;
+  __shared__ int wsum[16];
   if (packed) {
-    sanitize_steps(lens, B, T, cus, status, buf, carry);
+    sanitize_steps(lens, B, T, cus, status, wsum);
   } else if (threadIdx.x == 0) {
     *status = 0;
   }
@@ -271,22 +256,22 @@ __global__ __launch_bounds__(1024) void worklist_kernel(const int32_t* lens, int
   ev.B = B;
   ev.L = L;
   ev.T = T;
-  blkcum_steps(ev, rows_a, nullptr, blk_a, buf, carry);
+  blkcum_steps(ev, rows_a, nullptr, blk_a, wsum);
   // The second family's lists equal the first's when its blocks are as tall
   // (the bf16 backward: 16 rows and 16 keys): copied instead of rescanned.
   const bool same = rows_b == rows_a;
-  if (blk_b && !same) blkcum_steps(ev, rows_b, nullptr, blk_b, buf, carry);
+  if (blk_b && !same) blkcum_steps(ev, rows_b, nullptr, blk_b, wsum);
   sort_steps(ev, perm, keys);
   __syncthreads();
-  if (scum_a) blkcum_steps(ev, rows_a, perm, scum_a, buf, carry);
-  if (scum_b && !same) blkcum_steps(ev, rows_b, perm, scum_b, buf, carry);
+  if (scum_a) blkcum_steps(ev, rows_a, perm, scum_a, wsum);
+  if (scum_b && !same) blkcum_steps(ev, rows_b, perm, scum_b, wsum);
   if (same) {
     for (int i = threadIdx.x; i <= B; i += blockDim.x) {
       if (blk_b) blk_b[i] = blk_a[i];
       if (scum_b) scum_b[i] = scum_a[i];
     }
   }
-  if (vp && !packed) valid_tiles_steps(ev, perm, vp, buf, carry);
+  if (vp && !packed) valid_tiles_steps(ev, perm, vp, wsum);
 }
 
 static int launch_worklist(const int32_t* lens, bool packed, int B, int L, int T, int rows_a, int32_t* blk_a,
