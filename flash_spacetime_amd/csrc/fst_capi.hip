@@ -134,10 +134,89 @@ __device__ void blkcum_steps(const EventSpec& ev, int rows, const int32_t* perm,
 // length (ties by index; lengths past 2^18 - 1 count as 2^18 - 1), one
 // workgroup. Up to 1024 events each thread ranks one key by counting the
 // larger ones (the keys are distinct, so the ranks are a permutation; one
-// barrier, broadcast LDS reads); up to 8192 a bitonic sort in LDS. Past 8192
-// events the identity order is used.
+// barrier, broadcast LDS reads); up to 8192 a bitonic sort with the keys in
+// registers (bitonic_regs). Past 8192 events the identity order is used.
 constexpr int kSortMax = 8192;
 constexpr int kRankMax = 1024;
+
+__device__ int sort_key(const EventSpec& ev, int i) {
+  if (i >= ev.B) return -1;
+  int tok0, l;
+  event_range(ev, i, tok0, l);
+  l = l < (1 << 18) - 1 ? l : (1 << 18) - 1;
+  return (l << 13) | (kSortMax - 1 - i);
+}
+
+// One compare-exchange step at distance J < KPT: both keys of each pair are
+// in the thread's registers. Position p = KPT t + r; the pair's lower
+// position keeps the larger key where bit k of p is clear (a descending
+// block), the smaller one elsewhere.
+template <int KPT, int J>
+__device__ __forceinline__ void bitonic_in_thread(int* x, int k) {
+  if constexpr (J < KPT) {
+#pragma unroll
+    for (int r = 0; r < KPT; ++r)
+      if ((r & J) == 0) {
+        const int a = x[r], b = x[r | J];
+        const bool desc = ((KPT * (int)threadIdx.x + r) & k) == 0;
+        x[r] = desc ? max(a, b) : min(a, b);
+        x[r | J] = desc ? min(a, b) : max(a, b);
+      }
+  }
+}
+
+// Bitonic sort, descending, of the 1024 KPT keys thread t holds at
+// positions KPT t .. KPT t + KPT - 1 (registers x). Steps whose pairs lie in
+// one thread (distance j < KPT) or one wave (j < 64 KPT: lane shuffles) take
+// no barrier; the others (j >= 64 KPT) exchange through LDS, two barriers
+// each.
+template <int KPT>
+__device__ void bitonic_regs(int* x, int* keys) {
+  const int t = threadIdx.x;
+  for (int k = 2; k <= 1024 * KPT; k <<= 1)
+    for (int j = k >> 1; j > 0; j >>= 1) {
+      if (j < KPT) {
+        if (j == 1)
+          bitonic_in_thread<KPT, 1>(x, k);
+        else if (j == 2)
+          bitonic_in_thread<KPT, 2>(x, k);
+        else
+          bitonic_in_thread<KPT, 4>(x, k);
+      } else if (j < 64 * KPT) {
+#pragma unroll
+        for (int r = 0; r < KPT; ++r) {
+          const int p = KPT * t + r;
+          const int o = __shfl_xor(x[r], j / KPT);
+          const bool keep_max = ((p & j) == 0) == ((p & k) == 0);
+          x[r] = keep_max ? max(x[r], o) : min(x[r], o);
+        }
+      } else {
+#pragma unroll
+        for (int r = 0; r < KPT; ++r) keys[KPT * t + r] = x[r];
+        __syncthreads();
+#pragma unroll
+        for (int r = 0; r < KPT; ++r) {
+          const int p = KPT * t + r;
+          const int o = keys[p ^ j];
+          const bool keep_max = ((p & j) == 0) == ((p & k) == 0);
+          x[r] = keep_max ? max(x[r], o) : min(x[r], o);
+        }
+        __syncthreads();
+      }
+    }
+}
+
+template <int KPT>
+__device__ void sort_regs(const EventSpec& ev, int32_t* perm, int* keys) {
+  const int t = threadIdx.x;
+  int x[KPT];
+#pragma unroll
+  for (int r = 0; r < KPT; ++r) x[r] = sort_key(ev, KPT * t + r);
+  bitonic_regs<KPT>(x, keys);
+#pragma unroll
+  for (int r = 0; r < KPT; ++r)
+    if (KPT * t + r < ev.B) perm[KPT * t + r] = kSortMax - 1 - (x[r] & (kSortMax - 1));
+}
 
 __device__ void sort_steps(const EventSpec& ev, int32_t* perm, int* keys) {
   const int t = threadIdx.x, B = ev.B;
@@ -145,20 +224,9 @@ __device__ void sort_steps(const EventSpec& ev, int32_t* perm, int* keys) {
     for (int i = t; i < B; i += 1024) perm[i] = i;
     return;
   }
-  int p2 = 1;
-  while (p2 < B) p2 <<= 1;
-  for (int i = t; i < p2; i += 1024) {
-    int key = -1;
-    if (i < B) {
-      int tok0, l;
-      event_range(ev, i, tok0, l);
-      l = l < (1 << 18) - 1 ? l : (1 << 18) - 1;
-      key = (l << 13) | (kSortMax - 1 - i);
-    }
-    keys[i] = key;
-  }
-  __syncthreads();
   if (B <= kRankMax) {
+    if (t < B) keys[t] = sort_key(ev, t);
+    __syncthreads();
     if (t < B) {
       const int mine = keys[t];
       int rank = 0;
@@ -167,21 +235,12 @@ __device__ void sort_steps(const EventSpec& ev, int32_t* perm, int* keys) {
     }
     return;
   }
-  for (int k = 2; k <= p2; k <<= 1)
-    for (int j = k >> 1; j > 0; j >>= 1) {
-      for (int i = t; i < p2; i += 1024) {
-        const int l = i ^ j;
-        if (l > i) {
-          const int a = keys[i], b = keys[l];
-          if ((i & k) == 0 ? (a < b) : (a > b)) {
-            keys[i] = b;
-            keys[l] = a;
-          }
-        }
-      }
-      __syncthreads();
-    }
-  for (int i = t; i < B; i += 1024) perm[i] = kSortMax - 1 - (keys[i] & (kSortMax - 1));
+  if (B <= 2048)
+    sort_regs<2>(ev, perm, keys);
+  else if (B <= 4096)
+    sort_regs<4>(ev, perm, keys);
+  else
+    sort_regs<8>(ev, perm, keys);
 }
 
 // Packed offsets as the kernels read them: cus[b] = the running maximum of

@@ -122,7 +122,7 @@ def test_packed_sorted_schedule_is_deterministic():
     assert torch.equal(a[0], c[0]) and all(torch.equal(x, y) for x, y in zip(a[1], c[1]))
 
 
-@pytest.mark.parametrize("batch", [1, 5, 256, 1024, 1025, 3000, 8192, 9000])
+@pytest.mark.parametrize("batch", [1, 5, 256, 1024, 1025, 2048, 2049, 3000, 4096, 4097, 8192, 9000])
 def test_event_sort_order(batch):
     """The forward work list's event order (workspace ints B+1 .. 2B): events
     by decreasing length, ties by index, up to 8192 events (rank sort up to
