@@ -916,6 +916,13 @@ __global__ __launch_bounds__(256, OCC) void bwd_cols2_kernel(BwdParams prm) {
   using DT = DTiles<D>;
   constexpr int HW = Cfg::HW, NS = Cfg::NS, NCT = Cfg::NCT, NQ = DT::NQ, RGW = Cfg::RGW;
   constexpr bool QL = Cfg::QL;
+  // TR: the transposed qt / dO reads in QoTile::tr_frag's order, free of
+  // bank conflicts, with dk / dv regathered into 16-byte store order through
+  // LDS once per tile; elsewhere tr_frag_dmap's order, which needs no
+  // regather. Measured (bitwise equal): D = C = 64 with HP <= 8 cols -1.7 to
+  // -5 % (cfg4 3.15 -> 3.02 ms; H = 4 -2.4 %); C = 32 or 48, HP = 12 or
+  // D = 32 +0.6 to +6 %, so only there.
+  constexpr bool TR = QL && D == 64 && C == 64 && HP <= 8;
   constexpr int NP = D / 32;  // 32-feature parts of a row (QL)
   extern __shared__ __align__(16) unsigned char smem[];
   unsigned char* stU = smem;                 // u.E
@@ -1226,8 +1233,10 @@ __global__ __launch_bounds__(256, OCC) void bwd_cols2_kernel(BwdParams prm) {
         JFrag<bf16, NS> ot, qt;
         if constexpr (QL) {
           const int h = w * HW + hl;
-          ot.v = QoTile::tr_frag_dmap(qo + ((1 * HP + h) * NP + (q >> 1)) * 1024, q, g, n);
-          qt.v = QoTile::tr_frag_dmap(qo + ((0 * HP + h) * NP + (q >> 1)) * 1024, q, g, n);
+          const unsigned char* ob = qo + ((1 * HP + h) * NP + (q >> 1)) * 1024;
+          const unsigned char* qb = qo + ((0 * HP + h) * NP + (q >> 1)) * 1024;
+          ot.v = TR ? QoTile::tr_frag(ob, q, g, n) : QoTile::tr_frag_dmap(ob, q, g, n);
+          qt.v = TR ? QoTile::tr_frag(qb, q, g, n) : QoTile::tr_frag_dmap(qb, q, g, n);
         } else if constexpr (NS == 2) {
           ot.v = cat8(transpose_x16(DT::part(orw[hl][0], q), id), transpose_x16(DT::part(orw[hl][1], q), id));
           qt.v = cat8(transpose_x16(DT::part(qr[hl][0], q), id), transpose_x16(DT::part(qr[hl][1], q), id));
@@ -1255,8 +1264,35 @@ __global__ __launch_bounds__(256, OCC) void bwd_cols2_kernel(BwdParams prm) {
 
   // ---- store dk, dv (lane n = key) ----
   // Accumulator q holds features DTiles::dmap(q, g, r) (with the tiles in LDS
-  // (QL) the transposed reads' order): where D is a multiple of 32, 8
-  // consecutive features per lane group across the accumulator pair 2t, 2t + 1.
+  // (QL) the transposed reads' order), or under TR 16 q + 4 g + r, regathered
+  // into dmap order first: where D is a multiple of 32, 8 consecutive
+  // features per lane group across the accumulator pair 2t, 2t + 1.
+  [[maybe_unused]] bf16x8 kst[HW][NQ / 2 > 0 ? NQ / 2 : 1], vst[HW][NQ / 2 > 0 ? NQ / 2 : 1];
+  if constexpr (TR && DT::X32) {
+    // Wave-private 1 KB blocks per (head, tensor, 32-feature part), key n's
+    // row at 64 n: lane (g, n) writes features 4g + r and 16 + 4g + r and
+    // reads back 8g .. 8g + 7. The last chunk's barrier has freed the LDS.
+    static_assert(HP * NQ * 1024 <= Cfg::LDS_BYTES, "regather blocks exceed the LDS plan");
+#pragma unroll
+    for (int hl = 0; hl < HW; ++hl)
+#pragma unroll
+      for (int t = 0; t < NQ / 2; ++t) {
+        unsigned char* bk = smem + (((w * HW + hl) * 2 + 0) * (NQ / 2) + t) * 1024 + n * 64;
+        unsigned char* bv = smem + (((w * HW + hl) * 2 + 1) * (NQ / 2) + t) * 1024 + n * 64;
+        *reinterpret_cast<bf16x4*>(bk + 8 * g) = pack4(dK[hl][2 * t]);
+        *reinterpret_cast<bf16x4*>(bk + 32 + 8 * g) = pack4(dK[hl][2 * t + 1]);
+        *reinterpret_cast<bf16x4*>(bv + 8 * g) = pack4(dV[hl][2 * t]);
+        *reinterpret_cast<bf16x4*>(bv + 32 + 8 * g) = pack4(dV[hl][2 * t + 1]);
+      }
+    wave_lds_sync();
+#pragma unroll
+    for (int hl = 0; hl < HW; ++hl)
+#pragma unroll
+      for (int t = 0; t < NQ / 2; ++t) {
+        kst[hl][t] = *reinterpret_cast<const bf16x8*>(smem + (((w * HW + hl) * 2 + 0) * (NQ / 2) + t) * 1024 + n * 64 + 16 * g);
+        vst[hl][t] = *reinterpret_cast<const bf16x8*>(smem + (((w * HW + hl) * 2 + 1) * (NQ / 2) + t) * 1024 + n * 64 + 16 * g);
+      }
+  }
   if (key_ok) {
 #pragma unroll
     for (int hl = 0; hl < HW; ++hl) {
@@ -1267,8 +1303,13 @@ __global__ __launch_bounds__(256, OCC) void bwd_cols2_kernel(BwdParams prm) {
       if constexpr (DT::X32) {
 #pragma unroll
         for (int t = 0; t < NQ / 2; ++t) {
-          *reinterpret_cast<bf16x8*>(krow + DT::dmap(2 * t, g, 0)) = cat8(pack4(dK[hl][2 * t]), pack4(dK[hl][2 * t + 1]));
-          *reinterpret_cast<bf16x8*>(vrow + DT::dmap(2 * t, g, 0)) = cat8(pack4(dV[hl][2 * t]), pack4(dV[hl][2 * t + 1]));
+          if constexpr (TR) {
+            *reinterpret_cast<bf16x8*>(krow + DT::dmap(2 * t, g, 0)) = kst[hl][t];
+            *reinterpret_cast<bf16x8*>(vrow + DT::dmap(2 * t, g, 0)) = vst[hl][t];
+          } else {
+            *reinterpret_cast<bf16x8*>(krow + DT::dmap(2 * t, g, 0)) = cat8(pack4(dK[hl][2 * t]), pack4(dK[hl][2 * t + 1]));
+            *reinterpret_cast<bf16x8*>(vrow + DT::dmap(2 * t, g, 0)) = cat8(pack4(dV[hl][2 * t]), pack4(dV[hl][2 * t + 1]));
+          }
         }
       } else {
 #pragma unroll
